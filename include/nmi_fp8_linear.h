@@ -1,0 +1,133 @@
+/*
+ * nmi_fp8_linear.h -- C ABI of the MI355X (gfx950) fp8 W8A16 linear library (libnmi.so).
+ *
+ * The library computes, for bf16 activations x [M,K], OCP e4m3 weights W [N,K] and per-row
+ * float32 scales s [N]:
+ *
+ *     y[m,n] = bf16_rne( (sum_k float(W[n,k]) * float(x[m,k])) * s[n] )     y: [M,N] bf16
+ *
+ * with float32 accumulation and a single bf16 rounding.  All pointers are device pointers
+ * (hipMalloc / torch CUDA tensors) unless stated otherwise.  `stream` is a hipStream_t passed
+ * as void* (NULL = the null stream).  No entry point allocates device memory, synchronizes
+ * the device, or retains pointers after it returns; launches are asynchronous on `stream`.
+ *
+ * Return value: NMI_OK (0) on success; a negative NMI_ERR_* for argument errors detected on
+ * the host before anything is launched; a positive hipError_t value when a HIP call fails.
+ * nmi_last_error() describes the last failure of the calling thread.
+ *
+ * Layouts: x row m starts at x + m*ldx elements; W row n at W + n*ldw bytes; y row m at
+ * y + m*ldy elements.  Row-sliced calls pass offset pointers (W + r0*ldw, s + r0, y + r0)
+ * with ldy of the full output, as nemotron_infer's mamba block does for in_proj
+ * (csrc/include/model/mamba_block.cuh:386-391, 476-481).
+ *
+ * Requirements checked on every call (NMI_ERR_INVALID_ARG / NMI_ERR_ALIGNMENT otherwise):
+ *   M >= 1, N >= 1, K >= 16, K % 16 == 0, ldx >= K, ldw >= K, ldy >= N,
+ *   W and ldw 16-byte aligned, x and ldx*2 16-byte aligned, s 4-byte aligned,
+ *   y 2-byte aligned, no NULL pointers.
+ * The reference silently assumes K % 16 == 0 (ops/gemv.cuh:61-63 casts every row to uint4);
+ * this ABI rejects other K instead.
+ */
+#ifndef NMI_FP8_LINEAR_H
+#define NMI_FP8_LINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    NMI_OK = 0,
+    NMI_ERR_INVALID_ARG = -1,
+    NMI_ERR_ALIGNMENT = -2,
+    NMI_ERR_UNSUPPORTED = -3,
+    NMI_ERR_WORKSPACE = -4,
+    NMI_ERR_ALLOC = -5,
+};
+
+/* Version of this ABI (major*10000 + minor*100 + patch). */
+int nmi_abi_version(void);
+
+/* Human-readable description of the calling thread's last error ("" if none). */
+const char* nmi_last_error(void);
+
+/*
+ * M = 1 decode GEMV: y[n] = bf16_rne((sum_k e4m3(W[n,k]) * x[k]) * s[n]).
+ * Replaces nemotron::ops::gemv_fp8(x, W, w_scale, y, N, K, stream)
+ * (nemotron_infer/csrc/include/ops/gemv.cuh:92-104); same argument meaning, plus a status.
+ * x: [K] bf16, W: [N,K] e4m3 with row stride K, s: [N] f32, y: [N] bf16.
+ */
+int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, void* y_bf16,
+                 int N, int K, void* stream);
+
+/*
+ * General W8A16 linear with explicit strides and the reference's M == 1 dispatch:
+ * M == 1 -> the GEMV kernel, 2 <= M <= 16 -> the skinny MFMA kernel, M > 16 -> the
+ * MFMA GEMM.  Replaces the fp8 branch of mlp_block_forward_fp8
+ * (nemotron_infer/csrc/include/model/mlp_block.cuh:142-171) and the per-projection calls
+ * in attention_block.cuh:330-350,400-409 and mamba_block.cuh:383-391,419-423,476-481,508-509.
+ * Unlike the reference's M > 1 branch, activations are NOT quantized to e4m3
+ * (ops/gemm.cuh:257-307 is not reproduced): the product is computed on bf16 activations.
+ */
+int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
+                         const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
+                         void* stream);
+
+/*
+ * Prefill GEMM y[M,N] = bf16_rne((x[M,K] . e4m3(W[N,K])^T) * s[n]) on bf16 MFMA, any M >= 1.
+ * Replaces nemotron::ops::gemm_fp8(x_fp8, W_fp8, y_bf16, x_scale, w_scale, M, N, K, ws,
+ * ws_size, stream) (nemotron_infer/csrc/include/ops/gemm.cuh:325-403) including its
+ * per-row scale epilogue (gemm.cuh:227-238, 398-402), which here is fused and rounds once.
+ * x is bf16 (no activation scale); `workspace`/`workspace_bytes` may be NULL/0 -- the
+ * current kernels need none; the arguments are kept for the split-K variants.
+ */
+int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
+                       const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Device-side e4m3 decode of `n` codes through the kernels' own conversion helpers:
+ * out_f32[i] = float(e4m3(codes[i])) (the GEMV's decode), out_scaled[i] = out_f32[i] * scale
+ * (f32 RNE product, as in the GEMV epilogue), out_bf16[i] = bf16(e4m3(codes[i])) (the GEMM's
+ * weight-tile dequant; exact).  Test entry point for the 256-code bit-exact check; mirrors
+ * static_cast<float>(__nv_fp8_e4m3) (ops/gemv.cuh:40-42) and the per-row scale product of
+ * the epilogue (ops/gemv.cuh:87-88).  n must be a positive multiple of 4; codes 4-byte,
+ * out_f32/out_scaled 16-byte and out_bf16 8-byte aligned.
+ */
+int nmi_fp8_e4m3_decode(const void* codes, float* out_f32, float* out_scaled, void* out_bf16,
+                        float scale, int n, void* stream);
+
+/*
+ * Tuning knobs for sweeps ("gemv.ks", "gemv.unroll", "gemm.tile", "skinny.ks"); 0 restores
+ * the automatic choice.  Process-wide, not thread-safe against concurrent launches; results
+ * do not depend on them beyond float32 summation order.  No counterpart in the reference
+ * (its launch shapes are compile-time constants, ops/gemv.cuh:100-103).
+ */
+int nmi_tuning_set(const char* knob, int value);
+
+/*
+ * Bump allocator for transient per-block device workspace, on hipMalloc slabs.
+ * Replaces nemotron::BumpAllocator / default_allocator()
+ * (nemotron_infer/csrc/include/tensor/allocator.cuh:58-183) and the binding's
+ * reset_allocator()/free_allocator() (csrc/include/binding.cu:59-61).
+ *   nmi_alloc(bytes, &ptr)  128-byte aligned block from the current slab; a new slab
+ *                           (>= 64 MiB) is hipMalloc'd only when none fits.
+ *   nmi_alloc_rewind()      offset back to slab 0, slabs kept (no hipMalloc/hipFree).
+ *   nmi_alloc_reset()       hipFree every slab.
+ *   nmi_alloc_stats(&total_allocated, &num_slabs)   either pointer may be NULL.
+ * Thread-safe (one mutex); one process-global allocator per process, as in the reference.
+ */
+int nmi_alloc(size_t bytes, void** out_ptr);
+int nmi_alloc_rewind(void);
+int nmi_alloc_reset(void);
+int nmi_alloc_stats(size_t* total_allocated, size_t* num_slabs);
+
+/* hipDeviceSynchronize(); replaces the binding's sync() (csrc/include/binding.cu:62). */
+int nmi_sync(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NMI_FP8_LINEAR_H */

@@ -1,0 +1,68 @@
+"""ctypes binding of the C ABI in include/nmi_fp8_linear.h (libnmi.so).
+
+There is no CPU fallback: if the library is missing, ``lib()`` raises.  Build it with
+``python -m nemotron_infer_amd.build``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libnmi.so")
+
+NMI_OK = 0
+NMI_ERR_INVALID_ARG = -1
+NMI_ERR_ALIGNMENT = -2
+NMI_ERR_UNSUPPORTED = -3
+NMI_ERR_WORKSPACE = -4
+NMI_ERR_ALLOC = -5
+
+# Every symbol the header declares, with its ctypes signature.
+_vp, _i, _i64, _sz, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+SIGNATURES = {
+    "nmi_abi_version": ([], _i),
+    "nmi_last_error": ([], ctypes.c_char_p),
+    "nmi_gemv_fp8": ([_vp, _vp, _vp, _vp, _i, _i, _vp], _i),
+    "nmi_linear_fp8_w8a16": ([_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _vp], _i),
+    "nmi_gemm_fp8_w8a16": ([_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _vp, _sz, _vp], _i),
+    "nmi_fp8_e4m3_decode": ([_vp, _vp, _vp, _vp, _f, _i, _vp], _i),
+    "nmi_tuning_set": ([ctypes.c_char_p, _i], _i),
+    "nmi_alloc": ([_sz, ctypes.POINTER(_vp)], _i),
+    "nmi_alloc_rewind": ([], _i),
+    "nmi_alloc_reset": ([], _i),
+    "nmi_alloc_stats": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
+    "nmi_sync": ([], _i),
+}
+
+_lib = None
+
+
+class NmiError(RuntimeError):
+    def __init__(self, code: int, where: str, msg: str):
+        super().__init__(f"{where} failed with status {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    """Load libnmi.so once; raise if it is missing (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python -m nemotron_infer_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def check(rc: int, where: str) -> None:
+    if rc != NMI_OK:
+        raise NmiError(rc, where, lib().nmi_last_error().decode())
+
+
+def tuning_set(knob: str, value: int) -> None:
+    check(lib().nmi_tuning_set(knob.encode(), int(value)), "nmi_tuning_set")

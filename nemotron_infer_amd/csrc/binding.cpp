@@ -1,0 +1,127 @@
+// binding.cpp -- pybind11 module `binding`, the drop-in for nemotron_infer.csrc.binding.
+//
+// Same module name, constants and entry-point names/arities as the reference's
+// PYBIND11_MODULE(binding, m) (nemotron_infer/csrc/include/binding.cu:210-246; stub
+// nemotron_infer/csrc/binding.pyi).  All device pointers are passed as integers
+// (tensor.data_ptr()), every call is asynchronous on the null stream, and returns None, as in
+// the reference.  The module is C++ over the C ABI of libnmi.so (include/nmi_fp8_linear.h);
+// it never includes HIP headers.
+//
+// Built here: the fp8 linear hot path (linear_fp8, gemv_fp8) and the allocator/sync
+// entries.  Reference entries outside that path exist with the reference's arity and raise
+// NotImplementedError naming what is missing, so a caller fails loudly instead of computing
+// something else.
+#include <pybind11/pybind11.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "nmi_fp8_linear.h"
+
+namespace py = pybind11;
+
+namespace cfg {  // real-model configuration, as binding.cu:35-46
+constexpr int HIDDEN = 3136;
+constexpr int H = 96, P = 80, N = 128, G = 8, CONV_K = 4;
+constexpr int H_Q = 40, H_KV = 8, HEAD = 128;
+constexpr int INTER = 12544;
+constexpr int VOCAB = 131072;
+}  // namespace cfg
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != NMI_OK) throw std::runtime_error(std::string(what) + ": " + nmi_last_error());
+}
+
+const void* cp(uintptr_t p) { return reinterpret_cast<const void*>(p); }
+void* mp(uintptr_t p) { return reinterpret_cast<void*>(p); }
+const float* cf(uintptr_t p) { return reinterpret_cast<const float*>(p); }
+
+[[noreturn]] void not_built(const char* name) {
+    std::string msg = std::string(name) +
+                      " is not part of this build: nemotron_infer_amd implements the fp8 W8A16 linear hot "
+                      "path (linear_fp8, gemv_fp8) only";
+    PyErr_SetString(PyExc_NotImplementedError, msg.c_str());
+    throw py::error_already_set();
+}
+
+}  // namespace
+
+PYBIND11_MODULE(binding, m) {
+    m.doc() = "nemotron_infer_amd: MI355X fp8 W8A16 linear (drop-in for nemotron_infer.csrc.binding)";
+
+    m.attr("HIDDEN") = cfg::HIDDEN;
+    m.attr("H") = cfg::H;
+    m.attr("P") = cfg::P;
+    m.attr("N") = cfg::N;
+    m.attr("G") = cfg::G;
+    m.attr("CONV_K") = cfg::CONV_K;
+    m.attr("H_Q") = cfg::H_Q;
+    m.attr("H_KV") = cfg::H_KV;
+    m.attr("HEAD") = cfg::HEAD;
+    m.attr("INTER") = cfg::INTER;
+    m.attr("VOCAB") = cfg::VOCAB;
+    m.attr("CONV_DIM") = cfg::H * cfg::P + 2 * cfg::G * cfg::N;
+    m.attr("IN_PROJ") = cfg::H * cfg::P + (cfg::H * cfg::P + 2 * cfg::G * cfg::N) + cfg::H;
+
+    // binding.cu:59-62
+    m.def("reset_allocator", [] { check(nmi_alloc_rewind(), "reset_allocator"); });
+    m.def("free_allocator", [] { check(nmi_alloc_reset(), "free_allocator"); });
+    m.def("sync", [] { check(nmi_sync(), "sync"); });
+
+    // The fp8 W8A16 linear: y[M,N] = bf16((x[M,K] . e4m3(W[N,K])^T) * s[N]).  Not exported by
+    // the reference's module (its linears are reached only through the blocks); kept as the
+    // test and bench entry of this build.
+    m.def(
+        "linear_fp8",
+        [](uintptr_t x, int64_t ldx, uintptr_t w, int64_t ldw, uintptr_t s, uintptr_t y,
+           int64_t ldy, int M, int N, int K) {
+            check(nmi_linear_fp8_w8a16(cp(x), ldx, cp(w), ldw, cf(s), mp(y), ldy, M, N, K, nullptr),
+                  "linear_fp8");
+        },
+        py::arg("x"), py::arg("ldx"), py::arg("w"), py::arg("ldw"), py::arg("w_scale"), py::arg("y"),
+        py::arg("ldy"), py::arg("M"), py::arg("N"), py::arg("K"));
+    // ops/gemv.cuh:92-104 gemv_fp8(x, W, w_scale, y, N, K)
+    m.def(
+        "gemv_fp8",
+        [](uintptr_t x, uintptr_t w, uintptr_t s, uintptr_t y, int N, int K) {
+            check(nmi_gemv_fp8(cp(x), cp(w), cf(s), mp(y), N, K, nullptr), "gemv_fp8");
+        },
+        py::arg("x"), py::arg("W"), py::arg("w_scale"), py::arg("y"), py::arg("N"), py::arg("K"));
+
+    // Reference entries outside the fp8 linear path (binding.cu:231-245), reference arity.
+    m.def("embedding", [](uintptr_t, uintptr_t, uintptr_t, int) { not_built("embedding"); });
+    m.def("rmsnorm", [](uintptr_t, uintptr_t, uintptr_t, int) { not_built("rmsnorm"); });
+    m.def("lm_head", [](uintptr_t, uintptr_t, uintptr_t, int) { not_built("lm_head"); });
+    m.def("mamba_forward", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                              uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int, int, uintptr_t,
+                              uintptr_t) { not_built("mamba_forward"); });
+    m.def("mamba_decode", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                             uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                             int) { not_built("mamba_decode"); });
+    m.def("attn_forward", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                             int, uintptr_t, uintptr_t, int) { not_built("attn_forward"); });
+    m.def("attn_decode", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                            uintptr_t, int, int, uintptr_t) { not_built("attn_decode"); });
+    m.def("mlp_forward", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int) {
+        not_built("mlp_forward");
+    });
+    m.def("mamba_forward_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                                  uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                                  uintptr_t, int, int, uintptr_t, uintptr_t) {
+        not_built("mamba_forward_fp8");
+    });
+    m.def("mamba_decode_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                                 uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                                 uintptr_t, uintptr_t, uintptr_t, int) { not_built("mamba_decode_fp8"); });
+    m.def("attn_forward_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                                 uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int, uintptr_t,
+                                 uintptr_t, int) { not_built("attn_forward_fp8"); });
+    m.def("attn_decode_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                                uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int, int,
+                                uintptr_t) { not_built("attn_decode_fp8"); });
+    m.def("mlp_forward_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+                                uintptr_t, int) { not_built("mlp_forward_fp8"); });
+}

@@ -1,0 +1,180 @@
+// capi.cpp -- extern "C" boundary of libnmi.so (declared in include/nmi_fp8_linear.h).
+//
+// Validates every argument on the host before anything is launched (the reference checks
+// nothing: ops/gemv.cuh:92-104 and ops/gemm.cuh:325-403 launch unconditionally and ignore
+// return codes), records a per-thread error message, and dispatches on M as the reference's
+// fp8 blocks do (model/mlp_block.cuh:142: M == 1 -> GEMV, otherwise GEMM).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "nmi_fp8_linear.h"
+#include "nmi_launch.hpp"
+
+namespace nmi {
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return NMI_OK;
+    return fail((int)e, "%s: %s (hipError %d)", what, hipGetErrorString(e), (int)e);
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* s,
+                 const void* y, int64_t ldy, int M, int N, int K, const char* fn) {
+    if (!x || !w || !s || !y) return fail(NMI_ERR_INVALID_ARG, "%s: NULL pointer argument", fn);
+    if (M < 1 || N < 1) return fail(NMI_ERR_INVALID_ARG, "%s: M=%d N=%d must be >= 1", fn, M, N);
+    if (K < 16 || K % 16 != 0)
+        return fail(NMI_ERR_INVALID_ARG, "%s: K=%d must be a positive multiple of 16", fn, K);
+    if (ldx < K || ldw < K || ldy < N)
+        return fail(NMI_ERR_INVALID_ARG, "%s: strides ldx=%lld ldw=%lld ldy=%lld too small for K=%d N=%d",
+                    fn, (long long)ldx, (long long)ldw, (long long)ldy, K, N);
+    if (!aligned(w, 16) || ldw % 16 != 0)
+        return fail(NMI_ERR_ALIGNMENT, "%s: W and ldw must be 16-byte aligned", fn);
+    if (!aligned(x, 16) || ldx % 8 != 0)
+        return fail(NMI_ERR_ALIGNMENT, "%s: x and ldx*2 must be 16-byte aligned", fn);
+    if (!aligned(s, 4)) return fail(NMI_ERR_ALIGNMENT, "%s: w_scale must be 4-byte aligned", fn);
+    if (!aligned(y, 2)) return fail(NMI_ERR_ALIGNMENT, "%s: y must be 2-byte aligned", fn);
+    return NMI_OK;
+}
+
+std::mutex g_dev_mu;
+std::vector<DeviceInfo> g_devs;
+
+}  // namespace
+
+void set_last_error(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+}
+
+const DeviceInfo& device_info() {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    if ((int)g_devs.size() <= dev) g_devs.resize(dev + 1);
+    DeviceInfo& d = g_devs[dev];
+    if (d.device < 0) {
+        int cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cu > 0)
+            d.num_cu = cu;
+        d.device = dev;
+    }
+    return d;
+}
+
+Tuning& tuning() {
+    static Tuning t;
+    return t;
+}
+
+}  // namespace nmi
+
+using namespace nmi;
+
+extern "C" {
+
+int nmi_abi_version(void) { return 10000; }
+
+const char* nmi_last_error(void) { return g_last_error.c_str(); }
+
+int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, void* y_bf16,
+                 int N, int K, void* stream) {
+    int rc = check_linear(x_bf16, K, w_e4m3, K, w_scale, y_bf16, N, 1, N, K, "nmi_gemv_fp8");
+    if (rc) return rc;
+    return hip_status(launch_gemv_m1(static_cast<const uint16_t*>(x_bf16),
+                                     static_cast<const uint8_t*>(w_e4m3), K, w_scale,
+                                     static_cast<uint16_t*>(y_bf16), N, K,
+                                     static_cast<hipStream_t>(stream)),
+                      "nmi_gemv_fp8 launch");
+}
+
+int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
+                         const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
+                         void* stream) {
+    int rc = check_linear(x_bf16, ldx, w_e4m3, ldw, w_scale, y_bf16, ldy, M, N, K,
+                          "nmi_linear_fp8_w8a16");
+    if (rc) return rc;
+    const auto* x = static_cast<const uint16_t*>(x_bf16);
+    const auto* W = static_cast<const uint8_t*>(w_e4m3);
+    auto* y = static_cast<uint16_t*>(y_bf16);
+    auto st = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (M == 1) {
+        e = launch_gemv_m1(x, W, ldw, w_scale, y, N, K, st);
+    } else if (M <= 16) {
+        e = launch_gemv_skinny(x, ldx, W, ldw, w_scale, y, ldy, M, N, K, st);
+    } else {
+        e = launch_gemm(x, ldx, W, ldw, w_scale, y, ldy, M, N, K, st);
+    }
+    return hip_status(e, "nmi_linear_fp8_w8a16 launch");
+}
+
+int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
+                       const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    int rc = check_linear(x_bf16, ldx, w_e4m3, ldw, w_scale, y_bf16, ldy, M, N, K,
+                          "nmi_gemm_fp8_w8a16");
+    if (rc) return rc;
+    return hip_status(launch_gemm(static_cast<const uint16_t*>(x_bf16), ldx,
+                                  static_cast<const uint8_t*>(w_e4m3), ldw, w_scale,
+                                  static_cast<uint16_t*>(y_bf16), ldy, M, N, K,
+                                  static_cast<hipStream_t>(stream)),
+                      "nmi_gemm_fp8_w8a16 launch");
+}
+
+int nmi_fp8_e4m3_decode(const void* codes, float* out_f32, float* out_scaled, void* out_bf16,
+                        float scale, int n, void* stream) {
+    if (!codes || !out_f32 || !out_scaled || !out_bf16)
+        return fail(NMI_ERR_INVALID_ARG, "nmi_fp8_e4m3_decode: NULL pointer argument");
+    if (n < 4 || n % 4 != 0)
+        return fail(NMI_ERR_INVALID_ARG, "nmi_fp8_e4m3_decode: n=%d must be a positive multiple of 4", n);
+    if (!aligned(codes, 4) || !aligned(out_f32, 16) || !aligned(out_scaled, 16) || !aligned(out_bf16, 8))
+        return fail(NMI_ERR_ALIGNMENT, "nmi_fp8_e4m3_decode: misaligned buffer");
+    return hip_status(launch_decode(static_cast<const uint8_t*>(codes), out_f32, out_scaled,
+                                    static_cast<uint16_t*>(out_bf16), scale, n,
+                                    static_cast<hipStream_t>(stream)),
+                      "nmi_fp8_e4m3_decode launch");
+}
+
+int nmi_tuning_set(const char* knob, int value) {
+    if (!knob) return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: NULL knob");
+    Tuning& t = tuning();
+    if (!std::strcmp(knob, "gemv.ks")) t.gemv_ks = value;
+    else if (!std::strcmp(knob, "gemv.unroll")) t.gemv_unroll = value;
+    else if (!std::strcmp(knob, "gemm.tile")) t.gemm_tile = value;
+    else if (!std::strcmp(knob, "skinny.ks")) t.skinny_ks = value;
+    else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
+    return NMI_OK;
+}
+
+int nmi_sync(void) { return hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+
+}  // extern "C"

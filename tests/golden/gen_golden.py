@@ -1,0 +1,145 @@
+"""Generate the golden fixtures for the fp8 W8A16 linear path.
+
+Run:  python tests/golden/gen_golden.py      (writes tests/golden/*.npz and SHA256SUMS)
+
+Independence: this script does not import ``oracle/``.  Codes come from torch's own
+``float32 -> float8_e4m3fn`` cast, decoded values from torch's own ``float8_e4m3fn ->
+float32``, and expected outputs from float64 brute force.  The oracle is then checked
+against these files, so a mistake in the oracle's decode table, quantizer or linear shows
+up as a mismatch instead of being copied into the expectation.
+
+Inputs follow the reference's known-answer tests where it has them:
+* ``kat_gemv_n64_k3136``  -- GemvFP8Test.MatchesReference (tests/ops/test_gemm.cu:538-551):
+  x[i] = ((13 i) % 17) * 0.1f - 0.8f -> bf16;  W[i] = ((7 i) % 23) * 0.05f - 0.55f,
+  quantized per row (test_gemm.cu:516-529).
+* ``tiny_m4_n8_k16``      -- GemmFP8Test.Tiny (test_gemm.cu:310-337): x[i] = (i % 7) * 0.3f
+  - 1, W[i] = (i % 11) * 0.2f - 1.1f, per-row weight quant.  The reference quantizes x to
+  e4m3 there (W8A8); this build keeps x in bf16 (W8A16), so only the inputs are shared.
+Seeded cases cover what those leave open: ragged N and K/16 odd (``ragged_m3_n37_k208``),
+skinny M with per-row log-uniform scales (``skinny_m16_n48_k3136``), and special values
+(``special_nan_zero``: NaN codes 0x7F/0xFF, -0 codes, subnormal codes, an all-zero x row).
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32 = np.float32
+
+
+def torch_decode(codes: np.ndarray) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(codes, dtype=np.uint8)).view(torch.float8_e4m3fn)
+    return t.float().numpy()
+
+
+def torch_encode(q: np.ndarray) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).to(torch.float8_e4m3fn)
+    return t.view(torch.uint8).numpy().copy()
+
+
+def bf16_bits(f: np.ndarray) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(f, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def bf16_value(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def perrow_quant(wf: np.ndarray):
+    """test_gemm.cu:516-529 in float32 arithmetic, the cast done by torch."""
+    wf = wf.astype(F32)
+    rowmax = np.abs(wf).max(axis=1).astype(F32)
+    s = (rowmax / F32(448.0)).astype(F32)
+    s = np.where(s < F32(1e-10), F32(1.0) / F32(448.0), s).astype(F32)
+    inv = (F32(1.0) / s).astype(F32)
+    q = np.clip((wf * inv[:, None]).astype(F32), F32(-448.0), F32(448.0))
+    return torch_encode(q), s
+
+
+def fp64_linear(xb: np.ndarray, codes: np.ndarray, s: np.ndarray) -> np.ndarray:
+    x = bf16_value(np.atleast_2d(xb)).astype(np.float64)
+    w = torch_decode(codes).astype(np.float64)
+    return (x @ w.T) * s.astype(np.float64)[None, :]
+
+
+def save(name: str, **arrays):
+    path = os.path.join(HERE, name + ".npz")
+    np.savez_compressed(path, **arrays)
+    return path
+
+
+def main():
+    written = []
+
+    # 1. 256-entry decode table, as torch decodes float8_e4m3fn
+    lut = torch_decode(np.arange(256, dtype=np.uint8))
+    assert lut[0x7E] == 448.0 and lut[0x01] == 2.0 ** -9 and np.isnan(lut[0x7F]) and np.isnan(lut[0xFF])
+    assert lut[0x80] == 0.0 and np.signbit(lut[0x80]) and lut[0x38] == 1.0 and lut[0xFE] == -448.0
+    written.append(save("e4m3_lut", lut_bits=lut.view(np.uint32)))
+
+    # 2. GemvFP8Test.MatchesReference known-answer inputs
+    N, K = 64, 3136
+    i = np.arange(K, dtype=np.int64)
+    x_f = (((i * 13) % 17).astype(F32) * F32(0.1) - F32(0.8)).astype(F32)
+    j = np.arange(N * K, dtype=np.int64)
+    w_f = (((j * 7) % 23).astype(F32) * F32(0.05) - F32(0.55)).astype(F32).reshape(N, K)
+    xb = bf16_bits(x_f)
+    codes, s = perrow_quant(w_f)
+    written.append(save("kat_gemv_n64_k3136", x_f32=x_f, w_f32=w_f, x_bf16=xb[None, :],
+                        w_codes=codes, w_scale=s, y_f64=fp64_linear(xb, codes, s)))
+
+    # 3. GemmFP8Test.Tiny inputs, kept W8A16
+    M, N, K = 4, 8, 16
+    x_f = ((np.arange(M * K) % 7).astype(F32) * F32(0.3) - F32(1.0)).astype(F32).reshape(M, K)
+    w_f = ((np.arange(N * K) % 11).astype(F32) * F32(0.2) - F32(1.1)).astype(F32).reshape(N, K)
+    xb = bf16_bits(x_f)
+    codes, s = perrow_quant(w_f)
+    written.append(save("tiny_m4_n8_k16", x_f32=x_f, w_f32=w_f, x_bf16=xb, w_codes=codes,
+                        w_scale=s, y_f64=fp64_linear(xb, codes, s)))
+
+    rng = np.random.default_rng(20241201)
+
+    # 4. ragged N, K/16 odd, per-row quantized N(0, 0.02) weights
+    M, N, K = 3, 37, 208
+    w_f = (rng.standard_normal((N, K)) * 0.02).astype(F32)
+    x_f = rng.standard_normal((M, K)).astype(F32)
+    xb = bf16_bits(x_f)
+    codes, s = perrow_quant(w_f)
+    written.append(save("ragged_m3_n37_k208", x_bf16=xb, w_codes=codes, w_scale=s,
+                        y_f64=fp64_linear(xb, codes, s)))
+
+    # 5. skinny M=16, per-row log-uniform scales in [1e-4, 1e-2] (config-2 style)
+    M, N, K = 16, 48, 3136
+    codes = torch_encode(np.clip(rng.standard_normal((N, K)).astype(F32) * F32(64.0), -448, 448).astype(F32))
+    s = np.exp(rng.uniform(np.log(1e-4), np.log(1e-2), N)).astype(F32)
+    xb = bf16_bits(rng.standard_normal((M, K)).astype(F32))
+    written.append(save("skinny_m16_n48_k3136", x_bf16=xb, w_codes=codes, w_scale=s,
+                        y_f64=fp64_linear(xb, codes, s)))
+
+    # 6. special values: NaN codes, -0 codes, subnormals, all-zero activation row
+    M, N, K = 2, 8, 64
+    codes = torch_encode(np.clip(rng.standard_normal((N, K)).astype(F32) * F32(8.0), -448, 448).astype(F32))
+    codes[1, 5] = 0x7F                    # NaN
+    codes[2, 63] = 0xFF                   # -NaN
+    codes[3, :] = 0x80                    # -0 everywhere
+    codes[4, :] = np.arange(K, dtype=np.uint8) % 8   # subnormals 0..7 * 2^-9
+    s = np.full(N, 0.0078125, dtype=F32)
+    xb = bf16_bits(rng.standard_normal((M, K)).astype(F32))
+    xb[1, :] = 0                          # +0 activation row
+    written.append(save("special_nan_zero", x_bf16=xb, w_codes=codes, w_scale=s,
+                        y_f64=fp64_linear(xb, codes, s)))
+
+    with open(os.path.join(HERE, "SHA256SUMS"), "w") as f:
+        for p in sorted(written):
+            h = hashlib.sha256(open(p, "rb").read()).hexdigest()
+            f.write(f"{h}  {os.path.basename(p)}\n")
+    print("wrote", [os.path.basename(p) for p in written])
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,126 @@
+"""C ABI and binding checks that need no GPU: the library loads, exports every symbol that
+include/*.h declares, rejects bad arguments on the host before launching anything, and the
+pybind module mirrors the reference's module surface (names, arities, constants)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from nemotron_infer_amd import _lib
+from tests.conftest import ROOT
+
+
+def _declared_symbols():
+    syms = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        syms |= set(re.findall(r"\b(nmi_\w+)\s*\(", text))
+    return syms
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    declared = _declared_symbols()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(L, name), f"libnmi.so does not export {name}"
+    assert set(_lib.SIGNATURES) == declared, "ctypes signature table out of sync with the header"
+
+
+def test_abi_version():
+    assert _lib.lib().nmi_abi_version() == 10000
+
+
+FAKE = 0x10000          # 16-byte aligned, never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("args,code", [
+    # x, ldx, w, ldw, s, y, ldy, M, N, K
+    ((0, 64, FAKE, 64, FAKE, FAKE, 8, 1, 8, 64), _lib.NMI_ERR_INVALID_ARG),          # NULL x
+    ((FAKE, 64, FAKE, 64, FAKE, FAKE, 8, 0, 8, 64), _lib.NMI_ERR_INVALID_ARG),       # M = 0
+    ((FAKE, 64, FAKE, 64, FAKE, FAKE, 8, 1, 0, 64), _lib.NMI_ERR_INVALID_ARG),       # N = 0
+    ((FAKE, 72, FAKE, 72, FAKE, FAKE, 8, 1, 8, 72), _lib.NMI_ERR_INVALID_ARG),       # K % 16
+    ((FAKE, 64, FAKE, 64, FAKE, FAKE, 8, 1, 8, 0), _lib.NMI_ERR_INVALID_ARG),        # K = 0
+    ((FAKE, 32, FAKE, 64, FAKE, FAKE, 8, 2, 8, 64), _lib.NMI_ERR_INVALID_ARG),       # ldx < K
+    ((FAKE, 64, FAKE, 64, FAKE, FAKE, 4, 2, 8, 64), _lib.NMI_ERR_INVALID_ARG),       # ldy < N
+    ((FAKE, 64, FAKE + 8, 64, FAKE, FAKE, 8, 1, 8, 64), _lib.NMI_ERR_ALIGNMENT),     # W misaligned
+    ((FAKE, 64, FAKE, 72, FAKE, FAKE, 8, 1, 8, 64), _lib.NMI_ERR_ALIGNMENT),         # ldw % 16
+    ((FAKE + 2, 64, FAKE, 64, FAKE, FAKE, 8, 1, 8, 64), _lib.NMI_ERR_ALIGNMENT),     # x misaligned
+    ((FAKE, 68, FAKE, 64, FAKE, FAKE, 8, 2, 8, 64), _lib.NMI_ERR_ALIGNMENT),         # ldx*2 % 16
+    ((FAKE, 64, FAKE, 64, FAKE + 2, FAKE, 8, 1, 8, 64), _lib.NMI_ERR_ALIGNMENT),     # s misaligned
+    ((FAKE, 64, FAKE, 64, FAKE, FAKE + 1, 8, 1, 8, 64), _lib.NMI_ERR_ALIGNMENT),     # y misaligned
+])
+def test_linear_rejects_bad_arguments(args, code):
+    L = _lib.lib()
+    rc = L.nmi_linear_fp8_w8a16(*args, None)
+    assert rc == code
+    assert L.nmi_last_error().decode().startswith("nmi_linear_fp8_w8a16")
+    rc = L.nmi_gemm_fp8_w8a16(*args, None, 0, None)
+    assert rc == code
+
+
+def test_gemv_and_decode_reject_bad_arguments():
+    L = _lib.lib()
+    assert L.nmi_gemv_fp8(FAKE, FAKE, FAKE, FAKE, 8, 3136 + 8, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_gemv_fp8(FAKE, FAKE + 4, FAKE, FAKE, 8, 64, None) == _lib.NMI_ERR_ALIGNMENT
+    assert L.nmi_gemv_fp8(FAKE, FAKE, FAKE, 0, 8, 64, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_fp8_e4m3_decode(FAKE, FAKE, FAKE, FAKE, 1.0, 6, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_fp8_e4m3_decode(FAKE, FAKE + 4, FAKE, FAKE, 1.0, 8, None) == _lib.NMI_ERR_ALIGNMENT
+    assert L.nmi_tuning_set(b"no.such.knob", 1) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_alloc(16, None) == _lib.NMI_ERR_INVALID_ARG
+
+
+def test_allocator_stats_without_device():
+    total, nslabs = ctypes.c_size_t(123), ctypes.c_size_t(456)
+    assert _lib.lib().nmi_alloc_stats(ctypes.byref(total), ctypes.byref(nslabs)) == 0
+    assert total.value == 0 and nslabs.value == 0
+
+
+# Names and argument counts of the reference module (nemotron_infer/csrc/binding.pyi:4-83).
+REFERENCE_ARITY = {
+    "attn_decode": 11, "attn_decode_fp8": 15, "attn_forward": 11, "attn_forward_fp8": 15,
+    "embedding": 4, "free_allocator": 0, "lm_head": 4, "mamba_decode": 14, "mamba_decode_fp8": 16,
+    "mamba_forward": 15, "mamba_forward_fp8": 17, "mlp_forward": 6, "mlp_forward_fp8": 8,
+    "reset_allocator": 0, "rmsnorm": 4, "sync": 0,
+}
+REFERENCE_CONSTANTS = {
+    "CONV_DIM": 9728, "CONV_K": 4, "G": 8, "H": 96, "HEAD": 128, "HIDDEN": 3136, "H_KV": 8,
+    "H_Q": 40, "INTER": 12544, "IN_PROJ": 17504, "N": 128, "P": 80, "VOCAB": 131072,
+}
+
+
+def _arity(fn):
+    doc = fn.__doc__.splitlines()[0]
+    inner = doc[doc.index("(") + 1: doc.rindex(")")]
+    inner = inner[: inner.rindex(")")] if "->" in doc and inner.endswith(")") else inner
+    return 0 if not inner.strip() else inner.count(":")
+
+
+def test_binding_mirrors_reference_module():
+    from nemotron_infer_amd.csrc import binding as B
+
+    for name, val in REFERENCE_CONSTANTS.items():
+        assert getattr(B, name) == val, name
+    for name, n in REFERENCE_ARITY.items():
+        fn = getattr(B, name)
+        assert _arity(fn) == n, f"{name}: arity {_arity(fn)} != {n}"
+    assert _arity(B.linear_fp8) == 10 and _arity(B.gemv_fp8) == 6
+
+
+def test_out_of_scope_entries_fail_loudly():
+    from nemotron_infer_amd.csrc import binding as B
+
+    with pytest.raises(NotImplementedError, match="not part of this build"):
+        B.attn_decode_fp8(*([0] * 15))
+    with pytest.raises(NotImplementedError):
+        B.mamba_forward_fp8(*([0] * 17))
+
+
+def test_binding_reports_validation_errors():
+    from nemotron_infer_amd.csrc import binding as B
+
+    with pytest.raises(RuntimeError, match="K=72 must be a positive multiple of 16"):
+        B.linear_fp8(FAKE, 72, FAKE, 80, FAKE, FAKE, 8, 1, 8, 72)

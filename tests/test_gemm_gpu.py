@@ -1,0 +1,101 @@
+"""GPU parity of the prefill GEMM (bf16 MFMA over e4m3 weights dequantized in LDS) and of the
+M-dispatching linear entry point, against the torch fp32 dequant-then-F.linear oracle.
+
+Tolerance: rel_l2 <= 1e-3 and max |diff| <= 2 bf16 ulp at max(|ref|, 2^-8 rms(ref)).
+"""
+import numpy as np
+import pytest
+import torch
+
+from nemotron_infer_amd import _lib, ops, synth
+from oracle import linear
+from tests.conftest import load_golden
+from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_to_dev, w_to_dev,
+                            x_to_dev)
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(M, N, K, seed, scales="per_tensor", act="normal", outlier_frac=0.0):
+    w, s = synth.make_weight(N, K, seed, "cpu", scales=scales)
+    x = synth.make_act(M, K, seed + 1, "cpu", kind=act, outlier_frac=outlier_frac)
+    return x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy()
+
+
+@pytest.mark.parametrize("name", ["kat_gemv_n64_k3136", "tiny_m4_n8_k16", "ragged_m3_n37_k208",
+                                  "skinny_m16_n48_k3136", "special_nan_zero"])
+@pytest.mark.parametrize("entry", ["gemm", "linear"])
+def test_fixtures(name, entry):
+    g = load_golden(name)
+    announce("gemm_fixture", name, entry)
+    x, w, s = g["x_bf16"], g["w_codes"], g["w_scale"]
+    fn = ops.gemm_fp8_w8a16 if entry == "gemm" else ops.linear_fp8_w8a16
+    y = bits(fn(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
+    assert_parity(y, linear.bf16_rne(g["y_f64"].astype(np.float32)), f"{name} vs fp64")
+    assert_parity(y, oracle_bits(x, w, s), f"{name} vs torch oracle")
+
+
+@pytest.mark.parametrize("lin", synth.PREFILL_SET, ids=lambda l: l.name)
+def test_prefill_config3(lin):
+    """Config 3: M = 2048 with 0.1% x50 activation outliers, per-tensor scales."""
+    M = synth.PREFILL_M
+    announce("prefill", lin.name, M, lin.N, lin.K)
+    x, w, s = _case(M, lin.N, lin.K, 3000 + lin.N % 101, act=lin.act, outlier_frac=0.001)
+    y = bits(ops.gemm_fp8_w8a16(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
+    assert_parity(y, oracle_bits(x, w, s), f"prefill {lin.name}")
+
+
+@pytest.mark.parametrize("M", [2, 4, 8, 16])
+def test_skinny_config2(M):
+    """Config 2: M in {2,4,8,16} on the decode shapes with per-row log-uniform scales."""
+    for lin in synth.DECODE_SET:
+        announce("skinny", M, lin.name, lin.N, lin.K)
+        x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, scales="log_uniform", act=lin.act)
+        y = bits(ops.linear_fp8_w8a16(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
+        assert_parity(y, oracle_bits(x, w, s), f"M={M} {lin.name}")
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 37, 16), (100, 130, 80), (130, 257, 208), (1, 300, 3136),
+                                   (255, 129, 1040), (64, 64, 64), (300, 7168, 96)])
+def test_ragged_shapes(M, N, K):
+    announce("ragged", M, N, K)
+    x, w, s = _case(M, N, K, M * 131 + N * 7 + K, scales="log_uniform")
+    for fn in (ops.gemm_fp8_w8a16, ops.linear_fp8_w8a16):
+        y = bits(fn(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
+        assert_parity(y, oracle_bits(x, w, s), f"{fn.__name__} M={M} N={N} K={K}")
+
+
+def test_strided_operands():
+    """ldx > K, ldw > K, ldy > N: strided views (e.g. one slice of a fused buffer)."""
+    M, N, K = 96, 200, 320
+    announce("strided", M, N, K)
+    x, w, s = _case(M, N, K, 777, scales="log_uniform")
+    xbig = torch.zeros((M, K + 64), dtype=torch.bfloat16, device=DEV)
+    xbig[:, 32:32 + K] = x_to_dev(x)
+    wbig = torch.zeros((N, K + 48), dtype=torch.uint8, device=DEV)
+    wbig[:, 16:16 + K] = w_to_dev(w)
+    ybig = torch.full((M, N + 40), 7.0, dtype=torch.bfloat16, device=DEV)
+    sd = s_to_dev(s)
+    L = _lib.lib()
+    for entry in ("gemm", "linear"):
+        xv, wv, yv = xbig[:, 32:], wbig[:, 16:], ybig[:, 8:]
+        args = (xv.data_ptr(), xbig.stride(0), wv.data_ptr(), wbig.stride(0), sd.data_ptr(),
+                yv.data_ptr(), ybig.stride(0), M, N, K)
+        rc = (L.nmi_gemm_fp8_w8a16(*args, None, 0, None) if entry == "gemm"
+              else L.nmi_linear_fp8_w8a16(*args, None))
+        _lib.check(rc, entry)
+        torch.cuda.synchronize()
+        assert_parity(bits(ybig[:, 8:8 + N]), oracle_bits(x, w, s), f"strided {entry}")
+        assert torch.all(ybig[:, :8] == 7.0) and torch.all(ybig[:, 8 + N:] == 7.0)
+
+
+def test_gemm_power_of_two_linearity_and_determinism():
+    M, N, K = 2048, 3136, 12544
+    announce("gemm_linearity", M, N, K)
+    x, w, s = _case(M, N, K, 31337, act="relu2")
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    y = ops.gemm_fp8_w8a16(xd, wd, sd)
+    y_again = ops.gemm_fp8_w8a16(xd, wd, sd)
+    y2 = ops.gemm_fp8_w8a16((xd.float() * 0.5).to(torch.bfloat16), wd, sd)
+    assert torch.equal(y, y_again)
+    assert torch.equal(y2.float(), y.float() * 0.5)
