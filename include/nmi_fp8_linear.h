@@ -62,9 +62,9 @@ int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, v
                  int N, int K, void* stream);
 
 /*
- * General W8A16 linear with explicit strides and the reference's M == 1 dispatch:
- * M == 1 -> the GEMV kernel, 2 <= M <= 16 -> the skinny MFMA kernel, M > 16 -> the
- * MFMA GEMM.  Replaces the fp8 branch of mlp_block_forward_fp8
+ * General W8A16 linear with explicit strides and an M dispatch that refines the
+ * reference's M == 1 switch: M == 1 -> the GEMV kernel, 2 <= M <= 16 -> the skinny kernel
+ * (weight-streaming, bf16 MFMA), M > 16 -> the MFMA GEMM.  Replaces the fp8 branch of mlp_block_forward_fp8
  * (nemotron_infer/csrc/include/model/mlp_block.cuh:142-171) and the per-projection calls
  * in attention_block.cuh:330-350,400-409 and mamba_block.cuh:383-391,419-423,476-481,508-509.
  * Unlike the reference's M > 1 branch, activations are NOT quantized to e4m3
@@ -73,6 +73,44 @@ int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, v
 int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
                          const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
                          void* stream);
+
+/*
+ * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the skinny kernel
+ * (2 <= M <= 16) split K between workgroups (more parallelism for small N or long K).
+ * workspace: 256-byte aligned, at least nmi_linear_workspace_bytes(M, N, K) bytes, zero-filled
+ * before its first use; every launch leaves it ready for the next one.  NULL / too small ->
+ * the kernel runs without the split (same results up to float32 summation order).  Two
+ * launches that may run concurrently must not share a workspace.  The reference's blocks
+ * likewise hand a workspace to their prefill GEMMs (model/mlp_block.cuh:133,156,160-161).
+ */
+int nmi_linear_fp8_w8a16_ws(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
+                            const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Several weight matrices that share the activation x [M, K] in one dispatch (one kernel
+ * launch for M <= 16): q/k/v of an attention block, which the reference runs as three GEMVs
+ * on the same normed input (model/attention_block.cuh:400-402, 332-337), or the row slices of
+ * a Mamba in_proj (model/mamba_block.cuh:476-481, 386-391).  Group i computes
+ * y_i[M, N_i] = bf16((x . e4m3(W_i)^T) * s_i); each group is validated like
+ * nmi_linear_fp8_w8a16.  Workspace as for nmi_linear_fp8_w8a16_ws, sized for the sum of N_i.
+ */
+#define NMI_MAX_GROUPS 4
+typedef struct nmi_linear_group {
+    const void* w_e4m3;   /* [N, K] e4m3, row stride ldw bytes */
+    int64_t ldw;
+    const float* w_scale; /* [N] */
+    void* y_bf16;         /* [M, N] bf16, row stride ldy elements */
+    int64_t ldy;
+    int N;
+} nmi_linear_group;
+int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
+                                 const nmi_linear_group* groups, int ngroups, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* Workspace bytes the skinny kernel can use for M rows, total_n output rows (the sum over
+ * groups) and K on the current device; 0 when no split is planned. */
+size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K);
 
 /*
  * Prefill GEMM y[M,N] = bf16_rne((x[M,K] . e4m3(W[N,K])^T) * s[n]) on bf16 MFMA, any M >= 1.
@@ -99,8 +137,8 @@ int nmi_fp8_e4m3_decode(const void* codes, float* out_f32, float* out_scaled, vo
                         float scale, int n, void* stream);
 
 /*
- * Tuning knobs for sweeps ("gemv.ks", "gemv.unroll", "gemm.tile", "skinny.ks"); 0 restores
- * the automatic choice.  Process-wide, not thread-safe against concurrent launches; results
+ * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "skinny.ks",
+ * "skinny.kg", "skinny.u", "m1.path"); 0 restores the automatic choice.  Process-wide, not thread-safe against concurrent launches; results
  * do not depend on them beyond float32 summation order.  No counterpart in the reference
  * (its launch shapes are compile-time constants, ops/gemv.cuh:100-103).
  */

@@ -25,6 +25,9 @@ SIGNATURES = {
     "nmi_last_error": ([], ctypes.c_char_p),
     "nmi_gemv_fp8": ([_vp, _vp, _vp, _vp, _i, _i, _vp], _i),
     "nmi_linear_fp8_w8a16": ([_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _vp], _i),
+    "nmi_linear_fp8_w8a16_ws": ([_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _vp, _sz, _vp], _i),
+    "nmi_linear_fp8_w8a16_grouped": ([_vp, _i64, _i, _i, _vp, _i, _vp, _sz, _vp], _i),
+    "nmi_linear_workspace_bytes": ([_i, _i64, _i], _sz),
     "nmi_gemm_fp8_w8a16": ([_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _vp, _sz, _vp], _i),
     "nmi_fp8_e4m3_decode": ([_vp, _vp, _vp, _vp, _f, _i, _vp], _i),
     "nmi_tuning_set": ([ctypes.c_char_p, _i], _i),
@@ -34,6 +37,15 @@ SIGNATURES = {
     "nmi_alloc_stats": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
     "nmi_sync": ([], _i),
 }
+
+MAX_GROUPS = 4
+
+
+class LinearGroup(ctypes.Structure):
+    """nmi_linear_group of include/nmi_fp8_linear.h."""
+    _fields_ = [("w_e4m3", _vp), ("ldw", _i64), ("w_scale", _vp), ("y_bf16", _vp), ("ldy", _i64),
+                ("N", _i)]
+
 
 _lib = None
 

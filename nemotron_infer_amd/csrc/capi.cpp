@@ -114,25 +114,77 @@ int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, v
                       "nmi_gemv_fp8 launch");
 }
 
+namespace {
+
+// M-dispatch of one or more matrices sharing x: M == 1 -> GEMV, M <= 16 -> skinny MFMA
+// kernel, M > 16 -> MFMA GEMM (one launch per matrix).
+int dispatch(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng, void* ws,
+             size_t ws_bytes, hipStream_t st, const char* fn) {
+    hipError_t e = hipSuccess;
+    if (M == 1 && (tuning().m1_path != 2)) {
+        e = launch_gemv_m1_grouped(x, K, g, ng, st);
+    } else if (M <= 16) {
+        e = launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+    } else {
+        for (int i = 0; i < ng && e == hipSuccess; ++i)
+            e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, st);
+    }
+    return hip_status(e, fn);
+}
+
+int64_t total_rows(const nmi_linear_group* groups, int ngroups) {
+    int64_t r = 0;
+    for (int i = 0; i < ngroups; ++i) r += groups[i].N;
+    return r;
+}
+
+}  // namespace
+
 int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
                          const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
                          void* stream) {
-    int rc = check_linear(x_bf16, ldx, w_e4m3, ldw, w_scale, y_bf16, ldy, M, N, K,
-                          "nmi_linear_fp8_w8a16");
+    return nmi_linear_fp8_w8a16_ws(x_bf16, ldx, w_e4m3, ldw, w_scale, y_bf16, ldy, M, N, K, nullptr, 0,
+                                   stream);
+}
+
+int nmi_linear_fp8_w8a16_ws(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
+                            const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = workspace ? "nmi_linear_fp8_w8a16_ws" : "nmi_linear_fp8_w8a16";
+    int rc = check_linear(x_bf16, ldx, w_e4m3, ldw, w_scale, y_bf16, ldy, M, N, K, fn);
     if (rc) return rc;
-    const auto* x = static_cast<const uint16_t*>(x_bf16);
-    const auto* W = static_cast<const uint8_t*>(w_e4m3);
-    auto* y = static_cast<uint16_t*>(y_bf16);
-    auto st = static_cast<hipStream_t>(stream);
-    hipError_t e;
-    if (M == 1) {
-        e = launch_gemv_m1(x, W, ldw, w_scale, y, N, K, st);
-    } else if (M <= 16) {
-        e = launch_gemv_skinny(x, ldx, W, ldw, w_scale, y, ldy, M, N, K, st);
-    } else {
-        e = launch_gemm(x, ldx, W, ldw, w_scale, y, ldy, M, N, K, st);
+    if (workspace && !aligned(workspace, 256))
+        return fail(NMI_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", fn);
+    GemvGroup g{static_cast<const uint8_t*>(w_e4m3), ldw, w_scale, static_cast<uint16_t*>(y_bf16), ldy, N, 0, 0};
+    return dispatch(static_cast<const uint16_t*>(x_bf16), ldx, M, K, &g, 1, workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream), fn);
+}
+
+int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
+                                 const nmi_linear_group* groups, int ngroups, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    const char* fn = "nmi_linear_fp8_w8a16_grouped";
+    if (!groups || ngroups < 1 || ngroups > NMI_MAX_GROUPS)
+        return fail(NMI_ERR_INVALID_ARG, "%s: ngroups=%d must be in [1, %d]", fn, ngroups, NMI_MAX_GROUPS);
+    if (workspace && !aligned(workspace, 256))
+        return fail(NMI_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", fn);
+    if (total_rows(groups, ngroups) > (int64_t)1 << 30)
+        return fail(NMI_ERR_INVALID_ARG, "%s: too many rows in total", fn);
+    GemvGroup g[kMaxGroups];
+    for (int i = 0; i < ngroups; ++i) {
+        const nmi_linear_group& G = groups[i];
+        int rc = check_linear(x_bf16, ldx, G.w_e4m3, G.ldw, G.w_scale, G.y_bf16, G.ldy, M, G.N, K, fn);
+        if (rc) return rc;
+        g[i] = GemvGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
+                         static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0};
     }
-    return hip_status(e, "nmi_linear_fp8_w8a16 launch");
+    return dispatch(static_cast<const uint16_t*>(x_bf16), ldx, M, K, g, ngroups, workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream), fn);
+}
+
+size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) {
+    if (M < 1 || M > 16 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
+    return skinny_workspace_bytes(M, K, total_n, device_info().num_cu);
 }
 
 int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
@@ -168,9 +220,14 @@ int nmi_tuning_set(const char* knob, int value) {
     if (!knob) return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: NULL knob");
     Tuning& t = tuning();
     if (!std::strcmp(knob, "gemv.ks")) t.gemv_ks = value;
-    else if (!std::strcmp(knob, "gemv.unroll")) t.gemv_unroll = value;
+    else if (!std::strcmp(knob, "gemv.t")) t.gemv_t = value;
+    else if (!std::strcmp(knob, "gemv.p")) t.gemv_p = value;
+    else if (!std::strcmp(knob, "gemv.xg")) t.gemv_xg = value;
     else if (!std::strcmp(knob, "gemm.tile")) t.gemm_tile = value;
     else if (!std::strcmp(knob, "skinny.ks")) t.skinny_ks = value;
+    else if (!std::strcmp(knob, "skinny.kg")) t.skinny_kg = value;
+    else if (!std::strcmp(knob, "skinny.u")) t.skinny_u = value;
+    else if (!std::strcmp(knob, "m1.path")) t.m1_path = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

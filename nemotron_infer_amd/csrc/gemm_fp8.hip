@@ -151,14 +151,3 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
 
 }  // namespace nmi
 
-namespace nmi {
-
-// Skinny M (2..16): until the dedicated skinny kernel lands, the GEMM handles it (ragged M
-// is masked inside the tile).
-hipError_t launch_gemv_skinny(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
-                              const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
-                              hipStream_t stream) {
-    return launch_gemm(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-}
-
-}  // namespace nmi

@@ -4,21 +4,26 @@
 //
 // Same result contract as the reference's gemv_fp8_kernel
 // (nemotron_infer/csrc/include/ops/gemv.cuh:48-89, formula :19-20, epilogue :87-88); the
-// schedule is designed for CDNA4 instead:
+// schedule is designed for CDNA4 and for HBM3E instead of a warp-per-row port:
 //
-// * Wave64, one DPP row (16 lanes) per weight row: a wave covers 4 rows, a workgroup of
-//   4 waves covers 16 / 8 / 4 rows when KS = 1 / 2 / 4 of its waves split K between them.
-//   Lane j of a row reads the 16-byte chunks j, j+16, j+32, ... of that row, so one load
-//   instruction of a wave fetches 4 rows x 256 contiguous bytes.
-// * UNROLL 16-byte non-temporal loads per lane are issued before any of them is consumed
-//   (memory-level parallelism: the kernel is HBM-bound, 2 flop per weight byte).
-// * x is staged once per workgroup in LDS as float32, quarter-major (float4 quarter p of
-//   chunk c at [p][c]) so that the 16 lanes of a row read 16 consecutive float4 -- no bank
-//   conflicts -- and the 4 rows of a wave share them by broadcast.  K is processed in LDS
-//   windows of at most 1008 chunks (63 KiB).
-// * e4m3 -> f32 with v_cvt_pk_f32_fp8, float32 FMA accumulation, a DPP 16-lane reduction,
-//   then (KS > 1) an ordered sum of the K-slice partials through LDS, and the per-row scale
-//   and the single bf16 RNE rounding in the epilogue.
+// * A whole wave64 reads one weight row at a time: lane l takes the 16-byte chunks
+//   l, l + 64, l + 128, ... of its K slice, so every load instruction fetches 1 KiB of
+//   contiguous bytes (measured on MI355X: the fastest of the row-major access patterns).
+//   A wave covers T rows (the same chunk columns of each), and KS waves of a workgroup
+//   split K, so a workgroup of 4 waves covers (4 / KS) * T rows.
+// * All of a lane's weight loads (T * P of them, P = chunks per row per lane) are issued
+//   before any is consumed; the activation loads are issued first so that waiting for them
+//   leaves the weight loads in flight.  The schedules are chosen so that P is 2-4: many
+//   short-lived waves, every byte of W requested at kernel start.
+// * x either staged per workgroup in LDS as raw bf16 (half-major: the low 8 elements of every
+//   16-element chunk, then the high 8, so 64 lanes read 64 consecutive 16-byte words) or read
+//   by each lane straight from global memory (its own chunks, reused for its T rows).
+// * e4m3 -> bf16 pairs with v_cvt_scalef32_pk_bf16_fp8 (exact), v_dot2_f32_bf16 with float32
+//   accumulation (bf16 x bf16 products are exact in float32), a wave reduction (DPP within
+//   16-lane rows, then the four row sums in a fixed order), the KS K-slice partials summed in
+//   a fixed order through LDS, the per-row scale and a single bf16 RNE rounding.
+// * One launch may cover several matrices that share x and K (a group table in the kernel
+//   arguments): q/k/v of an attention block, or the row slices of a Mamba in_proj.
 #include "nmi_device.hpp"
 #include "nmi_launch.hpp"
 
@@ -27,143 +32,255 @@ namespace nmi {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kLanesPerRow = 16;
-constexpr int kRowsPerWave = 64 / kLanesPerRow;
-constexpr int kMaxWindowChunks = 1008;   // 1008 chunks * 64 B = 63 KiB, + the static partials < 64 KiB
+constexpr int kMaxWindowChunks = 1024;                  // bf16 x window: 1024 chunks * 32 B = 32 KiB
+constexpr int kXPieces = 2 * kMaxWindowChunks / 256;    // 16-byte x pieces per thread per window
 
-__device__ __forceinline__ float dot16(const uint4 w, const float* __restrict__ xq,
-                                       int qstride, float acc) {
-    // xq points at quarter 0 of the chunk; quarter p lives at xq + p * qstride.
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const f32x4 wf = e4m3x4_to_f32(words[p]);
-        const float4 xv = *reinterpret_cast<const float4*>(xq + p * qstride);
-        acc = __builtin_fmaf(wf.x, xv.x, acc);
-        acc = __builtin_fmaf(wf.y, xv.y, acc);
-        acc = __builtin_fmaf(wf.z, xv.z, acc);
-        acc = __builtin_fmaf(wf.w, xv.w, acc);
-    }
-    return acc;
+struct GemvArgs {
+    const uint16_t* x;
+    int K;
+    int window;           // chunks per LDS window
+    int ngroups;
+    GemvGroup g[kMaxGroups];
+};
+
+// 16 e4m3 codes times 16 bf16 activations (low and high 8 of the chunk), two accumulators.
+__device__ __forceinline__ void dot16(const uint4 w, const uint4 xl, const uint4 xh, float& a0,
+                                      float& a1) {
+    const uint2 p0 = e4m3x4_to_bf16(w.x), p1 = e4m3x4_to_bf16(w.y);
+    const uint2 p2 = e4m3x4_to_bf16(w.z), p3 = e4m3x4_to_bf16(w.w);
+    a0 = dot2_bf16(p0.x, xl.x, a0);
+    a1 = dot2_bf16(p0.y, xl.y, a1);
+    a0 = dot2_bf16(p1.x, xl.z, a0);
+    a1 = dot2_bf16(p1.y, xl.w, a1);
+    a0 = dot2_bf16(p2.x, xh.x, a0);
+    a1 = dot2_bf16(p2.y, xh.y, a1);
+    a0 = dot2_bf16(p3.x, xh.z, a0);
+    a1 = dot2_bf16(p3.y, xh.w, a1);
 }
 
-template <int KS, int UNROLL>
-__global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ W, int64_t ldw,
-    const float* __restrict__ s, uint16_t* __restrict__ y, int N, int K, int window_chunks) {
-    extern __shared__ float xs[];                       // [4][window_chunks][4] floats
-    constexpr int kRowGroups = kWaves / KS;
-    constexpr int kRowsPerWG = kRowGroups * kRowsPerWave;
+// KS: waves splitting K; T: rows per wave; P: 16-byte chunks per lane per row per batch;
+// XG: x read from global memory instead of LDS.
+template <int KS, int T, int P, bool XG>
+__global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
+    extern __shared__ uint4 xs[];                  // [half][window] (LDS mode)
+    constexpr int kRowGroups = kWaves / KS;        // waves with distinct rows
+    constexpr int kRowsPerWG = kRowGroups * T;
     __shared__ float partial[KS > 1 ? KS : 1][kRowsPerWG];
+
+    // Group of this workgroup (uniform scalar scan over <= kMaxGroups entries).
+    int gi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < args.ngroups && (int)blockIdx.x >= args.g[i].wg_begin) gi = i;
+    const GemvGroup grp = args.g[gi];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int r = lane >> 4;                // row within the wave
-    const int j = lane & 15;                // lane within the row
-    const int g = wave / KS;                // row group of this wave
+    const int g = wave / KS;                // row group (T rows) of this wave
     const int q = wave % KS;                // K slice of this wave
-    const int row = blockIdx.x * kRowsPerWG + g * kRowsPerWave + r;
-    const bool active = row < N;
-    const uint8_t* __restrict__ wrow = W + (int64_t)(active ? row : 0) * ldw;
-    const int C = K >> 4;                   // 16-byte chunks per row
-    const int qstride = window_chunks * 4;  // floats between quarters
+    const int row_base = ((int)blockIdx.x - grp.wg_begin) * kRowsPerWG + g * T;
+    const uint16_t* __restrict__ x = args.x;
+    const int C = args.K >> 4;              // 16-byte weight chunks per row
+    const int window = XG ? C : args.window;
 
-    float acc = 0.f;
-    for (int w0 = 0; w0 < C; w0 += window_chunks) {
-        const int wc = min(window_chunks, C - w0);
-        if (w0 != 0) __syncthreads();       // previous window fully consumed
-        // Stage x[w0*16 : (w0+wc)*16) as float32; each thread converts 8 bf16 (half a chunk).
-        for (int e = tid; e < wc * 2; e += 256) {
-            const uint4 v = load16(x + (int64_t)(w0 * 16 + e * 8));
-            const int c = e >> 1, h = e & 1;
-            float* dst0 = xs + (2 * h) * qstride + c * 4;
-            float* dst1 = xs + (2 * h + 1) * qstride + c * 4;
-            *reinterpret_cast<float4*>(dst0) =
-                float4{bf16lo_to_f32(v.x), bf16hi_to_f32(v.x), bf16lo_to_f32(v.y), bf16hi_to_f32(v.y)};
-            *reinterpret_cast<float4*>(dst1) =
-                float4{bf16lo_to_f32(v.z), bf16hi_to_f32(v.z), bf16lo_to_f32(v.w), bf16hi_to_f32(v.w)};
+    // Row t of this wave; rows past N read row N-1 (in bounds) and never store.
+    const uint8_t* __restrict__ wrow[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+        wrow[t] = grp.W + (int64_t)min(row_base + t, grp.N - 1) * grp.ldw;
+
+    // Loads are unconditional, from addresses clamped into the valid range, so that no
+    // branch separates them (a branch around a load makes the compiler wait for it); the
+    // values of clamped slots are never consumed.
+    float a0[T], a1[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) a0[t] = a1[t] = 0.f;
+    for (int w0 = 0; w0 < C; w0 += window) {
+        const int wc = min(window, C - w0);
+        // 1. activations of this window (LDS mode; issued first)
+        uint4 xr[XG ? 1 : kXPieces];
+        if constexpr (!XG) {
+#pragma unroll
+            for (int p = 0; p < kXPieces; ++p) {
+                const int e = min(tid + 256 * p, 2 * wc - 1);
+                xr[p] = load16(x + (int64_t)(w0 * 16 + e * 8));
+            }
         }
-        __syncthreads();
-
-        const int cb = (q * wc) / KS;
-        const int ce = ((q + 1) * wc) / KS;
-        if (active) {
-            const uint8_t* __restrict__ wwin = wrow + (int64_t)w0 * 16;
-            for (int c0 = cb + j; c0 < ce; c0 += UNROLL * kLanesPerRow) {
-                uint4 wv[UNROLL];
+        // 2. this wave's K slice [cb, ce) of the window
+        const int cb = w0 + (q * wc) / KS;
+        const int ce = w0 + ((q + 1) * wc) / KS;
+        const int clast = max(ce - 1, cb);
+        int c0 = cb + lane;
+        uint4 xl[XG ? P : 1], xh[XG ? P : 1];
+        uint4 wv[T][P];
+        if constexpr (XG) {
 #pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    const int c = c0 + u * kLanesPerRow;
-                    wv[u] = (c < ce) ? load_stream16(wwin + (int64_t)c * 16) : uint4{0, 0, 0, 0};
-                }
+            for (int i = 0; i < P; ++i) {
+                const int c = min(c0 + 64 * i, clast);
+                xl[i] = load16(x + (int64_t)c * 16);
+                xh[i] = load16(x + (int64_t)c * 16 + 8);
+            }
+        }
 #pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    const int c = c0 + u * kLanesPerRow;
-                    if (c < ce) acc = dot16(wv[u], xs + c * 4, qstride, acc);
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int i = 0; i < P; ++i)
+                wv[t][i] = load_stream16(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
+        // 3. stage x (LDS mode) once the previous window has been consumed
+        if constexpr (!XG) {
+            if (w0 != 0) __syncthreads();
+#pragma unroll
+            for (int p = 0; p < kXPieces; ++p) {
+                const int e = tid + 256 * p;
+                if (e < 2 * wc) xs[(e & 1) * window + (e >> 1)] = xr[p];
+            }
+            __syncthreads();
+        }
+        // 4. consume; further batches only when a lane's slice exceeds P chunks per row
+        for (;;) {
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                const int c = c0 + 64 * i;
+                if (c < ce) {
+                    uint4 lo, hi;
+                    if constexpr (XG) {
+                        lo = xl[i];
+                        hi = xh[i];
+                    } else {
+                        lo = xs[c - w0];
+                        hi = xs[window + c - w0];
+                    }
+#pragma unroll
+                    for (int t = 0; t < T; ++t) dot16(wv[t][i], lo, hi, a0[t], a1[t]);
                 }
             }
+            c0 += 64 * P;
+            if (c0 - lane >= ce) break;         // uniform across the wave
+            if constexpr (XG) {
+#pragma unroll
+                for (int i = 0; i < P; ++i) {
+                    const int c = min(c0 + 64 * i, clast);
+                    xl[i] = load16(x + (int64_t)c * 16);
+                    xh[i] = load16(x + (int64_t)c * 16 + 8);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int i = 0; i < P; ++i)
+                    wv[t][i] = load_stream16(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
         }
     }
 
-    acc = dpp_row_sum16(acc);
-    if constexpr (KS == 1) {
-        if (active && j == 0) y[row] = f32_to_bf16_rne(acc * s[row]);
-    } else {
-        if (j == 0) partial[q][g * kRowsPerWave + r] = acc;
-        __syncthreads();
-        if (q == 0 && j == 0 && active) {
-            float t = partial[0][g * kRowsPerWave + r];
+    // Wave sums in a fixed order: 16-lane DPP rows, then rows 0 + 1 + 2 + 3.
+    float sums[T];
 #pragma unroll
-            for (int qq = 1; qq < KS; ++qq) t += partial[qq][g * kRowsPerWave + r];
-            y[row] = f32_to_bf16_rne(t * s[row]);
+    for (int t = 0; t < T; ++t) sums[t] = wave_sum(a0[t] + a1[t]);
+    if constexpr (KS == 1) {
+        if (lane < T) {
+            float v = sums[0];
+#pragma unroll
+            for (int t = 1; t < T; ++t)
+                if (lane == t) v = sums[t];
+            const int row = row_base + lane;
+            if (row < grp.N) grp.y[row] = f32_to_bf16_rne(v * grp.s[row]);
+        }
+    } else {
+        if (lane == 0) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) partial[q][g * T + t] = sums[t];
+        }
+        __syncthreads();
+        if (q == 0 && lane < T) {
+            float v = partial[0][g * T + lane];
+#pragma unroll
+            for (int qq = 1; qq < KS; ++qq) v += partial[qq][g * T + lane];
+            const int row = row_base + lane;
+            if (row < grp.N) grp.y[row] = f32_to_bf16_rne(v * grp.s[row]);
         }
     }
 }
 
-template <int KS, int UNROLL>
-hipError_t launch_ks(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
-                     uint16_t* y, int N, int K, hipStream_t stream) {
-    constexpr int rows_per_wg = (kWaves / KS) * kRowsPerWave;
-    const int C = K >> 4;
-    const int window = C < kMaxWindowChunks ? C : kMaxWindowChunks;
-    const dim3 grid((N + rows_per_wg - 1) / rows_per_wg);
-    const size_t lds = (size_t)window * 16 * sizeof(float);
-    hipLaunchKernelGGL((gemv_fp8_m1_kernel<KS, UNROLL>), grid, dim3(256), lds, stream,
-                       x, W, ldw, s, y, N, K, window);
+template <int KS, int T, int P, bool XG>
+hipError_t launch_cfg(GemvArgs& a, hipStream_t stream) {
+    constexpr int rows_per_wg = (kWaves / KS) * T;
+    int wgs = 0;
+    for (int i = 0; i < a.ngroups; ++i) {
+        a.g[i].wg_begin = wgs;
+        wgs += (a.g[i].N + rows_per_wg - 1) / rows_per_wg;
+    }
+    const size_t lds = XG ? 0 : (size_t)a.window * 2 * sizeof(uint4);
+    hipLaunchKernelGGL((gemv_fp8_m1_kernel<KS, T, P, XG>), dim3(wgs), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
-template <int UNROLL>
-hipError_t launch_unroll(int ks, const uint16_t* x, const uint8_t* W, int64_t ldw,
-                         const float* s, uint16_t* y, int N, int K, hipStream_t stream) {
-    switch (ks) {
-        case 1: return launch_ks<1, UNROLL>(x, W, ldw, s, y, N, K, stream);
-        case 2: return launch_ks<2, UNROLL>(x, W, ldw, s, y, N, K, stream);
-        default: return launch_ks<4, UNROLL>(x, W, ldw, s, y, N, K, stream);
+template <int KS, int T, int P>
+hipError_t launch_xg(bool xg, GemvArgs& a, hipStream_t stream) {
+    return xg ? launch_cfg<KS, T, P, true>(a, stream) : launch_cfg<KS, T, P, false>(a, stream);
+}
+
+template <int KS, int T>
+hipError_t launch_p(int p, bool xg, GemvArgs& a, hipStream_t stream) {
+    switch (p) {
+        case 2: return launch_xg<KS, T, 2>(xg, a, stream);
+        case 3: return launch_xg<KS, T, 3>(xg, a, stream);
+        default: return launch_xg<KS, T, 4>(xg, a, stream);
+    }
+}
+
+template <int KS>
+hipError_t launch_t(int t, int p, bool xg, GemvArgs& a, hipStream_t stream) {
+    switch (t) {
+        case 1: return launch_p<KS, 1>(p, xg, a, stream);
+        case 2: return launch_p<KS, 2>(p, xg, a, stream);
+        default: return launch_p<KS, 4>(p, xg, a, stream);
     }
 }
 
 }  // namespace
 
+hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,
+                                  hipStream_t stream) {
+    const DeviceInfo& dev = device_info();
+    GemvArgs a{};
+    a.x = x;
+    a.K = K;
+    const int C = K >> 4;
+    a.window = C < kMaxWindowChunks ? C : kMaxWindowChunks;
+    a.ngroups = ngroups;
+    int64_t rows = 0;
+    for (int i = 0; i < ngroups; ++i) {
+        a.g[i] = groups[i];
+        rows += groups[i].N;
+    }
+    const Tuning& tn = tuning();
+    // K split: about 3-4 chunks per lane per row (KS waves of 64 lanes cover a row).
+    int ks = C <= 64 * 4 ? 1 : (C <= 2 * 64 * 4 ? 2 : 4);
+    if (tn.gemv_ks == 1 || tn.gemv_ks == 2 || tn.gemv_ks == 4) ks = tn.gemv_ks;
+    const int slice = (C + ks - 1) / ks;
+    int p = (slice + 63) / 64;
+    p = p <= 2 ? 2 : (p <= 3 ? 3 : 4);
+    if (tn.gemv_p >= 2 && tn.gemv_p <= 4) p = tn.gemv_p;
+    // Rows per wave: as many as keep about three workgroups per CU.
+    int t = 1;
+    for (int cand : {4, 2}) {
+        const int64_t wgs = (rows + (int64_t)(kWaves / ks) * cand - 1) / ((int64_t)(kWaves / ks) * cand);
+        if (wgs >= 3 * (int64_t)dev.num_cu) { t = cand; break; }
+    }
+    if (tn.gemv_t == 1 || tn.gemv_t == 2 || tn.gemv_t == 4) t = tn.gemv_t;
+    const bool xg = tn.gemv_xg == 1;
+    switch (ks) {
+        case 1: return launch_t<1>(t, p, xg, a, stream);
+        case 2: return launch_t<2>(t, p, xg, a, stream);
+        default: return launch_t<4>(t, p, xg, a, stream);
+    }
+}
+
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream) {
-    const DeviceInfo& dev = device_info();
-    // Fewest K-splitting waves that still give every CU at least two workgroups.
-    int ks = tuning().gemv_ks;
-    if (ks != 1 && ks != 2 && ks != 4) {
-        const int target = 2 * dev.num_cu;
-        ks = 4;
-        for (int cand : {1, 2, 4}) {
-            const int rows_per_wg = (kWaves / cand) * kRowsPerWave;
-            if ((N + rows_per_wg - 1) / rows_per_wg >= target) { ks = cand; break; }
-        }
-    }
-    switch (tuning().gemv_unroll) {
-        case 4: return launch_unroll<4>(ks, x, W, ldw, s, y, N, K, stream);
-        case 16: return launch_unroll<16>(ks, x, W, ldw, s, y, N, K, stream);
-        default: return launch_unroll<8>(ks, x, W, ldw, s, y, N, K, stream);
-    }
+    GemvGroup g{W, ldw, s, y, N, N, 0, 0};
+    return launch_gemv_m1_grouped(x, K, &g, 1, stream);
 }
 
 }  // namespace nmi

@@ -7,7 +7,8 @@
 //   exactly representable in bf16, so this is exact (used to stage weight tiles for MFMA).
 // * bf16 -> f32 by shifting the bit pattern; f32 -> bf16 round-to-nearest-even through
 //   v_cvt_pk_bf16_f32 (the conversion __float2bfloat16_rn performs in gemv.cuh:88).
-// * a 16-lane sum that uses DPP row operations (quad_perm, row_half_mirror, row_mirror).
+// * a 16-lane sum that uses DPP row operations (quad_perm, row_half_mirror, row_mirror), and
+//   a 64-lane sum built on it.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -34,6 +35,13 @@ __device__ __forceinline__ uint2 e4m3x4_to_bf16(uint32_t w) {
     return uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
+// c + a.lo * b.lo + a.hi * b.hi, a and b two packed bf16 each (v_dot2_f32_bf16; the
+// bf16 x bf16 products are exact in float32).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                          false);
+}
+
 // Two bf16 packed in a dword -> two floats (element 0 is the low half).
 __device__ __forceinline__ float bf16lo_to_f32(uint32_t d) { return __uint_as_float(d << 16); }
 __device__ __forceinline__ float bf16hi_to_f32(uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); }
@@ -55,6 +63,17 @@ __device__ __forceinline__ float dpp_row_sum16(float v) {
     v += dpp_f32<0x141>(v);  // row_half_mirror: 8 lanes
     v += dpp_f32<0x140>(v);  // row_mirror: 16 lanes
     return v;
+}
+
+// Sum over all 64 lanes in a fixed order: 16-lane DPP row sums, then (r0 + r1) + (r2 + r3).
+// Every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = dpp_row_sum16(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 // 16-byte global load that bypasses the caches' retention policy (streamed weights).

@@ -25,12 +25,42 @@ const DeviceInfo& device_info();
 // Tuning knobs (0 = automatic).  Set through nmi_tuning_set() for sweeps; never needed for
 // correctness.
 struct Tuning {
-    int gemv_ks = 0;       // waves of a workgroup that split K: 1, 2 or 4
-    int gemv_unroll = 0;   // 16-byte weight loads in flight per lane: 4, 8 or 16
+    int gemv_ks = 0;       // M = 1 GEMV: waves of a workgroup that split K (1, 2, 4)
+    int gemv_t = 0;        // M = 1 GEMV: weight rows per wave (1, 2, 4)
+    int gemv_p = 0;        // M = 1 GEMV: 16-byte chunks per lane per row per batch (2, 3, 4)
+    int gemv_xg = 0;       // M = 1 GEMV: 1 reads x from global memory instead of LDS
     int gemm_tile = 0;     // GEMM tile variant id (see gemm_fp8.hip)
-    int skinny_ks = 0;     // skinny-M kernel: waves of a workgroup that split K
+    int skinny_ks = 0;     // skinny kernel: waves of a workgroup that split K (1, 2, 4)
+    int skinny_kg = 0;     // skinny kernel: workgroups that split K (needs a workspace)
+    int skinny_u = 0;      // skinny kernel: 16-byte weight loads per lane per batch (8, 16)
+    int m1_path = 0;       // M = 1: 0 automatic, 1 DPP GEMV, 2 MFMA skinny kernel
 };
 Tuning& tuning();
+
+// One matrix of a grouped launch: W [N, K] (row stride ldw bytes), s [N], y [M, N] (row
+// stride ldy elements).  wg_begin and ws_col are filled in by the launchers.
+constexpr int kMaxGroups = 4;
+struct GemvGroup {
+    const uint8_t* W;
+    int64_t ldw;
+    const float* s;
+    uint16_t* y;
+    int64_t ldy;
+    int N;
+    int wg_begin;
+    int ws_col;
+};
+
+// M = 1 GEMV over up to kMaxGroups matrices that share x [K] (one launch).
+hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,
+                                  hipStream_t stream);
+
+// 1 <= M <= 16 on bf16 MFMA over up to kMaxGroups matrices sharing x [M, K].  With a
+// workspace of at least skinny_workspace_bytes() bytes (zero-filled before its first use; every
+// launch leaves it re-armed) K is also split between workgroups.
+size_t skinny_workspace_bytes(int M, int K, int64_t total_rows, int num_cu);
+hipError_t launch_skinny_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
+                                 int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);

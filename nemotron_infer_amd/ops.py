@@ -27,26 +27,82 @@ def _check_w(w: torch.Tensor) -> torch.Tensor:
     return w
 
 
+_WORKSPACE: dict[int, torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Per-device workspace of the skinny kernel's K split: zero-filled when (re)allocated,
+    kept for the process; every launch leaves it ready for the next.  Calls on one device
+    share it, so they must be ordered on one stream (as torch's current stream orders them).
+    Grows on demand -- make one eager call of the largest shape before capturing a graph."""
+    if nbytes <= 0:
+        return None
+    idx = torch.device(device).index or 0
+    ws = _WORKSPACE.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACE[idx] = ws
+    return ws
+
+
+def _as_2d(x: torch.Tensor):
+    x2 = x.unsqueeze(0) if x.dim() == 1 else x
+    if x2.dtype != torch.bfloat16:
+        raise TypeError("x must be bfloat16")
+    if x2.stride(-1) != 1:
+        raise ValueError("x must be contiguous in the last dimension")
+    return x2
+
+
 def linear_fp8_w8a16(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None, use_workspace: bool = True) -> torch.Tensor:
     """y[M, N] = bf16_rne((x[M, K] . e4m3(W[N, K])^T) * w_scale[N]) on the GPU."""
     w = _check_w(w)
     squeeze = x.dim() == 1
-    x2 = x.unsqueeze(0) if squeeze else x
-    if x2.dtype != torch.bfloat16 or w_scale.dtype != torch.float32:
-        raise TypeError("x must be bfloat16 and w_scale float32")
-    if x2.stride(-1) != 1 or w.stride(-1) != 1 or not w_scale.is_contiguous():
-        raise ValueError("x, W rows and w_scale must be contiguous in the last dimension")
+    x2 = _as_2d(x)
+    if w_scale.dtype != torch.float32:
+        raise TypeError("w_scale must be float32")
+    if w.stride(-1) != 1 or not w_scale.is_contiguous():
+        raise ValueError("W rows and w_scale must be contiguous in the last dimension")
     M, K = x2.shape
     N = w.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     y2 = out.view(M, N) if squeeze and out.dim() == 1 else out
-    rc = _lib.lib().nmi_linear_fp8_w8a16(
+    L = _lib.lib()
+    ws = workspace(x.device, L.nmi_linear_workspace_bytes(M, N, K)) if use_workspace else None
+    rc = L.nmi_linear_fp8_w8a16_ws(
         x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), w_scale.data_ptr(),
-        y2.data_ptr(), y2.stride(0), M, N, K, _stream())
-    _lib.check(rc, "nmi_linear_fp8_w8a16")
+        y2.data_ptr(), y2.stride(0), M, N, K,
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream())
+    _lib.check(rc, "nmi_linear_fp8_w8a16_ws")
     return out[0] if squeeze and out.dim() == 2 else out
+
+
+def linear_fp8_w8a16_grouped(x: torch.Tensor, weights, outs=None, use_workspace: bool = True):
+    """Several (W_i, s_i) sharing x in one dispatch: returns [y_i] with
+    y_i = bf16((x . e4m3(W_i)^T) * s_i) (e.g. q/k/v of an attention block)."""
+    x2 = _as_2d(x)
+    M, K = x2.shape
+    n = len(weights)
+    if not 1 <= n <= _lib.MAX_GROUPS:
+        raise ValueError(f"1..{_lib.MAX_GROUPS} groups")
+    if outs is None:
+        outs = [torch.empty((M, w.shape[0]), dtype=torch.bfloat16, device=x.device) for w, _ in weights]
+    arr = (_lib.LinearGroup * n)()
+    for i, ((w, s), y) in enumerate(zip(weights, outs)):
+        w = _check_w(w)
+        y2 = y.view(M, -1)
+        arr[i] = _lib.LinearGroup(w.data_ptr(), w.stride(0), s.data_ptr(), y2.data_ptr(), y2.stride(0),
+                                  w.shape[0])
+    L = _lib.lib()
+    total = sum(w.shape[0] for w, _ in weights)
+    ws = workspace(x.device, L.nmi_linear_workspace_bytes(M, total, K)) if use_workspace else None
+    rc = L.nmi_linear_fp8_w8a16_grouped(x2.data_ptr(), x2.stride(0), M, K, arr, n,
+                                        None if ws is None else ws.data_ptr(),
+                                        0 if ws is None else ws.numel(), _stream())
+    _lib.check(rc, "nmi_linear_fp8_w8a16_grouped")
+    return outs
 
 
 def gemv_fp8(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,

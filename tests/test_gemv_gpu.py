@@ -21,12 +21,15 @@ FIXTURES = ["kat_gemv_n64_k3136", "tiny_m4_n8_k16", "ragged_m3_n37_k208",
             "skinny_m16_n48_k3136", "special_nan_zero"]
 
 
+GEMV_KNOBS = ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg")
+
+
 @pytest.fixture(autouse=True)
 def _reset_tuning():
-    for k in ("gemv.ks", "gemv.unroll"):
+    for k in GEMV_KNOBS:
         _lib.tuning_set(k, 0)
     yield
-    for k in ("gemv.ks", "gemv.unroll"):
+    for k in GEMV_KNOBS:
         _lib.tuning_set(k, 0)
 
 
@@ -116,17 +119,23 @@ def test_gemv_real_shapes(label, N, K, act):
 
 
 @pytest.mark.parametrize("ks", [1, 2, 4])
-@pytest.mark.parametrize("unroll", [4, 8, 16])
-def test_gemv_every_schedule(ks, unroll):
-    """Every (K-split, unroll) instantiation against the oracle, incl. K beyond one LDS window
-    (K = 20000 -> 1250 chunks > the 1008-chunk window) and short K (one partial chunk group)."""
+@pytest.mark.parametrize("t", [1, 2, 4])
+@pytest.mark.parametrize("p", [2, 3, 4])
+def test_gemv_every_schedule(ks, t, p):
+    """Every (K-split waves, rows per wave, chunks per lane) instantiation with x from LDS and
+    from global memory, against the oracle: K beyond one LDS window (K = 20000 -> 1250 chunks >
+    the 1024-chunk window), slices longer than one batch (K = 12544 at ks = 1), short K (one
+    partial chunk group) and N not a multiple of the rows per workgroup."""
     _lib.tuning_set("gemv.ks", ks)
-    _lib.tuning_set("gemv.unroll", unroll)
-    for N, K in [(1000, 3136), (37, 20000), (130, 16), (67, 48), (300, 12544)]:
-        announce("gemv_schedule", ks, unroll, N, K)
-        x, w, s = _case(N, K, 7 * N + K, scales="log_uniform")
-        y = bits(ops.gemv_fp8(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
-        assert_parity(y, oracle_bits(x, w, s), f"ks={ks} unroll={unroll} N={N} K={K}")
+    _lib.tuning_set("gemv.t", t)
+    _lib.tuning_set("gemv.p", p)
+    for xg in (0, 1):
+        _lib.tuning_set("gemv.xg", xg)
+        for N, K in [(1000, 3136), (37, 20000), (130, 16), (67, 48), (300, 12544)]:
+            announce("gemv_schedule", ks, t, p, xg, N, K)
+            x, w, s = _case(N, K, 7 * N + K, scales="log_uniform")
+            y = bits(ops.gemv_fp8(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
+            assert_parity(y, oracle_bits(x, w, s), f"ks={ks} t={t} p={p} xg={xg} N={N} K={K}")
 
 
 # ------------------------------------------------------------------------------- properties

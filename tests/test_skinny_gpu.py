@@ -1,0 +1,196 @@
+"""GPU parity of the skinny kernel (1 <= M <= 16, bf16 MFMA over e4m3 weights converted in
+registers) and of the grouped entry point, against the torch fp32 dequant-then-F.linear oracle.
+
+Tolerance: rel_l2 <= 1e-3 and max |diff| <= 2 bf16 ulp at max(|ref|, 2^-8 rms(ref)).
+Size-independent properties: the workspace's arrival counters are re-armed after every
+launch (the workspace reads back zero there), repeated calls are bit-identical, a grouped call
+equals the separate calls under the same schedule, and M = 1 through this kernel agrees with
+the GEMV kernel within the tolerance.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from nemotron_infer_amd import _lib, ops, synth
+from oracle import linear
+from tests.conftest import load_golden
+from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_to_dev, w_to_dev,
+                            x_to_dev)
+
+pytestmark = pytest.mark.gpu
+
+KNOBS = ("skinny.ks", "skinny.kg", "skinny.u", "m1.path", "gemv.ks")
+
+
+@pytest.fixture(autouse=True)
+def _reset_tuning():
+    for k in KNOBS:
+        _lib.tuning_set(k, 0)
+    yield
+    for k in KNOBS:
+        _lib.tuning_set(k, 0)
+
+
+def _case(M, N, K, seed, scales="log_uniform", act="normal"):
+    w, s = synth.make_weight(N, K, seed, "cpu", scales=scales)
+    x = synth.make_act(M, K, seed + 1, "cpu", kind=act)
+    return x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy()
+
+
+def _run(x, w, s, use_ws):
+    return bits(ops.linear_fp8_w8a16(x_to_dev(x), w_to_dev(w), s_to_dev(s), use_workspace=use_ws))
+
+
+@pytest.mark.parametrize("name", ["kat_gemv_n64_k3136", "tiny_m4_n8_k16", "ragged_m3_n37_k208",
+                                  "skinny_m16_n48_k3136", "special_nan_zero"])
+@pytest.mark.parametrize("use_ws", [False, True])
+def test_fixtures_all_m(name, use_ws):
+    """Every fixture, every leading-row count 1..M of it, through the skinny kernel (M = 1 is
+    forced onto it with m1.path = 2)."""
+    g = load_golden(name)
+    x, w, s = g["x_bf16"], g["w_codes"], g["w_scale"]
+    ref64 = linear.bf16_rne(g["y_f64"].astype(np.float32))
+    _lib.tuning_set("m1.path", 2)
+    for M in range(1, x.shape[0] + 1):
+        announce("skinny_fixture", name, M, use_ws)
+        y = _run(x[:M], w, s, use_ws)
+        assert_parity(y, ref64[:M], f"{name} M={M} ws={use_ws} vs fp64")
+
+
+@pytest.mark.parametrize("M", list(range(1, 17)))
+def test_every_m_ragged(M):
+    """Ragged N (not a multiple of 16 or 64) and K (not a multiple of 64), both paths."""
+    _lib.tuning_set("m1.path", 2)
+    for N, K in [(37, 208), (1000, 3136), (130, 12544 + 16)]:
+        x, w, s = _case(M, N, K, 17 * M + N + K)
+        ref = oracle_bits(x, w, s)
+        for use_ws in (False, True):
+            announce("skinny_ragged", M, N, K, use_ws)
+            assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} ws={use_ws}")
+
+
+@pytest.mark.parametrize("ksw", [1, 2, 4])
+@pytest.mark.parametrize("u", [8, 16])
+@pytest.mark.parametrize("kg", [1, 3, 7])
+def test_every_schedule(ksw, u, kg):
+    """Each (waves splitting K, loads per batch, workgroups splitting K) instantiation, incl.
+    LDS windows (M = 16 stages 64 chunks per window) and K groups with a partial last group."""
+    _lib.tuning_set("skinny.ks", ksw)
+    _lib.tuning_set("skinny.u", u)
+    _lib.tuning_set("skinny.kg", kg)
+    for M, N, K in [(16, 300, 3136), (5, 77, 5120), (2, 1024, 1040)]:
+        announce("skinny_schedule", ksw, u, kg, M, N, K)
+        x, w, s = _case(M, N, K, 1000 * ksw + 100 * u + 10 * kg + M)
+        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"ksw={ksw} u={u} kg={kg} M={M}")
+
+
+@pytest.mark.parametrize("M", [2, 4, 8, 16])
+def test_config2_shapes_with_workspace(M):
+    """Config 2 (M in {2,4,8,16}, the six decode shapes, per-row log-uniform scales)."""
+    for lin in synth.DECODE_SET:
+        announce("skinny_config2_ws", M, lin.name)
+        x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, act=lin.act)
+        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} {lin.name}")
+
+
+def test_workspace_rearmed_and_deterministic():
+    """After a split-K launch the counters read back zero; repeated calls are bit-identical."""
+    M, N, K = 8, 3136, 12544
+    announce("skinny_rearm", M, N, K)
+    x, w, s = _case(M, N, K, 4)
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    nbytes = _lib.lib().nmi_linear_workspace_bytes(M, N, K)
+    assert nbytes > 0
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    outs = []
+    L = _lib.lib()
+    for _ in range(3):
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+        _lib.check(L.nmi_linear_fp8_w8a16_ws(xd.data_ptr(), K, wd.data_ptr(), K, sd.data_ptr(), y.data_ptr(),
+                                             N, M, N, K, ws.data_ptr(), nbytes, None), "ws")
+        torch.cuda.synchronize()
+        outs.append(bits(y))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    counters = ws[: 4 * 16384].cpu().numpy()
+    assert not counters.any(), "arrival counters not re-armed"
+    assert_parity(outs[0], oracle_bits(x, w, s), "rearm")
+
+
+def test_workspace_shared_between_shapes():
+    """One workspace used by calls of different shapes in turn (small N, then large N, then
+    small again): a counter slot is never overwritten by another call's partials."""
+    L = _lib.lib()
+    cases = [(16, 48, 3136), (2, 5120, 3136), (16, 48, 3136), (4, 1024, 12544), (2, 5120, 3136)]
+    nbytes = max(L.nmi_linear_workspace_bytes(M, N, K) for M, N, K in cases)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    for i, (M, N, K) in enumerate(cases):
+        announce("ws_shared", i, M, N, K)
+        x, w, s = _case(M, N, K, 90 + i)
+        xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+        _lib.check(L.nmi_linear_fp8_w8a16_ws(xd.data_ptr(), K, wd.data_ptr(), K, sd.data_ptr(), y.data_ptr(),
+                                             N, M, N, K, ws.data_ptr(), nbytes, None), "ws")
+        assert_parity(bits(y), oracle_bits(x, w, s), f"shared ws call {i}")
+    assert not ws[: 4 * 16384].cpu().numpy().any()
+
+
+def test_workspace_never_returns_stale_partials():
+    """The same shape (same workspace slots) with new inputs each call: every result must match
+    its own oracle, so no partial written by an earlier call can be read back."""
+    M, N, K = 4, 5120, 3136
+    w, s = synth.make_weight(N, K, 5, "cpu", scales="log_uniform")
+    wd, sd = w.to(DEV), s.to(DEV)
+    for i in range(4):
+        announce("stale_partials", i)
+        x = synth.make_act(M, K, 300 + i, "cpu")
+        y = ops.linear_fp8_w8a16(x.to(DEV), wd, sd)
+        xb = x.view(torch.int16).numpy().view(np.uint16)
+        assert_parity(bits(y), oracle_bits(xb, w.numpy(), s.numpy()), f"call {i}")
+
+
+def test_grouped_qkv_matches_separate():
+    """q|k|v in one launch (attention_block.cuh:400-402 runs them as three GEMVs) equals the
+    three separate calls under the same (pinned) schedule, bit for bit, for M = 1 on both
+    kernels and M = 4."""
+    lins = synth.DECODE_SET[:3]
+    for M in (1, 4):
+        for path in (1, 2):
+            if M > 1 and path == 1:
+                continue
+            _lib.tuning_set("m1.path", path)
+            _lib.tuning_set("skinny.kg", 2)
+            _lib.tuning_set("skinny.ks", 2)
+            _lib.tuning_set("gemv.ks", 2)
+            announce("grouped_qkv", M, path)
+            x = synth.make_act(M, 3136, 77, "cpu")
+            ws = [synth.make_weight(l.N, l.K, 70 + i, "cpu", scales="log_uniform") for i, l in enumerate(lins)]
+            xd = x.to(DEV)
+            wd = [(w.to(DEV), s.to(DEV)) for w, s in ws]
+            grouped = ops.linear_fp8_w8a16_grouped(xd, wd)
+            separate = [ops.linear_fp8_w8a16(xd, w, s) for w, s in wd]
+            torch.cuda.synchronize()
+            xb = x.view(torch.int16).numpy().view(np.uint16)
+            for (w, s), yg, ys, l in zip(ws, grouped, separate, lins):
+                assert np.array_equal(bits(yg), bits(ys)), f"{l.name} M={M} path={path}"
+                assert_parity(bits(yg), oracle_bits(xb, w.numpy(), s.numpy()), f"grouped {l.name}")
+
+
+def test_grouped_rejects_bad_groups():
+    L = _lib.lib()
+    arr = (_lib.LinearGroup * 5)()
+    assert L.nmi_linear_fp8_w8a16_grouped(0x10000, 64, 1, 64, arr, 5, None, 0, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_linear_fp8_w8a16_grouped(0x10000, 64, 1, 64, arr, 0, None, 0, None) == _lib.NMI_ERR_INVALID_ARG
+
+
+def test_m1_mfma_path_vs_gemv_full_size():
+    """M = 1 at config 0's full size through both kernels: both within tolerance of the oracle."""
+    N, K = 12544, 3136
+    announce("m1_paths", N, K)
+    x, w, s = _case(1, N, K, 5, scales="per_tensor")
+    ref = oracle_bits(x[0], w, s)
+    for path in (1, 2):
+        _lib.tuning_set("m1.path", path)
+        y = bits(ops.linear_fp8_w8a16(x_to_dev(x[0]), w_to_dev(w), s_to_dev(s)))
+        assert_parity(y, ref, f"m1.path={path}")
