@@ -1,23 +1,27 @@
 #!/usr/bin/env python3
 """bench.py -- fp8 (e4m3) W8A16 linear hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--no-extras]
 
 Headline (``value``): BASELINE config 1, the decode-step GEMV set of one attention block and
 one MLP block at M = 1 (q 3136->5120, k/v 3136->1024, o 5120->3136, up 3136->12544,
-down 12544->3136), six launches per step in the engine's order, replayed from a HIP graph.
-A step's algorithmic bytes are sum(N*K + 4N + 2K + 2N) = 117,427,456 B.  Weights rotate over
-ten copies (1.17 GB > the 256 MB Infinity Cache + L2), so every step streams from HBM.
-``value`` = bytes per step / measured time per step (GB/s, whole job, launch gaps included).
+down 12544->3136).  A step is launched as the engine's blocks would launch it: q|k|v in one
+grouped launch (they share the block's normed input, as model/attention_block.cuh:400-402
+runs them on one input), then o, up and down -- four launches, replayed from a HIP graph.
+A step's algorithmic bytes are sum(N*K + 4N + 2K + 2N) over the six matrices =
+117,427,456 B.  Weights rotate over ten copies (1.17 GB > the 256 MB Infinity Cache + L2),
+so every step streams W from HBM.  ``value`` = bytes per step / time per step (GB/s).
 
-``roofline`` -- the GEMV kernel (the dominant kernel of the step): its algorithmic bytes per
-launch over its average launch duration, from HIP events around each launch in a separate
-pass over the same rotated weights (HBM-bound; peak 8 TB/s).
+``roofline`` -- the M = 1 GEMV kernel (every launch of the step is one): algorithmic bytes per
+launch over the average launch duration, both from the timed region (graph replay, HIP events
+on the replay stream); HBM-bound, peak 8 TB/s.  ``launches`` gives each launch's own duration
+(a graph of that launch alone over the rotated copies) for comparison with rocprofv3.
 
-Also reported (same line): ``prefill_gemm`` (config 3, M = 2048, TFLOP/s vs 2.5 PFLOP/s dense
-bf16 MFMA), ``decode_stream`` (config 4, 92 GEMVs over a 42-layer weight set),
-``skinny`` (config 2, M in {2,4,8,16}) and ``cpu_baseline``: the torch CPU reference path
-(fp32 dequant then F.linear, oracle/linear.py) on a bounded sample of config 1.
+Also reported (same line): ``prefill_gemm`` (config 3, M = 2048, TFLOP/s against 2.5 PFLOP/s
+dense bf16 MFMA), ``skinny`` (config 2, M in {2,4,8,16}, same four launches per step),
+``decode_stream`` (config 4, the 42-layer weight stream, 84 launches) and ``cpu_baseline``:
+the torch CPU reference path (fp32 dequant then F.linear, oracle/linear.py) on a bounded
+sample of config 1, on this host's cores.
 """
 from __future__ import annotations
 
@@ -36,6 +40,11 @@ METRIC = "fp8 W8A16 GEMV achieved HBM GB/s (% of peak) at M=1; prefill GEMM TFLO
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 ROTATION_BYTES = 1 << 30
+# HBM bytes per launch of the config-1 step, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
+# script (scaled by a 256 MiB copy; profiles/gemv_m1_config1_decode_set.md).  Re-measured when the
+# GEMV kernels change; reported as roofline.traffic next to the algorithmic bytes.
+MEASURED_TRAFFIC = {"qkv_grouped": 22735968, "o_proj": 16327829, "up_proj": 39604013,
+                    "down_proj": 39762855}
 
 
 def log(*a):
@@ -48,136 +57,161 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
-    p.add_argument("--no-extras", action="store_true", help="headline and roofline only")
+    p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
+    p.add_argument("--pmc-calibration", action="store_true",
+                   help="first copy 256 MiB device-to-device three times (a kernel of known traffic "
+                        "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return p.parse_args()
 
 
-class Events:
-    """Elapsed GPU time between events on torch's current stream (our launch stream)."""
+class Timer:
+    """HIP events on a dedicated stream; everything timed is launched on that stream."""
 
-    def __init__(self, n):
+    def __init__(self):
         import torch
 
-        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        self.stream = torch.cuda.Stream()
+        self.t0 = torch.cuda.Event(enable_timing=True)
+        self.t1 = torch.cuda.Event(enable_timing=True)
 
-    def ms(self, i, j):
-        return self.ev[i].elapsed_time(self.ev[j])
+    def capture(self, fn):
+        import torch
+
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            fn()
+        return g
+
+    def time_replays(self, graphs):
+        """Run ``graphs`` (a list, replayed in order) between two events; return ms."""
+        import torch
+
+        torch.cuda.synchronize()
+        with torch.cuda.stream(self.stream):
+            self.t0.record(self.stream)
+            for g in graphs:
+                g.replay()
+            self.t1.record(self.stream)
+        torch.cuda.synchronize()
+        return self.t0.elapsed_time(self.t1)
 
 
-def prime_queue(ms=20):
-    """Spin the GPU briefly so the host can enqueue ahead of it (event deltas then measure GPU
-    time, not host launch latency)."""
+def rotated(dev, host, copies):
     import torch
 
-    try:
-        torch.cuda._sleep(int(ms * 2.0e6))
-    except Exception:
-        pass
+    base = [(w.to(dev), s.to(dev)) for w, s in host]
+    return [[(w.clone(), s.clone()) for w, s in base] for _ in range(copies)]
 
 
-def decode_set_weights(dev, rotation_bytes):
-    """Config-1 weights: seeded on the CPU (the same bytes feed the CPU baseline), copied to
-    the GPU, then cloned into enough copies to defeat the caches."""
-    import torch
-
+def decode_inputs():
+    """Config-1 weights and activations, seeded on the CPU (the same bytes feed the CPU
+    baseline)."""
     from nemotron_infer_amd import synth
 
-    host, dset = [], []
+    host = []
     for i, lin in enumerate(synth.DECODE_SET):
         w, s = synth.make_weight(lin.N, lin.K, 1000 + i, "cpu")
         x = synth.make_act(1, lin.K, 1100 + i, "cpu", kind=lin.act)
         host.append((lin, x, w, s))
-    set_bytes = sum(l.weight_bytes for l in synth.DECODE_SET)
-    copies = max(2, math.ceil(rotation_bytes / set_bytes))
-    base = [(lin, x.to(dev), w.to(dev), s.to(dev)) for lin, x, w, s in host]
-    for _ in range(copies):
-        dset.append([(lin, x, w.clone(), s.clone(),
-                      torch.empty((1, lin.N), dtype=torch.bfloat16, device=dev)) for lin, x, w, s in base])
-    return host, dset
+    return host
 
 
-def capture(fn, stream):
+def make_step(ops, xs, mats, ys, ws_use=True):
+    """One decode step over one weight copy: q|k|v grouped, then o, up, down."""
+    (wq, sq), (wk, sk), (wv, sv), (wo, so), (wu, su), (wd, sd) = mats
+    x_attn, x_o, x_up, x_down = xs
+    y_qkv, y_o, y_up, y_down = ys
+
+    def step():
+        ops.linear_fp8_w8a16_grouped(x_attn, [(wq, sq), (wk, sk), (wv, sv)], outs=y_qkv,
+                                     use_workspace=ws_use)
+        ops.linear_fp8_w8a16(x_o, wo, so, out=y_o, use_workspace=ws_use)
+        ops.linear_fp8_w8a16(x_up, wu, su, out=y_up, use_workspace=ws_use)
+        ops.linear_fp8_w8a16(x_down, wd, sd, out=y_down, use_workspace=ws_use)
+
+    return step
+
+
+def step_buffers(dev, M, K_attn=3136):
     import torch
 
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        fn()
-    return g
+    from nemotron_infer_amd import synth
+
+    L = synth.DECODE_SET
+    y_qkv = [torch.empty((M, l.N), dtype=torch.bfloat16, device=dev) for l in L[:3]]
+    return (y_qkv, torch.empty((M, L[3].N), dtype=torch.bfloat16, device=dev),
+            torch.empty((M, L[4].N), dtype=torch.bfloat16, device=dev),
+            torch.empty((M, L[5].N), dtype=torch.bfloat16, device=dev))
 
 
-def bench_decode_set(args, dev):
+def bench_decode_set(args, dev, host):
     import torch
 
     from nemotron_infer_amd import ops, synth
 
-    host, dset = decode_set_weights(dev, ROTATION_BYTES)
-    R = len(dset)
+    set_bytes = sum(l.weight_bytes for l in synth.DECODE_SET)
+    R = max(2, math.ceil(ROTATION_BYTES / set_bytes))
+    copies = rotated(dev, [(w, s) for _, _, w, s in host], R)
+    xs = (host[0][1].to(dev), host[3][1].to(dev), host[4][1].to(dev), host[5][1].to(dev))
+    ys = step_buffers(dev, 1)
+    steps = [make_step(ops, xs, copies[r], ys) for r in range(R)]
     step_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l in synth.DECODE_SET)
 
-    def step(r):
-        for lin, x, w, s, y in dset[r]:
-            ops.linear_fp8_w8a16(x, w, s, out=y)
-
-    # eager warm-up (also initialises per-device state before capture)
-    for i in range(max(args.warmup, R)):
-        step(i % R)
+    for i in range(max(args.warmup, R)):          # eager warm-up, also before any capture
+        steps[i % R]()
     torch.cuda.synchronize()
-
-    stream = torch.cuda.Stream()
-    graph_all = capture(lambda: [step(r) for r in range(R)], stream)
+    T = Timer()
+    g_all = T.capture(lambda: [s() for s in steps])
     tail = args.steps % R
-    graph_tail = capture(lambda: [step(r) for r in range(tail)], stream) if tail else None
-    for _ in range(max(1, args.warmup // R)):
-        graph_all.replay()
-    torch.cuda.synchronize()
-
-    ev = Events(2)
-    torch.cuda.synchronize()
-    ev.ev[0].record()
-    for _ in range(args.steps // R):
-        graph_all.replay()
-    if graph_tail is not None:
-        graph_tail.replay()
-    ev.ev[1].record()
-    torch.cuda.synchronize()
-    ms_total = ev.ms(0, 1)
-    ms_per_step = ms_total / args.steps
+    g_tail = T.capture(lambda: [steps[r]() for r in range(tail)]) if tail else None
+    T.time_replays([g_all] * max(1, args.warmup // R))
+    graphs = [g_all] * (args.steps // R) + ([g_tail] if g_tail is not None else [])
+    ms = T.time_replays(graphs)
+    ms_per_step = ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Kernel durations: one event between consecutive launches, eager, queue primed.
-    reps = max(4, min(args.steps, 40))
-    n = reps * len(synth.DECODE_SET)
-    kev = Events(n + 1)
-    prime_queue()
-    i = 0
-    kev.ev[0].record()
-    for rep in range(reps):
-        for lin, x, w, s, y in dset[rep % R]:
-            ops.linear_fp8_w8a16(x, w, s, out=y)
-            i += 1
-            kev.ev[i].record()
-    torch.cuda.synchronize()
-    per = {l.name: [] for l in synth.DECODE_SET}
-    for k in range(n):
-        lin = synth.DECODE_SET[k % len(synth.DECODE_SET)]
-        per[lin.name].append(kev.ms(k, k + 1))
-    kernels = {}
-    tot_b, tot_ms = 0, 0.0
-    for lin in synth.DECODE_SET:
-        d = sorted(per[lin.name])[len(per[lin.name]) // 2]
-        b = synth.linear_bytes(1, lin.N, lin.K)
-        kernels[lin.name] = {"N": lin.N, "K": lin.K, "us": round(d * 1e3, 2),
-                             "GB/s": round(b / (d * 1e-3) / 1e9, 1)}
-        tot_b += b
-        tot_ms += d
-    achieved = tot_b / (tot_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gemv_fp8_m1_kernel",
-                "per_launch_bytes_avg": tot_b // len(synth.DECODE_SET),
-                "per_launch_us_avg": round(tot_ms * 1e3 / len(synth.DECODE_SET), 2)}
+    # Each launch of the step alone: a graph of that launch over the R copies.
+    L = synth.DECODE_SET
+    launches = {}
+    groups = [("qkv_grouped", [0, 1, 2]), ("o_proj", [3]), ("up_proj", [4]), ("down_proj", [5])]
+    for name, idx in groups:
+        def one(r, idx=idx):
+            if len(idx) > 1:
+                ops.linear_fp8_w8a16_grouped(xs[0], [copies[r][i] for i in idx], outs=ys[0])
+            else:
+                i = idx[0]
+                ops.linear_fp8_w8a16(xs[{3: 1, 4: 2, 5: 3}[i]], *copies[r][i], out=ys[{3: 1, 4: 2, 5: 3}[i]])
+        g = T.capture(lambda: [one(r) for r in range(R)])
+        T.time_replays([g])
+        t = T.time_replays([g] * 5) / (5 * R)
+        b = sum(synth.linear_bytes(1, L[i].N, L[i].K) for i in idx)
+        launches[name] = {"N": sum(L[i].N for i in idx), "K": L[idx[0]].K, "bytes": b,
+                          "us": round(t * 1e3, 2), "GB/s": round(b / (t * 1e-3) / 1e9, 1)}
+    # The six matrices as six separate launches (the reference's launch structure).
+    def six(r):
+        for i, l in enumerate(L):
+            xi = xs[0] if i < 3 else xs[{3: 1, 4: 2, 5: 3}[i]]
+            yi = ys[0][i] if i < 3 else ys[{3: 1, 4: 2, 5: 3}[i]]
+            ops.linear_fp8_w8a16(xi, *copies[r][i], out=yi)
+    g6 = T.capture(lambda: [six(r) for r in range(R)])
+    T.time_replays([g6])
+    t6 = T.time_replays([g6] * 5) / (5 * R)
+    separate = {"launches": 6, "us_per_step": round(t6 * 1e3, 2),
+                "GB/s": round(step_bytes / (t6 * 1e-3) / 1e9, 1)}
+
+    n_launch = len(groups)
+    traffic = sum(MEASURED_TRAFFIC.values()) // len(MEASURED_TRAFFIC)
+    roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per launch (x2.0 / x1.0 copy "
+                                  "calibration), profiles/gemv_m1_config1_decode_set.md",
+                "kernel": "gemv_fp8_m1_kernel (every launch of the step)",
+                "launches_per_step": n_launch,
+                "per_launch_bytes_avg": step_bytes // n_launch,
+                "per_launch_us_avg": round(ms_per_step * 1e3 / n_launch, 3)}
+    del copies, steps, g_all, g_tail, g6
     return dict(value=value, ms_per_step=ms_per_step, step_bytes=step_bytes, copies=R,
-                roofline=roofline, kernels=kernels, host=host)
+                roofline=roofline, launches=launches, separate=separate)
 
 
 def bench_prefill(dev, reps=20):
@@ -187,6 +221,7 @@ def bench_prefill(dev, reps=20):
 
     out = {}
     tot_f, tot_ms = 0, 0.0
+    T = Timer()
     for i, lin in enumerate(synth.PREFILL_SET):
         M = synth.PREFILL_M
         w, s = synth.make_weight(lin.N, lin.K, 3000 + i, dev)
@@ -194,25 +229,50 @@ def bench_prefill(dev, reps=20):
         y = torch.empty((M, lin.N), dtype=torch.bfloat16, device=dev)
         for _ in range(3):
             ops.gemm_fp8_w8a16(x, w, s, out=y)
-        torch.cuda.synchronize()
-        ev = Events(reps + 1)
-        prime_queue(5)
-        ev.ev[0].record()
-        for r in range(reps):
-            ops.gemm_fp8_w8a16(x, w, s, out=y)
-            ev.ev[r + 1].record()
-        torch.cuda.synchronize()
-        d = sorted(ev.ms(r, r + 1) for r in range(reps))[reps // 2]
+        g = T.capture(lambda: [ops.gemm_fp8_w8a16(x, w, s, out=y) for _ in range(reps)])
+        T.time_replays([g])
+        d = T.time_replays([g]) / reps
         fl = synth.linear_flops(M, lin.N, lin.K)
         out[lin.name] = {"M": M, "N": lin.N, "K": lin.K, "us": round(d * 1e3, 1),
                          "TFLOP/s": round(fl / (d * 1e-3) / 1e12, 1)}
         tot_f += fl
         tot_ms += d
-        del w, s, x, y
+        del w, s, x, y, g
     tf = tot_f / (tot_ms * 1e-3) / 1e12
     return {"workload": "config3_prefill_m2048", "tflops": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_kernel",
             "shapes": out}
+
+
+def bench_skinny(dev, host, reps=20):
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    set_bytes = sum(l.weight_bytes for l in synth.DECODE_SET)
+    R = max(2, math.ceil(ROTATION_BYTES / set_bytes))
+    copies = rotated(dev, [(w, s) for _, _, w, s in host], R)
+    res = {}
+    T = Timer()
+    L = synth.DECODE_SET
+    for M in (2, 4, 8, 16):
+        xs = tuple(synth.make_act(M, L[i].K, 2200 + M + i, dev, kind=L[i].act) for i in (0, 3, 4, 5))
+        ys = step_buffers(dev, M)
+        steps = [make_step(ops, xs, copies[r], ys) for r in range(R)]
+        for s in steps:
+            s()
+        torch.cuda.synchronize()
+        g = T.capture(lambda: [s() for s in steps])
+        T.time_replays([g])
+        n = max(1, reps // R)
+        ms = T.time_replays([g] * n) / (n * R)
+        b = sum(synth.linear_bytes(M, l.N, l.K) for l in L)
+        f = sum(synth.linear_flops(M, l.N, l.K) for l in L)
+        res[f"M={M}"] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                         "TFLOP/s": round(f / (ms * 1e-3) / 1e12, 2)}
+        del g, steps
+    del copies
+    return {"workload": "config2_skinny_decode_set", "launches_per_step": 4, "results": res}
 
 
 def bench_decode_stream(dev, reps=5):
@@ -222,96 +282,65 @@ def bench_decode_stream(dev, reps=5):
 
     layers = synth.decode_stream_layers()
     acts = {}
-    mats = []
+    calls = []
+    total_bytes = weight_bytes = 0
+
+    def act(K, kind):
+        if (K, kind) not in acts:
+            acts[(K, kind)] = synth.make_act(1, K, 41000 + K, dev, kind=kind)
+        return acts[(K, kind)]
+
     for li, kind, lins in layers:
+        mats = []
         for j, lin in enumerate(lins):
             w, s = synth.make_weight(lin.N, lin.K, 40000 + 10 * li + j, dev)
-            if (lin.K, lin.act) not in acts:
-                acts[(lin.K, lin.act)] = synth.make_act(1, lin.K, 41000 + lin.K, dev, kind=lin.act)
-            y = torch.empty((1, lin.N), dtype=torch.bfloat16, device=dev)
-            mats.append((lin, acts[(lin.K, lin.act)], w, s, y))
-    total_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l, *_ in mats)
-    weight_bytes = sum(l.N * l.K for l, *_ in mats)
+            mats.append((lin, w, s, torch.empty((1, lin.N), dtype=torch.bfloat16, device=dev)))
+            total_bytes += synth.linear_bytes(1, lin.N, lin.K)
+            weight_bytes += lin.N * lin.K
+        if kind == "attn":
+            q, k, v, o = mats
+            calls.append(("grouped", q[0].K, [(q[1], q[2]), (k[1], k[2]), (v[1], v[2])], [q[3], k[3], v[3]]))
+            calls.append(("single", o))
+        else:
+            for m in mats:
+                calls.append(("single", m))
 
     def run():
-        for lin, x, w, s, y in mats:
-            ops.linear_fp8_w8a16(x, w, s, out=y)
+        for c in calls:
+            if c[0] == "grouped":
+                ops.linear_fp8_w8a16_grouped(act(c[1], "normal"), c[2], outs=c[3])
+            else:
+                lin, w, s, y = c[1]
+                ops.linear_fp8_w8a16(act(lin.K, lin.act), w, s, out=y)
 
     run()
     torch.cuda.synchronize()
-    g = capture(run, torch.cuda.Stream())
-    g.replay()
-    torch.cuda.synchronize()
-    ev = Events(2)
-    ev.ev[0].record()
-    for _ in range(reps):
-        g.replay()
-    ev.ev[1].record()
-    torch.cuda.synchronize()
-    ms = ev.ms(0, 1) / reps
+    T = Timer()
+    g = T.capture(run)
+    T.time_replays([g])
+    ms = T.time_replays([g] * reps) / reps
     gbs = total_bytes / (ms * 1e-3) / 1e9
-    n_gemv = len(mats)
-    del mats
-    return {"workload": "config4_42layer_decode_stream", "gemvs": n_gemv,
+    n_gemv = sum(len(l[2]) for l in layers)
+    n_launch = len(calls)
+    del calls, g
+    return {"workload": "config4_42layer_decode_stream", "gemvs": n_gemv, "launches": n_launch,
             "bytes": total_bytes, "weight_bytes": weight_bytes, "ms": round(ms, 4),
             "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
             "tok_per_s_ceiling": round(1e3 / ms, 1)}
 
 
-def bench_skinny(dev, host_sets, reps=20):
-    import torch
-
-    from nemotron_infer_amd import ops, synth
-
-    res = {}
-    copies = []
-    set_bytes = sum(l.weight_bytes for l in synth.DECODE_SET)
-    R = max(2, math.ceil(ROTATION_BYTES / set_bytes))
-    base = [(lin, w.to(dev), s.to(dev)) for lin, x, w, s in host_sets]
-    for _ in range(R):
-        copies.append([(lin, w.clone(), s.clone()) for lin, w, s in base])
-    for M in (2, 4, 8, 16):
-        xs = [synth.make_act(M, lin.K, 2200 + M, dev, kind=lin.act) for lin in synth.DECODE_SET]
-        ys = [torch.empty((M, lin.N), dtype=torch.bfloat16, device=dev) for lin in synth.DECODE_SET]
-
-        def step(r):
-            for (lin, w, s), x, y in zip(copies[r], xs, ys):
-                ops.linear_fp8_w8a16(x, w, s, out=y)
-
-        for r in range(R):
-            step(r)
-        torch.cuda.synchronize()
-        g = capture(lambda: [step(r) for r in range(R)], torch.cuda.Stream())
-        g.replay()
-        torch.cuda.synchronize()
-        ev = Events(2)
-        ev.ev[0].record()
-        for _ in range(max(1, reps // R)):
-            g.replay()
-        ev.ev[1].record()
-        torch.cuda.synchronize()
-        nsteps = max(1, reps // R) * R
-        ms = ev.ms(0, 1) / nsteps
-        b = sum(synth.linear_bytes(M, l.N, l.K) for l in synth.DECODE_SET)
-        f = sum(synth.linear_flops(M, l.N, l.K) for l in synth.DECODE_SET)
-        res[f"M={M}"] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
-                         "TFLOP/s": round(f / (ms * 1e-3) / 1e12, 2)}
-    del copies
-    return {"workload": "config2_skinny_decode_set", "results": res}
-
-
-def cpu_baseline(host_sets, seconds):
+def cpu_baseline(host, seconds):
     """The reference's CPU path (tools/ref_full_model.py:44-49,137, restated in
     oracle/linear.py): fp32 dequant of W, F.linear in fp32, bf16 rounding -- on config 1's
-    bytes, for about ``seconds`` of work."""
+    bytes, for about ``seconds`` of work, with torch's intra-op threads on this host."""
     import numpy as np
     import torch
 
     from nemotron_infer_amd import synth
     from oracle import linear as olin
 
-    data = [(x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy()) for _, x, w, s in host_sets]
-    step_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l, *_ in host_sets)
+    data = [(x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy()) for _, x, w, s in host]
+    step_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l, *_ in host)
     threads = torch.get_num_threads()
     olin.linear_fp8_w8a16(*data[0])          # warm-up
     t0 = time.perf_counter()
@@ -342,30 +371,42 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the fp8 linear "
-              f"path is single-GPU, multi-GPU sharding is a design note in DESIGN.md", file=sys.stderr)
+              f"path is single-GPU, and how it would shard is a design note (DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     import torch
 
-    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    from nemotron_infer_amd import synth
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
     dev = "cuda:0"
     torch.cuda.set_device(0)
     t0 = time.time()
+    if args.pmc_calibration:
+        a = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+    host = decode_inputs()
     log("decode set (config 1) ...")
-    d = bench_decode_set(args, dev)
-    log(f"decode set: {d['value']:.1f} GB/s, {d['ms_per_step'] * 1e3:.2f} us/step; kernel {d['roofline']['achieved']} GB/s")
+    d = bench_decode_set(args, dev, host)
+    log(f"decode set: {d['value']:.1f} GB/s, {d['ms_per_step'] * 1e3:.2f} us/step")
     extras = {}
     if not args.no_extras:
         log("prefill GEMM (config 3) ...")
         extras["prefill_gemm"] = bench_prefill(dev)
         log(f"prefill: {extras['prefill_gemm']['tflops']} TFLOP/s")
         log("skinny M (config 2) ...")
-        extras["skinny"] = bench_skinny(dev, d["host"])
+        extras["skinny"] = bench_skinny(dev, host)
         log("decode stream (config 4) ...")
         extras["decode_stream"] = bench_decode_stream(dev)
         log(f"stream: {extras['decode_stream']['GB/s']} GB/s")
     torch.cuda.empty_cache()
     log("cpu baseline ...")
-    cpu = cpu_baseline(d["host"], args.cpu_seconds)
+    cpu = cpu_baseline(host, args.cpu_seconds)
     line = {
         "metric": METRIC,
         "value": round(d["value"], 1),
@@ -377,17 +418,19 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16",
         "data": "synthetic (seeded N(0,0.02) weights -> e4m3 per-tensor scale; bf16 N(0,1) / relu^2 activations)",
         "config": {"workload": "config1_decode_gemv_set_m1",
-                   "shapes": {k: [v["N"], v["K"]] for k, v in d["kernels"].items()},
+                   "shapes": {l.name: [l.N, l.K] for l in synth.DECODE_SET},
                    "M": 1, "bytes_per_step": d["step_bytes"],
                    "weight_copies_rotated": d["copies"],
-                   "operands": "W e4m3 [N,K] + f32 per-row scale, x bf16, y bf16, f32 accumulate",
-                   "launch": "HIP graph of the six GEMV launches per step"},
+                   "operands": "W e4m3 [N,K] (converted exactly to bf16) + f32 per-row scale, x bf16, "
+                               "f32 accumulation, y bf16",
+                   "launch": "HIP graph; per step: q|k|v grouped, o, up, down (4 launches)"},
         "roofline": d["roofline"],
         "cpu_baseline": cpu,
-        "kernels": d["kernels"],
+        "launches": d["launches"],
+        "six_separate_launches": d["separate"],
         **extras,
         "wall_s": round(time.time() - t0, 1),
     }
