@@ -137,16 +137,396 @@ __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Large tiles: BM x BN x 64 with 4 waves of (BM/2) x (BN/2) (128 x 128 for 256 x 256), W as
+// the MFMA A operand (16 weight rows per block) and x as B, so each lane ends with four
+// consecutive output columns n of one row m: one 8-byte store and one scale per n.
+// Double-buffered in dynamic LDS (2 x (BM + BN) x 64 bf16 = 128 KiB at 256 x 256), one
+// barrier per K step, global loads of step t+1 in flight during the MFMAs of step t.
+// Workgroups are dispatched to the 8 XCDs round-robin; tile t is given to the workgroup
+// that lands on XCD t / ceil(T / 8), so each XCD works through a contiguous run of tiles
+// (n fastest: consecutive tiles share their x rows in that XCD's L2).
+// Loads read clamped in-range addresses unconditionally; K-tail pieces are zeroed in
+// registers before the LDS store (rows past M or N only feed outputs that are not stored).
+struct GemmArgs {
+    const uint16_t* x;
+    int64_t ldx;
+    const uint8_t* W;
+    int64_t ldw;
+    const float* s;
+    uint16_t* y;
+    int64_t ldy;
+    int M, N, K;
+    int tiles_m, tiles_n, per_xcd;
+    int vec_store;          // y 8-byte aligned and ldy % 4 == 0
+};
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmArgs a) {
+    constexpr int BK = kBK;
+    constexpr int WTM = BM / 2, WTN = BN / 2;      // wave tile (m x n)
+    constexpr int TM = WTM / 16, TN = WTN / 16;    // 16 x 16 MFMA tiles per wave
+    constexpr int XP = BM * (BK / 8) / 256;        // 16-byte x pieces per thread per K step
+    constexpr int WP = BN * (BK / 16) / 256;       // 16-byte W pieces per thread per K step
+    constexpr int STAGE = (BM + BN) * BK;          // bf16 elements per LDS stage
+    static_assert(XP >= 1 && WP >= 1, "tile too small for 256 threads");
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+
+    const int g = (int)blockIdx.x;
+    const int local = g >> 3;
+    const int tile = (g & 7) * a.per_xcd + local;
+    if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
+    const int tm = tile / a.tiles_n;
+    const int tn = tile - tm * a.tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int M = a.M, N = a.N, K = a.K;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wn = wave & 1, wm = wave >> 1;
+
+    uint4 rx[XP], rw[WP];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int p = tid + 256 * i;
+            const int row = p >> 3, kc = p & 7;
+            const int gm = min(m0 + row, M - 1), gk = min(k0 + kc * 8, K - 8);
+            rx[i] = load16(a.x + (int64_t)gm * a.ldx + gk);
+        }
+#pragma unroll
+        for (int i = 0; i < WP; ++i) {
+            const int p = tid + 256 * i;
+            const int row = p >> 2, kc = p & 3;
+            const int gn = min(n0 + row, N - 1), gk = min(k0 + kc * 16, K - 16);
+            rw[i] = load16(a.W + (int64_t)gn * a.ldw + gk);
+        }
+    };
+    auto sstore = [&](int buf, int k0) {
+        uint16_t* Ws = lds + buf * STAGE;
+        uint16_t* Xs = Ws + BN * BK;
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int p = tid + 256 * i;
+            const int row = p >> 3, kc = p & 7;
+            const uint4 v = (k0 + kc * 8 < K) ? rx[i] : uint4{0, 0, 0, 0};
+            *reinterpret_cast<uint4*>(Xs + row * BK + ((kc ^ (row & 7)) << 3)) = v;
+        }
+#pragma unroll
+        for (int i = 0; i < WP; ++i) {
+            const int p = tid + 256 * i;
+            const int row = p >> 2, kc = p & 3;
+            const uint4 w = (k0 + kc * 16 < K) ? rw[i] : uint4{0, 0, 0, 0};
+            const uint2 d0 = e4m3x4_to_bf16(w.x), d1 = e4m3x4_to_bf16(w.y);
+            const uint2 d2 = e4m3x4_to_bf16(w.z), d3 = e4m3x4_to_bf16(w.w);
+            const int c0 = 2 * kc, c1 = 2 * kc + 1;
+            *reinterpret_cast<uint4*>(Ws + row * BK + ((c0 ^ (row & 7)) << 3)) = uint4{d0.x, d0.y, d1.x, d1.y};
+            *reinterpret_cast<uint4*>(Ws + row * BK + ((c1 ^ (row & 7)) << 3)) = uint4{d2.x, d2.y, d3.x, d3.y};
+        }
+    };
+
+    f32x4 acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int KT = (K + BK - 1) / BK;
+    gload(0);
+    sstore(0, 0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < KT) gload((kt + 1) * BK);
+        const uint16_t* Ws = lds + buf * STAGE;
+        const uint16_t* Xs = Ws + BN * BK;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const int chunk = ks * 4 + (lane >> 4);
+            bf16x8 af[TN], bfr[TM];
+#pragma unroll
+            for (int i = 0; i < TN; ++i) {
+                const int row = wn * WTN + i * 16 + (lane & 15);
+                af[i] = *reinterpret_cast<const bf16x8*>(Ws + row * BK + ((chunk ^ (row & 7)) << 3));
+            }
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int row = wm * WTM + j * 16 + (lane & 15);
+                bfr[j] = *reinterpret_cast<const bf16x8*>(Xs + row * BK + ((chunk ^ (row & 7)) << 3));
+            }
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < KT) sstore(buf ^ 1, (kt + 1) * BK);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds D[n = 4 (lane / 16) + r][m = lane % 16] of each 16 x 16 tile.
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+        const int n = n0 + wn * WTN + i * 16 + 4 * (lane >> 4);
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = a.s[min(n + r, N - 1)];
+        const bool full = a.vec_store && (n + 3 < N);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            const int m = m0 + wm * WTM + j * 16 + (lane & 15);
+            if (m >= M) continue;
+            uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
+            const uint16_t b0 = f32_to_bf16_rne(acc[i][j][0] * sc[0]);
+            const uint16_t b1 = f32_to_bf16_rne(acc[i][j][1] * sc[1]);
+            const uint16_t b2 = f32_to_bf16_rne(acc[i][j][2] * sc[2]);
+            const uint16_t b3 = f32_to_bf16_rne(acc[i][j][3] * sc[3]);
+            if (full) {
+                *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
+                                                      (uint32_t)b2 | ((uint32_t)b3 << 16)};
+            } else {
+                if (n < N) yp[0] = b0;
+                if (n + 1 < N) yp[1] = b1;
+                if (n + 2 < N) yp[2] = b2;
+                if (n + 3 < N) yp[3] = b3;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// 32 x 32 x 16 MFMA variant of the large-tile kernel: the same tiles, LDS layout, XCD order
+// and epilogue, but v_mfma_f32_32x32x16_bf16 (half the fragment registers per k step of the
+// 16 x 16 x 32 form), with the fragments of k step s+1 read from LDS while the MFMAs of
+// step s run (two fragment register sets).  Operand layouts (gfx950): A lane l holds row
+// l % 32, k 8 (l / 32) .. +7; B lane l holds column l % 32, the same k; D register r of lane l
+// is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+template <int BM, int BN, int NW, bool B64>
+__global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const GemmArgs a) {
+    constexpr int BK = kBK;
+    constexpr int NT = NW * 64;                     // threads
+    constexpr int WGN = NW == 8 ? 4 : 2;            // waves along n
+    constexpr int WTM = BM / 2, WTN = BN / WGN;     // wave tile (m x n)
+    constexpr int TM = WTM / 32, TN = WTN / 32;     // 32 x 32 MFMA tiles per wave
+    constexpr int XP = BM * (BK / 8) / NT;
+    constexpr int WP = BN * (BK / 16) / NT;
+    constexpr int STAGE = (BM + BN) * BK;
+    static_assert(XP >= 1 && WP >= 1 && TM >= 1 && TN >= 1, "tile too small");
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+
+    const int g = (int)blockIdx.x;
+    const int local = g >> 3;
+    const int tile = (g & 7) * a.per_xcd + local;
+    if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
+    const int tm = tile / a.tiles_n;
+    const int tn = tile - tm * a.tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int M = a.M, N = a.N, K = a.K;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wn = wave % WGN, wm = wave / WGN;
+
+    uint4 rx[XP], rw[WP];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int p = tid + NT * i;
+            const int row = p >> 3, kc = p & 7;
+            const int gm = min(m0 + row, M - 1), gk = min(k0 + kc * 8, K - 8);
+            rx[i] = load16(a.x + (int64_t)gm * a.ldx + gk);
+        }
+#pragma unroll
+        for (int i = 0; i < WP; ++i) {
+            const int p = tid + NT * i;
+            const int row = p >> 2, kc = p & 3;
+            const int gn = min(n0 + row, N - 1), gk = min(k0 + kc * 16, K - 16);
+            rw[i] = load16(a.W + (int64_t)gn * a.ldw + gk);
+        }
+    };
+    // LDS tile layouts.  B64 = false: rows of eight 16-byte chunks, chunk c of row r at
+    // c ^ (r & 7).  B64 = true: the low and high 8 bytes of every chunk in two planes of
+    // 64-byte rows, chunk c of row r at c ^ ((r >> 2) & 7), so that fragments are read with
+    // ds_read_b64 (measured on MI355X: ~1.6x the LDS read throughput of ds_read_b128) and
+    // the 32 rows one read touches fall in distinct banks.
+    auto put16 = [&](uint16_t* T, int rows, int row, int c, uint4 v) {
+        if constexpr (B64) {
+            const int off = row * 32 + ((c ^ ((row >> 2) & 7)) << 2);          // in bf16 elements
+            *reinterpret_cast<uint2*>(T + off) = uint2{v.x, v.y};
+            *reinterpret_cast<uint2*>(T + rows * 32 + off) = uint2{v.z, v.w};
+        } else {
+            *reinterpret_cast<uint4*>(T + row * BK + ((c ^ (row & 7)) << 3)) = v;
+        }
+    };
+    auto get16 = [&](const uint16_t* T, int rows, int row, int c) -> bf16x8 {
+        if constexpr (B64) {
+            const int off = row * 32 + ((c ^ ((row >> 2) & 7)) << 2);
+            const uint2 lo = *reinterpret_cast<const uint2*>(T + off);
+            const uint2 hi = *reinterpret_cast<const uint2*>(T + rows * 32 + off);
+            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+            return __builtin_bit_cast(bf16x8, u32x4_t{lo.x, lo.y, hi.x, hi.y});
+        } else {
+            return *reinterpret_cast<const bf16x8*>(T + row * BK + ((c ^ (row & 7)) << 3));
+        }
+    };
+    auto sstore = [&](int buf, int k0) {
+        uint16_t* Ws = lds + buf * STAGE;
+        uint16_t* Xs = Ws + BN * BK;
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int p = tid + NT * i;
+            const int row = p >> 3, kc = p & 7;
+            const uint4 v = (k0 + kc * 8 < K) ? rx[i] : uint4{0, 0, 0, 0};
+            put16(Xs, BM, row, kc, v);
+        }
+#pragma unroll
+        for (int i = 0; i < WP; ++i) {
+            const int p = tid + NT * i;
+            const int row = p >> 2, kc = p & 3;
+            const uint4 w = (k0 + kc * 16 < K) ? rw[i] : uint4{0, 0, 0, 0};
+            const uint2 d0 = e4m3x4_to_bf16(w.x), d1 = e4m3x4_to_bf16(w.y);
+            const uint2 d2 = e4m3x4_to_bf16(w.z), d3 = e4m3x4_to_bf16(w.w);
+            put16(Ws, BN, row, 2 * kc, uint4{d0.x, d0.y, d1.x, d1.y});
+            put16(Ws, BN, row, 2 * kc + 1, uint4{d2.x, d2.y, d3.x, d3.y});
+        }
+    };
+    // Fragments of k step s (16 k = chunks 2s, 2s+1) from LDS stage `buf`.
+    auto frags = [&](int buf, int s, bf16x8 (&af)[TN], bf16x8 (&bfr)[TM]) {
+        const uint16_t* Ws = lds + buf * STAGE;
+        const uint16_t* Xs = Ws + BN * BK;
+        const int chunk = 2 * s + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < TN; ++i) af[i] = get16(Ws, BN, wn * WTN + i * 32 + (lane & 31), chunk);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) bfr[j] = get16(Xs, BM, wm * WTM + j * 32 + (lane & 31), chunk);
+    };
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int KT = (K + BK - 1) / BK;
+    bf16x8 af0[TN], bf0[TM], af1[TN], bf1[TM];
+    gload(0);
+    sstore(0, 0);
+    __syncthreads();
+    frags(0, 0, af0, bf0);
+    for (int kt = 0; kt < KT; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < KT) gload((kt + 1) * BK);
+#pragma unroll
+        for (int s = 0; s < BK / 16; s += 2) {
+            frags(buf, s + 1, af1, bf1);
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af0[i], bf0[j], acc[i][j], 0, 0, 0);
+            if (s + 2 < BK / 16) frags(buf, s + 2, af0, bf0);
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af1[i], bf1[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < KT) sstore(buf ^ 1, (kt + 1) * BK);
+        __syncthreads();
+        if (kt + 1 < KT) frags(buf ^ 1, 0, af0, bf0);
+    }
+
+    // Epilogue: register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+            const int n = n0 + wn * WTN + i * 32 + 8 * gq + 4 * (lane >> 5);
+            float sc[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[r] = a.s[min(n + r, N - 1)];
+            const bool full = a.vec_store && (n + 3 < N);
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int m = m0 + wm * WTM + j * 32 + (lane & 31);
+                if (m >= M) continue;
+                uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
+                const uint16_t b0 = f32_to_bf16_rne(acc[i][j][4 * gq + 0] * sc[0]);
+                const uint16_t b1 = f32_to_bf16_rne(acc[i][j][4 * gq + 1] * sc[1]);
+                const uint16_t b2 = f32_to_bf16_rne(acc[i][j][4 * gq + 2] * sc[2]);
+                const uint16_t b3 = f32_to_bf16_rne(acc[i][j][4 * gq + 3] * sc[3]);
+                if (full) {
+                    *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
+                                                          (uint32_t)b2 | ((uint32_t)b3 << 16)};
+                } else {
+                    if (n < N) yp[0] = b0;
+                    if (n + 1 < N) yp[1] = b1;
+                    if (n + 2 < N) yp[2] = b2;
+                    if (n + 3 < N) yp[3] = b3;
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, bool M32, int NW = 4, bool B64 = false>
+hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s,
+                      uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+    constexpr size_t lds = 2 * (size_t)(BM + BN) * kBK * sizeof(uint16_t);
+    constexpr auto kernel = M32 ? &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64> : &gemm_fp8_w8a16_big_kernel<BM, BN>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0};
+    a.tiles_m = (M + BM - 1) / BM;
+    a.tiles_n = (N + BN - 1) / BN;
+    const int T = a.tiles_m * a.tiles_n;
+    a.per_xcd = (T + 7) / 8;
+    a.vec_store = ((reinterpret_cast<uintptr_t>(y) & 7) == 0 && (ldy & 3) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(kernel, dim3(8 * a.per_xcd), dim3(M32 ? NW * 64 : 256), lds, stream, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
                        hipStream_t stream) {
-    constexpr int BM = 128, BN = 128;
-    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm_fp8_w8a16_kernel<BM, BN>), grid, dim3(256), 0, stream,
-                       x, ldx, W, ldw, s, y, ldy, M, N, K);
-    return hipGetLastError();
+    int tile = tuning().gemm_tile;
+    if (tile < 1 || tile > 13) {
+        // Measured on MI355X (config 3): 256 x 256 tiles on 8 waves (32 x 32 MFMA) where there
+        // are enough of them to fill the 256 CUs at least 1.5 times, 256 x 128 on 8 waves when
+        // N is short (e.g. down_proj N = 3136: 104 tiles of 256 x 256), 128 x 128 for small M.
+        const DeviceInfo& dev = device_info();
+        const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+        if (M < 512) tile = 1;
+        else tile = (big * 2 >= 3 * (int64_t)dev.num_cu) ? 8 : 9;
+    }
+    switch (tile) {
+        case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 3: return launch_big<256, 128, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 4: return launch_big<128, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 5: return launch_big<256, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 6: return launch_big<256, 128, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 7: return launch_big<128, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 8: return launch_big<256, 256, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 9: return launch_big<256, 128, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 10: return launch_big<256, 256, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 11: return launch_big<256, 256, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 12: return launch_big<256, 128, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 13: return launch_big<256, 128, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        default: {
+            constexpr int BM = 128, BN = 128;
+            const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+            hipLaunchKernelGGL((gemm_fp8_w8a16_kernel<BM, BN>), grid, dim3(256), 0, stream,
+                               x, ldx, W, ldw, s, y, ldy, M, N, K);
+            return hipGetLastError();
+        }
+    }
 }
 
 }  // namespace nmi

@@ -89,6 +89,37 @@ def test_strided_operands():
         assert torch.all(ybig[:, :8] == 7.0) and torch.all(ybig[:, 8 + N:] == 7.0)
 
 
+@pytest.fixture
+def _gemm_tile_reset():
+    yield
+    _lib.tuning_set("gemm.tile", 0)
+
+
+@pytest.mark.parametrize("tile", list(range(1, 14)))
+def test_every_tile_variant(tile, _gemm_tile_reset):
+    """Each GEMM tile variant (128x128; 256x256, 256x128, 128x256 with W as the A operand, on
+    16x16x32 or 32x32x16 MFMA) on
+    ragged M and N, K not a multiple of the 64-wide K step, and strided / misaligned y."""
+    _lib.tuning_set("gemm.tile", tile)
+    for M, N, K in [(300, 520, 1040), (17, 37, 16), (513, 777, 3136), (256, 256, 64)]:
+        announce("gemm_tile", tile, M, N, K)
+        x, w, s = _case(M, N, K, tile * 1000 + M + N + K, scales="log_uniform")
+        y = bits(ops.gemm_fp8_w8a16(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
+        assert_parity(y, oracle_bits(x, w, s), f"tile={tile} M={M} N={N} K={K}")
+    # y with an odd row stride and a 2-byte offset: the 8-byte store path must switch off
+    M, N, K = 300, 260, 320
+    x, w, s = _case(M, N, K, 4242 + tile, scales="log_uniform")
+    ybig = torch.full((M, N + 3), 5.0, dtype=torch.bfloat16, device=DEV)
+    yv = ybig[:, 1:1 + N]
+    sd = s_to_dev(s)
+    xd, wd = x_to_dev(x), w_to_dev(w)
+    _lib.check(_lib.lib().nmi_gemm_fp8_w8a16(xd.data_ptr(), K, wd.data_ptr(), K, sd.data_ptr(), yv.data_ptr(),
+                                             ybig.stride(0), M, N, K, None, 0, None), "strided y")
+    torch.cuda.synchronize()
+    assert_parity(bits(ybig[:, 1:1 + N]), oracle_bits(x, w, s), f"tile={tile} strided y")
+    assert torch.all(ybig[:, 0] == 5.0) and torch.all(ybig[:, 1 + N:] == 5.0)
+
+
 def test_gemm_power_of_two_linearity_and_determinism():
     M, N, K = 2048, 3136, 12544
     announce("gemm_linearity", M, N, K)
