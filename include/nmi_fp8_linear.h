@@ -109,7 +109,8 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                                  size_t workspace_bytes, void* stream);
 
 /* Workspace bytes the skinny kernel can use for M rows, total_n output rows (the sum over
- * groups) and K on the current device; 0 when no split is planned. */
+ * groups) and K on the current device; 0 when the selected kernel needs none (the default
+ * 4x4x4 skinny kernel splits K inside the workgroup only). */
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K);
 
 /*
@@ -137,8 +138,9 @@ int nmi_fp8_e4m3_decode(const void* codes, float* out_f32, float* out_scaled, vo
                         float scale, int n, void* stream);
 
 /*
- * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "skinny.ks",
- * "skinny.kg", "skinny.u", "m1.path"); 0 restores the automatic choice.  Process-wide, not thread-safe against concurrent launches; results
+ * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "skinny.path",
+ * "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path"); 0 restores the
+ * automatic choice.  Process-wide, not thread-safe against concurrent launches; results
  * do not depend on them beyond float32 summation order.  No counterpart in the reference
  * (its launch shapes are compile-time constants, ops/gemv.cuh:100-103).
  */

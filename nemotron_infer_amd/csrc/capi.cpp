@@ -124,7 +124,10 @@ int dispatch(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng,
     if (M == 1 && (tuning().m1_path != 2)) {
         e = launch_gemv_m1_grouped(x, K, g, ng, st);
     } else if (M <= 16) {
-        e = launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+        if (tuning().skinny_path == 1 || (M == 1 && tuning().m1_path == 2))
+            e = launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+        else
+            e = launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
     } else {
         for (int i = 0; i < ng && e == hipSuccess; ++i)
             e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, st);
@@ -184,6 +187,9 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
 
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) {
     if (M < 1 || M > 16 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
+    // only the split-K 16x16x32 kernel uses a workspace (selected with "skinny.path" = 1,
+    // or "m1.path" = 2 for M = 1)
+    if (!(tuning().skinny_path == 1 || (M == 1 && tuning().m1_path == 2))) return 0;
     return skinny_workspace_bytes(M, K, total_n, device_info().num_cu);
 }
 
@@ -228,6 +234,10 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "skinny.kg")) t.skinny_kg = value;
     else if (!std::strcmp(knob, "skinny.u")) t.skinny_u = value;
     else if (!std::strcmp(knob, "m1.path")) t.m1_path = value;
+    else if (!std::strcmp(knob, "skinny.path")) t.skinny_path = value;
+    else if (!std::strcmp(knob, "s4.ks")) t.s4_ks = value;
+    else if (!std::strcmp(knob, "s4.t")) t.s4_t = value;
+    else if (!std::strcmp(knob, "s4.u")) t.s4_u = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

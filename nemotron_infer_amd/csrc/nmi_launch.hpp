@@ -33,7 +33,11 @@ struct Tuning {
     int skinny_ks = 0;     // skinny kernel: waves of a workgroup that split K (1, 2, 4)
     int skinny_kg = 0;     // skinny kernel: workgroups that split K (needs a workspace)
     int skinny_u = 0;      // skinny kernel: 16-byte weight loads per lane per batch (8, 16)
-    int m1_path = 0;       // M = 1: 0 automatic, 1 DPP GEMV, 2 MFMA skinny kernel
+    int m1_path = 0;       // M = 1: 0 automatic, 1 GEMV kernel, 2 skinny kernel
+    int skinny_path = 0;   // 2 <= M <= 16: 0 automatic (4x4x4 kernel), 1 split-K 16x16x32 kernel
+    int s4_ks = 0;         // 4x4x4 skinny kernel: waves splitting K (1, 2, 4)
+    int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
+    int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
 };
 Tuning& tuning();
 
@@ -61,6 +65,10 @@ hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* gro
 size_t skinny_workspace_bytes(int M, int K, int64_t total_rows, int num_cu);
 hipError_t launch_skinny_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
                                  int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+// 2 <= M <= 16 on 4x4x4 MFMA with coalesced weight reads (no workspace).
+hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
+                                  int ngroups, hipStream_t stream);
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);

@@ -21,7 +21,7 @@ from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_t
 
 pytestmark = pytest.mark.gpu
 
-KNOBS = ("skinny.ks", "skinny.kg", "skinny.u", "m1.path", "gemv.ks")
+KNOBS = ("skinny.ks", "skinny.kg", "skinny.u", "m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u")
 
 
 @pytest.fixture(autouse=True)
@@ -46,13 +46,16 @@ def _run(x, w, s, use_ws):
 @pytest.mark.parametrize("name", ["kat_gemv_n64_k3136", "tiny_m4_n8_k16", "ragged_m3_n37_k208",
                                   "skinny_m16_n48_k3136", "special_nan_zero"])
 @pytest.mark.parametrize("use_ws", [False, True])
-def test_fixtures_all_m(name, use_ws):
-    """Every fixture, every leading-row count 1..M of it, through the skinny kernel (M = 1 is
-    forced onto it with m1.path = 2)."""
+@pytest.mark.parametrize("path", [0, 1])
+def test_fixtures_all_m(name, use_ws, path):
+    """Every fixture, every leading-row count 1..M of it, through both skinny kernels (the 4x4x4
+    kernel, path 0, and the split-K 16x16x32 kernel, path 1; M = 1 is forced onto the latter
+    with m1.path = 2)."""
     g = load_golden(name)
     x, w, s = g["x_bf16"], g["w_codes"], g["w_scale"]
     ref64 = linear.bf16_rne(g["y_f64"].astype(np.float32))
     _lib.tuning_set("m1.path", 2)
+    _lib.tuning_set("skinny.path", path)
     for M in range(1, x.shape[0] + 1):
         announce("skinny_fixture", name, M, use_ws)
         y = _run(x[:M], w, s, use_ws)
@@ -61,14 +64,17 @@ def test_fixtures_all_m(name, use_ws):
 
 @pytest.mark.parametrize("M", list(range(1, 17)))
 def test_every_m_ragged(M):
-    """Ragged N (not a multiple of 16 or 64) and K (not a multiple of 64), both paths."""
+    """Ragged N (not a multiple of 4, 16 or 64) and K (not a multiple of 64), both kernels and
+    both workspace modes."""
     _lib.tuning_set("m1.path", 2)
     for N, K in [(37, 208), (1000, 3136), (130, 12544 + 16)]:
         x, w, s = _case(M, N, K, 17 * M + N + K)
         ref = oracle_bits(x, w, s)
-        for use_ws in (False, True):
-            announce("skinny_ragged", M, N, K, use_ws)
-            assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} ws={use_ws}")
+        for path in (0, 1):
+            _lib.tuning_set("skinny.path", path)
+            for use_ws in (False, True):
+                announce("skinny_ragged", M, N, K, path, use_ws)
+                assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} path={path} ws={use_ws}")
 
 
 @pytest.mark.parametrize("ksw", [1, 2, 4])
@@ -77,6 +83,7 @@ def test_every_m_ragged(M):
 def test_every_schedule(ksw, u, kg):
     """Each (waves splitting K, loads per batch, workgroups splitting K) instantiation, incl.
     LDS windows (M = 16 stages 64 chunks per window) and K groups with a partial last group."""
+    _lib.tuning_set("skinny.path", 1)
     _lib.tuning_set("skinny.ks", ksw)
     _lib.tuning_set("skinny.u", u)
     _lib.tuning_set("skinny.kg", kg)
@@ -86,18 +93,39 @@ def test_every_schedule(ksw, u, kg):
         assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"ksw={ksw} u={u} kg={kg} M={M}")
 
 
+@pytest.mark.parametrize("ks", [1, 2, 4])
+@pytest.mark.parametrize("t", [1, 2])
+@pytest.mark.parametrize("u", [2, 4, 8])
+def test_s4_every_schedule(ks, t, u):
+    """Each (waves splitting K, row groups per wave, chunks per lane) instantiation of the 4x4x4
+    kernel for M in {2, 5, 8, 16} (1, 2 and 4 groups of activation rows), with several LDS
+    windows (K = 3136 at M = 16: 64-chunk windows) and N not a multiple of the rows per
+    workgroup."""
+    _lib.tuning_set("s4.ks", ks)
+    _lib.tuning_set("s4.t", t)
+    _lib.tuning_set("s4.u", u)
+    for M, N, K in [(2, 300, 3136), (5, 77, 5120), (8, 130, 1040), (16, 264, 3136)]:
+        announce("s4_schedule", ks, t, u, M, N, K)
+        x, w, s = _case(M, N, K, 100 * ks + 10 * t + u + M)
+        assert_parity(_run(x, w, s, False), oracle_bits(x, w, s), f"ks={ks} t={t} u={u} M={M}")
+
+
 @pytest.mark.parametrize("M", [2, 4, 8, 16])
-def test_config2_shapes_with_workspace(M):
-    """Config 2 (M in {2,4,8,16}, the six decode shapes, per-row log-uniform scales)."""
+@pytest.mark.parametrize("path", [0, 1])
+def test_config2_shapes(M, path):
+    """Config 2 (M in {2,4,8,16}, the six decode shapes, per-row log-uniform scales), both
+    kernels (the split-K one with its workspace)."""
+    _lib.tuning_set("skinny.path", path)
     for lin in synth.DECODE_SET:
-        announce("skinny_config2_ws", M, lin.name)
+        announce("skinny_config2", M, path, lin.name)
         x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, act=lin.act)
-        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} {lin.name}")
+        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} path={path} {lin.name}")
 
 
 def test_workspace_rearmed_and_deterministic():
     """After a split-K launch the counters read back zero; repeated calls are bit-identical."""
     M, N, K = 8, 3136, 12544
+    _lib.tuning_set("skinny.path", 1)
     announce("skinny_rearm", M, N, K)
     x, w, s = _case(M, N, K, 4)
     xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
@@ -121,6 +149,7 @@ def test_workspace_rearmed_and_deterministic():
 def test_workspace_shared_between_shapes():
     """One workspace used by calls of different shapes in turn (small N, then large N, then
     small again): a counter slot is never overwritten by another call's partials."""
+    _lib.tuning_set("skinny.path", 1)
     L = _lib.lib()
     cases = [(16, 48, 3136), (2, 5120, 3136), (16, 48, 3136), (4, 1024, 12544), (2, 5120, 3136)]
     nbytes = max(L.nmi_linear_workspace_bytes(M, N, K) for M, N, K in cases)
@@ -139,6 +168,7 @@ def test_workspace_shared_between_shapes():
 def test_workspace_never_returns_stale_partials():
     """The same shape (same workspace slots) with new inputs each call: every result must match
     its own oracle, so no partial written by an earlier call can be read back."""
+    _lib.tuning_set("skinny.path", 1)
     M, N, K = 4, 5120, 3136
     w, s = synth.make_weight(N, K, 5, "cpu", scales="log_uniform")
     wd, sd = w.to(DEV), s.to(DEV)
@@ -163,6 +193,8 @@ def test_grouped_qkv_matches_separate():
             _lib.tuning_set("skinny.kg", 2)
             _lib.tuning_set("skinny.ks", 2)
             _lib.tuning_set("gemv.ks", 2)
+            _lib.tuning_set("s4.t", 1)
+            _lib.tuning_set("s4.ks", 1)
             announce("grouped_qkv", M, path)
             x = synth.make_act(M, 3136, 77, "cpu")
             ws = [synth.make_weight(l.N, l.K, 70 + i, "cpu", scales="log_uniform") for i, l in enumerate(lins)]
