@@ -121,11 +121,16 @@ namespace {
 int dispatch(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng, void* ws,
              size_t ws_bytes, hipStream_t st, const char* fn) {
     hipError_t e = hipSuccess;
-    if (M == 1 && (tuning().m1_path != 2)) {
+    if (M == 1 && tuning().m1_path == 3) {
+        e = launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
+    } else if (M == 1 && (tuning().m1_path != 2)) {
         e = launch_gemv_m1_grouped(x, K, g, ng, st);
     } else if (M <= 16) {
-        if (tuning().skinny_path == 1 || (M == 1 && tuning().m1_path == 2))
+        const int path = tuning().skinny_path;
+        if (path == 1 || (M == 1 && tuning().m1_path == 2))
             e = launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+        else if ((path == 3 && M <= 4) || (path == 0 && M == 2))   // measured: GEMV kernel wins at M = 2
+            e = launch_gemv_grouped(x, ldx, M, K, g, ng, st);
         else
             e = launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
     } else {

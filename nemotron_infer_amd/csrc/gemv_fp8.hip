@@ -37,6 +37,8 @@ constexpr int kXPieces = 2 * kMaxWindowChunks / 256;    // 16-byte x pieces per 
 
 struct GemvArgs {
     const uint16_t* x;
+    int64_t ldx;          // elements between activation rows (MR > 1)
+    int M;                // activation rows (<= MR)
     int K;
     int window;           // chunks per LDS window
     int ngroups;
@@ -58,14 +60,35 @@ __device__ __forceinline__ void dot16(const uint4 w, const uint4 xl, const uint4
     a1 = dot2_bf16(p3.y, xh.w, a1);
 }
 
+// dot16 for MR activation rows: the codes are converted once.
+template <int MR>
+__device__ __forceinline__ void dot16_rows(const uint4 w, const uint4 (&xl)[MR], const uint4 (&xh)[MR],
+                                           float (&a0)[MR], float (&a1)[MR]) {
+    const uint2 p0 = e4m3x4_to_bf16(w.x), p1 = e4m3x4_to_bf16(w.y);
+    const uint2 p2 = e4m3x4_to_bf16(w.z), p3 = e4m3x4_to_bf16(w.w);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        a0[m] = dot2_bf16(p0.x, xl[m].x, a0[m]);
+        a1[m] = dot2_bf16(p0.y, xl[m].y, a1[m]);
+        a0[m] = dot2_bf16(p1.x, xl[m].z, a0[m]);
+        a1[m] = dot2_bf16(p1.y, xl[m].w, a1[m]);
+        a0[m] = dot2_bf16(p2.x, xh[m].x, a0[m]);
+        a1[m] = dot2_bf16(p2.y, xh[m].y, a1[m]);
+        a0[m] = dot2_bf16(p3.x, xh[m].z, a0[m]);
+        a1[m] = dot2_bf16(p3.y, xh[m].w, a1[m]);
+    }
+}
+
 // KS: waves splitting K; T: rows per wave; P: 16-byte chunks per lane per row per batch;
-// XG: x read from global memory instead of LDS.
-template <int KS, int T, int P, bool XG>
+// XG: x read from global memory instead of LDS; MR: activation rows computed together
+// (M <= MR; rows >= M are zero and never stored -- the weight codes are converted once and
+// reused for every activation row).
+template <int KS, int T, int P, bool XG, int MR>
 __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
-    extern __shared__ uint4 xs[];                  // [half][window] (LDS mode)
+    extern __shared__ uint4 xs[];                  // [m][half][window] (LDS mode)
     constexpr int kRowGroups = kWaves / KS;        // waves with distinct rows
     constexpr int kRowsPerWG = kRowGroups * T;
-    __shared__ float partial[KS > 1 ? KS : 1][kRowsPerWG];
+    __shared__ float partial[KS > 1 ? KS : 1][kRowsPerWG][MR];
 
     // Group of this workgroup (uniform scalar scan over <= kMaxGroups entries).
     int gi = 0;
@@ -93,9 +116,11 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
     // Loads are unconditional, from addresses clamped into the valid range, so that no
     // branch separates them (a branch around a load makes the compiler wait for it); the
     // values of clamped slots are never consumed.
-    float a0[T], a1[T];
+    float a0[T][MR], a1[T][MR];
 #pragma unroll
-    for (int t = 0; t < T; ++t) a0[t] = a1[t] = 0.f;
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) a0[t][m] = a1[t][m] = 0.f;
     for (int w0 = 0; w0 < C; w0 += window) {
         const int wc = min(window, C - w0);
         // 1. activations of this window (LDS mode; issued first)
@@ -103,8 +128,10 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
         if constexpr (!XG) {
 #pragma unroll
             for (int p = 0; p < kXPieces; ++p) {
-                const int e = min(tid + 256 * p, 2 * wc - 1);
-                xr[p] = load16(x + (int64_t)(w0 * 16 + e * 8));
+                const int e = min(tid + 256 * p, 2 * wc * args.M - 1);
+                const int mm = MR == 1 ? 0 : e / (2 * wc);
+                const int ee = e - mm * 2 * wc;
+                xr[p] = load16(x + (int64_t)mm * args.ldx + (int64_t)(w0 * 16 + ee * 8));
             }
         }
         // 2. this wave's K slice [cb, ce) of the window
@@ -113,6 +140,7 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
         const int clast = max(ce - 1, cb);
         int c0 = cb + lane;
         uint4 xl[XG ? P : 1], xh[XG ? P : 1];
+        static_assert(!XG || MR == 1, "x from global memory is for one activation row");
         uint4 wv[T][P];
         if constexpr (XG) {
 #pragma unroll
@@ -133,7 +161,11 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
 #pragma unroll
             for (int p = 0; p < kXPieces; ++p) {
                 const int e = tid + 256 * p;
-                if (e < 2 * wc) xs[(e & 1) * window + (e >> 1)] = xr[p];
+                if (e < 2 * wc * args.M) {
+                    const int mm = MR == 1 ? 0 : e / (2 * wc);
+                    const int ee = e - mm * 2 * wc;
+                    xs[(mm * 2 + (ee & 1)) * window + (ee >> 1)] = xr[p];
+                }
             }
             __syncthreads();
         }
@@ -143,16 +175,24 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
             for (int i = 0; i < P; ++i) {
                 const int c = c0 + 64 * i;
                 if (c < ce) {
-                    uint4 lo, hi;
                     if constexpr (XG) {
-                        lo = xl[i];
-                        hi = xh[i];
-                    } else {
-                        lo = xs[c - w0];
-                        hi = xs[window + c - w0];
-                    }
 #pragma unroll
-                    for (int t = 0; t < T; ++t) dot16(wv[t][i], lo, hi, a0[t], a1[t]);
+                        for (int t = 0; t < T; ++t) dot16(wv[t][i], xl[i], xh[i], a0[t][0], a1[t][0]);
+                    } else if constexpr (MR == 1) {
+                        const uint4 lo = xs[c - w0], hi = xs[window + c - w0];
+#pragma unroll
+                        for (int t = 0; t < T; ++t) dot16(wv[t][i], lo, hi, a0[t][0], a1[t][0]);
+                    } else {
+                        uint4 lo[MR], hi[MR];
+#pragma unroll
+                        for (int m = 0; m < MR; ++m) {
+                            const int mm = m < args.M ? m : 0;       // rows >= M: never stored
+                            lo[m] = xs[(2 * mm) * window + c - w0];
+                            hi[m] = xs[(2 * mm + 1) * window + c - w0];
+                        }
+#pragma unroll
+                        for (int t = 0; t < T; ++t) dot16_rows<MR>(wv[t][i], lo, hi, a0[t], a1[t]);
+                    }
                 }
             }
             c0 += 64 * P;
@@ -174,35 +214,45 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
     }
 
     // Wave sums in a fixed order: 16-lane DPP rows, then rows 0 + 1 + 2 + 3.
-    float sums[T];
+    float sums[T][MR];
 #pragma unroll
-    for (int t = 0; t < T; ++t) sums[t] = wave_sum(a0[t] + a1[t]);
-    if constexpr (KS == 1) {
-        if (lane < T) {
-            float v = sums[0];
+    for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int t = 1; t < T; ++t)
-                if (lane == t) v = sums[t];
-            const int row = row_base + lane;
-            if (row < grp.N) grp.y[row] = f32_to_bf16_rne(v * grp.s[row]);
-        }
-    } else {
+        for (int m = 0; m < MR; ++m) sums[t][m] = wave_sum(a0[t][m] + a1[t][m]);
+    if constexpr (KS > 1) {
         if (lane == 0) {
 #pragma unroll
-            for (int t = 0; t < T; ++t) partial[q][g * T + t] = sums[t];
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) partial[q][g * T + t][m] = sums[t][m];
         }
         __syncthreads();
-        if (q == 0 && lane < T) {
-            float v = partial[0][g * T + lane];
+        if (q != 0) return;
 #pragma unroll
-            for (int qq = 1; qq < KS; ++qq) v += partial[qq][g * T + lane];
-            const int row = row_base + lane;
-            if (row < grp.N) grp.y[row] = f32_to_bf16_rne(v * grp.s[row]);
-        }
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                float v = partial[0][g * T + t][m];
+#pragma unroll
+                for (int qq = 1; qq < KS; ++qq) v += partial[qq][g * T + t][m];
+                sums[t][m] = v;
+            }
+    }
+    // Lane t * MR + m stores row row_base + t of activation row m.
+    if (lane < T * MR) {
+        float v = 0.f;
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (lane == t * MR + m) v = sums[t][m];
+        const int t = lane / MR, m = lane % MR;
+        const int row = row_base + t;
+        if (row < grp.N && m < args.M) grp.y[(int64_t)m * grp.ldy + row] = f32_to_bf16_rne(v * grp.s[row]);
     }
 }
 
-template <int KS, int T, int P, bool XG>
+template <int KS, int T, int P, bool XG, int MR>
 hipError_t launch_cfg(GemvArgs& a, hipStream_t stream) {
     constexpr int rows_per_wg = (kWaves / KS) * T;
     int wgs = 0;
@@ -210,14 +260,16 @@ hipError_t launch_cfg(GemvArgs& a, hipStream_t stream) {
         a.g[i].wg_begin = wgs;
         wgs += (a.g[i].N + rows_per_wg - 1) / rows_per_wg;
     }
-    const size_t lds = XG ? 0 : (size_t)a.window * 2 * sizeof(uint4);
-    hipLaunchKernelGGL((gemv_fp8_m1_kernel<KS, T, P, XG>), dim3(wgs), dim3(256), lds, stream, a);
+    const size_t lds = XG ? 0 : (size_t)a.window * 2 * MR * sizeof(uint4);
+    hipLaunchKernelGGL((gemv_fp8_m1_kernel<KS, T, P, XG, MR>), dim3(wgs), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
 template <int KS, int T, int P>
 hipError_t launch_xg(bool xg, GemvArgs& a, hipStream_t stream) {
-    return xg ? launch_cfg<KS, T, P, true>(a, stream) : launch_cfg<KS, T, P, false>(a, stream);
+    if (a.M == 1) return xg ? launch_cfg<KS, T, P, true, 1>(a, stream) : launch_cfg<KS, T, P, false, 1>(a, stream);
+    if (a.M == 2) return launch_cfg<KS, T, P, false, 2>(a, stream);
+    return launch_cfg<KS, T, P, false, 4>(a, stream);
 }
 
 template <int KS, int T>
@@ -240,14 +292,18 @@ hipError_t launch_t(int t, int p, bool xg, GemvArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,
-                                  hipStream_t stream) {
+hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
+                               int ngroups, hipStream_t stream) {
     const DeviceInfo& dev = device_info();
     GemvArgs a{};
     a.x = x;
+    a.ldx = ldx;
+    a.M = M;
     a.K = K;
     const int C = K >> 4;
-    a.window = C < kMaxWindowChunks ? C : kMaxWindowChunks;
+    const int mr = M == 1 ? 1 : (M == 2 ? 2 : 4);
+    const int wmax = kMaxWindowChunks / mr;        // 2 * mr * window pieces <= 8 per thread
+    a.window = C < wmax ? C : wmax;
     a.ngroups = ngroups;
     int64_t rows = 0;
     for (int i = 0; i < ngroups; ++i) {
@@ -269,12 +325,17 @@ hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* gro
         if (wgs >= 3 * (int64_t)dev.num_cu) { t = cand; break; }
     }
     if (tn.gemv_t == 1 || tn.gemv_t == 2 || tn.gemv_t == 4) t = tn.gemv_t;
-    const bool xg = tn.gemv_xg == 1;
+    const bool xg = tn.gemv_xg == 1 && M == 1;
     switch (ks) {
         case 1: return launch_t<1>(t, p, xg, a, stream);
         case 2: return launch_t<2>(t, p, xg, a, stream);
         default: return launch_t<4>(t, p, xg, a, stream);
     }
+}
+
+hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,
+                                  hipStream_t stream) {
+    return launch_gemv_grouped(x, K, 1, K, groups, ngroups, stream);
 }
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,

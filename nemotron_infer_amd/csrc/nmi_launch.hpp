@@ -33,8 +33,9 @@ struct Tuning {
     int skinny_ks = 0;     // skinny kernel: waves of a workgroup that split K (1, 2, 4)
     int skinny_kg = 0;     // skinny kernel: workgroups that split K (needs a workspace)
     int skinny_u = 0;      // skinny kernel: 16-byte weight loads per lane per batch (8, 16)
-    int m1_path = 0;       // M = 1: 0 automatic, 1 GEMV kernel, 2 skinny kernel
-    int skinny_path = 0;   // 2 <= M <= 16: 0 automatic (4x4x4 kernel), 1 split-K 16x16x32 kernel
+    int m1_path = 0;       // M = 1: 0 automatic, 1 GEMV kernel, 2 split-K skinny kernel, 3 4x4x4 kernel
+    int skinny_path = 0;   // 2 <= M <= 16: 0 automatic, 1 split-K 16x16x32 kernel, 2 4x4x4 kernel,
+                           // 3 GEMV kernel (M <= 4)
     int s4_ks = 0;         // 4x4x4 skinny kernel: waves splitting K (1, 2, 4)
     int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
@@ -69,6 +70,10 @@ hipError_t launch_skinny_grouped(const uint16_t* x, int64_t ldx, int M, int K, c
 // 2 <= M <= 16 on 4x4x4 MFMA with coalesced weight reads (no workspace).
 hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
                                   int ngroups, hipStream_t stream);
+
+// The GEMV kernel for 1 <= M <= 4 activation rows (x row stride ldx elements).
+hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
+                               int ngroups, hipStream_t stream);
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);

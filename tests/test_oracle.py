@@ -179,3 +179,27 @@ def test_fixtures_catch_planted_mistakes():
             caught[label] = caught.get(label, False) or not r["ok"]
     missed = [k for k, v in caught.items() if not v]
     assert len(caught) == 7 and not missed, f"planted mistakes not caught: {missed}"
+
+
+# ---------------------------------------------------------------------------- parity gate
+def test_parity_gate_allows_isolated_rounding_flip_and_rejects_systematic_ones():
+    """A one-ulp flip on the element that dominates ||ref|| passes (float32 summation order can
+    put an exact value on either side of a bf16 rounding boundary); truncating instead of
+    rounding to nearest even, or a sub-ulp scale error, flips many elements and fails; a
+    one-element error of three ulp fails."""
+    g = load_golden("skinny_m16_n48_k3136")
+    yf = (linear.bf16_to_f32(g["x_bf16"]).astype(np.float64)
+          @ e4m3.decode_lut().astype(np.float64)[g["w_codes"]].T) * g["w_scale"].astype(np.float64)
+    ref = linear.bf16_rne(yf.astype(np.float32))
+    big = np.unravel_index(np.argmax(np.abs(linear.bf16_to_f32(ref))), ref.shape)
+    flipped = ref.copy()
+    flipped[big] = flipped[big] + 1                       # next bf16 value: one ulp away
+    r = linear.parity(flipped, ref)
+    assert r["ok"] and r["n_flip"] == 1 and r["rel_l2"] == 0.0
+    truncated = (yf.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    assert not linear.parity(truncated, ref)["ok"]       # RNE replaced by truncation
+    scaled = linear.bf16_rne((yf * (1 + 2.0 ** -10)).astype(np.float32))
+    assert not linear.parity(scaled, ref)["ok"]          # sub-ulp systematic scale error
+    wrong = ref.copy()
+    wrong[big] = wrong[big] + 3
+    assert not linear.parity(wrong, ref)["ok"]

@@ -226,3 +226,22 @@ def test_m1_mfma_path_vs_gemv_full_size():
         _lib.tuning_set("m1.path", path)
         y = bits(ops.linear_fp8_w8a16(x_to_dev(x[0]), w_to_dev(w), s_to_dev(s)))
         assert_parity(y, ref, f"m1.path={path}")
+
+
+@pytest.mark.parametrize("ks", [1, 2, 4])
+@pytest.mark.parametrize("t", [1, 2, 4])
+@pytest.mark.parametrize("p", [2, 3, 4])
+def test_gemv_kernel_small_m(ks, t, p):
+    """The GEMV kernel computing 2..4 activation rows at once (skinny.path = 3): every
+    (K-split, rows per wave, chunks per lane) instantiation, M = 3 on the 4-row variant, K past
+    one LDS window (K = 10000 at M = 4 -> 625 chunks > 256), ragged N."""
+    for k, v in (("skinny.path", 3), ("gemv.ks", ks), ("gemv.t", t), ("gemv.p", p)):
+        _lib.tuning_set(k, v)
+    try:
+        for M, N, K in [(2, 300, 3136), (3, 77, 5120), (4, 130, 10000), (4, 1000, 208)]:
+            announce("gemv_small_m", ks, t, p, M, N, K)
+            x, w, s = _case(M, N, K, 1000 * ks + 100 * t + 10 * p + M)
+            assert_parity(_run(x, w, s, False), oracle_bits(x, w, s), f"ks={ks} t={t} p={p} M={M} N={N} K={K}")
+    finally:
+        for k in ("gemv.ks", "gemv.t", "gemv.p"):
+            _lib.tuning_set(k, 0)
