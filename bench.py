@@ -19,7 +19,9 @@ on the replay stream); HBM-bound, peak 8 TB/s.  ``launches`` gives each launch's
 
 Also reported (same line): ``prefill_gemm`` (config 3, M = 2048, TFLOP/s against 2.5 PFLOP/s
 dense bf16 MFMA), ``skinny`` (config 2, M in {2,4,8,16}, same four launches per step),
-``decode_stream`` (config 4, the 42-layer weight stream, 84 launches) and ``cpu_baseline``:
+``decode_stream`` (config 4, the 42-layer weight stream, 84 launches), ``mlp_block`` (the fp8
+MLP block, decode and prefill, fused against the reference's five-launch structure) and
+``cpu_baseline``:
 the torch CPU reference path (fp32 dequant then F.linear, oracle/linear.py) on a bounded
 sample of config 1, on this host's cores.
 """
@@ -329,6 +331,73 @@ def bench_decode_stream(dev, reps=5):
             "tok_per_s_ceiling": round(1e3 / ms, 1)}
 
 
+def bench_mlp_block(dev, reps=5):
+    """The fp8 MLP block (mlp_forward_fp8): RMSNorm -> up -> relu^2 -> down -> residual.
+    Decode (M = 1, weights rotated over copies totalling > 1 GB): the fused block (two
+    launches) against separate launches in the reference's order (rmsnorm, up, relu^2, down,
+    add; relu^2 as two torch bf16 ops, so six launches where the reference has five).  Prefill
+    (M = 2048): three launches."""
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    H, I = synth.HIDDEN, synth.INTER
+    up = synth.make_weight(I, H, 5000, dev)
+    dn = synth.make_weight(H, I, 5001, dev)
+    nw = (1.0 + 0.1 * torch.randn(H, generator=torch.Generator(device=dev).manual_seed(5002), device=dev)).float()
+    blk_bytes = synth.linear_bytes(1, I, H) + synth.linear_bytes(1, H, I) + 4 * H + 2 * H
+    R = max(2, math.ceil(ROTATION_BYTES / (2 * H * I)))
+    copies = [(up[0].clone(), up[1].clone(), dn[0].clone(), dn[1].clone()) for _ in range(R)]
+    x = synth.make_act(1, H, 5003, dev)
+    out = torch.empty_like(x)
+    h = torch.empty_like(x)
+    yu = torch.empty((1, I), dtype=torch.bfloat16, device=dev)
+    act = torch.empty_like(yu)
+    yd = torch.empty_like(x)
+
+    def fused(r):
+        uw, us, dw, ds = copies[r]
+        ops.mlp_forward_fp8(x, nw, uw, us, dw, ds, out=out)
+
+    def unfused(r):
+        uw, us, dw, ds = copies[r]
+        ops.rmsnorm_bf16(x, nw, out=h)
+        ops.linear_fp8_w8a16(h, uw, us, out=yu)
+        torch.relu_(yu)
+        torch.mul(yu, yu, out=act)
+        ops.linear_fp8_w8a16(act, dw, ds, out=yd)
+        torch.add(x, yd, out=out)
+
+    T = Timer()
+    res = {}
+    for name, fn in (("fused_2_launches", fused), ("separate_6_launches", unfused)):
+        for r in range(R):
+            fn(r)
+        torch.cuda.synchronize()
+        g = T.capture(lambda: [fn(r) for r in range(R)])
+        T.time_replays([g])
+        t = T.time_replays([g] * reps) / (reps * R)
+        res[name] = {"us": round(t * 1e3, 2), "GB/s": round(blk_bytes / (t * 1e-3) / 1e9, 1)}
+        del g
+    del copies
+    # prefill chunk
+    M = synth.PREFILL_M
+    xp = synth.make_act(M, H, 5004, dev)
+    op = torch.empty_like(xp)
+    for _ in range(2):
+        ops.mlp_forward_fp8(xp, nw, *up, *dn, out=op)
+    torch.cuda.synchronize()
+    g = T.capture(lambda: [ops.mlp_forward_fp8(xp, nw, *up, *dn, out=op) for _ in range(reps)])
+    T.time_replays([g])
+    t = T.time_replays([g]) / reps
+    fl = synth.linear_flops(M, I, H) + synth.linear_flops(M, H, I)
+    del g
+    return {"workload": "mlp_forward_fp8 block (hidden 3136, inter 12544)",
+            "decode_m1": {"bytes": blk_bytes, "weight_copies_rotated": R, **res},
+            "prefill_m2048": {"us": round(t * 1e3, 1), "TFLOP/s": round(fl / (t * 1e-3) / 1e12, 1),
+                              "launches": 3}}
+
+
 def cpu_baseline(host, seconds):
     """The reference's CPU path (tools/ref_full_model.py:44-49,137, restated in
     oracle/linear.py): fp32 dequant of W, F.linear in fp32, bf16 rounding -- on config 1's
@@ -404,6 +473,9 @@ def main():
         log("decode stream (config 4) ...")
         extras["decode_stream"] = bench_decode_stream(dev)
         log(f"stream: {extras['decode_stream']['GB/s']} GB/s")
+        log("mlp block ...")
+        extras["mlp_block"] = bench_mlp_block(dev)
+        log(f"mlp block: {extras['mlp_block']['decode_m1']}")
     torch.cuda.empty_cache()
     log("cpu baseline ...")
     cpu = cpu_baseline(host, args.cpu_seconds)

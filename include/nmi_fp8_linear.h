@@ -8,8 +8,9 @@
  *
  * with float32 accumulation and a single bf16 rounding.  All pointers are device pointers
  * (hipMalloc / torch CUDA tensors) unless stated otherwise.  `stream` is a hipStream_t passed
- * as void* (NULL = the null stream).  No entry point allocates device memory, synchronizes
- * the device, or retains pointers after it returns; launches are asynchronous on `stream`.
+ * as void* (NULL = the null stream).  No entry point allocates device memory (except nmi_alloc,
+ * and nmi_mlp_forward_fp8 called without a workspace), synchronizes the device (except
+ * nmi_sync), or retains pointers after it returns; launches are asynchronous on `stream`.
  *
  * Return value: NMI_OK (0) on success; a negative NMI_ERR_* for argument errors detected on
  * the host before anything is launched; a positive hipError_t value when a HIP call fails.
@@ -137,6 +138,43 @@ int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int6
  */
 int nmi_fp8_e4m3_decode(const void* codes, float* out_f32, float* out_scaled, void* out_bf16,
                         float scale, int n, void* stream);
+
+/*
+ * RMSNorm of M rows of bf16 activations; replaces rmsnorm_bf16(in0, out0, weight, rows, cols,
+ * eps, stream) (nemotron_infer/csrc/include/ops/reduce.cuh:229-244) and the binding's
+ * rmsnorm(in, out, w, M) (csrc/include/binding.cu:71-73: cols = HIDDEN, eps = 1e-5):
+ *     y[m,k] = bf16_rne(x[m,k] * (r_m * w[k])),   r_m = 1 / sqrt(sum_k x[m,k]^2 / K + eps)
+ * with a float32 sum of squares in a fixed order (the reference reduces in its own order and
+ * uses rsqrtf; results agree up to rare last-bit differences).  x, y: [M, K] contiguous bf16;
+ * w: [K] float32.  Requires M >= 1, K >= 8, K % 8 == 0, x, y and w 16-byte aligned.
+ */
+int nmi_rmsnorm_bf16(const void* x_bf16, const float* w, void* y_bf16, int M, int K, float eps, void* stream);
+
+/*
+ * The fp8 MLP block; replaces mlp_block_forward_fp8<HIDDEN, INTER>(input, w, out, M, stream)
+ * (nemotron_infer/csrc/include/model/mlp_block.cuh:121-176) and the binding's
+ * mlp_forward_fp8(input, block_norm_w, up_w, up_s, down_w, down_s, out, M)
+ * (csrc/include/binding.cu:201-208: hidden = 3136, inter = 12544, eps = 1e-5):
+ *     h   = rmsnorm(input)                                      [M, hidden]  bf16
+ *     act = bf16_rne(relu(bf16_rne((h . W_up^T) * up_s))^2)      [M, inter]   bf16
+ *     out = bf16_rne(input + bf16_rne((act . W_down^T) * down_s)) [M, hidden]  bf16
+ * input, out: [M, hidden] contiguous bf16 (out may be input); norm_w [hidden] float32;
+ * up_w [inter, hidden] e4m3 and up_s [inter]; down_w [hidden, inter] e4m3 and down_s [hidden].
+ * The projections are W8A16 for every M: the reference quantizes prefill activations to e4m3
+ * (mlp_block.cuh:151-171), this library keeps them bf16.  M <= 2 takes two launches (the
+ * RMSNorm applied while the up projection stages its activations, relu^2 and the residual add
+ * in the projections' stores), larger M three (a separate RMSNorm).
+ * workspace: nmi_mlp_workspace_bytes(M, hidden, inter) bytes, 16-byte aligned, no
+ * initialisation needed; calls that may overlap in time need distinct workspaces.  NULL
+ * takes it from the bump allocator (nmi_alloc, so a slab may be hipMalloc'd), valid until
+ * nmi_alloc_rewind(), as the reference's blocks do (binding.cu:7-9).
+ * Requires M >= 1, hidden and inter positive multiples of 16, input, norm_w and both weights
+ * 16-byte aligned, scales 4-byte aligned, out 2-byte aligned.
+ */
+size_t nmi_mlp_workspace_bytes(int M, int hidden, int inter);
+int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void* up_w_e4m3, const float* up_scale,
+                        const void* down_w_e4m3, const float* down_scale, void* out_bf16, int M, int hidden,
+                        int inter, float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "skinny.path",

@@ -30,6 +30,9 @@ SIGNATURES = {
     "nmi_linear_workspace_bytes": ([_i, _i64, _i], _sz),
     "nmi_gemm_fp8_w8a16": ([_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _vp, _sz, _vp], _i),
     "nmi_fp8_e4m3_decode": ([_vp, _vp, _vp, _vp, _f, _i, _vp], _i),
+    "nmi_rmsnorm_bf16": ([_vp, _vp, _vp, _i, _i, _f, _vp], _i),
+    "nmi_mlp_workspace_bytes": ([_i, _i, _i], _sz),
+    "nmi_mlp_forward_fp8": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp], _i),
     "nmi_tuning_set": ([ctypes.c_char_p, _i], _i),
     "nmi_alloc": ([_sz, ctypes.POINTER(_vp)], _i),
     "nmi_alloc_rewind": ([], _i),

@@ -7,10 +7,10 @@
 // the reference.  The module is C++ over the C ABI of libnmi.so (include/nmi_fp8_linear.h);
 // it never includes HIP headers.
 //
-// Built here: the fp8 linear hot path (linear_fp8, gemv_fp8) and the allocator/sync
-// entries.  Reference entries outside that path exist with the reference's arity and raise
-// NotImplementedError naming what is missing, so a caller fails loudly instead of computing
-// something else.
+// Built here: the fp8 linear hot path (linear_fp8, gemv_fp8), the fp8 MLP block
+// (mlp_forward_fp8), rmsnorm, and the allocator/sync entries.  Reference entries outside that
+// path exist with the reference's arity and raise NotImplementedError naming what is missing,
+// so a caller fails loudly instead of computing something else.
 #include <pybind11/pybind11.h>
 
 #include <cstdint>
@@ -27,6 +27,7 @@ constexpr int H = 96, P = 80, N = 128, G = 8, CONV_K = 4;
 constexpr int H_Q = 40, H_KV = 8, HEAD = 128;
 constexpr int INTER = 12544;
 constexpr int VOCAB = 131072;
+constexpr float EPS = 1e-5f;
 }  // namespace cfg
 
 namespace {
@@ -42,7 +43,7 @@ const float* cf(uintptr_t p) { return reinterpret_cast<const float*>(p); }
 [[noreturn]] void not_built(const char* name) {
     std::string msg = std::string(name) +
                       " is not part of this build: nemotron_infer_amd implements the fp8 W8A16 linear hot "
-                      "path (linear_fp8, gemv_fp8) only";
+                      "path (linear_fp8, gemv_fp8), mlp_forward_fp8 and rmsnorm only";
     PyErr_SetString(PyExc_NotImplementedError, msg.c_str());
     throw py::error_already_set();
 }
@@ -91,9 +92,28 @@ PYBIND11_MODULE(binding, m) {
         },
         py::arg("x"), py::arg("W"), py::arg("w_scale"), py::arg("y"), py::arg("N"), py::arg("K"));
 
+    // binding.cu:71-73 rmsnorm(in, out, w, M): [M, HIDDEN] bf16, eps 1e-5
+    m.def(
+        "rmsnorm",
+        [](uintptr_t in, uintptr_t out, uintptr_t w, int M) {
+            check(nmi_rmsnorm_bf16(cp(in), cf(w), mp(out), M, cfg::HIDDEN, cfg::EPS, nullptr), "rmsnorm");
+        },
+        py::arg("input"), py::arg("out"), py::arg("w"), py::arg("M"));
+    // binding.cu:201-208 mlp_forward_fp8(input, block_norm_w, up_w, up_s, down_w, down_s, out, M):
+    // transient buffers from the bump allocator, valid until reset_allocator(), as in the reference.
+    m.def(
+        "mlp_forward_fp8",
+        [](uintptr_t input, uintptr_t norm_w, uintptr_t up_w, uintptr_t up_s, uintptr_t down_w, uintptr_t down_s,
+           uintptr_t out, int M) {
+            check(nmi_mlp_forward_fp8(cp(input), cf(norm_w), cp(up_w), cf(up_s), cp(down_w), cf(down_s), mp(out), M,
+                                      cfg::HIDDEN, cfg::INTER, cfg::EPS, nullptr, 0, nullptr),
+                  "mlp_forward_fp8");
+        },
+        py::arg("input"), py::arg("block_norm_w"), py::arg("up_w"), py::arg("up_s"), py::arg("down_w"),
+        py::arg("down_s"), py::arg("out"), py::arg("M"));
+
     // Reference entries outside the fp8 linear path (binding.cu:231-245), reference arity.
     m.def("embedding", [](uintptr_t, uintptr_t, uintptr_t, int) { not_built("embedding"); });
-    m.def("rmsnorm", [](uintptr_t, uintptr_t, uintptr_t, int) { not_built("rmsnorm"); });
     m.def("lm_head", [](uintptr_t, uintptr_t, uintptr_t, int) { not_built("lm_head"); });
     m.def("mamba_forward", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
                               uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int, int, uintptr_t,
@@ -122,6 +142,4 @@ PYBIND11_MODULE(binding, m) {
     m.def("attn_decode_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
                                 uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int, int,
                                 uintptr_t) { not_built("attn_decode_fp8"); });
-    m.def("mlp_forward_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
-                                uintptr_t, int) { not_built("mlp_forward_fp8"); });
 }

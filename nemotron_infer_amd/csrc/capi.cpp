@@ -95,7 +95,59 @@ Tuning& tuning() {
 
 }  // namespace nmi
 
+namespace nmi {
+
+// M == 1 -> GEMV kernel, M == 2 -> GEMV kernel (measured faster than the MFMA kernels there),
+// M <= 16 -> 4x4x4 MFMA skinny kernel, M > 16 -> MFMA GEMM.
+Path choose_path(int M) {
+    const Tuning& t = tuning();
+    if (M == 1) {
+        if (t.m1_path == 3) return Path::Skinny4;
+        if (t.m1_path == 2) return Path::Skinny;
+        return Path::Gemv;
+    }
+    if (M <= 16) {
+        if (t.skinny_path == 1) return Path::Skinny;
+        if ((t.skinny_path == 3 && M <= 4) || (t.skinny_path == 0 && M == 2)) return Path::Gemv;
+        return Path::Skinny4;
+    }
+    return Path::Gemm;
+}
+
+hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng, void* ws,
+                           size_t ws_bytes, hipStream_t st, const Norm& norm) {
+    const Path path = choose_path(M);
+    if (norm.w && path != Path::Gemv) return hipErrorInvalidValue;
+    switch (path) {
+        case Path::Gemv: return launch_gemv_grouped(x, ldx, M, K, g, ng, st, norm);
+        case Path::Skinny: return launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+        case Path::Skinny4: return launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
+        case Path::Gemm: break;
+    }
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < ng && e == hipSuccess; ++i)
+        e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, st, g[i].epi);
+    return e;
+}
+
+}  // namespace nmi
+
 using namespace nmi;
+
+namespace {
+
+int dispatch(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng, void* ws,
+             size_t ws_bytes, hipStream_t st, const char* fn) {
+    return hip_status(dispatch_linear(x, ldx, M, K, g, ng, ws, ws_bytes, st), fn);
+}
+
+int64_t total_rows(const nmi_linear_group* groups, int ngroups) {
+    int64_t r = 0;
+    for (int i = 0; i < ngroups; ++i) r += groups[i].N;
+    return r;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -114,39 +166,6 @@ int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, v
                       "nmi_gemv_fp8 launch");
 }
 
-namespace {
-
-// M-dispatch of one or more matrices sharing x: M == 1 -> GEMV, M <= 16 -> skinny MFMA
-// kernel, M > 16 -> MFMA GEMM (one launch per matrix).
-int dispatch(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng, void* ws,
-             size_t ws_bytes, hipStream_t st, const char* fn) {
-    hipError_t e = hipSuccess;
-    if (M == 1 && tuning().m1_path == 3) {
-        e = launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
-    } else if (M == 1 && (tuning().m1_path != 2)) {
-        e = launch_gemv_m1_grouped(x, K, g, ng, st);
-    } else if (M <= 16) {
-        const int path = tuning().skinny_path;
-        if (path == 1 || (M == 1 && tuning().m1_path == 2))
-            e = launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
-        else if ((path == 3 && M <= 4) || (path == 0 && M == 2))   // measured: GEMV kernel wins at M = 2
-            e = launch_gemv_grouped(x, ldx, M, K, g, ng, st);
-        else
-            e = launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
-    } else {
-        for (int i = 0; i < ng && e == hipSuccess; ++i)
-            e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, st);
-    }
-    return hip_status(e, fn);
-}
-
-int64_t total_rows(const nmi_linear_group* groups, int ngroups) {
-    int64_t r = 0;
-    for (int i = 0; i < ngroups; ++i) r += groups[i].N;
-    return r;
-}
-
-}  // namespace
 
 int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
                          const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,

@@ -28,7 +28,7 @@ constexpr int kBK = 64;
 template <int BM, int BN>
 __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ W, int64_t ldw,
-    const float* __restrict__ s, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
+    const float* __restrict__ s, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, const Epi epi) {
     constexpr int WM = BM / 2, WN = BN / 2;      // wave tile
     constexpr int TM = WM / 16, TN = WN / 16;    // MFMA tiles per wave
     constexpr int A_PER = BM * (kBK / 8) / 256;  // 16-byte bf16 chunks per thread
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int m = m0 + wm * WM + i * 16 + (lane >> 4) * 4 + t;
-                if (m < M) y[(int64_t)m * ldy + n] = f32_to_bf16_rne(acc[i][jn][t] * sc);
+                if (m < M) y[(int64_t)m * ldy + n] = epilogue(acc[i][jn][t], sc, epi.kind, epi.res, (int64_t)m * epi.ldres + n);
             }
         }
     }
@@ -159,6 +159,7 @@ struct GemmArgs {
     int M, N, K;
     int tiles_m, tiles_n, per_xcd;
     int vec_store;          // y 8-byte aligned and ldy % 4 == 0
+    Epi epi;
 };
 
 template <int BM, int BN>
@@ -278,10 +279,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
             const int m = m0 + wm * WTM + j * 16 + (lane & 15);
             if (m >= M) continue;
             uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
-            const uint16_t b0 = f32_to_bf16_rne(acc[i][j][0] * sc[0]);
-            const uint16_t b1 = f32_to_bf16_rne(acc[i][j][1] * sc[1]);
-            const uint16_t b2 = f32_to_bf16_rne(acc[i][j][2] * sc[2]);
-            const uint16_t b3 = f32_to_bf16_rne(acc[i][j][3] * sc[3]);
+            const int64_t ro = (int64_t)m * a.epi.ldres + n;
+            const int64_t rl = ro + (N - 1 - n);    // last in-bounds residual of this row
+            const uint16_t b0 = epilogue(acc[i][j][0], sc[0], a.epi.kind, a.epi.res, min(ro, rl));
+            const uint16_t b1 = epilogue(acc[i][j][1], sc[1], a.epi.kind, a.epi.res, min(ro + 1, rl));
+            const uint16_t b2 = epilogue(acc[i][j][2], sc[2], a.epi.kind, a.epi.res, min(ro + 2, rl));
+            const uint16_t b3 = epilogue(acc[i][j][3], sc[3], a.epi.kind, a.epi.res, min(ro + 3, rl));
             if (full) {
                 *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
                                                       (uint32_t)b2 | ((uint32_t)b3 << 16)};
@@ -455,10 +458,12 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
                 const int m = m0 + wm * WTM + j * 32 + (lane & 31);
                 if (m >= M) continue;
                 uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
-                const uint16_t b0 = f32_to_bf16_rne(acc[i][j][4 * gq + 0] * sc[0]);
-                const uint16_t b1 = f32_to_bf16_rne(acc[i][j][4 * gq + 1] * sc[1]);
-                const uint16_t b2 = f32_to_bf16_rne(acc[i][j][4 * gq + 2] * sc[2]);
-                const uint16_t b3 = f32_to_bf16_rne(acc[i][j][4 * gq + 3] * sc[3]);
+                const int64_t ro = (int64_t)m * a.epi.ldres + n;
+                const int64_t rl = ro + (N - 1 - n);    // last in-bounds residual of this row
+                const uint16_t b0 = epilogue(acc[i][j][4 * gq + 0], sc[0], a.epi.kind, a.epi.res, min(ro, rl));
+                const uint16_t b1 = epilogue(acc[i][j][4 * gq + 1], sc[1], a.epi.kind, a.epi.res, min(ro + 1, rl));
+                const uint16_t b2 = epilogue(acc[i][j][4 * gq + 2], sc[2], a.epi.kind, a.epi.res, min(ro + 2, rl));
+                const uint16_t b3 = epilogue(acc[i][j][4 * gq + 3], sc[3], a.epi.kind, a.epi.res, min(ro + 3, rl));
                 if (full) {
                     *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
                                                           (uint32_t)b2 | ((uint32_t)b3 << 16)};
@@ -475,13 +480,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
 
 template <int BM, int BN, bool M32, int NW = 4, bool B64 = false>
 hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s,
-                      uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+                      uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi) {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * kBK * sizeof(uint16_t);
     constexpr auto kernel = M32 ? &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64> : &gemm_fp8_w8a16_big_kernel<BM, BN>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0};
+    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0, epi};
     a.tiles_m = (M + BM - 1) / BM;
     a.tiles_n = (N + BN - 1) / BN;
     const int T = a.tiles_m * a.tiles_n;
@@ -495,7 +500,7 @@ hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
 
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
-                       hipStream_t stream) {
+                       hipStream_t stream, const Epi& epi) {
     int tile = tuning().gemm_tile;
     if (tile < 1 || tile > 13) {
         // Measured on MI355X (config 3): 256 x 256 tiles on 8 waves (32 x 32 MFMA) where there
@@ -507,23 +512,23 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
         else tile = (big * 2 >= 3 * (int64_t)dev.num_cu) ? 8 : 9;
     }
     switch (tile) {
-        case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 3: return launch_big<256, 128, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 4: return launch_big<128, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 5: return launch_big<256, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 6: return launch_big<256, 128, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 7: return launch_big<128, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 8: return launch_big<256, 256, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 9: return launch_big<256, 128, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 10: return launch_big<256, 256, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 11: return launch_big<256, 256, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 12: return launch_big<256, 128, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
-        case 13: return launch_big<256, 128, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream);
+        case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 3: return launch_big<256, 128, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 4: return launch_big<128, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 5: return launch_big<256, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 6: return launch_big<256, 128, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 7: return launch_big<128, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 8: return launch_big<256, 256, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 9: return launch_big<256, 128, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 10: return launch_big<256, 256, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 11: return launch_big<256, 256, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 12: return launch_big<256, 128, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 13: return launch_big<256, 128, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
         default: {
             constexpr int BM = 128, BN = 128;
             const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
             hipLaunchKernelGGL((gemm_fp8_w8a16_kernel<BM, BN>), grid, dim3(256), 0, stream,
-                               x, ldx, W, ldw, s, y, ldy, M, N, K);
+                               x, ldx, W, ldw, s, y, ldy, M, N, K, epi);
             return hipGetLastError();
         }
     }

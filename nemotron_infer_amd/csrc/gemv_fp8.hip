@@ -24,6 +24,10 @@
 //   a fixed order through LDS, the per-row scale and a single bf16 RNE rounding.
 // * One launch may cover several matrices that share x and K (a group table in the kernel
 //   arguments): q/k/v of an attention block, or the row slices of a Mamba in_proj.
+// * Fused block ops: the RMSNorm that precedes every block's first linear can be applied while
+//   x is staged (NORM: each workgroup reduces the row's sum of squares in the same fixed order
+//   as the standalone kernel in rmsnorm.hip, so both give identical bf16 activations), and the
+//   store can apply relu^2 or a residual add (epilogue() in nmi_device.hpp).
 #include "nmi_device.hpp"
 #include "nmi_launch.hpp"
 
@@ -33,7 +37,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kMaxWindowChunks = 1024;                  // bf16 x window: 1024 chunks * 32 B = 32 KiB
-constexpr int kXPieces = 2 * kMaxWindowChunks / 256;    // 16-byte x pieces per thread per window
+constexpr int kMaxXPieces = 2 * kMaxWindowChunks / 256; // 16-byte x pieces per thread per window
 
 struct GemvArgs {
     const uint16_t* x;
@@ -42,6 +46,8 @@ struct GemvArgs {
     int K;
     int window;           // chunks per LDS window
     int ngroups;
+    const float* norm_w;  // NORM: RMSNorm weight [K]
+    float eps;            // NORM: RMSNorm epsilon
     GemvGroup g[kMaxGroups];
 };
 
@@ -82,13 +88,19 @@ __device__ __forceinline__ void dot16_rows(const uint4 w, const uint4 (&xl)[MR],
 // KS: waves splitting K; T: rows per wave; P: 16-byte chunks per lane per row per batch;
 // XG: x read from global memory instead of LDS; MR: activation rows computed together
 // (M <= MR; rows >= M are zero and never stored -- the weight codes are converted once and
-// reused for every activation row).
-template <int KS, int T, int P, bool XG, int MR>
+// reused for every activation row); XP: 16-byte x pieces per thread per window (LDS mode;
+// 256 * XP >= 2 * window * MR); NORM: x is RMSNorm-ed while staged (one window covers K; the
+// pieces are then [MR][XP / MR], piece (m, p) being the 8 activations at 8 * (tid + 256 p) of
+// row m).
+template <int KS, int T, int P, bool XG, int MR, int XP, bool NORM>
 __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
+    static_assert(!NORM || (!XG && XP % MR == 0), "NORM stages x in LDS, XP / MR pieces per row");
     extern __shared__ uint4 xs[];                  // [m][half][window] (LDS mode)
     constexpr int kRowGroups = kWaves / KS;        // waves with distinct rows
     constexpr int kRowsPerWG = kRowGroups * T;
+    constexpr int XPR = XP / MR;                   // NORM: pieces per thread per activation row
     __shared__ float partial[KS > 1 ? KS : 1][kRowsPerWG][MR];
+    __shared__ float red[NORM ? kWaves : 1][MR];
 
     // Group of this workgroup (uniform scalar scan over <= kMaxGroups entries).
     int gi = 0;
@@ -123,11 +135,27 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
         for (int m = 0; m < MR; ++m) a0[t][m] = a1[t][m] = 0.f;
     for (int w0 = 0; w0 < C; w0 += window) {
         const int wc = min(window, C - w0);
-        // 1. activations of this window (LDS mode; issued first)
-        uint4 xr[XG ? 1 : kXPieces];
-        if constexpr (!XG) {
+        // 1. activations of this window (LDS mode; issued first), and the RMSNorm weights
+        uint4 xr[XG ? 1 : XP];
+        [[maybe_unused]] float4 gr[NORM ? 2 * XPR : 1];
+        if constexpr (NORM) {
 #pragma unroll
-            for (int p = 0; p < kXPieces; ++p) {
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int p = 0; p < XPR; ++p) {
+                    const int ee = min(tid + 256 * p, 2 * wc - 1);
+                    const int mm = m < args.M ? m : 0;      // rows >= M: never stored
+                    xr[m * XPR + p] = load16(x + (int64_t)mm * args.ldx + (int64_t)ee * 8);
+                }
+#pragma unroll
+            for (int p = 0; p < XPR; ++p) {
+                const int ee = min(tid + 256 * p, 2 * wc - 1);
+                gr[2 * p] = *reinterpret_cast<const float4*>(args.norm_w + ee * 8);
+                gr[2 * p + 1] = *reinterpret_cast<const float4*>(args.norm_w + ee * 8 + 4);
+            }
+        } else if constexpr (!XG) {
+#pragma unroll
+            for (int p = 0; p < XP; ++p) {
                 const int e = min(tid + 256 * p, 2 * wc * args.M - 1);
                 const int mm = MR == 1 ? 0 : e / (2 * wc);
                 const int ee = e - mm * 2 * wc;
@@ -156,10 +184,39 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
             for (int i = 0; i < P; ++i)
                 wv[t][i] = load_stream16(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
         // 3. stage x (LDS mode) once the previous window has been consumed
-        if constexpr (!XG) {
+        if constexpr (NORM) {
+            // Sum of squares of each activation row: per thread over its pieces in order, then
+            // the wave sum, then the four waves (0 + 1) + (2 + 3).
+            float ss[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                ss[m] = 0.f;
+#pragma unroll
+                for (int p = 0; p < XPR; ++p)
+                    if (tid + 256 * p < 2 * wc) ss[m] = sumsq8(xr[m * XPR + p], ss[m]);
+                ss[m] = wave_sum(ss[m]);
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int m = 0; m < MR; ++m) red[wave][m] = ss[m];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const float r = rms_factor((red[0][m] + red[1][m]) + (red[2][m] + red[3][m]), args.K, args.eps);
+#pragma unroll
+                for (int p = 0; p < XPR; ++p) {
+                    const int ee = tid + 256 * p;
+                    if (ee < 2 * wc && m < args.M)
+                        xs[(m * 2 + (ee & 1)) * window + (ee >> 1)] =
+                            rms_scale8(xr[m * XPR + p], gr[2 * p], gr[2 * p + 1], r);
+                }
+            }
+            __syncthreads();
+        } else if constexpr (!XG) {
             if (w0 != 0) __syncthreads();
 #pragma unroll
-            for (int p = 0; p < kXPieces; ++p) {
+            for (int p = 0; p < XP; ++p) {
                 const int e = tid + 256 * p;
                 if (e < 2 * wc * args.M) {
                     const int mm = MR == 1 ? 0 : e / (2 * wc);
@@ -248,11 +305,13 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
                 if (lane == t * MR + m) v = sums[t][m];
         const int t = lane / MR, m = lane % MR;
         const int row = row_base + t;
-        if (row < grp.N && m < args.M) grp.y[(int64_t)m * grp.ldy + row] = f32_to_bf16_rne(v * grp.s[row]);
+        if (row < grp.N && m < args.M)
+            grp.y[(int64_t)m * grp.ldy + row] =
+                epilogue(v, grp.s[row], grp.epi.kind, grp.epi.res, (int64_t)m * grp.epi.ldres + row);
     }
 }
 
-template <int KS, int T, int P, bool XG, int MR>
+template <int KS, int T, int P, bool XG, int MR, int XP, bool NORM>
 hipError_t launch_cfg(GemvArgs& a, hipStream_t stream) {
     constexpr int rows_per_wg = (kWaves / KS) * T;
     int wgs = 0;
@@ -261,50 +320,91 @@ hipError_t launch_cfg(GemvArgs& a, hipStream_t stream) {
         wgs += (a.g[i].N + rows_per_wg - 1) / rows_per_wg;
     }
     const size_t lds = XG ? 0 : (size_t)a.window * 2 * MR * sizeof(uint4);
-    hipLaunchKernelGGL((gemv_fp8_m1_kernel<KS, T, P, XG, MR>), dim3(wgs), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL((gemv_fp8_m1_kernel<KS, T, P, XG, MR, XP, NORM>), dim3(wgs), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
+// x staging mode: from global memory (M = 1), LDS with XP pieces per thread, or LDS with the
+// RMSNorm applied (M <= 2).
+struct Mode {
+    bool xg;
+    bool norm;
+    int mr;
+    int xp;
+};
+
 template <int KS, int T, int P>
-hipError_t launch_xg(bool xg, GemvArgs& a, hipStream_t stream) {
-    if (a.M == 1) return xg ? launch_cfg<KS, T, P, true, 1>(a, stream) : launch_cfg<KS, T, P, false, 1>(a, stream);
-    if (a.M == 2) return launch_cfg<KS, T, P, false, 2>(a, stream);
-    return launch_cfg<KS, T, P, false, 4>(a, stream);
+hipError_t launch_mode(const Mode& md, GemvArgs& a, hipStream_t stream) {
+    if (md.xg) return launch_cfg<KS, T, P, true, 1, 1, false>(a, stream);
+    if (md.norm) {
+        if (md.mr == 1) {
+            switch (md.xp) {
+                case 2: return launch_cfg<KS, T, P, false, 1, 2, true>(a, stream);
+                case 4: return launch_cfg<KS, T, P, false, 1, 4, true>(a, stream);
+                default: return launch_cfg<KS, T, P, false, 1, 8, true>(a, stream);
+            }
+        }
+        return md.xp <= 4 ? launch_cfg<KS, T, P, false, 2, 4, true>(a, stream)
+                          : launch_cfg<KS, T, P, false, 2, 8, true>(a, stream);
+    }
+    if (md.mr == 1) {
+        switch (md.xp) {
+            case 2: return launch_cfg<KS, T, P, false, 1, 2, false>(a, stream);
+            case 4: return launch_cfg<KS, T, P, false, 1, 4, false>(a, stream);
+            default: return launch_cfg<KS, T, P, false, 1, 8, false>(a, stream);
+        }
+    }
+    if (md.mr == 2) {
+        return md.xp <= 4 ? launch_cfg<KS, T, P, false, 2, 4, false>(a, stream)
+                          : launch_cfg<KS, T, P, false, 2, 8, false>(a, stream);
+    }
+    return launch_cfg<KS, T, P, false, 4, 8, false>(a, stream);
 }
 
 template <int KS, int T>
-hipError_t launch_p(int p, bool xg, GemvArgs& a, hipStream_t stream) {
+hipError_t launch_p(int p, const Mode& md, GemvArgs& a, hipStream_t stream) {
     switch (p) {
-        case 2: return launch_xg<KS, T, 2>(xg, a, stream);
-        case 3: return launch_xg<KS, T, 3>(xg, a, stream);
-        default: return launch_xg<KS, T, 4>(xg, a, stream);
+        case 2: return launch_mode<KS, T, 2>(md, a, stream);
+        case 3: return launch_mode<KS, T, 3>(md, a, stream);
+        default: return launch_mode<KS, T, 4>(md, a, stream);
     }
 }
 
 template <int KS>
-hipError_t launch_t(int t, int p, bool xg, GemvArgs& a, hipStream_t stream) {
+hipError_t launch_t(int t, int p, const Mode& md, GemvArgs& a, hipStream_t stream) {
     switch (t) {
-        case 1: return launch_p<KS, 1>(p, xg, a, stream);
-        case 2: return launch_p<KS, 2>(p, xg, a, stream);
-        default: return launch_p<KS, 4>(p, xg, a, stream);
+        case 1: return launch_p<KS, 1>(p, md, a, stream);
+        case 2: return launch_p<KS, 2>(p, md, a, stream);
+        default: return launch_p<KS, 4>(p, md, a, stream);
     }
 }
 
+int pow2_pieces(int need) { return need <= 2 ? 2 : (need <= 4 ? 4 : 8); }
+
 }  // namespace
 
+bool gemv_norm_supported(int M, int K) {
+    const int C = K >> 4;
+    return (M == 1 || M == 2) && 2 * C <= 256 * (8 / M);
+}
+
 hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
-                               int ngroups, hipStream_t stream) {
+                               int ngroups, hipStream_t stream, const Norm& norm) {
     const DeviceInfo& dev = device_info();
+    if (norm.w && !gemv_norm_supported(M, K)) return hipErrorInvalidValue;
     GemvArgs a{};
     a.x = x;
     a.ldx = ldx;
     a.M = M;
     a.K = K;
+    a.norm_w = norm.w;
+    a.eps = norm.eps;
     const int C = K >> 4;
     const int mr = M == 1 ? 1 : (M == 2 ? 2 : 4);
     const int wmax = kMaxWindowChunks / mr;        // 2 * mr * window pieces <= 8 per thread
     a.window = C < wmax ? C : wmax;
     a.ngroups = ngroups;
+    static_assert(2 * kMaxWindowChunks <= 256 * kMaxXPieces, "window larger than the staging pieces");
     int64_t rows = 0;
     for (int i = 0; i < ngroups; ++i) {
         a.g[i] = groups[i];
@@ -325,17 +425,21 @@ hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, con
         if (wgs >= 3 * (int64_t)dev.num_cu) { t = cand; break; }
     }
     if (tn.gemv_t == 1 || tn.gemv_t == 2 || tn.gemv_t == 4) t = tn.gemv_t;
-    const bool xg = tn.gemv_xg == 1 && M == 1;
+    Mode md{};
+    md.norm = norm.w != nullptr;
+    md.xg = !md.norm && tn.gemv_xg == 1 && M == 1;
+    md.mr = mr;
+    md.xp = md.norm ? mr * pow2_pieces((2 * C + 255) / 256) : pow2_pieces((2 * a.window * mr + 255) / 256);
     switch (ks) {
-        case 1: return launch_t<1>(t, p, xg, a, stream);
-        case 2: return launch_t<2>(t, p, xg, a, stream);
-        default: return launch_t<4>(t, p, xg, a, stream);
+        case 1: return launch_t<1>(t, p, md, a, stream);
+        case 2: return launch_t<2>(t, p, md, a, stream);
+        default: return launch_t<4>(t, p, md, a, stream);
     }
 }
 
 hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,
                                   hipStream_t stream) {
-    return launch_gemv_grouped(x, K, 1, K, groups, ngroups, stream);
+    return launch_gemv_grouped(x, K, 1, K, groups, ngroups, stream, Norm{});
 }
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,

@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "nmi_launch.hpp"
+
 namespace nmi {
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -50,6 +52,58 @@ __device__ __forceinline__ float bf16hi_to_f32(uint32_t d) { return __uint_as_fl
 // f32 -> bf16 bits, round to nearest even (hardware v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Output epilogues fused into the stores of the linear kernels.  The linear's own result is
+// v = bf16_rne(acc * s); kEpiRelu2 stores bf16_rne(max(v, 0)^2) and kEpiResidual stores
+// bf16_rne(res + v).  A bf16 x bf16 product is exact in float32, and a float32 sum of two bf16
+// is either exact or within 2^-24 relative of an operand that is itself the nearest bf16, so
+// both round to the bf16 the reference's bf16 arithmetic gives on the rounded linear output
+// (relu^2 as __hfma2_relu then __hmul2, ops/elementwise.cuh:256-272; residual as __hadd2,
+// :241-244; used at model/mlp_block.cuh:145-147, 163-165 and 173-175).  relu keeps NaN
+// (NaN < 0 is false).  res[off] is read only for kEpiResidual.
+__device__ __forceinline__ uint16_t epilogue(float acc, float s, int epi, const uint16_t* res, int64_t off) {
+    const uint16_t v = f32_to_bf16_rne(acc * s);
+    if (epi == kEpiRelu2) {
+        float f = bf16_to_f32(v);
+        f = f < 0.f ? 0.f : f;
+        return f32_to_bf16_rne(f * f);
+    }
+    if (epi == kEpiResidual) return f32_to_bf16_rne(bf16_to_f32(res[off]) + bf16_to_f32(v));
+    return v;
+}
+
+// RMSNorm pieces: 8 consecutive bf16 activations in 16 bytes.  sumsq8 continues a float32
+// fma chain over the 8 elements in order; rms_scale8 returns bf16_rne(x * (r * g)) for each
+// element (the reference's order of operations, ops/reduce.cuh:190-206).
+__device__ __forceinline__ float sumsq8(const uint4 v, float acc) {
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = bf16lo_to_f32(d[i]), hi = bf16hi_to_f32(d[i]);
+        acc = __builtin_fmaf(lo, lo, acc);
+        acc = __builtin_fmaf(hi, hi, acc);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+}
+
+__device__ __forceinline__ uint4 rms_scale8(const uint4 v, const float4 g0, const float4 g1, float r) {
+    return uint4{pack_bf16(bf16lo_to_f32(v.x) * (r * g0.x), bf16hi_to_f32(v.x) * (r * g0.y)),
+                 pack_bf16(bf16lo_to_f32(v.y) * (r * g0.z), bf16hi_to_f32(v.y) * (r * g0.w)),
+                 pack_bf16(bf16lo_to_f32(v.z) * (r * g1.x), bf16hi_to_f32(v.z) * (r * g1.y)),
+                 pack_bf16(bf16lo_to_f32(v.w) * (r * g1.z), bf16hi_to_f32(v.w) * (r * g1.w))};
+}
+
+// 1 / sqrt(mean + eps) with correctly rounded float32 division and square root (HIP's default
+// for '/' and sqrtf); the reference uses rsqrtf (ops/reduce.cuh:174).
+__device__ __forceinline__ float rms_factor(float sumsq, int K, float eps) {
+    return 1.0f / sqrtf(sumsq / (float)K + eps);
 }
 
 template <int CTRL>

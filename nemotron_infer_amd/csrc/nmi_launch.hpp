@@ -42,6 +42,15 @@ struct Tuning {
 };
 Tuning& tuning();
 
+// Fused output epilogue of a linear (computed by epilogue() in nmi_device.hpp): none, relu^2,
+// or the residual add out = res + y with res [M, N] at row stride ldres elements.
+enum : int { kEpiNone = 0, kEpiRelu2 = 1, kEpiResidual = 2 };
+struct Epi {
+    int kind = 0;
+    const uint16_t* res = nullptr;
+    int64_t ldres = 0;
+};
+
 // One matrix of a grouped launch: W [N, K] (row stride ldw bytes), s [N], y [M, N] (row
 // stride ldy elements).  wg_begin and ws_col are filled in by the launchers.
 constexpr int kMaxGroups = 4;
@@ -54,6 +63,15 @@ struct GemvGroup {
     int N;
     int wg_begin;
     int ws_col;
+    Epi epi;
+};
+
+// RMSNorm of the activations (model/mlp_block.cuh:140, ops/reduce.cuh:135-244):
+// y[m, k] = bf16_rne(x[m, k] * (r_m * w[k])), r_m = 1 / sqrt(sum_k x[m, k]^2 / K + eps), the sum
+// in float32 in a fixed order that the GEMV kernel's fused form repeats exactly.
+struct Norm {
+    const float* w = nullptr;   // [K] float32; nullptr: no normalisation
+    float eps = 0.f;
 };
 
 // M = 1 GEMV over up to kMaxGroups matrices that share x [K] (one launch).
@@ -71,22 +89,35 @@ hipError_t launch_skinny_grouped(const uint16_t* x, int64_t ldx, int M, int K, c
 hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
                                   int ngroups, hipStream_t stream);
 
-// The GEMV kernel for 1 <= M <= 4 activation rows (x row stride ldx elements).
+// The GEMV kernel for 1 <= M <= 4 activation rows (x row stride ldx elements).  With norm.w
+// set (only where gemv_norm_supported(M, K)), x is the raw input and every workgroup applies
+// the RMSNorm while staging it, with results identical to launch_rmsnorm's.
+bool gemv_norm_supported(int M, int K);
 hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
-                               int ngroups, hipStream_t stream);
+                               int ngroups, hipStream_t stream, const Norm& norm = Norm{});
+
+// RMSNorm of M rows of K bf16 activations (K % 8 == 0): y [M, K] (row stride ldy) from x [M, K]
+// (row stride ldx), one 256-thread workgroup per row.
+hipError_t launch_rmsnorm(const uint16_t* x, int64_t ldx, const Norm& norm, uint16_t* y, int64_t ldy,
+                          int M, int K, hipStream_t stream);
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);
 
-hipError_t launch_gemv_skinny(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
-                              const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
-                              hipStream_t stream);
-
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
-                       hipStream_t stream);
+                       hipStream_t stream, const Epi& epi = Epi{});
 
 hipError_t launch_decode(const uint8_t* codes, float* out_f32, float* out_scaled,
                          uint16_t* out_bf16, float scale, int n, hipStream_t stream);
+
+// Kernel chosen for a linear with M activation rows (tuning knobs may override).
+enum class Path { Gemv, Skinny, Skinny4, Gemm };
+Path choose_path(int M);
+
+// One or more linears sharing x [M, K] on the kernel choose_path(M) names (GEMM: one launch per
+// matrix).  norm (GEMV path only, where gemv_norm_supported) applies the RMSNorm to x first.
+hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng, void* ws,
+                           size_t ws_bytes, hipStream_t stream, const Norm& norm = Norm{});
 
 }  // namespace nmi

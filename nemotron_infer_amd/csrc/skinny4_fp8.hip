@@ -216,7 +216,9 @@ __global__ __launch_bounds__(256) void skinny4_fp8_kernel(const Skinny4Args a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int n = row_base + 4 * t + r;
-                    if (n < grp.N) grp.y[(int64_t)m * grp.ldy + n] = f32_to_bf16_rne(acc[t][g][r] * grp.s[n]);
+                    if (n < grp.N)
+                        grp.y[(int64_t)m * grp.ldy + n] = epilogue(acc[t][g][r], grp.s[n], grp.epi.kind, grp.epi.res,
+                                                                   (int64_t)m * grp.epi.ldres + n);
                 }
             }
     }

@@ -205,7 +205,8 @@ __global__ __launch_bounds__(256) void skinny_fp8_kernel(const SkinnyArgs a) {
                     for (int g2 = 0; g2 < a.kgroups; ++g2)
                         tsum += __hip_atomic_load(src + (int64_t)g2 * M * a.ws_ld, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
-                    grp.y[(int64_t)m * grp.ldy + n] = f32_to_bf16_rne(tsum * grp.s[n]);
+                    grp.y[(int64_t)m * grp.ldy + n] =
+                        epilogue(tsum, grp.s[n], grp.epi.kind, grp.epi.res, (int64_t)m * grp.epi.ldres + n);
                 }
             }
         }
@@ -215,7 +216,9 @@ __global__ __launch_bounds__(256) void skinny_fp8_kernel(const SkinnyArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int n = row0 + 4 * a4 + i;
-            if (n < grp.N) grp.y[(int64_t)m * grp.ldy + n] = f32_to_bf16_rne(v[i] * grp.s[n]);
+            if (n < grp.N)
+                grp.y[(int64_t)m * grp.ldy + n] =
+                    epilogue(v[i], grp.s[n], grp.epi.kind, grp.epi.res, (int64_t)m * grp.epi.ldres + n);
         }
     }
 }

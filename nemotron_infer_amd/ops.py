@@ -133,6 +133,55 @@ def gemm_fp8_w8a16(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
     return out
 
 
+def rmsnorm_bf16(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm of bf16 rows (ops/reduce.cuh:229-244): y = bf16(x * (1/sqrt(mean(x^2) + eps) * w))."""
+    x2 = _as_2d(x)
+    if not x2.is_contiguous() or w.dtype != torch.float32 or not w.is_contiguous():
+        raise ValueError("x must be contiguous bf16 and w contiguous float32")
+    M, K = x2.shape
+    if out is None:
+        out = torch.empty_like(x)
+    rc = _lib.lib().nmi_rmsnorm_bf16(x2.data_ptr(), w.data_ptr(), out.data_ptr(), M, K, eps, _stream())
+    _lib.check(rc, "nmi_rmsnorm_bf16")
+    return out
+
+
+_BLOCK_WS: dict[int, torch.Tensor] = {}
+
+
+def mlp_forward_fp8(x: torch.Tensor, norm_w: torch.Tensor, up_w: torch.Tensor, up_s: torch.Tensor,
+                    down_w: torch.Tensor, down_s: torch.Tensor, out: torch.Tensor | None = None,
+                    eps: float = 1e-5, use_workspace: bool = True) -> torch.Tensor:
+    """The fp8 MLP block (model/mlp_block.cuh:121-176): out = x + down(relu(up(rmsnorm(x)))^2).
+    x, out: [M, hidden] bf16; up_w [inter, hidden], down_w [hidden, inter] e4m3 with per-row
+    float32 scales.  The transient buffers come from a per-device tensor kept for the process
+    (or, with use_workspace=False, from the library's bump allocator)."""
+    x2 = _as_2d(x)
+    if not x2.is_contiguous():
+        raise ValueError("x must be contiguous")
+    up_w, down_w = _check_w(up_w), _check_w(down_w)
+    M, hidden = x2.shape
+    inter = up_w.shape[0]
+    if out is None:
+        out = torch.empty_like(x)
+    L = _lib.lib()
+    ws = None
+    if use_workspace:
+        need = L.nmi_mlp_workspace_bytes(M, hidden, inter)
+        idx = x.device.index or 0
+        ws = _BLOCK_WS.get(idx)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=x.device)
+            _BLOCK_WS[idx] = ws
+    rc = L.nmi_mlp_forward_fp8(x2.data_ptr(), norm_w.data_ptr(), up_w.data_ptr(), up_s.data_ptr(),
+                               down_w.data_ptr(), down_s.data_ptr(), out.data_ptr(), M, hidden, inter, eps,
+                               None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+                               _stream())
+    _lib.check(rc, "nmi_mlp_forward_fp8")
+    return out
+
+
 def decode_e4m3(codes: torch.Tensor, scale: float):
     """Device decode of uint8 codes through the kernels' conversion helpers.
     Returns (f32 values, f32 values * scale, bf16 values)."""

@@ -115,7 +115,8 @@ def bf16_ulp(a: np.ndarray) -> np.ndarray:
 
 
 def parity(y_bits: np.ndarray, ref_bits: np.ndarray, ulp_tol: float = 2.0,
-           rel_l2_tol: float = 1e-3, floor_frac: float = 2.0 ** -8, flip_frac: float = 0.01):
+           rel_l2_tol: float = 1e-3, floor_frac: float = 2.0 ** -8, flip_frac: float = 0.01,
+           mag: np.ndarray | None = None):
     """Compare a bf16 result with the bf16-rounded oracle.
 
     * max |y - ref| <= ``ulp_tol`` bf16 ulp taken at ``max(|ref|, floor_frac * rms(ref))``
@@ -130,22 +131,26 @@ def parity(y_bits: np.ndarray, ref_bits: np.ndarray, ulp_tol: float = 2.0,
     * NaN positions must agree exactly.
     Also returned: ``rel_l2_all``, the plain rel_l2 over every element (one flip on an element
     that dominates ||ref|| -- e.g. with per-row scales spread over two decades -- can alone
-    exceed 1e-3)."""
+    exceed 1e-3).
+
+    ``mag`` (optional, float, shape of ``ref``) replaces |ref| as the magnitude at which ulps
+    are taken: for a rounded sum such as a residual add, the larger summand, since a one-ulp
+    difference in a summand is many ulps of a result that cancels towards zero."""
     y = bf16_to_f32(y_bits).astype(np.float64)
     r = bf16_to_f32(ref_bits).astype(np.float64)
     nan_y, nan_r = np.isnan(y), np.isnan(r)
     nan_ok = bool(np.array_equal(nan_y, nan_r))
     fin = ~(nan_y | nan_r)
     y, r = y[fin], r[fin]
+    m = np.abs(r) if mag is None else np.maximum(np.abs(np.asarray(mag, np.float64)[fin]), np.abs(r))
     if r.size == 0:
         return dict(ok=nan_ok, rel_l2=0.0, rel_l2_all=0.0, max_ulp=0.0, nan_ok=nan_ok, n=0,
                     n_diff=0, n_flip=0)
     denom = np.linalg.norm(r)
     d = y - r
     rms = float(np.sqrt(np.mean(r * r)))
-    mag = np.maximum(np.abs(r), floor_frac * rms)
-    ulps = np.abs(d) / bf16_ulp(mag)
-    exact_ulp = np.abs(d) / bf16_ulp(np.abs(r))          # at the reference's own magnitude
+    ulps = np.abs(d) / bf16_ulp(np.maximum(m, floor_frac * rms))
+    exact_ulp = np.abs(d) / bf16_ulp(m)                  # at the reference's own magnitude
     flip = (d != 0) & (exact_ulp <= 1.0)
     big = np.where(flip, 0.0, d)
     rel_all = float(np.linalg.norm(d) / denom) if denom > 0 else float(np.linalg.norm(d))

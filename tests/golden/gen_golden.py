@@ -18,6 +18,14 @@ Inputs follow the reference's known-answer tests where it has them:
 Seeded cases cover what those leave open: ragged N and K/16 odd (``ragged_m3_n37_k208``),
 skinny M with per-row log-uniform scales (``skinny_m16_n48_k3136``), and special values
 (``special_nan_zero``: NaN codes 0x7F/0xFF, -0 codes, subnormal codes, an all-zero x row).
+
+The MLP block fixture ``mlp_block_h64_i256_s8`` follows tools/dump_mlp_block.py:15-53: torch
+seed 2024, HIDDEN 64, INTER 256, S 8, EPS 1e-5, the same draws in the same order, and its fp32
+HF forward as ``expected_f32`` (the expectation of test_mlp_block.cu:155-185, which quantizes
+both weights per row as test_mlp_block.cu:57-70 does and feeds the input as bf16).  It also
+holds ``chain_f64``: the block computed in float64 with a bf16 rounding after every step, as
+the fp8 block's M == 1 path stores its intermediates (mlp_block.cuh:140-148, 173-175), the
+rounding done here on the float64 bit pattern.
 """
 from __future__ import annotations
 
@@ -65,6 +73,18 @@ def fp64_linear(xb: np.ndarray, codes: np.ndarray, s: np.ndarray) -> np.ndarray:
     x = bf16_value(np.atleast_2d(xb)).astype(np.float64)
     w = torch_decode(codes).astype(np.float64)
     return (x @ w.T) * s.astype(np.float64)[None, :]
+
+
+def bf16_from_f64(v: np.ndarray) -> np.ndarray:
+    """float64 -> bf16 bits with one round-to-nearest-even on the float64 bit pattern (keep the
+    top 7 explicit mantissa bits).  Normal bf16 range only (checked)."""
+    v = np.ascontiguousarray(v, np.float64)
+    a = np.abs(v)
+    assert np.all(np.isfinite(v)) and np.all((a == 0) | ((a >= 2.0 ** -126) & (a < 2.0 ** 127)))
+    u = v.view(np.uint64)
+    lsb = (u >> np.uint64(45)) & np.uint64(1)
+    r = ((u + np.uint64((1 << 44) - 1) + lsb) >> np.uint64(45)) << np.uint64(45)
+    return bf16_bits(r.view(np.float64).astype(F32))    # exact: 8 significant bits
 
 
 def save(name: str, **arrays):
@@ -133,6 +153,40 @@ def main():
     xb[1, :] = 0                          # +0 activation row
     written.append(save("special_nan_zero", x_bf16=xb, w_codes=codes, w_scale=s,
                         y_f64=fp64_linear(xb, codes, s)))
+
+    # 7. MLP block (tools/dump_mlp_block.py:15-53)
+    H, I, S, EPS = 64, 256, 8, 1e-5
+    g = torch.Generator().manual_seed(2024)
+    norm_w = torch.randn(H, generator=g, dtype=torch.float32)
+    up_w = torch.randn(I, H, generator=g, dtype=torch.float32) * 0.1
+    down_w = torch.randn(H, I, generator=g, dtype=torch.float32) * 0.1
+    x = torch.randn(1, S, H, generator=g, dtype=torch.float32).reshape(S, H)
+    with torch.no_grad():
+        var = x.pow(2).mean(-1, keepdim=True)
+        hs = (x * torch.rsqrt(var + EPS)) * norm_w
+        up = hs @ up_w.T
+        act = torch.relu(up).pow(2)
+        down = act @ down_w.T
+        expected = x + down
+    up_codes, up_s = perrow_quant(up_w.numpy())
+    down_codes, down_s = perrow_quant(down_w.numpy())
+    xb = bf16_bits(x.numpy())
+    # float64 chain with bf16 rounding after every step
+    xf = bf16_value(xb).astype(np.float64)
+    ss = (xf * xf).sum(axis=1, keepdims=True)
+    r = 1.0 / np.sqrt(ss / H + EPS)
+    hb = bf16_from_f64(xf * r * norm_w.numpy().astype(np.float64)[None, :])
+    upb = bf16_from_f64(fp64_linear(hb, up_codes, up_s))
+    upv = bf16_value(upb).astype(np.float64)
+    actb = bf16_from_f64(np.maximum(upv, 0.0) ** 2)
+    downb = bf16_from_f64(fp64_linear(actb, down_codes, down_s))
+    outb = bf16_from_f64(xf + bf16_value(downb).astype(np.float64))
+    written.append(save("mlp_block_h64_i256_s8", x_f32=x.numpy(), x_bf16=xb, norm_w=norm_w.numpy(),
+                        up_w_f32=up_w.numpy(), down_w_f32=down_w.numpy(), up_codes=up_codes, up_scale=up_s,
+                        down_codes=down_codes, down_scale=down_s, expected_f32=expected.numpy(),
+                        normed_f32=hs.numpy(), up_f32=up.numpy(), act_f32=act.numpy(), down_f32=down.numpy(),
+                        chain_normed=hb, chain_up=upb, chain_act=actb, chain_down=downb, chain_f64=outb,
+                        eps=np.float32(EPS)))
 
     with open(os.path.join(HERE, "SHA256SUMS"), "w") as f:
         for p in sorted(written):

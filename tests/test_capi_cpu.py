@@ -116,6 +116,8 @@ def test_out_of_scope_entries_fail_loudly():
     with pytest.raises(NotImplementedError, match="not part of this build"):
         B.attn_decode_fp8(*([0] * 15))
     with pytest.raises(NotImplementedError):
+        B.mlp_forward(*([0] * 6))
+    with pytest.raises(NotImplementedError):
         B.mamba_forward_fp8(*([0] * 17))
 
 
@@ -124,3 +126,57 @@ def test_binding_reports_validation_errors():
 
     with pytest.raises(RuntimeError, match="K=72 must be a positive multiple of 16"):
         B.linear_fp8(FAKE, 72, FAKE, 80, FAKE, FAKE, 8, 1, 8, 72)
+
+
+def test_rmsnorm_rejects_bad_arguments():
+    L = _lib.lib()
+    assert L.nmi_rmsnorm_bf16(0, FAKE, FAKE, 1, 64, 1e-5, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_rmsnorm_bf16(FAKE, FAKE, FAKE, 0, 64, 1e-5, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_rmsnorm_bf16(FAKE, FAKE, FAKE, 1, 12, 1e-5, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_rmsnorm_bf16(FAKE + 2, FAKE, FAKE, 1, 64, 1e-5, None) == _lib.NMI_ERR_ALIGNMENT
+    assert L.nmi_rmsnorm_bf16(FAKE, FAKE + 4, FAKE, 1, 64, 1e-5, None) == _lib.NMI_ERR_ALIGNMENT
+    assert L.nmi_last_error().decode().startswith("nmi_rmsnorm_bf16")
+
+
+def test_mlp_workspace_bytes():
+    L = _lib.lib()
+    # M <= 2 (GEMV path): only act [M, inter] bf16; otherwise also normed [M, hidden]
+    assert L.nmi_mlp_workspace_bytes(1, 3136, 12544) == 12544 * 2
+    assert L.nmi_mlp_workspace_bytes(2, 3136, 12544) == 2 * 12544 * 2
+    assert L.nmi_mlp_workspace_bytes(3, 3136, 12544) == 3 * 12544 * 2 + ((3 * 3136 * 2 + 255) // 256) * 256
+    assert L.nmi_mlp_workspace_bytes(64, 64, 256) == 64 * 256 * 2 + 64 * 64 * 2
+    assert L.nmi_mlp_workspace_bytes(0, 3136, 12544) == 0
+
+
+@pytest.mark.parametrize("M,hidden,inter,offs,code", [
+    (0, 64, 256, {}, _lib.NMI_ERR_INVALID_ARG),
+    (1, 72, 256, {}, _lib.NMI_ERR_INVALID_ARG),          # hidden % 16
+    (1, 64, 264, {}, _lib.NMI_ERR_INVALID_ARG),          # inter % 16
+    (1, 64, 256, {0: 2}, _lib.NMI_ERR_ALIGNMENT),        # input
+    (1, 64, 256, {1: 4}, _lib.NMI_ERR_ALIGNMENT),        # norm_w
+    (1, 64, 256, {2: 8}, _lib.NMI_ERR_ALIGNMENT),        # up_w
+    (1, 64, 256, {4: 8}, _lib.NMI_ERR_ALIGNMENT),        # down_w
+    (1, 64, 256, {5: 2}, _lib.NMI_ERR_ALIGNMENT),        # down_s
+    (1, 64, 256, {6: 1}, _lib.NMI_ERR_ALIGNMENT),        # out
+    (1, 64, 256, {"ws": 8}, _lib.NMI_ERR_ALIGNMENT),     # workspace
+    (1, 64, 256, {"ws_bytes": 16}, _lib.NMI_ERR_WORKSPACE),
+])
+def test_mlp_rejects_bad_arguments(M, hidden, inter, offs, code):
+    L = _lib.lib()
+    ptrs = [FAKE + offs.get(i, 0) for i in range(7)]
+    ws = FAKE + offs.get("ws", 0)
+    ws_bytes = offs.get("ws_bytes", 1 << 20)
+    rc = L.nmi_mlp_forward_fp8(*ptrs, M, hidden, inter, 1e-5, ws, ws_bytes, None)
+    assert rc == code
+    assert L.nmi_last_error().decode().startswith("nmi_mlp_forward_fp8")
+    ptrs[3] = 0
+    assert L.nmi_mlp_forward_fp8(*ptrs, 1, 64, 256, 1e-5, FAKE, 1 << 20, None) == _lib.NMI_ERR_INVALID_ARG
+
+
+def test_binding_block_entries_validate():
+    from nemotron_infer_amd.csrc import binding as B
+
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        B.rmsnorm(FAKE + 2, FAKE, FAKE, 1)
+    with pytest.raises(RuntimeError, match="M=0"):
+        B.mlp_forward_fp8(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0)
