@@ -120,7 +120,19 @@ __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
         __syncthreads();
     }
 
-    // Epilogue: lane holds D[(lane>>4)*4 + t][lane & 15] of each 16x16 tile.
+    // Epilogue: lane holds D[(lane>>4)*4 + t][lane & 15] of each 16x16 tile.  Residuals are
+    // loaded (clamped in bounds) before the first store.
+    uint16_t rres[TN][TM][4];
+#pragma unroll
+    for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int n = min(n0 + wn * WN + jn * 16 + (lane & 15), N - 1);
+                const int m = min(m0 + wm * WM + i * 16 + (lane >> 4) * 4 + t, M - 1);
+                rres[jn][i][t] = epi.kind == kEpiResidual ? epi.res[(int64_t)m * epi.ldres + n] : 0;
+            }
 #pragma unroll
     for (int jn = 0; jn < TN; ++jn) {
         const int n = n0 + wn * WN + jn * 16 + (lane & 15);
@@ -131,7 +143,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int m = m0 + wm * WM + i * 16 + (lane >> 4) * 4 + t;
-                if (m < M) y[(int64_t)m * ldy + n] = epilogue(acc[i][jn][t], sc, epi.kind, epi.res, (int64_t)m * epi.ldres + n);
+                if (m < M) y[(int64_t)m * ldy + n] = epilogue(acc[i][jn][t], sc, epi.kind, rres[jn][i][t]);
             }
         }
     }
@@ -159,6 +171,7 @@ struct GemmArgs {
     int M, N, K;
     int tiles_m, tiles_n, per_xcd;
     int vec_store;          // y 8-byte aligned and ldy % 4 == 0
+    int vec_res;            // residual 8-byte aligned and ldres % 4 == 0
     Epi epi;
 };
 
@@ -267,6 +280,19 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
     }
 
     // Epilogue: lane holds D[n = 4 (lane / 16) + r][m = lane % 16] of each 16 x 16 tile.
+    // Residuals are loaded (clamped in bounds) before the first store.
+    uint2 rres[TN][TM];
+    if (a.epi.kind == kEpiResidual) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int n = n0 + wn * WTN + i * 16 + 4 * (lane >> 4);
+                const int m = min(m0 + wm * WTM + j * 16 + (lane & 15), M - 1);
+                const int64_t row = (int64_t)m * a.epi.ldres;
+                rres[i][j] = load_res4(a.epi.res, row + min(n, N - 1), row + N - 1, a.vec_res && n + 3 < N);
+            }
+    }
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
         const int n = n0 + wn * WTN + i * 16 + 4 * (lane >> 4);
@@ -279,12 +305,11 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
             const int m = m0 + wm * WTM + j * 16 + (lane & 15);
             if (m >= M) continue;
             uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
-            const int64_t ro = (int64_t)m * a.epi.ldres + n;
-            const int64_t rl = ro + (N - 1 - n);    // last in-bounds residual of this row
-            const uint16_t b0 = epilogue(acc[i][j][0], sc[0], a.epi.kind, a.epi.res, min(ro, rl));
-            const uint16_t b1 = epilogue(acc[i][j][1], sc[1], a.epi.kind, a.epi.res, min(ro + 1, rl));
-            const uint16_t b2 = epilogue(acc[i][j][2], sc[2], a.epi.kind, a.epi.res, min(ro + 2, rl));
-            const uint16_t b3 = epilogue(acc[i][j][3], sc[3], a.epi.kind, a.epi.res, min(ro + 3, rl));
+            const uint2 rv = rres[i][j];
+            const uint16_t b0 = epilogue(acc[i][j][0], sc[0], a.epi.kind, (uint16_t)rv.x);
+            const uint16_t b1 = epilogue(acc[i][j][1], sc[1], a.epi.kind, (uint16_t)(rv.x >> 16));
+            const uint16_t b2 = epilogue(acc[i][j][2], sc[2], a.epi.kind, (uint16_t)rv.y);
+            const uint16_t b3 = epilogue(acc[i][j][3], sc[3], a.epi.kind, (uint16_t)(rv.y >> 16));
             if (full) {
                 *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
                                                       (uint32_t)b2 | ((uint32_t)b3 << 16)};
@@ -444,6 +469,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
     }
 
     // Epilogue: register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
+    // Residuals are loaded (clamped in bounds) before the first store.
+    uint2 rres[TN][4][TM];
+    if (a.epi.kind == kEpiResidual) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    const int n = n0 + wn * WTN + i * 32 + 8 * gq + 4 * (lane >> 5);
+                    const int m = min(m0 + wm * WTM + j * 32 + (lane & 31), M - 1);
+                    const int64_t row = (int64_t)m * a.epi.ldres;
+                    rres[i][gq][j] = load_res4(a.epi.res, row + min(n, N - 1), row + N - 1, a.vec_res && n + 3 < N);
+                }
+    }
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
 #pragma unroll
@@ -458,12 +498,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
                 const int m = m0 + wm * WTM + j * 32 + (lane & 31);
                 if (m >= M) continue;
                 uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
-                const int64_t ro = (int64_t)m * a.epi.ldres + n;
-                const int64_t rl = ro + (N - 1 - n);    // last in-bounds residual of this row
-                const uint16_t b0 = epilogue(acc[i][j][4 * gq + 0], sc[0], a.epi.kind, a.epi.res, min(ro, rl));
-                const uint16_t b1 = epilogue(acc[i][j][4 * gq + 1], sc[1], a.epi.kind, a.epi.res, min(ro + 1, rl));
-                const uint16_t b2 = epilogue(acc[i][j][4 * gq + 2], sc[2], a.epi.kind, a.epi.res, min(ro + 2, rl));
-                const uint16_t b3 = epilogue(acc[i][j][4 * gq + 3], sc[3], a.epi.kind, a.epi.res, min(ro + 3, rl));
+                const uint2 rv = rres[i][gq][j];
+                const uint16_t b0 = epilogue(acc[i][j][4 * gq + 0], sc[0], a.epi.kind, (uint16_t)rv.x);
+                const uint16_t b1 = epilogue(acc[i][j][4 * gq + 1], sc[1], a.epi.kind, (uint16_t)(rv.x >> 16));
+                const uint16_t b2 = epilogue(acc[i][j][4 * gq + 2], sc[2], a.epi.kind, (uint16_t)rv.y);
+                const uint16_t b3 = epilogue(acc[i][j][4 * gq + 3], sc[3], a.epi.kind, (uint16_t)(rv.y >> 16));
                 if (full) {
                     *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
                                                           (uint32_t)b2 | ((uint32_t)b3 << 16)};
@@ -486,12 +525,13 @@ hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0, epi};
+    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0, 0, epi};
     a.tiles_m = (M + BM - 1) / BM;
     a.tiles_n = (N + BN - 1) / BN;
     const int T = a.tiles_m * a.tiles_n;
     a.per_xcd = (T + 7) / 8;
     a.vec_store = ((reinterpret_cast<uintptr_t>(y) & 7) == 0 && (ldy & 3) == 0) ? 1 : 0;
+    a.vec_res = ((reinterpret_cast<uintptr_t>(epi.res) & 7) == 0 && (epi.ldres & 3) == 0) ? 1 : 0;
     hipLaunchKernelGGL(kernel, dim3(8 * a.per_xcd), dim3(M32 ? NW * 64 : 256), lds, stream, a);
     return hipGetLastError();
 }

@@ -305,9 +305,11 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
                 if (lane == t * MR + m) v = sums[t][m];
         const int t = lane / MR, m = lane % MR;
         const int row = row_base + t;
-        if (row < grp.N && m < args.M)
+        if (row < grp.N && m < args.M) {
+            const int64_t o = (int64_t)m * grp.epi.ldres + row;
             grp.y[(int64_t)m * grp.ldy + row] =
-                epilogue(v, grp.s[row], grp.epi.kind, grp.epi.res, (int64_t)m * grp.epi.ldres + row);
+                epilogue(v, grp.s[row], grp.epi.kind, grp.epi.kind == kEpiResidual ? grp.epi.res[o] : 0);
+        }
     }
 }
 

@@ -63,16 +63,27 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 // both round to the bf16 the reference's bf16 arithmetic gives on the rounded linear output
 // (relu^2 as __hfma2_relu then __hmul2, ops/elementwise.cuh:256-272; residual as __hadd2,
 // :241-244; used at model/mlp_block.cuh:145-147, 163-165 and 173-175).  relu keeps NaN
-// (NaN < 0 is false).  res[off] is read only for kEpiResidual.
-__device__ __forceinline__ uint16_t epilogue(float acc, float s, int epi, const uint16_t* res, int64_t off) {
+// (NaN < 0 is false).  `res` is the residual's bf16 bits (used only for kEpiResidual).
+// Kernels load the residual before their first store: y may be the residual itself (in place),
+// so a load issued after a store to y could not be moved ahead of it and would wait on memory
+// once per store.
+__device__ __forceinline__ uint16_t epilogue(float acc, float s, int epi, uint16_t res) {
     const uint16_t v = f32_to_bf16_rne(acc * s);
     if (epi == kEpiRelu2) {
         float f = bf16_to_f32(v);
         f = f < 0.f ? 0.f : f;
         return f32_to_bf16_rne(f * f);
     }
-    if (epi == kEpiResidual) return f32_to_bf16_rne(bf16_to_f32(res[off]) + bf16_to_f32(v));
+    if (epi == kEpiResidual) return f32_to_bf16_rne(bf16_to_f32(res) + bf16_to_f32(v));
     return v;
+}
+
+// Residual elements off .. off + 3 of one row (clamped to its last element `last`), packed as
+// four bf16; one 8-byte load when `vec` (then all four are in bounds and 8-byte aligned).
+__device__ __forceinline__ uint2 load_res4(const uint16_t* res, int64_t off, int64_t last, bool vec) {
+    if (vec) return *reinterpret_cast<const uint2*>(res + off);
+    return uint2{(uint32_t)res[min(off, last)] | ((uint32_t)res[min(off + 1, last)] << 16),
+                 (uint32_t)res[min(off + 2, last)] | ((uint32_t)res[min(off + 3, last)] << 16)};
 }
 
 // RMSNorm pieces: 8 consecutive bf16 activations in 16 bytes.  sumsq8 continues a float32

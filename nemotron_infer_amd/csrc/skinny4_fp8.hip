@@ -207,6 +207,18 @@ __global__ __launch_bounds__(256) void skinny4_fp8_kernel(const Skinny4Args a) {
         }
     }
     if (lane < 4) {
+        // residuals first (clamped in bounds), then the stores
+        uint16_t rres[T][G][4];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    rres[t][g][r] = grp.epi.kind == kEpiResidual
+                                        ? grp.epi.res[(int64_t)min(4 * g + li, M - 1) * grp.epi.ldres +
+                                                      min(row_base + 4 * t + r, grp.N - 1)]
+                                        : 0;
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -217,8 +229,7 @@ __global__ __launch_bounds__(256) void skinny4_fp8_kernel(const Skinny4Args a) {
                 for (int r = 0; r < 4; ++r) {
                     const int n = row_base + 4 * t + r;
                     if (n < grp.N)
-                        grp.y[(int64_t)m * grp.ldy + n] = epilogue(acc[t][g][r], grp.s[n], grp.epi.kind, grp.epi.res,
-                                                                   (int64_t)m * grp.epi.ldres + n);
+                        grp.y[(int64_t)m * grp.ldy + n] = epilogue(acc[t][g][r], grp.s[n], grp.epi.kind, rres[t][g][r]);
                 }
             }
     }

@@ -59,6 +59,11 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, 
     return __builtin_bit_cast(bf16x8, u32x4_t{a, b, c, d});
 }
 
+// Residual bits of output (m, n), n clamped into the row (read only for kEpiResidual).
+__device__ __forceinline__ uint16_t residual(const GemvGroup& grp, int m, int n) {
+    return grp.epi.kind == kEpiResidual ? grp.epi.res[(int64_t)m * grp.epi.ldres + min(n, grp.N - 1)] : 0;
+}
+
 template <int U, int KSW>
 __global__ __launch_bounds__(256) void skinny_fp8_kernel(const SkinnyArgs a) {
     extern __shared__ uint4 xs[];                 // [M][rs] words, then one zero word
@@ -196,6 +201,9 @@ __global__ __launch_bounds__(256) void skinny_fp8_kernel(const SkinnyArgs a) {
         __syncthreads();
         if (!last_flag) return;
         if (q == 0 && m < M) {
+            uint16_t rres[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rres[i] = residual(grp, m, row0 + 4 * a4 + i);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int n = row0 + 4 * a4 + i;
@@ -205,20 +213,20 @@ __global__ __launch_bounds__(256) void skinny_fp8_kernel(const SkinnyArgs a) {
                     for (int g2 = 0; g2 < a.kgroups; ++g2)
                         tsum += __hip_atomic_load(src + (int64_t)g2 * M * a.ws_ld, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
-                    grp.y[(int64_t)m * grp.ldy + n] =
-                        epilogue(tsum, grp.s[n], grp.epi.kind, grp.epi.res, (int64_t)m * grp.epi.ldres + n);
+                    grp.y[(int64_t)m * grp.ldy + n] = epilogue(tsum, grp.s[n], grp.epi.kind, rres[i]);
                 }
             }
         }
         if (tid == 0) __hip_atomic_store(a.counters + rb_all, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if (q == 0 && m < M) {
         const f32x4 v = red[0][t][lane];
+        uint16_t rres[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rres[i] = residual(grp, m, row0 + 4 * a4 + i);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int n = row0 + 4 * a4 + i;
-            if (n < grp.N)
-                grp.y[(int64_t)m * grp.ldy + n] =
-                    epilogue(v[i], grp.s[n], grp.epi.kind, grp.epi.res, (int64_t)m * grp.epi.ldres + n);
+            if (n < grp.N) grp.y[(int64_t)m * grp.ldy + n] = epilogue(v[i], grp.s[n], grp.epi.kind, rres[i]);
         }
     }
 }
