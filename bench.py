@@ -45,8 +45,8 @@ ROTATION_BYTES = 1 << 30
 # HBM bytes per launch of the config-1 step, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
 # script (scaled by a 256 MiB copy; profiles/gemv_m1_config1_decode_set.md).  Re-measured when the
 # GEMV kernels change; reported as roofline.traffic next to the algorithmic bytes.
-MEASURED_TRAFFIC = {"qkv_grouped": 22735968, "o_proj": 16327829, "up_proj": 39604013,
-                    "down_proj": 39762855}
+MEASURED_TRAFFIC = {"qkv_grouped": 22724078, "o_proj": 16323558, "up_proj": 39597227,
+                    "down_proj": 39766161}
 
 
 def log(*a):
