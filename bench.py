@@ -242,7 +242,7 @@ def bench_prefill(dev, reps=20):
         del w, s, x, y, g
     tf = tot_f / (tot_ms * 1e-3) / 1e12
     return {"workload": "config3_prefill_m2048", "tflops": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_kernel",
+            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_m32_kernel (pipelined, 256x256 or 256x128 tiles)",
             "shapes": out}
 
 

@@ -13,7 +13,7 @@
 //   (16 codes per lane) into registers, converts the codes to bf16 with
 //   v_cvt_scalef32_pk_bf16_fp8 (exact), and writes both tiles to LDS, double-buffered so
 //   the global loads of step t+1 overlap the MFMAs of step t.
-// * LDS rows are 64 bf16 (eight 16-byte chunks); chunk c of row r is stored at c ^ (r & 7),
+// * LDS rows are 64 bf16 (eight 16-byte chunks); chunk c of row r is stored at swz(r, c),
 //   which spreads the 16 rows an MFMA operand read touches over all banks.
 // * Epilogue: acc * s[n] in float32, one bf16 RNE rounding, masked for ragged M and N.
 #include "nmi_device.hpp"
@@ -24,6 +24,14 @@ namespace nmi {
 namespace {
 
 constexpr int kBK = 64;
+
+// LDS position of 16-byte chunk c (of 8) in a 128-byte tile row.  An MFMA operand read has 16
+// consecutive lanes on 16 consecutive rows at the same chunk; with 64 four-byte banks, rows r
+// and r + 2 start on the same bank, so the chunk is permuted by bits 1-3 of the row: the 16 rows
+// then cover 16 distinct 16-byte bank groups (an XOR with row & 7 left rows r and r + 8 on the
+// same group, a two-way conflict measured with SQ_LDS_BANK_CONFLICT).  Row-order writes (8 or 4
+// lanes per row) stay conflict-free.
+__device__ __forceinline__ int swz(int row, int c) { return c ^ ((row >> 1) & 7); }
 
 template <int BM, int BN>
 __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
@@ -67,7 +75,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
         for (int i = 0; i < A_PER; ++i) {
             const int id = tid + 256 * i;
             const int row = id >> 3, kc = id & 7;
-            *reinterpret_cast<uint4*>(A + row * kBK + ((kc ^ (row & 7)) << 3)) = ra[i];
+            *reinterpret_cast<uint4*>(A + row * kBK + (swz(row, kc) << 3)) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < B_PER; ++i) {
@@ -76,8 +84,8 @@ __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
             const uint2 d0 = e4m3x4_to_bf16(rb[i].x), d1 = e4m3x4_to_bf16(rb[i].y);
             const uint2 d2 = e4m3x4_to_bf16(rb[i].z), d3 = e4m3x4_to_bf16(rb[i].w);
             const int c0 = 2 * kc, c1 = 2 * kc + 1;
-            *reinterpret_cast<uint4*>(B + row * kBK + ((c0 ^ (row & 7)) << 3)) = uint4{d0.x, d0.y, d1.x, d1.y};
-            *reinterpret_cast<uint4*>(B + row * kBK + ((c1 ^ (row & 7)) << 3)) = uint4{d2.x, d2.y, d3.x, d3.y};
+            *reinterpret_cast<uint4*>(B + row * kBK + (swz(row, c0) << 3)) = uint4{d0.x, d0.y, d1.x, d1.y};
+            *reinterpret_cast<uint4*>(B + row * kBK + (swz(row, c1) << 3)) = uint4{d2.x, d2.y, d3.x, d3.y};
         }
     };
 
@@ -103,12 +111,12 @@ __global__ __launch_bounds__(256) void gemm_fp8_w8a16_kernel(
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int row = wm * WM + i * 16 + (lane & 15);
-                af[i] = *reinterpret_cast<const bf16x8*>(A + row * kBK + ((chunk ^ (row & 7)) << 3));
+                af[i] = *reinterpret_cast<const bf16x8*>(A + row * kBK + (swz(row, chunk) << 3));
             }
 #pragma unroll
             for (int jn = 0; jn < TN; ++jn) {
                 const int row = wn * WN + jn * 16 + (lane & 15);
-                bfr[jn] = *reinterpret_cast<const bf16x8*>(B + row * kBK + ((chunk ^ (row & 7)) << 3));
+                bfr[jn] = *reinterpret_cast<const bf16x8*>(B + row * kBK + (swz(row, chunk) << 3));
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -225,7 +233,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
             const int p = tid + 256 * i;
             const int row = p >> 3, kc = p & 7;
             const uint4 v = (k0 + kc * 8 < K) ? rx[i] : uint4{0, 0, 0, 0};
-            *reinterpret_cast<uint4*>(Xs + row * BK + ((kc ^ (row & 7)) << 3)) = v;
+            *reinterpret_cast<uint4*>(Xs + row * BK + (swz(row, kc) << 3)) = v;
         }
 #pragma unroll
         for (int i = 0; i < WP; ++i) {
@@ -235,8 +243,8 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
             const uint2 d0 = e4m3x4_to_bf16(w.x), d1 = e4m3x4_to_bf16(w.y);
             const uint2 d2 = e4m3x4_to_bf16(w.z), d3 = e4m3x4_to_bf16(w.w);
             const int c0 = 2 * kc, c1 = 2 * kc + 1;
-            *reinterpret_cast<uint4*>(Ws + row * BK + ((c0 ^ (row & 7)) << 3)) = uint4{d0.x, d0.y, d1.x, d1.y};
-            *reinterpret_cast<uint4*>(Ws + row * BK + ((c1 ^ (row & 7)) << 3)) = uint4{d2.x, d2.y, d3.x, d3.y};
+            *reinterpret_cast<uint4*>(Ws + row * BK + (swz(row, c0) << 3)) = uint4{d0.x, d0.y, d1.x, d1.y};
+            *reinterpret_cast<uint4*>(Ws + row * BK + (swz(row, c1) << 3)) = uint4{d2.x, d2.y, d3.x, d3.y};
         }
     };
 
@@ -262,12 +270,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
 #pragma unroll
             for (int i = 0; i < TN; ++i) {
                 const int row = wn * WTN + i * 16 + (lane & 15);
-                af[i] = *reinterpret_cast<const bf16x8*>(Ws + row * BK + ((chunk ^ (row & 7)) << 3));
+                af[i] = *reinterpret_cast<const bf16x8*>(Ws + row * BK + (swz(row, chunk) << 3));
             }
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const int row = wm * WTM + j * 16 + (lane & 15);
-                bfr[j] = *reinterpret_cast<const bf16x8*>(Xs + row * BK + ((chunk ^ (row & 7)) << 3));
+                bfr[j] = *reinterpret_cast<const bf16x8*>(Xs + row * BK + (swz(row, chunk) << 3));
             }
 #pragma unroll
             for (int i = 0; i < TN; ++i)
@@ -330,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
 // step s run (two fragment register sets).  Operand layouts (gfx950): A lane l holds row
 // l % 32, k 8 (l / 32) .. +7; B lane l holds column l % 32, the same k; D register r of lane l
 // is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-template <int BM, int BN, int NW, bool B64>
+template <int BM, int BN, int NW, bool B64, bool PIPE>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const GemmArgs a) {
     constexpr int BK = kBK;
     constexpr int NT = NW * 64;                     // threads
@@ -375,7 +383,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
         }
     };
     // LDS tile layouts.  B64 = false: rows of eight 16-byte chunks, chunk c of row r at
-    // c ^ (r & 7).  B64 = true: the low and high 8 bytes of every chunk in two planes of
+    // swz(r, c).  B64 = true: the low and high 8 bytes of every chunk in two planes of
     // 64-byte rows, chunk c of row r at c ^ ((r >> 2) & 7), so that fragments are read with
     // ds_read_b64 (measured on MI355X: ~1.6x the LDS read throughput of ds_read_b128) and
     // the 32 rows one read touches fall in distinct banks.
@@ -385,7 +393,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             *reinterpret_cast<uint2*>(T + off) = uint2{v.x, v.y};
             *reinterpret_cast<uint2*>(T + rows * 32 + off) = uint2{v.z, v.w};
         } else {
-            *reinterpret_cast<uint4*>(T + row * BK + ((c ^ (row & 7)) << 3)) = v;
+            *reinterpret_cast<uint4*>(T + row * BK + (swz(row, c) << 3)) = v;
         }
     };
     auto get16 = [&](const uint16_t* T, int rows, int row, int c) -> bf16x8 {
@@ -396,12 +404,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
             return __builtin_bit_cast(bf16x8, u32x4_t{lo.x, lo.y, hi.x, hi.y});
         } else {
-            return *reinterpret_cast<const bf16x8*>(T + row * BK + ((c ^ (row & 7)) << 3));
+            return *reinterpret_cast<const bf16x8*>(T + row * BK + (swz(row, c) << 3));
         }
     };
-    auto sstore = [&](int buf, int k0) {
-        uint16_t* Ws = lds + buf * STAGE;
-        uint16_t* Xs = Ws + BN * BK;
+    auto sstore_x = [&](int buf, int k0) {
+        uint16_t* Xs = lds + buf * STAGE + BN * BK;
 #pragma unroll
         for (int i = 0; i < XP; ++i) {
             const int p = tid + NT * i;
@@ -409,6 +416,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             const uint4 v = (k0 + kc * 8 < K) ? rx[i] : uint4{0, 0, 0, 0};
             put16(Xs, BM, row, kc, v);
         }
+    };
+    auto sstore_w = [&](int buf, int k0) {
+        uint16_t* Ws = lds + buf * STAGE;
 #pragma unroll
         for (int i = 0; i < WP; ++i) {
             const int p = tid + NT * i;
@@ -419,6 +429,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             put16(Ws, BN, row, 2 * kc, uint4{d0.x, d0.y, d1.x, d1.y});
             put16(Ws, BN, row, 2 * kc + 1, uint4{d2.x, d2.y, d3.x, d3.y});
         }
+    };
+    auto sstore = [&](int buf, int k0) {
+        sstore_x(buf, k0);
+        sstore_w(buf, k0);
     };
     // Fragments of k step s (16 k = chunks 2s, 2s+1) from LDS stage `buf`.
     auto frags = [&](int buf, int s, bf16x8 (&af)[TN], bf16x8 (&bfr)[TM]) {
@@ -445,27 +459,43 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
     sstore(0, 0);
     __syncthreads();
     frags(0, 0, af0, bf0);
+    auto mfmas = [&](const bf16x8 (&af)[TN], const bf16x8 (&bfr)[TM]) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    };
     for (int kt = 0; kt < KT; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * BK);
+        const bool more = kt + 1 < KT;
+        if (more) gload((kt + 1) * BK);
+        if constexpr (PIPE) {
+            // The next tile's LDS stage (buf ^ 1) was last read before the previous barrier, so
+            // its stores go between this tile's MFMA groups: the matrix cores keep working
+            // while the x tile and the converted W tile are written.
+            static_assert(BK / 16 == 4, "four k steps per tile");
+            frags(buf, 1, af1, bf1);
+            mfmas(af0, bf0);
+            frags(buf, 2, af0, bf0);
+            mfmas(af1, bf1);
+            frags(buf, 3, af1, bf1);
+            if (more) sstore_x(buf ^ 1, (kt + 1) * BK);
+            mfmas(af0, bf0);
+            if (more) sstore_w(buf ^ 1, (kt + 1) * BK);
+            mfmas(af1, bf1);
+        } else {
 #pragma unroll
-        for (int s = 0; s < BK / 16; s += 2) {
-            frags(buf, s + 1, af1, bf1);
-#pragma unroll
-            for (int i = 0; i < TN; ++i)
-#pragma unroll
-                for (int j = 0; j < TM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af0[i], bf0[j], acc[i][j], 0, 0, 0);
-            if (s + 2 < BK / 16) frags(buf, s + 2, af0, bf0);
-#pragma unroll
-            for (int i = 0; i < TN; ++i)
-#pragma unroll
-                for (int j = 0; j < TM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af1[i], bf1[j], acc[i][j], 0, 0, 0);
+            for (int s = 0; s < BK / 16; s += 2) {
+                frags(buf, s + 1, af1, bf1);
+                mfmas(af0, bf0);
+                if (s + 2 < BK / 16) frags(buf, s + 2, af0, bf0);
+                mfmas(af1, bf1);
+            }
+            if (more) sstore(buf ^ 1, (kt + 1) * BK);
         }
-        if (kt + 1 < KT) sstore(buf ^ 1, (kt + 1) * BK);
         __syncthreads();
-        if (kt + 1 < KT) frags(buf ^ 1, 0, af0, bf0);
+        if (more) frags(buf ^ 1, 0, af0, bf0);
     }
 
     // Epilogue: register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
@@ -517,11 +547,12 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
     }
 }
 
-template <int BM, int BN, bool M32, int NW = 4, bool B64 = false>
+template <int BM, int BN, bool M32, int NW = 4, bool B64 = false, bool PIPE = false>
 hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s,
                       uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi) {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * kBK * sizeof(uint16_t);
-    constexpr auto kernel = M32 ? &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64> : &gemm_fp8_w8a16_big_kernel<BM, BN>;
+    constexpr auto kernel =
+        M32 ? &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64, PIPE> : &gemm_fp8_w8a16_big_kernel<BM, BN>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
@@ -542,14 +573,15 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
                        hipStream_t stream, const Epi& epi) {
     int tile = tuning().gemm_tile;
-    if (tile < 1 || tile > 13) {
-        // Measured on MI355X (config 3): 256 x 256 tiles on 8 waves (32 x 32 MFMA) where there
-        // are enough of them to fill the 256 CUs at least 1.5 times, 256 x 128 on 8 waves when
-        // N is short (e.g. down_proj N = 3136: 104 tiles of 256 x 256), 128 x 128 for small M.
+    if (tile < 1 || tile > 19) {
+        // Measured on MI355X (config 3): the pipelined 8-wave kernels (32 x 32 MFMA, the next
+        // tile's LDS stores between the MFMA groups); 256 x 256 tiles where there are at least
+        // 3/4 as many as CUs (up_proj 392, qkv 224), else 256 x 128 (down_proj, N = 3136: 104
+        // tiles of 256 x 256); 128 x 128 for small M.
         const DeviceInfo& dev = device_info();
         const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
         if (M < 512) tile = 1;
-        else tile = (big * 2 >= 3 * (int64_t)dev.num_cu) ? 8 : 9;
+        else tile = (4 * big >= 3 * (int64_t)dev.num_cu) ? 14 : 15;
     }
     switch (tile) {
         case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
@@ -564,6 +596,12 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
         case 11: return launch_big<256, 256, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
         case 12: return launch_big<256, 128, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
         case 13: return launch_big<256, 128, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 14: return launch_big<256, 256, true, 8, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 15: return launch_big<256, 128, true, 8, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 16: return launch_big<256, 256, true, 8, true, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 17: return launch_big<256, 128, true, 8, true, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 18: return launch_big<256, 256, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 19: return launch_big<256, 128, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
         default: {
             constexpr int BM = 128, BN = 128;
             const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
