@@ -126,7 +126,7 @@ hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGro
     }
     hipError_t e = hipSuccess;
     for (int i = 0; i < ng && e == hipSuccess; ++i)
-        e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, st, g[i].epi);
+        e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, st, g[i].epi, ws, ws_bytes);
     return e;
 }
 
@@ -210,7 +210,8 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
 }
 
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) {
-    if (M < 1 || M > 16 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
+    if (M < 1 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
+    if (M > 16) return gemm_workspace_bytes(M);       // stream-K partials of the GEMM
     // only the split-K 16x16x32 kernel uses a workspace (selected with "skinny.path" = 1,
     // or "m1.path" = 2 for M = 1)
     if (!(tuning().skinny_path == 1 || (M == 1 && tuning().m1_path == 2))) return 0;
@@ -220,15 +221,15 @@ size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) {
 int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
                        const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
                        void* workspace, size_t workspace_bytes, void* stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     int rc = check_linear(x_bf16, ldx, w_e4m3, ldw, w_scale, y_bf16, ldy, M, N, K,
                           "nmi_gemm_fp8_w8a16");
     if (rc) return rc;
+    if (workspace && !aligned(workspace, 256))
+        return fail(NMI_ERR_ALIGNMENT, "nmi_gemm_fp8_w8a16: workspace must be 256-byte aligned");
     return hip_status(launch_gemm(static_cast<const uint16_t*>(x_bf16), ldx,
                                   static_cast<const uint8_t*>(w_e4m3), ldw, w_scale,
                                   static_cast<uint16_t*>(y_bf16), ldy, M, N, K,
-                                  static_cast<hipStream_t>(stream)),
+                                  static_cast<hipStream_t>(stream), Epi{}, workspace, workspace_bytes),
                       "nmi_gemm_fp8_w8a16 launch");
 }
 
@@ -262,6 +263,7 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s4.ks")) t.s4_ks = value;
     else if (!std::strcmp(knob, "s4.t")) t.s4_t = value;
     else if (!std::strcmp(knob, "s4.u")) t.s4_u = value;
+    else if (!std::strcmp(knob, "gemm.sk")) t.gemm_sk = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

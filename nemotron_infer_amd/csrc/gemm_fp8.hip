@@ -181,6 +181,11 @@ struct GemmArgs {
     int vec_store;          // y 8-byte aligned and ldy % 4 == 0
     int vec_res;            // residual 8-byte aligned and ldres % 4 == 0
     Epi epi;
+    // Stream-K (m32 kernels): sk_total = tiles * K steps (0: one tile per workgroup); the
+    // workspace's flag slots (zero at rest) and fp32 partial tiles, one per workgroup.
+    int64_t sk_total;
+    uint32_t* sk_flags;
+    float* sk_part;
 };
 
 template <int BM, int BN>
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
 // step s run (two fragment register sets).  Operand layouts (gfx950): A lane l holds row
 // l % 32, k 8 (l / 32) .. +7; B lane l holds column l % 32, the same k; D register r of lane l
 // is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-template <int BM, int BN, int NW, bool B64, bool PIPE>
+template <int BM, int BN, int NW, bool B64, bool PIPE, bool SK>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const GemmArgs a) {
     constexpr int BK = kBK;
     constexpr int NT = NW * 64;                     // threads
@@ -351,14 +356,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
     static_assert(XP >= 1 && WP >= 1 && TM >= 1 && TN >= 1, "tile too small");
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
 
-    const int g = (int)blockIdx.x;
-    const int local = g >> 3;
-    const int tile = (g & 7) * a.per_xcd + local;
-    if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
-    const int tm = tile / a.tiles_n;
-    const int tn = tile - tm * a.tiles_n;
-    const int m0 = tm * BM, n0 = tn * BN;
     const int M = a.M, N = a.N, K = a.K;
+    const int KT = (K + BK - 1) / BK;
+    int m0 = 0, n0 = 0;                             // origin of the tile being computed
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -446,19 +446,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
     };
 
     f32x16 acc[TN][TM];
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const int KT = (K + BK - 1) / BK;
     bf16x8 af0[TN], bf0[TM], af1[TN], bf1[TM];
-    gload(0);
-    sstore(0, 0);
-    __syncthreads();
-    frags(0, 0, af0, bf0);
     auto mfmas = [&](const bf16x8 (&af)[TN], const bf16x8 (&bfr)[TM]) {
 #pragma unroll
         for (int i = 0; i < TN; ++i)
@@ -466,9 +454,23 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             for (int j = 0; j < TM; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     };
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        const bool more = kt + 1 < KT;
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    };
+    // acc += the K steps [kb, ke) of the tile at (m0, n0).
+    auto run = [&](int kb, int ke) {
+    gload(kb * BK);
+    sstore(0, kb * BK);
+    __syncthreads();
+    frags(0, 0, af0, bf0);
+    for (int kt = kb; kt < ke; ++kt) {
+        const int buf = (kt - kb) & 1;
+        const bool more = kt + 1 < ke;
         if (more) gload((kt + 1) * BK);
         if constexpr (PIPE) {
             // The next tile's LDS stage (buf ^ 1) was last read before the previous barrier, so
@@ -497,11 +499,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
         __syncthreads();
         if (more) frags(buf ^ 1, 0, af0, bf0);
     }
+    };
 
     // Epilogue: register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
     // Residuals are loaded (clamped in bounds) before the first store.
+    auto store = [&]() {
     uint2 rres[TN][4][TM];
-    if (a.epi.kind == kEpiResidual) {
+    if (!SK && a.epi.kind == kEpiResidual) {     // (the stream-K kernel is not used with a residual)
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -545,63 +549,219 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             }
         }
     }
+    };
+
+    if constexpr (!SK) {
+        // One tile per workgroup, XCD-ordered: workgroup g runs on XCD g % 8, which takes the
+        // consecutive tiles [x * per_xcd, (x + 1) * per_xcd).
+        const int g = (int)blockIdx.x;
+        const int local = g >> 3;
+        const int tile = (g & 7) * a.per_xcd + local;
+        if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
+        const int tm = tile / a.tiles_n;
+        m0 = tm * BM;
+        n0 = (tile - tm * a.tiles_n) * BN;
+        zero_acc();
+        run(0, KT);
+        store();
+    } else {
+
+    // Stream-K, one independent problem per XCD: workgroup g runs on XCD x = g % 8, which
+    // owns the consecutive tiles [x T / 8, (x + 1) T / 8).  Their K steps, flattened
+    // tile-major, are split evenly between the XCD's Gx = G / 8 workgroups: local workgroup
+    // v = g / 8 owns [v total / Gx, (v + 1) total / Gx).  A tile cut between workgroups is
+    // finished by the one holding its last K step: the others store fp32 partial tiles (slot =
+    // their workgroup id) and raise a flag; the finisher starts from the partials, added in
+    // decreasing workgroup order, then runs its own K steps and stores the output.  Each workgroup walks its range backwards, so its
+    // partial (the head of its last tile) is written first and the tile it finishes (the tail of
+    // its first) comes last.  A finisher only waits for workgroups g - 8, g - 16, ..., which are
+    // dispatched before it and never wait on it: no co-residency is needed for progress.
+    constexpr int ACC = TN * TM * 16;               // fp32 accumulators per thread
+    // (All of this is wave-uniform and kept in scalar registers: the 256 x 256 kernel has no
+    // vector registers to spare.  tiles * K steps < 2^31 is checked on the host.)
+    const int g = (int)blockIdx.x;
+    const int Gx = (int)gridDim.x >> 3;
+    const int xcd = g & 7, v = g >> 3;
+    const int T = a.tiles_m * a.tiles_n;
+    const int tb = xcd * T / 8, te = (xcd + 1) * T / 8;
+    const int total = (te - tb) * KT;
+    const int start = __builtin_amdgcn_readfirstlane((int)((int64_t)v * total / Gx));
+    const int end = __builtin_amdgcn_readfirstlane((int)((int64_t)(v + 1) * total / Gx));
+    for (int it = end; it > start;) {
+        const int tl = __builtin_amdgcn_readfirstlane((it - 1) / KT);     // tile within the XCD's range
+        const int tile = tb + tl;
+        const int t0 = tl * KT;
+        const int kb = max(start, t0) - t0, ke = it - t0;
+        const int tm = tile / a.tiles_n;
+        m0 = tm * BM;
+        n0 = (tile - tm * a.tiles_n) * BN;
+        zero_acc();
+        if (ke == KT && kb > 0) {
+            // finisher: start from the partials of the local workgroups holding K steps
+            // [0, kb), added in decreasing workgroup order, before this workgroup's own steps
+            const int first = __builtin_amdgcn_readfirstlane((int)(((int64_t)(t0 + 1) * Gx - 1) / total));
+            for (int cv = v - 1; cv >= first; --cv) {
+                if ((int64_t)cv * total / Gx == (int64_t)(cv + 1) * total / Gx) continue;   // empty range
+                const int c = 8 * cv + xcd;             // their workgroup id
+                if (tid == 0) {
+                    // bounded wait: the bound turns a lost flag into a wrong tile, not a hang
+                    for (int spin = 0; spin < (1 << 26); ++spin) {
+                        if (__hip_atomic_load(a.sk_flags + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u)
+                            break;
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                }
+                __syncthreads();
+                const uint64_t* part =
+                    reinterpret_cast<const uint64_t*>(a.sk_part) + (size_t)c * (ACC / 2) * NT + tid;
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) {
+                        uint64_t pr[8];
+#pragma unroll
+                        for (int r = 0; r < 8; ++r)
+                            pr[r] = __hip_atomic_load(part + (size_t)((i * TM + j) * 8 + r) * NT, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                        for (int r = 0; r < 8; ++r) {
+                            acc[i][j][2 * r] += __uint_as_float((uint32_t)pr[r]);
+                            acc[i][j][2 * r + 1] += __uint_as_float((uint32_t)(pr[r] >> 32));
+                        }
+                    }
+                __syncthreads();                        // slot c has been read: re-arm its flag
+                if (tid == 0) __hip_atomic_store(a.sk_flags + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        run(kb, ke);
+        if (ke < KT) {
+            // contributor (this workgroup's last K steps): partial tile to slot g, then the flag
+            uint64_t* part = reinterpret_cast<uint64_t*>(a.sk_part) + (size_t)g * (ACC / 2) * NT + tid;
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        const uint64_t pr = (uint64_t)__float_as_uint(acc[i][j][r]) |
+                                            ((uint64_t)__float_as_uint(acc[i][j][r + 1]) << 32);
+                        __hip_atomic_store(part + (size_t)(((i * TM + j) * 16 + r) / 2) * NT, pr, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);    // one 32 x 32 tile at a time (registers)
+                }
+            __builtin_amdgcn_s_waitcnt(0);              // the partial's stores have completed
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(a.sk_flags + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            store();
+        }
+        it = t0 + kb;
+        __syncthreads();
+    }
+    }
 }
 
+// Stream-K workspace: the flag slots share the 64 KiB counter region of the skinny kernel's
+// workspace layout (zero at rest in both), then one fp32 partial tile per workgroup.
+constexpr size_t kSkFlagBytes = 64 * 1024;
+
+template <int BM, int BN, int NW>
+constexpr size_t sk_partial_bytes() {
+    constexpr int WGN = NW == 8 ? 4 : 2;
+    return (size_t)NW * 64 * ((BM / 2 / 32) * (BN / WGN / 32) * 16) * sizeof(float);
+}
+
+// sk: use the stream-K form when the workspace allows (tuning knob gemm.sk: 1 forces it, 2
+// forbids it).
 template <int BM, int BN, bool M32, int NW = 4, bool B64 = false, bool PIPE = false>
 hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s,
-                      uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi) {
+                      uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi,
+                      void* ws, size_t ws_bytes, bool sk = false) {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * kBK * sizeof(uint16_t);
     constexpr auto kernel =
-        M32 ? &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64, PIPE> : &gemm_fp8_w8a16_big_kernel<BM, BN>;
+        M32 ? &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64, PIPE, false> : &gemm_fp8_w8a16_big_kernel<BM, BN>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0, 0, epi};
+    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0, 0, epi, 0, nullptr, nullptr};
     a.tiles_m = (M + BM - 1) / BM;
     a.tiles_n = (N + BN - 1) / BN;
     const int T = a.tiles_m * a.tiles_n;
     a.per_xcd = (T + 7) / 8;
     a.vec_store = ((reinterpret_cast<uintptr_t>(y) & 7) == 0 && (ldy & 3) == 0) ? 1 : 0;
     a.vec_res = ((reinterpret_cast<uintptr_t>(epi.res) & 7) == 0 && (epi.ldres & 3) == 0) ? 1 : 0;
+    if constexpr (M32 && PIPE) {
+        constexpr auto sk_kernel = &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64, PIPE, true>;
+        static const hipError_t sk_attr = hipFuncSetAttribute(reinterpret_cast<const void*>(sk_kernel),
+                                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (sk_attr != hipSuccess) return sk_attr;
+        static const int occ = [] {
+            int o = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, reinterpret_cast<const void*>(sk_kernel), NW * 64,
+                                                             lds) != hipSuccess ||
+                o < 1)
+                o = 1;
+            return o;
+        }();
+        const int G = device_info().num_cu * occ;
+        const int knob = tuning().gemm_sk;
+        const bool fits = ws && ws_bytes >= kSkFlagBytes + (size_t)G * sk_partial_bytes<BM, BN, NW>() && G % 8 == 0 &&
+                          G * 4 <= (int)kSkFlagBytes && (int64_t)T * ((K + kBK - 1) / kBK) < ((int64_t)1 << 31);
+        if (fits && epi.kind != kEpiResidual && knob != 2 && (knob == 1 || sk)) {
+            a.sk_total = (int64_t)T * ((K + kBK - 1) / kBK);
+            a.sk_flags = static_cast<uint32_t*>(ws);
+            a.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);
+            hipLaunchKernelGGL(sk_kernel, dim3(G), dim3(NW * 64), lds, stream, a);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL(kernel, dim3(8 * a.per_xcd), dim3(M32 ? NW * 64 : 256), lds, stream, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
+size_t gemm_workspace_bytes(int M) {
+    if (M < 512 || tuning().gemm_sk != 1) return 0;
+    return kSkFlagBytes + (size_t)device_info().num_cu * sk_partial_bytes<256, 256, 8>();
+}
+
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
-                       hipStream_t stream, const Epi& epi) {
+                       hipStream_t stream, const Epi& epi, void* ws, size_t ws_bytes) {
     int tile = tuning().gemm_tile;
     if (tile < 1 || tile > 19) {
-        // Measured on MI355X (config 3): the pipelined 8-wave kernels (32 x 32 MFMA, the next
-        // tile's LDS stores between the MFMA groups); 256 x 256 tiles where there are at least
-        // 3/4 as many as CUs (up_proj 392, qkv 224), else 256 x 128 (down_proj, N = 3136: 104
-        // tiles of 256 x 256); 128 x 128 for small M.
+        // Measured on MI355X (config 3, steady state): the pipelined 8-wave kernels (32 x 32
+        // MFMA, the next tile's LDS stores between the MFMA groups); 256 x 256 tiles where there
+        // are at least 3/4 as many as CUs (up_proj 392, qkv 224), else 256 x 128 (down_proj,
+        // N = 3136: 104 tiles of 256 x 256); 128 x 128 for small M.  The stream-K form (knob
+        // gemm.sk = 1) fills the idle CUs of a partial last round but measured no faster: the GEMM
+        // runs power-limited (~1.5 GHz under load), so idle CUs cost less than they seem.
         const DeviceInfo& dev = device_info();
         const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
         if (M < 512) tile = 1;
         else tile = (4 * big >= 3 * (int64_t)dev.num_cu) ? 14 : 15;
     }
     switch (tile) {
-        case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 3: return launch_big<256, 128, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 4: return launch_big<128, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 5: return launch_big<256, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 6: return launch_big<256, 128, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 7: return launch_big<128, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 8: return launch_big<256, 256, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 9: return launch_big<256, 128, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 10: return launch_big<256, 256, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 11: return launch_big<256, 256, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 12: return launch_big<256, 128, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 13: return launch_big<256, 128, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 14: return launch_big<256, 256, true, 8, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 15: return launch_big<256, 128, true, 8, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 16: return launch_big<256, 256, true, 8, true, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 17: return launch_big<256, 128, true, 8, true, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 18: return launch_big<256, 256, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
-        case 19: return launch_big<256, 128, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
+        case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 3: return launch_big<256, 128, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 4: return launch_big<128, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 5: return launch_big<256, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 6: return launch_big<256, 128, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 7: return launch_big<128, 256, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 8: return launch_big<256, 256, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 9: return launch_big<256, 128, true, 8>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 10: return launch_big<256, 256, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 11: return launch_big<256, 256, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 12: return launch_big<256, 128, true, 8, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 13: return launch_big<256, 128, true, 4, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 14: return launch_big<256, 256, true, 8, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 15: return launch_big<256, 128, true, 8, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 16: return launch_big<256, 256, true, 8, true, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 17: return launch_big<256, 128, true, 8, true, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 18: return launch_big<256, 256, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 19: return launch_big<256, 128, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         default: {
             constexpr int BM = 128, BN = 128;
             const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);

@@ -39,6 +39,7 @@ struct Tuning {
     int s4_ks = 0;         // 4x4x4 skinny kernel: waves splitting K (1, 2, 4)
     int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
+    int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
 };
 Tuning& tuning();
 
@@ -104,9 +105,14 @@ hipError_t launch_rmsnorm(const uint16_t* x, int64_t ldx, const Norm& norm, uint
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);
 
+// Prefill GEMM.  With tuning knob gemm.sk = 1 and a workspace of at least
+// gemm_workspace_bytes(M) bytes (zero-filled before its first use; every launch leaves its flag
+// region zero again) the large-tile kernels split the K steps of all tiles evenly between the
+// CUs (stream-K); otherwise one tile per workgroup.
+size_t gemm_workspace_bytes(int M);
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
-                       hipStream_t stream, const Epi& epi = Epi{});
+                       hipStream_t stream, const Epi& epi = Epi{}, void* ws = nullptr, size_t ws_bytes = 0);
 
 hipError_t launch_decode(const uint8_t* codes, float* out_f32, float* out_scaled,
                          uint16_t* out_bf16, float scale, int n, hipStream_t stream);

@@ -119,16 +119,20 @@ def gemv_fp8(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
 
 
 def gemm_fp8_w8a16(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
-    """Prefill GEMM on bf16 MFMA for any M (ops/gemm.cuh:325-403 replacement)."""
+                   out: torch.Tensor | None = None, use_workspace: bool = True) -> torch.Tensor:
+    """Prefill GEMM on bf16 MFMA for any M (ops/gemm.cuh:325-403 replacement).  With the
+    per-device workspace the large-tile kernels may split K between workgroups (stream-K)."""
     w = _check_w(w)
     M, K = x.shape
     N = w.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    rc = _lib.lib().nmi_gemm_fp8_w8a16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
-                                       w_scale.data_ptr(), out.data_ptr(), out.stride(0), M, N, K,
-                                       None, 0, _stream())
+    L = _lib.lib()
+    ws = workspace(x.device, L.nmi_linear_workspace_bytes(M, N, K)) if use_workspace else None
+    rc = L.nmi_gemm_fp8_w8a16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                              w_scale.data_ptr(), out.data_ptr(), out.stride(0), M, N, K,
+                              None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+                              _stream())
     _lib.check(rc, "nmi_gemm_fp8_w8a16")
     return out
 

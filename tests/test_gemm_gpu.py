@@ -130,3 +130,76 @@ def test_gemm_power_of_two_linearity_and_determinism():
     y2 = ops.gemm_fp8_w8a16((xd.float() * 0.5).to(torch.bfloat16), wd, sd)
     assert torch.equal(y, y_again)
     assert torch.equal(y2.float(), y.float() * 0.5)
+
+
+@pytest.fixture
+def _sk_reset():
+    yield
+    _lib.tuning_set("gemm.sk", 0)
+    _lib.tuning_set("gemm.tile", 0)
+
+
+def _gemm_ws(M, N, K):
+    nbytes = _lib.lib().nmi_linear_workspace_bytes(max(M, 512), N, K)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+
+
+def _gemm_call(xd, wd, sd, y, ws):
+    M, K = xd.shape
+    N = wd.shape[0]
+    _lib.check(_lib.lib().nmi_gemm_fp8_w8a16(xd.data_ptr(), K, wd.data_ptr(), K, sd.data_ptr(), y.data_ptr(), N,
+                                             M, N, K, ws.data_ptr(), ws.numel(), None), "gemm with workspace")
+
+
+@pytest.mark.parametrize("tile", [14, 15])
+def test_stream_k_forced_on_small_problems(tile, _sk_reset):
+    """Stream-K forced (gemm.sk = 1) where tiles are few: each tile is cut between many
+    workgroups holding a few K steps each (and some hold none), on ragged M, N and K.  Every
+    call leaves the workspace's flag region zero (re-armed), and repeated calls are
+    bit-identical (fixed summation order)."""
+    _lib.tuning_set("gemm.tile", tile)
+    _lib.tuning_set("gemm.sk", 1)
+    for M, N, K in [(513, 777, 3136), (300, 520, 1040), (256, 256, 64), (600, 300, 12544), (17, 37, 16)]:
+        announce("stream_k_forced", tile, M, N, K)
+        x, w, s = _case(M, N, K, 7 * tile + M + N + K, scales="log_uniform")
+        xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+        ws = _gemm_ws(M, N, K)
+        y1 = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+        y2 = torch.empty_like(y1)
+        _gemm_call(xd, wd, sd, y1, ws)
+        _gemm_call(xd, wd, sd, y2, ws)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(ws[:64 * 1024]) == 0, "flag region not re-armed"
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+        assert_parity(bits(y1), oracle_bits(x, w, s), f"stream-K tile={tile} M={M} N={N} K={K}")
+
+
+def test_stream_k_large_matches_oracle_and_replays_in_a_graph(_sk_reset):
+    """M = 1536 on up_proj's shape (294 tiles of 256 x 256 for 256 CUs: two rounds, the second
+    15% full) in stream-K form.  The result matches the oracle and the data-parallel kernel
+    within the parity gate; replays of a captured graph (with eager work between them) equal
+    the eager call."""
+    M, N, K = 1536, 12544, 3136
+    announce("stream_k_large", M, N, K)
+    x, w, s = _case(M, N, K, 99)
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    y_dp = ops.gemm_fp8_w8a16(xd, wd, sd)
+    ref = oracle_bits(x, w, s)
+    assert_parity(bits(y_dp), ref, "data parallel")
+    _lib.tuning_set("gemm.sk", 1)
+    y = ops.gemm_fp8_w8a16(xd, wd, sd)
+    assert_parity(bits(y), ref, "stream-K")
+    out = torch.empty_like(y)
+    stream = torch.cuda.Stream()
+    ops.gemm_fp8_w8a16(xd, wd, sd, out=out)                 # workspace allocated before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        ops.gemm_fp8_w8a16(xd, wd, sd, out=out)
+    for rep in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), y.view(torch.int16)), rep
+        ops.gemm_fp8_w8a16(xd, wd, sd, out=y)               # eager work between replays
+        torch.cuda.synchronize()
