@@ -343,7 +343,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_big_kernel(const GemmAr
 // step s run (two fragment register sets).  Operand layouts (gfx950): A lane l holds row
 // l % 32, k 8 (l / 32) .. +7; B lane l holds column l % 32, the same k; D register r of lane l
 // is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-template <int BM, int BN, int NW, bool B64, bool PIPE, bool SK>
+// PIPE: 0 the next tile's LDS stores after the MFMAs; 1 between the MFMA groups; 2 also each
+// group's fragment reads interleaved one by one with the previous group's MFMAs; 3 as 2 with the
+// wave's issue priority raised while it issues MFMAs.
+template <int BM, int BN, int NW, bool B64, int PIPE, bool SK>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const GemmArgs a) {
     constexpr int BK = kBK;
     constexpr int NT = NW * 64;                     // threads
@@ -454,6 +457,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             for (int j = 0; j < TM; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     };
+    auto mfmas_half = [&](const bf16x8 (&af)[TN], const bf16x8 (&bfr)[TM], int h) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = h * (TM / 2); j < (h + 1) * (TM / 2); ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    };
     auto zero_acc = [&]() {
 #pragma unroll
         for (int i = 0; i < TN; ++i)
@@ -477,15 +487,49 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
             // its stores go between this tile's MFMA groups: the matrix cores keep working
             // while the x tile and the converted W tile are written.
             static_assert(BK / 16 == 4, "four k steps per tile");
-            frags(buf, 1, af1, bf1);
-            mfmas(af0, bf0);
-            frags(buf, 2, af0, bf0);
-            mfmas(af1, bf1);
-            frags(buf, 3, af1, bf1);
-            if (more) sstore_x(buf ^ 1, (kt + 1) * BK);
-            mfmas(af0, bf0);
-            if (more) sstore_w(buf ^ 1, (kt + 1) * BK);
-            mfmas(af1, bf1);
+            // fragment reads of the next k step, then the MFMAs of this one (independent)
+            auto step = [&](int s_next, bf16x8 (&afn)[TN], bf16x8 (&bfn)[TM], const bf16x8 (&af)[TN],
+                            const bf16x8 (&bfr)[TM]) {
+                frags(buf, s_next, afn, bfn);
+                if constexpr (PIPE >= 3) __builtin_amdgcn_s_setprio(1);
+                mfmas(af, bfr);
+                if constexpr (PIPE >= 3) __builtin_amdgcn_s_setprio(0);
+                if constexpr (PIPE >= 2) {
+#pragma unroll
+                    for (int q = 0; q < TN + TM; ++q) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // one LDS read
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, TN * TM - (TN + TM), 0);
+                }
+            };
+            if constexpr (PIPE >= 2) {
+                // k steps 0-2 with the reads of steps 1-3 under them; then k step 3 in two halves
+                // (m rows j < TM/2, then the rest) with the x stores before the first and the
+                // converted W stores before the second.
+                static_assert(TM % 2 == 0, "k step 3 is split along m");
+                step(1, af1, bf1, af0, bf0);
+                step(2, af0, bf0, af1, bf1);
+                step(3, af1, bf1, af0, bf0);
+                if (more) sstore_x(buf ^ 1, (kt + 1) * BK);
+                if constexpr (PIPE >= 3) __builtin_amdgcn_s_setprio(1);
+                mfmas_half(af1, bf1, 0);
+                if constexpr (PIPE >= 3) __builtin_amdgcn_s_setprio(0);
+                if (more) sstore_w(buf ^ 1, (kt + 1) * BK);
+                if constexpr (PIPE >= 3) __builtin_amdgcn_s_setprio(1);
+                mfmas_half(af1, bf1, 1);
+                if constexpr (PIPE >= 3) __builtin_amdgcn_s_setprio(0);
+            } else {
+                frags(buf, 1, af1, bf1);
+                mfmas(af0, bf0);
+                frags(buf, 2, af0, bf0);
+                mfmas(af1, bf1);
+                frags(buf, 3, af1, bf1);
+                if (more) sstore_x(buf ^ 1, (kt + 1) * BK);
+                mfmas(af0, bf0);
+                if (more) sstore_w(buf ^ 1, (kt + 1) * BK);
+                mfmas(af1, bf1);
+            }
         } else {
 #pragma unroll
             for (int s = 0; s < BK / 16; s += 2) {
@@ -674,7 +718,7 @@ constexpr size_t sk_partial_bytes() {
 
 // sk: use the stream-K form when the workspace allows (tuning knob gemm.sk: 1 forces it, 2
 // forbids it).
-template <int BM, int BN, bool M32, int NW = 4, bool B64 = false, bool PIPE = false>
+template <int BM, int BN, bool M32, int NW = 4, bool B64 = false, int PIPE = 0>
 hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s,
                       uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi,
                       void* ws, size_t ws_bytes, bool sk = false) {
@@ -691,7 +735,7 @@ hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
     a.per_xcd = (T + 7) / 8;
     a.vec_store = ((reinterpret_cast<uintptr_t>(y) & 7) == 0 && (ldy & 3) == 0) ? 1 : 0;
     a.vec_res = ((reinterpret_cast<uintptr_t>(epi.res) & 7) == 0 && (epi.ldres & 3) == 0) ? 1 : 0;
-    if constexpr (M32 && PIPE) {
+    if constexpr (M32 && PIPE != 0) {
         constexpr auto sk_kernel = &gemm_fp8_w8a16_m32_kernel<BM, BN, NW, B64, PIPE, true>;
         static const hipError_t sk_attr = hipFuncSetAttribute(reinterpret_cast<const void*>(sk_kernel),
                                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -731,9 +775,10 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
                        hipStream_t stream, const Epi& epi, void* ws, size_t ws_bytes) {
     int tile = tuning().gemm_tile;
-    if (tile < 1 || tile > 19) {
+    if (tile < 1 || tile > 23) {
         // Measured on MI355X (config 3, steady state): the pipelined 8-wave kernels (32 x 32
-        // MFMA, the next tile's LDS stores between the MFMA groups); 256 x 256 tiles where there
+        // MFMA, the next tile's LDS stores between the MFMA groups, each group's fragment reads
+        // interleaved with the previous group's MFMAs: +2% over clustered); 256 x 256 tiles where there
         // are at least 3/4 as many as CUs (up_proj 392, qkv 224), else 256 x 128 (down_proj,
         // N = 3136: 104 tiles of 256 x 256); 128 x 128 for small M.  The stream-K form (knob
         // gemm.sk = 1) fills the idle CUs of a partial last round but measured no faster: the GEMM
@@ -741,7 +786,7 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
         const DeviceInfo& dev = device_info();
         const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
         if (M < 512) tile = 1;
-        else tile = (4 * big >= 3 * (int64_t)dev.num_cu) ? 14 : 15;
+        else tile = (4 * big >= 3 * (int64_t)dev.num_cu) ? 20 : 21;
     }
     switch (tile) {
         case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
@@ -762,6 +807,10 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
         case 17: return launch_big<256, 128, true, 8, true, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         case 18: return launch_big<256, 256, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         case 19: return launch_big<256, 128, true, 4, false, true>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 20: return launch_big<256, 256, true, 8, false, 2>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 21: return launch_big<256, 128, true, 8, false, 2>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 22: return launch_big<256, 256, true, 8, false, 3>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
+        case 23: return launch_big<256, 128, true, 8, false, 3>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         default: {
             constexpr int BM = 128, BN = 128;
             const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);

@@ -95,7 +95,7 @@ def _gemm_tile_reset():
     _lib.tuning_set("gemm.tile", 0)
 
 
-@pytest.mark.parametrize("tile", list(range(1, 20)))
+@pytest.mark.parametrize("tile", list(range(1, 24)))
 def test_every_tile_variant(tile, _gemm_tile_reset):
     """Each GEMM tile variant (128x128; 256x256, 256x128, 128x256 with W as the A operand, on
     16x16x32 or 32x32x16 MFMA) on
