@@ -251,7 +251,7 @@ def bench_prefill(dev, reps=20):
         del w, s, x, y, g
     tf = tot_f / (tot_ms * 1e-3) / 1e12
     return {"workload": "config3_prefill_m2048", "tflops": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_m32_kernel (pipelined, 256x256 or 256x128 tiles)",
+            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_dma_kernel (4 waves, 256x256 tiles, DMA-fed LDS; stream-K when tiles < CUs / 2)",
             "shapes": out}
 
 
@@ -404,7 +404,8 @@ def bench_mlp_block(dev, reps=5):
     return {"workload": "mlp_forward_fp8 block (hidden 3136, inter 12544)",
             "decode_m1": {"bytes": blk_bytes, "weight_copies_rotated": R, **res},
             "prefill_m2048": {"us": round(t * 1e3, 1), "TFLOP/s": round(fl / (t * 1e-3) / 1e12, 1),
-                              "launches": 3}}
+                              "launches": 4,
+                              "steps": "rmsnorm; stream-K flag clear; up GEMM + relu^2; down GEMM (stream-K) + residual"}}
 
 
 def cpu_baseline(host, seconds):

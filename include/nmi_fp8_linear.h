@@ -78,10 +78,13 @@ int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, in
 
 /*
  * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the skinny kernel
- * (2 <= M <= 16) split K between workgroups (more parallelism for small N or long K).
+ * (2 <= M <= 16, split-K variant) split K between workgroups, and the prefill GEMM (M >= 512)
+ * split the k tiles of a few large tiles between all CUs (stream-K: fp32 partial tiles and
+ * per-workgroup flags in the workspace; used when the 256 x 256 tiles cover at most half of
+ * the CUs, e.g. N = 3136 at M = 2048).
  * workspace: 256-byte aligned, at least nmi_linear_workspace_bytes(M, N, K) bytes, zero-filled
  * before its first use; every launch leaves it ready for the next one.  NULL / too small ->
- * the kernel runs without the split (same results up to float32 summation order).  Two
+ * the kernels run without the split (same results up to float32 summation order).  Two
  * launches that may run concurrently must not share a workspace.  The reference's blocks
  * likewise hand a workspace to their prefill GEMMs (model/mlp_block.cuh:133,156,160-161).
  */
@@ -110,9 +113,10 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                                  const nmi_linear_group* groups, int ngroups, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
-/* Workspace bytes the skinny kernel can use for M rows, total_n output rows (the sum over
- * groups) and K on the current device; 0 when the selected kernel needs none (the default
- * 4x4x4 skinny kernel splits K inside the workgroup only). */
+/* Workspace bytes the kernels can use for M rows, total_n output rows (the sum over groups)
+ * and K on the current device; 0 when the selected kernel needs none (the GEMV, the default
+ * 4x4x4 skinny kernel, which splits K inside the workgroup only, and M < 512).  For M >= 512
+ * about 64 MiB: a 64 KiB flag region and one 256 x 256 fp32 partial tile per CU. */
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K);
 
 /*
@@ -120,8 +124,8 @@ size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K);
  * Replaces nemotron::ops::gemm_fp8(x_fp8, W_fp8, y_bf16, x_scale, w_scale, M, N, K, ws,
  * ws_size, stream) (nemotron_infer/csrc/include/ops/gemm.cuh:325-403) including its
  * per-row scale epilogue (gemm.cuh:227-238, 398-402), which here is fused and rounds once.
- * x is bf16 (no activation scale); `workspace`/`workspace_bytes` may be NULL/0 -- the
- * current kernels need none; the arguments are kept for the split-K variants.
+ * x is bf16 (no activation scale); `workspace`/`workspace_bytes` as for
+ * nmi_linear_fp8_w8a16_ws (NULL/0: every tile in one workgroup, no stream-K).
  */
 int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
                        const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
@@ -165,7 +169,8 @@ int nmi_rmsnorm_bf16(const void* x_bf16, const float* w, void* y_bf16, int M, in
  * RMSNorm applied while the up projection stages its activations, relu^2 and the residual add
  * in the projections' stores), larger M three (a separate RMSNorm).
  * workspace: nmi_mlp_workspace_bytes(M, hidden, inter) bytes, 16-byte aligned, no
- * initialisation needed; calls that may overlap in time need distinct workspaces.  NULL
+ * initialisation needed (from M = 512 it includes the GEMMs' stream-K region, whose flags each
+ * call zeroes with one small kernel); calls that may overlap in time need distinct workspaces.  NULL
  * takes it from the bump allocator (nmi_alloc, so a slab may be hipMalloc'd), valid until
  * nmi_alloc_rewind(), as the reference's blocks do (binding.cu:7-9).
  * Requires M >= 1, hidden and inter positive multiples of 16, input, norm_w and both weights

@@ -7,7 +7,9 @@
 // ride on the linears: relu^2 and the residual add are output epilogues of the up and down
 // projections, and where the up projection runs on the GEMV kernel (M <= 2) the RMSNorm is
 // applied while that kernel stages its activations -- two launches and one [M, inter] buffer.
-// For larger M the RMSNorm is its own launch (rmsnorm.hip) into a second buffer.
+// For larger M the RMSNorm is its own launch (rmsnorm.hip) into a second buffer, and from
+// M = 512 (the GEMM path) the workspace also holds the GEMMs' stream-K region, whose flags one
+// small kernel zeroes at the start of every call.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -34,12 +36,15 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Workspace layout: act [M, inter] bf16, then normed [M, hidden] bf16 when the RMSNorm is
-// not fused into the up projection.
+// Workspace layout: the prefill GEMM's stream-K region (M >= 512: flags, then partial tiles),
+// act [M, inter] bf16, then normed [M, hidden] bf16 when the RMSNorm is not fused into the up
+// projection.
 bool norm_fused(int M, int hidden) { return choose_path(M) == Path::Gemv && gemv_norm_supported(M, hidden); }
 
+size_t gemm_region(int M) { return choose_path(M) == Path::Gemm ? round256(gemm_workspace_bytes(M)) : 0; }
+
 size_t mlp_bytes(int M, int hidden, int inter) {
-    size_t b = round256((size_t)M * inter * 2);
+    size_t b = gemm_region(M) + round256((size_t)M * inter * 2);
     if (!norm_fused(M, hidden)) b += round256((size_t)M * hidden * 2);
     return b;
 }
@@ -97,8 +102,16 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
     hipStream_t st = static_cast<hipStream_t>(stream);
     const uint16_t* in = static_cast<const uint16_t*>(input_bf16);
     uint16_t* out = static_cast<uint16_t*>(out_bf16);
-    uint16_t* act = static_cast<uint16_t*>(workspace);
+    char* base = static_cast<char*>(workspace);
+    const size_t gws = gemm_region(M);
+    void* gemm_ws = gws ? base : nullptr;        // the GEMMs' stream-K flags and partial tiles
+    uint16_t* act = reinterpret_cast<uint16_t*>(base + gws);
     const Norm norm{norm_w, eps};
+    if (gws) {
+        // the workspace may hold anything (bump-allocated or reused): zero the flag region
+        const hipError_t ez = launch_sk_flags_clear(gemm_ws, st);
+        if (ez != hipSuccess) return hip_status(ez, fn);
+    }
 
     // up projection with relu^2: act = bf16(relu(bf16(h . up^T * s))^2)
     GemvGroup up{static_cast<const uint8_t*>(up_w_e4m3), hidden, up_scale, act, inter, inter, 0, 0,
@@ -107,16 +120,15 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
     if (norm_fused(M, hidden)) {
         e = dispatch_linear(in, hidden, M, hidden, &up, 1, nullptr, 0, st, norm);
     } else {
-        uint16_t* normed = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(workspace) +
-                                                       round256((size_t)M * inter * 2));
+        uint16_t* normed = reinterpret_cast<uint16_t*>(base + gws + round256((size_t)M * inter * 2));
         e = launch_rmsnorm(in, hidden, norm, normed, hidden, M, hidden, st);
-        if (e == hipSuccess) e = dispatch_linear(normed, hidden, M, hidden, &up, 1, nullptr, 0, st);
+        if (e == hipSuccess) e = dispatch_linear(normed, hidden, M, hidden, &up, 1, gemm_ws, gws, st);
     }
     if (e != hipSuccess) return hip_status(e, fn);
     // down projection with the residual: out = bf16(input + bf16(act . down^T * s))
     GemvGroup down{static_cast<const uint8_t*>(down_w_e4m3), inter, down_scale, out, hidden, hidden, 0, 0,
                    Epi{kEpiResidual, in, hidden}};
-    return hip_status(dispatch_linear(act, inter, M, inter, &down, 1, nullptr, 0, st), fn);
+    return hip_status(dispatch_linear(act, inter, M, inter, &down, 1, gemm_ws, gws, st), fn);
 }
 
 }  // extern "C"

@@ -16,6 +16,8 @@
 // * LDS rows are 64 bf16 (eight 16-byte chunks); chunk c of row r is stored at swz(r, c),
 //   which spreads the 16 rows an MFMA operand read touches over all banks.
 // * Epilogue: acc * s[n] in float32, one bf16 RNE rounding, masked for ragged M and N.
+#include <type_traits>
+
 #include "nmi_device.hpp"
 #include "nmi_launch.hpp"
 
@@ -706,6 +708,385 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_fp8_w8a16_m32_kernel(const Ge
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// DMA-fed 256 x 256 kernel: 4 waves (one per SIMD), each a 128 x 128 tile of 32 x 32 x 16
+// MFMAs with the 256 fp32 accumulators per lane in AGPRs.  Both operands go global -> LDS
+// with global_load_lds_dwordx4 (no register staging, no LDS store instructions): x as bf16,
+// W as the raw e4m3 codes.  W fragments are converted to bf16 after the LDS read (one
+// v_cvt_scalef32_pk_bf16_fp8 per 2 codes, one k step ahead of their MFMAs).  Three LDS stages
+// of 48 KiB (W 256 x 64 codes, x 256 x 64 bf16); the DMA of k tile t + 2 is issued while
+// tile t is multiplied, and one s_barrier per k tile publishes the next stage.
+//
+// k order inside a 64-wide k tile: the MFMA's 16-wide k step s, lane half h, element e
+// (0..7) is k = 32 (s / 2) + 16 h + 8 (s % 2) + e.  A lane's 16 consecutive W codes
+// (k = 32 j + 16 h .. + 15) then feed k steps 2 j and 2 j + 1, and its x fragment for step s is
+// the 16-byte chunk 4 (s / 2) + 2 h + s % 2 of the row: one 16-byte LDS read each.  Both
+// operands use the same order, so the sum over the tile is unchanged.
+//
+// LDS layouts (bank groups of 256 B, 16 lanes per ds_read_b128 pass): W rows are 64 B
+// (four 16-byte chunks), chunk q of row r at q ^ ((r >> 2) & 3); x rows are 128 B, chunk c
+// of row r at swz(r, c).  A fragment read (16 consecutive rows, one logical chunk) then hits
+// 16 distinct bank groups, and every DMA instruction writes 1 KiB of consecutive LDS: lane l
+// fetches the global chunk that belongs at LDS offset 16 l.
+//
+// Requirements (checked on the host): K % 64 == 0; x, W 16-byte aligned, ldx % 8 == 0,
+// ldw % 16 == 0; M * ldx * 2 and N * ldw below 2^31 (32-bit DMA offsets).
+constexpr int kDmaStage = 256 * 64 + 256 * 64 * 2;    // bytes per LDS stage
+constexpr int kDmaStages = 3;
+constexpr size_t kDmaPartialBytes = (size_t)256 * 256 * sizeof(float);   // one fp32 256 x 256 tile
+
+// 16 bytes per lane from base + off to LDS [lds_addr + 16 lane].  Inline asm so that the
+// compiler does not track the LDS write (it would wait for every outstanding DMA before any
+// LDS read); completion is waited for with an explicit vmcnt before the barrier that
+// publishes the stage.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
+                 : "memory", "m0");
+}
+
+template <bool SK>
+__global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmArgs a) {
+    constexpr int NT = 256, BK = kBK, W_STAGE = 256 * 64, TN = 4, TM = 4;
+    typedef __attribute__((address_space(3))) void lds_void;
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds_u16[];      // one name for the dynamic LDS
+    uint8_t* const lds = reinterpret_cast<uint8_t*>(lds_u16);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int M = a.M, N = a.N, K = a.K, KT = K / BK;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
+    int m0 = 0, n0 = 0;
+
+    f32x16 acc[TN][TM];
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    };
+
+    // acc += k tiles [kb, ke) of the tile at (m0, n0).  Entered and left with no DMA in flight
+    // and every wave past its last LDS read.
+    auto run = [&](int kb, int ke) {
+        // The lane-derived offsets below are recomputed per call from an opaque copy of the
+        // thread id: hoisted to kernel scope, they stayed live across the stream-K bookkeeping
+        // and were spilled, and their reloads put vmcnt waits inside the k loop.
+        int tid_r;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tid_r) : "v"(tid));
+        const int lane = tid_r & 63, h = lane >> 5, l32 = lane & 31;
+        // DMA sources, 32-bit byte offsets from the operand bases.  W instruction i of this wave:
+        // rows (4 i + wave) * 16 + lane / 4, LDS chunk lane % 4; x instruction i: rows
+        // (4 i + wave) * 8 + lane / 8, LDS chunk lane % 8.  Rows past M or N are clamped (their
+        // results are not stored).
+        uint32_t woff[4], xoff[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = (4 * i + wave) * 16 + (lane >> 2);
+            const int q = (lane & 3) ^ ((r >> 2) & 3);
+            woff[i] = (uint32_t)(min(n0 + r, N - 1) * a.ldw + 16 * q);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = (4 * i + wave) * 8 + (lane >> 3);
+            xoff[i] = (uint32_t)((min(m0 + r, M - 1) * a.ldx + 8 * swz(r, lane & 7)) * 2);
+        }
+        // LDS byte addresses of the stage being read, the next one and the one being filled
+        // (rotated every k tile)
+        uint32_t s_cur = lds0, s_nxt = lds0 + kDmaStage, s_dma = lds0 + 2 * kDmaStage;
+        // DMA part 0: the W tile; parts 1, 2: the two halves of the x tile
+        auto dma_to = [&](uint32_t base, int kt, int part, int k) {
+            if (part == 0) {
+                dma16(a.W + (int64_t)kt * BK, woff[k], base + (4 * k + wave) * 16 * 64);
+            } else {
+                const int i = 4 * (part - 1) + k;
+                dma16(reinterpret_cast<const uint8_t*>(a.x) + (int64_t)kt * BK * 2, xoff[i],
+                      base + W_STAGE + (4 * i + wave) * 8 * 128);
+            }
+        };
+        auto rd_x = [&](uint32_t sb, int s, int j) -> bf16x8 {
+            const uint8_t* base = lds + (sb - lds0) + W_STAGE;
+            const int c = 4 * (s >> 1) + 2 * h + (s & 1);
+            const int r = wm * 128 + j * 32 + l32;
+            return *reinterpret_cast<const bf16x8*>(base + r * 128 + swz(r, c) * 16);
+        };
+        auto rd_w = [&](uint32_t sb, int jp, int i) -> uint4 {
+            const uint8_t* base = lds + (sb - lds0);
+            const int r = wn * 128 + i * 32 + l32;
+            return *reinterpret_cast<const uint4*>(base + r * 64 + (((2 * jp + h) ^ ((r >> 2) & 3)) * 16));
+        };
+        // conversion c (0..15) of a W code pair set, half t: fragment c / 4, 32-bit word c % 4
+        auto cvt1 = [&](const uint4 (&wr)[4], int t, int c, u32x4 (&cf)[4]) {
+            const int i = c >> 2, e = c & 3;
+            const uint32_t w = (e >> 1) ? (t ? wr[i].w : wr[i].y) : (t ? wr[i].z : wr[i].x);
+            const bf16x2 v = (e & 1) ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true)
+                                     : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false);
+            cf[i][e] = __builtin_bit_cast(uint32_t, v);
+        };
+        auto mf = [&](const u32x4 (&cf)[4], const bf16x8 (&xf)[4], int q) {
+            const int i = q >> 2, j = q & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, cf[i]), xf[j], acc[i][j], 0, 0, 0);
+        };
+
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dma_to(s_cur, kb, p, k);
+        if (kb + 1 < ke) {
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) dma_to(s_nxt, kb + 1, p, k);
+            asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+        uint4 wr0[4], wr1[4];
+        bf16x8 xa[4], xb[4];
+        u32x4 cA[4], cB[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            wr0[i] = rd_w(s_cur, 0, i);
+            xa[i] = rd_x(s_cur, 0, i);
+        }
+#pragma unroll
+        for (int c = 0; c < 16; ++c) cvt1(wr0, 0, c, cA);
+
+        // One k tile in an explicit order: every k step is 16 groups of one MFMA plus at most
+        // one LDS read, one conversion and one DMA, fenced so that the compiler keeps them apart.
+        auto iter = [&](int kt, auto pf_tag) {
+            constexpr bool pf = decltype(pf_tag)::value;   // issue the DMA of k tile kt + 2
+            const uint32_t st = s_cur, nst = s_nxt;
+            const bool more = pf || kt + 1 < ke;
+            // k step 0: MFMAs (cA, xa); reads x step 1 -> xb, W pair 1 -> wr1; DMA part 0;
+            // cB <- wr0 half 1
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                mf(cA, xa, q);
+                if (q < 4) xb[q] = rd_x(st, 1, q);
+                else if (q < 8) wr1[q - 4] = rd_w(st, 1, q - 4);
+                if (pf && (q & 3) == 2) dma_to(s_dma, kt + 2, 0, q >> 2);
+                cvt1(wr0, 1, q, cB);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // k step 1: MFMAs (cB, xb); reads x step 2 -> xa; DMA part 1; cA <- wr1 half 0
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                mf(cB, xb, q);
+                if (q < 4) xa[q] = rd_x(st, 2, q);
+                if (pf && (q & 3) == 2) dma_to(s_dma, kt + 2, 1, q >> 2);
+                cvt1(wr1, 0, q, cA);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // k step 2: MFMAs (cA, xa); reads x step 3 -> xb; DMA part 2; cB <- wr1 half 1
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                mf(cA, xa, q);
+                if (q < 4) xb[q] = rd_x(st, 3, q);
+                if (pf && (q & 3) == 2) dma_to(s_dma, kt + 2, 2, q >> 2);
+                cvt1(wr1, 1, q, cB);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // k step 3: MFMAs (cB, xb); after two of them the barrier that publishes the next
+            // stage (this wave's DMAs for it have landed: at most the 12 of k tile kt + 2 are
+            // outstanding), then the next tile's W pair 0 and x step 0, and its step-0
+            // conversions in the second half
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                mf(cB, xb, q);
+                if (more) {
+                    if (q == 1) {
+                        if (pf) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                    }
+                    if (q >= 2 && q < 6) wr0[q - 2] = rd_w(nst, 0, q - 2);
+                    else if (q >= 6 && q < 10) xa[q - 6] = rd_x(nst, 0, q - 6);
+                    if (q >= 8) {
+                        cvt1(wr0, 0, 2 * (q - 8), cA);
+                        cvt1(wr0, 0, 2 * (q - 8) + 1, cA);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const uint32_t t = s_cur;
+            s_cur = s_nxt;
+            s_nxt = s_dma;
+            s_dma = t;
+        };
+        int kt = kb;
+        for (; kt + 2 < ke; ++kt) iter(kt, std::true_type{});
+        for (; kt < ke; ++kt) iter(kt, std::false_type{});
+        // every wave past its last LDS read before the stages are refilled
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+
+    // Epilogue: register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
+    // Residuals (clamped in bounds) are loaded before the first store in the data-parallel form;
+    // the stream-K form loads each next to its use (the 128 registers of the preload spilled the
+    // accumulators there).
+    auto store = [&]() {
+        uint2 rres[TN][4][TM];
+        if (!SK && a.epi.kind == kEpiResidual) {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) {
+                        const int n = n0 + wn * 128 + i * 32 + 8 * gq + 4 * h;
+                        const int m = min(m0 + wm * 128 + j * 32 + l32, M - 1);
+                        const int64_t row = (int64_t)m * a.epi.ldres;
+                        rres[i][gq][j] = load_res4(a.epi.res, row + min(n, N - 1), row + N - 1, a.vec_res && n + 3 < N);
+                    }
+        }
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                const int n = n0 + wn * 128 + i * 32 + 8 * gq + 4 * h;
+                float sc[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sc[r] = a.s[min(n + r, N - 1)];
+                const bool full = a.vec_store && (n + 3 < N);
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    const int m = m0 + wm * 128 + j * 32 + l32;
+                    if (m >= M) continue;
+                    uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
+                    uint2 rv = rres[i][gq][j];
+                    if (SK && a.epi.kind == kEpiResidual) {
+                        const int64_t row = (int64_t)m * a.epi.ldres;
+                        rv = load_res4(a.epi.res, row + min(n, N - 1), row + N - 1, a.vec_res && n + 3 < N);
+                    }
+                    const uint16_t b0 = epilogue(acc[i][j][4 * gq + 0], sc[0], a.epi.kind, (uint16_t)rv.x);
+                    const uint16_t b1 = epilogue(acc[i][j][4 * gq + 1], sc[1], a.epi.kind, (uint16_t)(rv.x >> 16));
+                    const uint16_t b2 = epilogue(acc[i][j][4 * gq + 2], sc[2], a.epi.kind, (uint16_t)rv.y);
+                    const uint16_t b3 = epilogue(acc[i][j][4 * gq + 3], sc[3], a.epi.kind, (uint16_t)(rv.y >> 16));
+                    if (full) {
+                        *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
+                                                              (uint32_t)b2 | ((uint32_t)b3 << 16)};
+                    } else {
+                        if (n < N) yp[0] = b0;
+                        if (n + 1 < N) yp[1] = b1;
+                        if (n + 2 < N) yp[2] = b2;
+                        if (n + 3 < N) yp[3] = b3;
+                    }
+                }
+            }
+        }
+    };
+
+    if constexpr (!SK) {
+        // One tile per workgroup, XCD-ordered: workgroup g runs on XCD g % 8, which takes the
+        // consecutive tiles [x * per_xcd, (x + 1) * per_xcd).
+        const int g = (int)blockIdx.x;
+        const int local = g >> 3;
+        const int tile = (g & 7) * a.per_xcd + local;
+        if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
+        const int tm = tile / a.tiles_n;
+        m0 = tm * 256;
+        n0 = (tile - tm * a.tiles_n) * 256;
+        zero_acc();
+        run(0, KT);
+        store();
+    } else {
+        // Stream-K as in the 8-wave kernel: per-XCD problems, each workgroup a contiguous range
+        // of (tile, k tile) steps walked backwards; the workgroup holding a tile's last k tile
+        // finishes it with the partials of the others (slot = their workgroup id, each thread's
+        // 256 floats contiguous).
+        constexpr int ACC = TN * TM * 16;
+        const int g = (int)blockIdx.x;
+        const int Gx = (int)gridDim.x >> 3;
+        const int xcd = g & 7, v = g >> 3;
+        const int T = a.tiles_m * a.tiles_n;
+        const int tb = xcd * T / 8, te = (xcd + 1) * T / 8;
+        const int total = (te - tb) * KT;
+        const int start = __builtin_amdgcn_readfirstlane((int)((int64_t)v * total / Gx));
+        const int end = __builtin_amdgcn_readfirstlane((int)((int64_t)(v + 1) * total / Gx));
+        for (int it = end; it > start;) {
+            const int tl = __builtin_amdgcn_readfirstlane((it - 1) / KT);
+            const int tile = tb + tl;
+            const int t0 = tl * KT;
+            const int kb = max(start, t0) - t0, ke = it - t0;
+            const int tm = tile / a.tiles_n;
+            m0 = tm * 256;
+            n0 = (tile - tm * a.tiles_n) * 256;
+            zero_acc();
+            run(kb, ke);
+            if (ke == KT && kb > 0) {
+                // finisher: add the partials of the local workgroups holding k tiles [0, kb), in
+                // decreasing workgroup order, to this workgroup's own sum.  Each contributor wrote
+                // that partial first (ranges are walked backwards) and this is the finisher's
+                // last segment, so the flags are normally up.  (Adding before the own k tiles
+                // forced the accumulators through scratch around the k loop.)
+                const int first = __builtin_amdgcn_readfirstlane((int)(((int64_t)(t0 + 1) * Gx - 1) / total));
+                for (int cv = v - 1; cv >= first; --cv) {
+                    if ((int64_t)cv * total / Gx == (int64_t)(cv + 1) * total / Gx) continue;   // empty range
+                    const int c = 8 * cv + xcd;
+                    if (tid == 0) {
+                        // bounded wait: the bound turns a lost flag into a wrong tile, not a hang
+                        for (int spin = 0; spin < (1 << 26); ++spin) {
+                            if (__hip_atomic_load(a.sk_flags + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u)
+                                break;
+                            __builtin_amdgcn_s_sleep(1);
+                        }
+                    }
+                    __syncthreads();
+                    // slot c: 8-byte piece p of thread t at (p * 256 + t) * 8 (2 KiB per piece)
+                    uint64_t slot_off = (uint64_t)c * kDmaPartialBytes;
+                    asm volatile("" : "+s"(slot_off));  // derived addresses computed here, not hoisted
+                    const char* slot = reinterpret_cast<const char*>(a.sk_part) + slot_off;
+#pragma unroll
+                    for (int i = 0; i < TN; ++i)
+#pragma unroll
+                        for (int j = 0; j < TM; ++j) {
+                            uint64_t pr[8];
+#pragma unroll
+                            for (int r = 0; r < 8; ++r)
+                                pr[r] = __hip_atomic_load(
+                                    reinterpret_cast<const uint64_t*>(slot + (size_t)((i * TM + j) * 8 + r) * NT * 8) + tid,
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                            for (int r = 0; r < 8; ++r) {
+                                acc[i][j][2 * r] += __uint_as_float((uint32_t)pr[r]);
+                                acc[i][j][2 * r + 1] += __uint_as_float((uint32_t)(pr[r] >> 32));
+                            }
+                        }
+                    __syncthreads();                    // slot c has been read: re-arm its flag
+                    if (tid == 0) __hip_atomic_store(a.sk_flags + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            if (ke < KT) {
+                // contributor: partial tile to slot g, then the flag
+                uint64_t slot_off = (uint64_t)g * kDmaPartialBytes;
+                asm volatile("" : "+s"(slot_off));      // derived addresses computed here, not hoisted
+                char* slot = reinterpret_cast<char*>(a.sk_part) + slot_off;
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) {
+#pragma unroll
+                        for (int r = 0; r < 16; r += 2) {
+                            const uint64_t pr = (uint64_t)__float_as_uint(acc[i][j][r]) |
+                                                ((uint64_t)__float_as_uint(acc[i][j][r + 1]) << 32);
+                            __hip_atomic_store(
+                                reinterpret_cast<uint64_t*>(slot + (size_t)((i * TM + j) * 8 + r / 2) * NT * 8) + tid, pr,
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    }
+                __builtin_amdgcn_s_waitcnt(0);          // the partial's stores have completed
+                __syncthreads();
+                if (tid == 0) __hip_atomic_store(a.sk_flags + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                store();
+            }
+            it = t0 + kb;
+        }
+    }
+}
+
 // Stream-K workspace: the flag slots share the 64 KiB counter region of the skinny kernel's
 // workspace layout (zero at rest in both), then one fp32 partial tile per workgroup.
 constexpr size_t kSkFlagBytes = 64 * 1024;
@@ -764,18 +1145,83 @@ hipError_t launch_big(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
     return hipGetLastError();
 }
 
+// Whether the DMA-fed kernel can take the operands (16-byte aligned DMA sources with 32-bit
+// offsets, whole 64-wide k tiles).
+bool dma_supported(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, int M, int N, int K) {
+    return K % kBK == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0 &&
+           ldx % 8 == 0 && ldw % 16 == 0 && (int64_t)M * ldx * 2 < ((int64_t)1 << 31) &&
+           (int64_t)N * ldw < ((int64_t)1 << 31);
+}
+
+// The DMA-fed kernel: one tile per workgroup, or stream-K over all CUs when the tiles cover at
+// most half of them and the workspace holds the flags and one partial tile per workgroup
+// (tuning knob gemm.sk: 1 forces stream-K where the workspace allows, 2 forbids it).
+// Measured on MI355X (config 3, steady state): stream-K 950 vs 792 TFLOP/s on down_proj (104
+// tiles), but 955 vs 1002 on up_proj (392 tiles) and 879 vs 1050 on qkv (224 tiles): with every
+// CU busy the clock drops (~1.85 vs ~2.3 GHz with 104 busy) and the partial tiles cost traffic,
+// so filling a partly idle last round does not pay.
+hipError_t launch_dma(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s, uint16_t* y,
+                      int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi, void* ws, size_t ws_bytes) {
+    constexpr int lds = kDmaStages * kDmaStage;
+    constexpr auto dp_kernel = &gemm_fp8_w8a16_dma_kernel<false>;
+    constexpr auto sk_kernel = &gemm_fp8_w8a16_dma_kernel<true>;
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(dp_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(sk_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    lds);
+        return e;
+    }();
+    if (attr != hipSuccess) return attr;
+    GemmArgs a{x, ldx, W, ldw, s, y, ldy, M, N, K, 0, 0, 0, 0, 0, epi, 0, nullptr, nullptr};
+    a.tiles_m = (M + 255) / 256;
+    a.tiles_n = (N + 255) / 256;
+    const int T = a.tiles_m * a.tiles_n;
+    a.per_xcd = (T + 7) / 8;
+    a.vec_store = ((reinterpret_cast<uintptr_t>(y) & 7) == 0 && (ldy & 3) == 0) ? 1 : 0;
+    a.vec_res = ((reinterpret_cast<uintptr_t>(epi.res) & 7) == 0 && (epi.ldres & 3) == 0) ? 1 : 0;
+    const int G = device_info().num_cu;             // one 144 KiB workgroup per CU
+    const bool fits = ws && ws_bytes >= kSkFlagBytes + (size_t)G * kDmaPartialBytes && G % 8 == 0 &&
+                      G * 4 <= (int)kSkFlagBytes && (int64_t)T * (K / kBK) < ((int64_t)1 << 31);
+    const int knob = tuning().gemm_sk;
+    if (fits && knob != 2 && (knob == 1 || 2 * (int64_t)T <= G)) {
+        a.sk_total = (int64_t)T * (K / kBK);
+        a.sk_flags = static_cast<uint32_t*>(ws);
+        a.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);
+        hipLaunchKernelGGL(sk_kernel, dim3(G), dim3(256), lds, stream, a);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(dp_kernel, dim3(8 * a.per_xcd), dim3(256), lds, stream, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
+namespace {
+__global__ __launch_bounds__(256) void sk_flags_clear_kernel(uint32_t* __restrict__ flags) {
+    for (int i = (int)threadIdx.x; i < (int)(kSkFlagBytes / 4); i += 256) flags[i] = 0u;
+}
+}  // namespace
+
+hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream) {
+    hipLaunchKernelGGL(sk_flags_clear_kernel, dim3(1), dim3(256), 0, stream, static_cast<uint32_t*>(ws));
+    return hipGetLastError();
+}
+
 size_t gemm_workspace_bytes(int M) {
-    if (M < 512 || tuning().gemm_sk != 1) return 0;
-    return kSkFlagBytes + (size_t)device_info().num_cu * sk_partial_bytes<256, 256, 8>();
+    if (M < 512 || tuning().gemm_sk == 2) return 0;
+    // the larger of the two stream-K forms (DMA-fed kernel; 8-wave kernels with gemm.sk = 1)
+    const size_t part = kDmaPartialBytes > sk_partial_bytes<256, 256, 8>() ? kDmaPartialBytes
+                                                                            : sk_partial_bytes<256, 256, 8>();
+    return kSkFlagBytes + (size_t)device_info().num_cu * part;
 }
 
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
                        hipStream_t stream, const Epi& epi, void* ws, size_t ws_bytes) {
     int tile = tuning().gemm_tile;
-    if (tile < 1 || tile > 23) {
+    if (tile < 1 || tile > 24) {
         // Measured on MI355X (config 3, steady state): the pipelined 8-wave kernels (32 x 32
         // MFMA, the next tile's LDS stores between the MFMA groups, each group's fragment reads
         // interleaved with the previous group's MFMAs: +2% over clustered); 256 x 256 tiles where there
@@ -786,9 +1232,12 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
         const DeviceInfo& dev = device_info();
         const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
         if (M < 512) tile = 1;
+        else if (dma_supported(x, ldx, W, ldw, M, N, K)) tile = 24;
         else tile = (4 * big >= 3 * (int64_t)dev.num_cu) ? 20 : 21;
     }
+    if (tile == 24 && !dma_supported(x, ldx, W, ldw, M, N, K)) tile = 20;
     switch (tile) {
+        case 24: return launch_dma(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         case 2: return launch_big<256, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         case 3: return launch_big<256, 128, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         case 4: return launch_big<128, 256, false>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);

@@ -105,11 +105,14 @@ hipError_t launch_rmsnorm(const uint16_t* x, int64_t ldx, const Norm& norm, uint
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);
 
-// Prefill GEMM.  With tuning knob gemm.sk = 1 and a workspace of at least
-// gemm_workspace_bytes(M) bytes (zero-filled before its first use; every launch leaves its flag
-// region zero again) the large-tile kernels split the K steps of all tiles evenly between the
-// CUs (stream-K); otherwise one tile per workgroup.
+// Prefill GEMM.  Given a workspace of at least gemm_workspace_bytes(M) bytes whose first 64 KiB
+// (the flag region) are zero -- every launch leaves them zero again -- the DMA-fed kernel splits
+// the k tiles of all tiles evenly between the CUs (stream-K) when the tiles cover at most half
+// of them (tuning knob gemm.sk = 1: always, also for the 8-wave kernels; 2: never); otherwise
+// one tile per workgroup.  launch_sk_flags_clear zeroes the flag region (one small kernel, safe
+// under graph capture).
 size_t gemm_workspace_bytes(int M);
+hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream);
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
                        hipStream_t stream, const Epi& epi = Epi{}, void* ws = nullptr, size_t ws_bytes = 0);

@@ -95,11 +95,12 @@ def _gemm_tile_reset():
     _lib.tuning_set("gemm.tile", 0)
 
 
-@pytest.mark.parametrize("tile", list(range(1, 24)))
+@pytest.mark.parametrize("tile", list(range(1, 25)))
 def test_every_tile_variant(tile, _gemm_tile_reset):
     """Each GEMM tile variant (128x128; 256x256, 256x128, 128x256 with W as the A operand, on
-    16x16x32 or 32x32x16 MFMA) on
-    ragged M and N, K not a multiple of the 64-wide K step, and strided / misaligned y."""
+    16x16x32 or 32x32x16 MFMA; 24 = the DMA-fed kernel, which hands K not a multiple of 64 to
+    the 8-wave kernel) on ragged M and N, K not a multiple of the 64-wide K step, and strided /
+    misaligned y."""
     _lib.tuning_set("gemm.tile", tile)
     for M, N, K in [(300, 520, 1040), (17, 37, 16), (513, 777, 3136), (256, 256, 64)]:
         announce("gemm_tile", tile, M, N, K)
@@ -183,11 +184,12 @@ def test_stream_k_large_matches_oracle_and_replays_in_a_graph(_sk_reset):
     announce("stream_k_large", M, N, K)
     x, w, s = _case(M, N, K, 99)
     xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    _lib.tuning_set("gemm.sk", 2)
     y_dp = ops.gemm_fp8_w8a16(xd, wd, sd)
     ref = oracle_bits(x, w, s)
     assert_parity(bits(y_dp), ref, "data parallel")
-    _lib.tuning_set("gemm.sk", 1)
-    y = ops.gemm_fp8_w8a16(xd, wd, sd)
+    _lib.tuning_set("gemm.sk", 0)
+    y = ops.gemm_fp8_w8a16(xd, wd, sd)                      # DMA kernel, stream-K form
     assert_parity(bits(y), ref, "stream-K")
     out = torch.empty_like(y)
     stream = torch.cuda.Stream()
@@ -203,3 +205,45 @@ def test_stream_k_large_matches_oracle_and_replays_in_a_graph(_sk_reset):
         assert torch.equal(out.view(torch.int16), y.view(torch.int16)), rep
         ops.gemm_fp8_w8a16(xd, wd, sd, out=y)               # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("sk", [0, 2], ids=["stream_k", "data_parallel"])
+def test_dma_kernel_forms(sk, _sk_reset):
+    """The DMA-fed 256 x 256 kernel (tile 24) in both forms on ragged M and N: one, two and three
+    64-wide k tiles (the pipeline's prologue and two-tile tail without the steady loop), few
+    tiles cut between many workgroups (stream-K: some hold no k tile at all), and long K.
+    Repeated calls are bit-identical and leave the flag region zero."""
+    _lib.tuning_set("gemm.tile", 24)
+    _lib.tuning_set("gemm.sk", sk)
+    for M, N, K in [(513, 777, 64), (700, 1000, 128), (300, 520, 192), (1030, 2100, 1024),
+                    (256, 256, 3136), (600, 300, 12544), (1, 40, 256)]:
+        announce("dma_form", sk, M, N, K)
+        x, w, s = _case(M, N, K, 11 * sk + M + N + K, scales="log_uniform")
+        xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+        ws = _gemm_ws(M, N, K)
+        y1 = torch.full((M, N), 3.0, dtype=torch.bfloat16, device=DEV)
+        y2 = torch.empty_like(y1)
+        _gemm_call(xd, wd, sd, y1, ws)
+        _gemm_call(xd, wd, sd, y2, ws)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(ws[:64 * 1024]) == 0, "flag region not re-armed"
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+        assert_parity(bits(y1), oracle_bits(x, w, s), f"dma sk={sk} M={M} N={N} K={K}")
+
+
+def test_dma_kernel_forms_agree_on_config3(_sk_reset):
+    """Stream-K and data-parallel forms of the DMA kernel on down_proj's shape (104 tiles, K =
+    12544: tiles cut between two or three workgroups) agree within the parity gate, and both
+    match the oracle."""
+    M, N, K = 2048, 3136, 12544
+    announce("dma_forms_config3", M, N, K)
+    x, w, s = _case(M, N, K, 4321, act="relu2")
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    ref = oracle_bits(x, w, s)
+    _lib.tuning_set("gemm.sk", 2)
+    y_dp = ops.gemm_fp8_w8a16(xd, wd, sd)
+    _lib.tuning_set("gemm.sk", 0)
+    y_sk = ops.gemm_fp8_w8a16(xd, wd, sd)
+    assert_parity(bits(y_dp), ref, "dma data parallel")
+    assert_parity(bits(y_sk), ref, "dma stream-K")
+    assert_parity(bits(y_sk), bits(y_dp), "stream-K vs data parallel")

@@ -74,11 +74,15 @@ def _dev(nw, upw, ups, dnw, dns):
 
 
 def _composed(x, nw, upw, ups, dnw, dns):
+    # The block hands its GEMMs (M >= 512) a workspace -- stream-K for the few tiles of the down
+    # projection -- and its smaller-M linears none; the composition does the same, so that both
+    # run the same kernels in the same form (same float32 summation order).
+    ws = x.shape[0] >= 512
     h = ops.rmsnorm_bf16(x, nw, EPS)
-    up = ops.linear_fp8_w8a16(h, upw, ups, use_workspace=False)
+    up = ops.linear_fp8_w8a16(h, upw, ups, use_workspace=ws)
     r = torch.relu(up)
     act = r * r
-    down = ops.linear_fp8_w8a16(act, dnw, dns, use_workspace=False)
+    down = ops.linear_fp8_w8a16(act, dnw, dns, use_workspace=ws)
     return x + down
 
 
