@@ -188,6 +188,9 @@ struct GemmArgs {
     int64_t sk_total;
     uint32_t* sk_flags;
     float* sk_part;
+    // DMA-fed kernel's epilogue: s 16-byte aligned; y and the residual 16-byte aligned with row
+    // strides that keep every row so (16-byte row pieces)
+    int vec_scale, vec16, vec16_res;
 };
 
 template <int BM, int BN>
@@ -922,60 +925,78 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
 
-    // Epilogue: register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
-    // Residuals (clamped in bounds) are loaded before the first store in the data-parallel form;
-    // the stream-K form loads each next to its use (the 128 registers of the preload spilled the
-    // accumulators there).
+    // Epilogue through LDS (free after the k loop): each lane rounds v = bf16(acc * s[n]) and
+    // writes it to a bf16 copy of the tile (rows of 256 padded to 520 bytes, so that the 32 rows
+    // of one 8-byte write fall in distinct banks); then every thread takes 16-byte row pieces,
+    // applies relu^2 or adds the residual (both act on the rounded v, as the separate bf16 steps
+    // do), and stores them: full 512-byte row runs per wave instead of 16-byte pieces of 32 rows.
+    // Register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
+    constexpr int PITCH = 520;                      // bytes per staged row
     auto store = [&]() {
-        uint2 rres[TN][4][TM];
-        if (!SK && a.epi.kind == kEpiResidual) {
-#pragma unroll
-            for (int i = 0; i < TN; ++i)
-#pragma unroll
-                for (int gq = 0; gq < 4; ++gq)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) {
-                        const int n = n0 + wn * 128 + i * 32 + 8 * gq + 4 * h;
-                        const int m = min(m0 + wm * 128 + j * 32 + l32, M - 1);
-                        const int64_t row = (int64_t)m * a.epi.ldres;
-                        rres[i][gq][j] = load_res4(a.epi.res, row + min(n, N - 1), row + N - 1, a.vec_res && n + 3 < N);
-                    }
-        }
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-                const int n = n0 + wn * 128 + i * 32 + 8 * gq + 4 * h;
+                const int nl = wn * 128 + i * 32 + 8 * gq + 4 * h;           // n within the tile
+                const int n = n0 + nl;
                 float sc[4];
+                if (a.vec_scale && n + 3 < N) {
+                    const float4 s4 = *reinterpret_cast<const float4*>(a.s + n);
+                    sc[0] = s4.x; sc[1] = s4.y; sc[2] = s4.z; sc[3] = s4.w;
+                } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sc[r] = a.s[min(n + r, N - 1)];
-                const bool full = a.vec_store && (n + 3 < N);
+                    for (int r = 0; r < 4; ++r) sc[r] = a.s[min(n + r, N - 1)];
+                }
 #pragma unroll
                 for (int j = 0; j < TM; ++j) {
-                    const int m = m0 + wm * 128 + j * 32 + l32;
-                    if (m >= M) continue;
-                    uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
-                    uint2 rv = rres[i][gq][j];
-                    if (SK && a.epi.kind == kEpiResidual) {
-                        const int64_t row = (int64_t)m * a.epi.ldres;
-                        rv = load_res4(a.epi.res, row + min(n, N - 1), row + N - 1, a.vec_res && n + 3 < N);
-                    }
-                    const uint16_t b0 = epilogue(acc[i][j][4 * gq + 0], sc[0], a.epi.kind, (uint16_t)rv.x);
-                    const uint16_t b1 = epilogue(acc[i][j][4 * gq + 1], sc[1], a.epi.kind, (uint16_t)(rv.x >> 16));
-                    const uint16_t b2 = epilogue(acc[i][j][4 * gq + 2], sc[2], a.epi.kind, (uint16_t)rv.y);
-                    const uint16_t b3 = epilogue(acc[i][j][4 * gq + 3], sc[3], a.epi.kind, (uint16_t)(rv.y >> 16));
-                    if (full) {
-                        *reinterpret_cast<uint2*>(yp) = uint2{(uint32_t)b0 | ((uint32_t)b1 << 16),
-                                                              (uint32_t)b2 | ((uint32_t)b3 << 16)};
-                    } else {
-                        if (n < N) yp[0] = b0;
-                        if (n + 1 < N) yp[1] = b1;
-                        if (n + 2 < N) yp[2] = b2;
-                        if (n + 3 < N) yp[3] = b3;
-                    }
+                    const int ml = wm * 128 + j * 32 + l32;
+                    const uint32_t lo = (uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 0] * sc[0]) |
+                                        ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 1] * sc[1]) << 16);
+                    const uint32_t hi = (uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 2] * sc[2]) |
+                                        ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 3] * sc[3]) << 16);
+                    *reinterpret_cast<uint2*>(lds + ml * PITCH + nl * 2) = uint2{lo, hi};
                 }
             }
         }
+        __syncthreads();
+        // 32 threads per row (16 bytes = 8 columns each), 8 rows per pass of the workgroup
+        const int c8 = (tid & 31) * 8;
+        const int n = n0 + c8;
+        const bool full = a.vec16 && n + 7 < N;
+        for (int row = tid >> 5; row < 256; row += 8) {
+            const int m = m0 + row;
+            if (m >= M) break;
+            const uint2* src = reinterpret_cast<const uint2*>(lds + row * PITCH + c8 * 2);   // 8-byte aligned
+            const uint2 v0 = src[0], v1 = src[1];
+            uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
+            uint32_t w[4] = {v0.x, v0.y, v1.x, v1.y};
+            if (a.epi.kind == kEpiRelu2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = relu2_bf16x2(w[e]);
+            } else if (a.epi.kind == kEpiResidual) {
+                const uint16_t* rp = a.epi.res + (int64_t)m * a.epi.ldres + n;
+                uint32_t rv[4];
+                if (full && a.vec16_res) {
+                    const uint4 r4 = *reinterpret_cast<const uint4*>(rp);
+                    rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        rv[e] = (n + 2 * e < N ? (uint32_t)rp[2 * e] : 0u) |
+                                ((n + 2 * e + 1 < N ? (uint32_t)rp[2 * e + 1] : 0u) << 16);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = add_bf16x2(w[e], rv[e]);
+            }
+            if (full) {
+                *reinterpret_cast<uint4*>(yp) = uint4{w[0], w[1], w[2], w[3]};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (n + e < N) yp[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+        __syncthreads();                            // the staging area is the next run's LDS
     };
 
     if constexpr (!SK) {
@@ -1181,6 +1202,9 @@ hipError_t launch_dma(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
     a.per_xcd = (T + 7) / 8;
     a.vec_store = ((reinterpret_cast<uintptr_t>(y) & 7) == 0 && (ldy & 3) == 0) ? 1 : 0;
     a.vec_res = ((reinterpret_cast<uintptr_t>(epi.res) & 7) == 0 && (epi.ldres & 3) == 0) ? 1 : 0;
+    a.vec_scale = (reinterpret_cast<uintptr_t>(s) & 15) == 0 ? 1 : 0;
+    a.vec16 = ((reinterpret_cast<uintptr_t>(y) & 15) == 0 && (ldy & 7) == 0) ? 1 : 0;
+    a.vec16_res = ((reinterpret_cast<uintptr_t>(epi.res) & 15) == 0 && (epi.ldres & 7) == 0) ? 1 : 0;
     const int G = device_info().num_cu;             // one 144 KiB workgroup per CU
     const bool fits = ws && ws_bytes >= kSkFlagBytes + (size_t)G * kDmaPartialBytes && G % 8 == 0 &&
                       G * 4 <= (int)kSkFlagBytes && (int64_t)T * (K / kBK) < ((int64_t)1 << 31);
