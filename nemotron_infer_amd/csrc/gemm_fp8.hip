@@ -762,7 +762,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
     int m0 = 0, n0 = 0;
 
     f32x16 acc[TN][TM];
-    auto zero_acc = [&]() {
+    auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -773,7 +773,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
 
     // acc += k tiles [kb, ke) of the tile at (m0, n0).  Entered and left with no DMA in flight
     // and every wave past its last LDS read.
-    auto run = [&](int kb, int ke) {
+    auto run = [&](int kb, int ke) __attribute__((always_inline)) {
         // The lane-derived offsets below are recomputed per call from an opaque copy of the
         // thread id: hoisted to kernel scope, they stayed live across the stream-K bookkeeping
         // and were spilled, and their reloads put vmcnt waits inside the k loop.
@@ -932,68 +932,104 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
     // do), and stores them: full 512-byte row runs per wave instead of 16-byte pieces of 32 rows.
     // Register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
     constexpr int PITCH = 520;                      // bytes per staged row
-    auto store = [&]() {
+    auto store = [&]() __attribute__((always_inline)) {
+        // tiles wholly inside N take the branch-free path (one uniform test)
+        const bool inner = n0 + 256 <= N;
+        // the lane's 64 scales: one batch of loads (data-parallel form), or one batch per
+        // 32-column block i (stream-K form, which has fewer registers to spare)
+        constexpr int SB = SK ? 1 : TN;
+        auto load_scales = [&](int i0, float (&sc)[SB][4][4]) {
+            if (inner && a.vec_scale) {
+#pragma unroll
+                for (int i = 0; i < SB; ++i)
+#pragma unroll
+                    for (int gq = 0; gq < 4; ++gq) {
+                        const float4 s4 =
+                            *reinterpret_cast<const float4*>(a.s + n0 + wn * 128 + (i0 + i) * 32 + 8 * gq + 4 * h);
+                        sc[i][gq][0] = s4.x; sc[i][gq][1] = s4.y; sc[i][gq][2] = s4.z; sc[i][gq][3] = s4.w;
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < SB; ++i)
+#pragma unroll
+                    for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            sc[i][gq][r] = a.s[min(n0 + wn * 128 + (i0 + i) * 32 + 8 * gq + 4 * h + r, N - 1)];
+            }
+        };
+        float sc[SB][4][4];
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
+            if (i % SB == 0) load_scales(i, sc);
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
                 const int nl = wn * 128 + i * 32 + 8 * gq + 4 * h;           // n within the tile
-                const int n = n0 + nl;
-                float sc[4];
-                if (a.vec_scale && n + 3 < N) {
-                    const float4 s4 = *reinterpret_cast<const float4*>(a.s + n);
-                    sc[0] = s4.x; sc[1] = s4.y; sc[2] = s4.z; sc[3] = s4.w;
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) sc[r] = a.s[min(n + r, N - 1)];
-                }
+                const float* sg = sc[i % SB][gq];
 #pragma unroll
                 for (int j = 0; j < TM; ++j) {
                     const int ml = wm * 128 + j * 32 + l32;
-                    const uint32_t lo = (uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 0] * sc[0]) |
-                                        ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 1] * sc[1]) << 16);
-                    const uint32_t hi = (uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 2] * sc[2]) |
-                                        ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * gq + 3] * sc[3]) << 16);
+                    const uint32_t lo = pack_bf16(acc[i][j][4 * gq + 0] * sg[0], acc[i][j][4 * gq + 1] * sg[1]);
+                    const uint32_t hi = pack_bf16(acc[i][j][4 * gq + 2] * sg[2], acc[i][j][4 * gq + 3] * sg[3]);
                     *reinterpret_cast<uint2*>(lds + ml * PITCH + nl * 2) = uint2{lo, hi};
                 }
             }
         }
         __syncthreads();
-        // 32 threads per row (16 bytes = 8 columns each), 8 rows per pass of the workgroup
+        // 32 threads per row (16 bytes = 8 columns each), 8 rows per pass of the workgroup,
+        // eight passes per batch: the batch's LDS reads are issued before its stores
         const int c8 = (tid & 31) * 8;
         const int n = n0 + c8;
-        const bool full = a.vec16 && n + 7 < N;
-        for (int row = tid >> 5; row < 256; row += 8) {
-            const int m = m0 + row;
-            if (m >= M) break;
-            const uint2* src = reinterpret_cast<const uint2*>(lds + row * PITCH + c8 * 2);   // 8-byte aligned
-            const uint2 v0 = src[0], v1 = src[1];
-            uint16_t* yp = a.y + (int64_t)m * a.ldy + n;
-            uint32_t w[4] = {v0.x, v0.y, v1.x, v1.y};
-            if (a.epi.kind == kEpiRelu2) {
+        const int rows = min(256, M - m0);
+        const bool full = a.vec16 && (inner || n + 7 < N);
+        const bool res16 = a.epi.kind == kEpiResidual && full && a.vec16_res;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = relu2_bf16x2(w[e]);
-            } else if (a.epi.kind == kEpiResidual) {
-                const uint16_t* rp = a.epi.res + (int64_t)m * a.epi.ldres + n;
-                uint32_t rv[4];
-                if (full && a.vec16_res) {
-                    const uint4 r4 = *reinterpret_cast<const uint4*>(rp);
-                    rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
+        for (int batch = 0; batch < 4; ++batch) {
+            uint32_t w[8][4];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const int row = (tid >> 5) + 8 * (8 * batch + p);
+                const uint2* src = reinterpret_cast<const uint2*>(lds + row * PITCH + c8 * 2);   // 8-byte aligned
+                const uint2 v0 = src[0], v1 = src[1];
+                w[p][0] = v0.x; w[p][1] = v0.y; w[p][2] = v1.x; w[p][3] = v1.y;
+            }
+            if (a.epi.kind == kEpiResidual) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    const int row = (tid >> 5) + 8 * (8 * batch + p);
+                    if (row >= rows) continue;
+                    const uint16_t* rp = a.epi.res + (int64_t)(m0 + row) * a.epi.ldres + n;
+                    uint32_t rv[4];
+                    if (res16) {
+                        const uint4 r4 = *reinterpret_cast<const uint4*>(rp);
+                        rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            rv[e] = (n + 2 * e < N ? (uint32_t)rp[2 * e] : 0u) |
+                                    ((n + 2 * e + 1 < N ? (uint32_t)rp[2 * e + 1] : 0u) << 16);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[p][e] = add_bf16x2(w[p][e], rv[e]);
+                }
+            } else if (a.epi.kind == kEpiRelu2) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[p][e] = relu2_bf16x2(w[p][e]);
+            }
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const int row = (tid >> 5) + 8 * (8 * batch + p);
+                if (row >= rows) continue;
+                uint16_t* yp = a.y + (int64_t)(m0 + row) * a.ldy + n;
+                if (full) {
+                    *reinterpret_cast<uint4*>(yp) = uint4{w[p][0], w[p][1], w[p][2], w[p][3]};
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        rv[e] = (n + 2 * e < N ? (uint32_t)rp[2 * e] : 0u) |
-                                ((n + 2 * e + 1 < N ? (uint32_t)rp[2 * e + 1] : 0u) << 16);
+                    for (int e = 0; e < 8; ++e)
+                        if (n + e < N) yp[e] = (uint16_t)(w[p][e >> 1] >> (16 * (e & 1)));
                 }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = add_bf16x2(w[e], rv[e]);
-            }
-            if (full) {
-                *reinterpret_cast<uint4*>(yp) = uint4{w[0], w[1], w[2], w[3]};
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (n + e < N) yp[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
             }
         }
         __syncthreads();                            // the staging area is the next run's LDS
@@ -1015,14 +1051,26 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
     } else {
         // Stream-K as in the 8-wave kernel: per-XCD problems, each workgroup a contiguous range
         // of (tile, k tile) steps walked backwards; the workgroup holding a tile's last k tile
-        // finishes it with the partials of the others (slot = their workgroup id, each thread's
-        // 256 floats contiguous).
+        // finishes it with the partials of the others (slot = their workgroup id).
         constexpr int ACC = TN * TM * 16;
         const int g = (int)blockIdx.x;
         const int Gx = (int)gridDim.x >> 3;
         const int xcd = g & 7, v = g >> 3;
         const int T = a.tiles_m * a.tiles_n;
-        const int tb = xcd * T / 8, te = (xcd + 1) * T / 8;
+        const int xb = xcd * T / 8, te = (xcd + 1) * T / 8;
+        // The XCD's full rounds of tiles go one per workgroup, as in the data-parallel form;
+        // only the tiles of its last, partly filled round are split (stream-K over [tb, te)).
+        const int rounds = (te - xb) / Gx;
+        for (int r = 0; r < rounds; ++r) {
+            const int tile = xb + r * Gx + v;
+            const int tm = tile / a.tiles_n;
+            m0 = tm * 256;
+            n0 = (tile - tm * a.tiles_n) * 256;
+            zero_acc();
+            run(0, KT);
+            store();
+        }
+        const int tb = xb + rounds * Gx;
         const int total = (te - tb) * KT;
         const int start = __builtin_amdgcn_readfirstlane((int)((int64_t)v * total / Gx));
         const int end = __builtin_amdgcn_readfirstlane((int)((int64_t)(v + 1) * total / Gx));

@@ -78,20 +78,6 @@ __device__ __forceinline__ uint16_t epilogue(float acc, float s, int epi, uint16
     return v;
 }
 
-// epilogue()'s relu^2 and residual steps on two packed bf16 (low half first) that are already
-// the rounded linear outputs v.
-__device__ __forceinline__ uint32_t relu2_bf16x2(uint32_t w) {
-    float lo = bf16_to_f32((uint16_t)w), hi = bf16_to_f32((uint16_t)(w >> 16));
-    lo = lo < 0.f ? 0.f : lo;
-    hi = hi < 0.f ? 0.f : hi;
-    return (uint32_t)f32_to_bf16_rne(lo * lo) | ((uint32_t)f32_to_bf16_rne(hi * hi) << 16);
-}
-__device__ __forceinline__ uint32_t add_bf16x2(uint32_t v, uint32_t res) {
-    const float lo = bf16_to_f32((uint16_t)res) + bf16_to_f32((uint16_t)v);
-    const float hi = bf16_to_f32((uint16_t)(res >> 16)) + bf16_to_f32((uint16_t)(v >> 16));
-    return (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
-}
-
 // Residual elements off .. off + 3 of one row (clamped to its last element `last`), packed as
 // four bf16; one 8-byte load when `vec` (then all four are in bounds and 8-byte aligned).
 __device__ __forceinline__ uint2 load_res4(const uint16_t* res, int64_t off, int64_t last, bool vec) {
@@ -114,8 +100,21 @@ __device__ __forceinline__ float sumsq8(const uint4 v, float acc) {
     return acc;
 }
 
+// Two f32 -> two bf16 (lo in the low half), round to nearest even: one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    return (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
+// epilogue()'s relu^2 and residual steps on two packed bf16 (low half first) that are already
+// the rounded linear outputs v.
+__device__ __forceinline__ uint32_t relu2_bf16x2(uint32_t w) {
+    float lo = bf16lo_to_f32(w), hi = bf16hi_to_f32(w);
+    lo = lo < 0.f ? 0.f : lo;
+    hi = hi < 0.f ? 0.f : hi;
+    return pack_bf16(lo * lo, hi * hi);
+}
+__device__ __forceinline__ uint32_t add_bf16x2(uint32_t v, uint32_t res) {
+    return pack_bf16(bf16lo_to_f32(res) + bf16lo_to_f32(v), bf16hi_to_f32(res) + bf16hi_to_f32(v));
 }
 
 __device__ __forceinline__ uint4 rms_scale8(const uint4 v, const float4 g0, const float4 g1, float r) {
