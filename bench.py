@@ -2,6 +2,7 @@
 """bench.py -- fp8 (e4m3) W8A16 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--no-extras]
+                    [--only prefill|block]
 
 Headline (``value``): BASELINE config 1, the decode-step GEMV set of one attention block and
 one MLP block at M = 1 (q 3136->5120, k/v 3136->1024, o 5120->3136, up 3136->12544,
@@ -60,6 +61,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
+    p.add_argument("--only", choices=["prefill", "block"],
+                   help="run one extra leg alone and print its JSON record (for profiling that leg); "
+                        "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
                    help="first copy 256 MiB device-to-device three times (a kernel of known traffic "
                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -469,6 +473,10 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         del a, b
+    if args.only:
+        leg = bench_prefill(dev) if args.only == "prefill" else bench_mlp_block(dev)
+        print(json.dumps(leg), flush=True)
+        return
     host = decode_inputs()
     log("decode set (config 1) ...")
     d = bench_decode_set(args, dev, host)

@@ -16,6 +16,7 @@
 // * LDS rows are 64 bf16 (eight 16-byte chunks); chunk c of row r is stored at swz(r, c),
 //   which spreads the 16 rows an MFMA operand read touches over all banks.
 // * Epilogue: acc * s[n] in float32, one bf16 RNE rounding, masked for ragged M and N.
+#include <algorithm>
 #include <type_traits>
 
 #include "nmi_device.hpp"
@@ -1271,13 +1272,16 @@ hipError_t launch_dma(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
 }  // namespace
 
 namespace {
-__global__ __launch_bounds__(256) void sk_flags_clear_kernel(uint32_t* __restrict__ flags) {
-    for (int i = (int)threadIdx.x; i < (int)(kSkFlagBytes / 4); i += 256) flags[i] = 0u;
+__global__ __launch_bounds__(256) void sk_flags_clear_kernel(uint32_t* __restrict__ flags, int n) {
+    for (int i = (int)threadIdx.x; i < n; i += 256) flags[i] = 0u;
 }
 }  // namespace
 
+// Zeroes the flags the stream-K forms use: one per workgroup of their grid (num_cu x the
+// kernel's occupancy, at most 4 for any of them), not the whole 64 KiB region.
 hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream) {
-    hipLaunchKernelGGL(sk_flags_clear_kernel, dim3(1), dim3(256), 0, stream, static_cast<uint32_t*>(ws));
+    const int n = (int)std::min<size_t>((size_t)4 * device_info().num_cu, kSkFlagBytes / 4);
+    hipLaunchKernelGGL(sk_flags_clear_kernel, dim3(1), dim3(256), 0, stream, static_cast<uint32_t*>(ws), n);
     return hipGetLastError();
 }
 
