@@ -6,21 +6,27 @@
 
 Headline (``value``): BASELINE config 1, the decode-step GEMV set of one attention block and
 one MLP block at M = 1 (q 3136->5120, k/v 3136->1024, o 5120->3136, up 3136->12544,
-down 12544->3136).  A step is launched as the engine's blocks would launch it: q|k|v in one
-grouped launch (they share the block's normed input, as model/attention_block.cuh:400-402
-runs them on one input), then o, up and down -- four launches, replayed from a HIP graph.
-A step's algorithmic bytes are sum(N*K + 4N + 2K + 2N) over the six matrices =
-117,427,456 B.  Weights rotate over ten copies (1.17 GB > the 256 MB Infinity Cache + L2),
-so every step streams W from HBM.  ``value`` = bytes per step / time per step (GB/s).
+down 12544->3136), each GEMV on its own seeded activation as config 1 defines them.  A step is
+one GEMV chain launch (nmi_gemv_chain): phases q|k|v (grouped: they share one input, as
+model/attention_block.cuh:400-402 runs them), o, up, down, replayed from a HIP graph.  A step's
+algorithmic bytes are sum(N*K + 4N + 2K + 2N) over the six matrices = 117,427,456 B.  Weights
+rotate over ten copies (1.17 GB > the 256 MB Infinity Cache + L2), so every step streams W
+from HBM.  ``value`` = bytes per step / time per step (GB/s).
 
-``roofline`` -- the M = 1 GEMV kernel (every launch of the step is one): algorithmic bytes per
-launch over the average launch duration, both from the timed region (graph replay, HIP events
-on the replay stream); HBM-bound, peak 8 TB/s.  ``launches`` gives each launch's own duration
-(a graph of that launch alone over the rotated copies) for comparison with rocprofv3.
+Reported beside it on the same line: ``engine_four_launches`` (q|k|v grouped, o, up, down as
+four GEMV launches, the launch structure of the engine's blocks, where attention and the MLP's
+relu^2 separate the GEMVs), ``launches`` (each of those launches alone), ``six_separate_launches``
+(the reference's launch structure) and ``chain_dependent`` (one chain launch in which o reads
+q's output, up o's and down up's, each phase waiting for the previous one).
+
+``roofline`` -- the chain kernel (one launch per step): algorithmic bytes per launch over the
+launch duration, both from the timed region (graph replay, HIP events on the replay stream);
+HBM-bound, peak 8 TB/s.
 
 Also reported (same line): ``prefill_gemm`` (config 3, M = 2048, TFLOP/s against 2.5 PFLOP/s
 dense bf16 MFMA; steady state: timed after 0.3 s of untimed replays), ``skinny`` (config 2, M in {2,4,8,16}, same four launches per step),
-``decode_stream`` (config 4, the 42-layer weight stream, 84 launches), ``mlp_block`` (the fp8
+``decode_stream`` (config 4, the 42-layer weight stream: one 84-phase chain launch, and as 84
+launches), ``mlp_block`` (the fp8
 MLP block, decode and prefill, fused against the reference's five-launch structure) and
 ``cpu_baseline``:
 the torch CPU reference path (fp32 dequant then F.linear, oracle/linear.py) on a bounded
@@ -44,9 +50,10 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 ROTATION_BYTES = 1 << 30
 # HBM bytes per launch of the config-1 step, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
-# script (scaled by a 256 MiB copy; profiles/gemv_m1_config1_decode_set.md).  Re-measured when the
-# GEMV kernels change; reported as roofline.traffic next to the algorithmic bytes.
-MEASURED_TRAFFIC = {"qkv_grouped": 22724078, "o_proj": 16323558, "up_proj": 39597227,
+# script (scaled by a 256 MiB copy): the chain launch (profiles/gemv_chain_config1_decode_set.md)
+# and the four engine-structured launches (profiles/gemv_m1_config1_decode_set.md).  Re-measured
+# when the GEMV kernels change; reported as roofline.traffic next to the algorithmic bytes.
+MEASURED_TRAFFIC = {"chain": 118419347, "qkv_grouped": 22724078, "o_proj": 16323558, "up_proj": 39597227,
                     "down_proj": 39766161}
 
 
@@ -150,6 +157,20 @@ def step_buffers(dev, M, K_attn=3136):
             torch.empty((M, L[5].N), dtype=torch.bfloat16, device=dev))
 
 
+def make_chain(ops, xs, mats, ys, dependent=False):
+    """The step as one GEMV chain launch: phases q|k|v, o, up, down.  dependent: each phase reads
+    the previous phase's output (q -> o -> up -> down chain by shape: 5120, 3136, 12544) and
+    waits for it; otherwise every phase reads its own config-1 activation."""
+    (wq, sq), (wk, sk), (wv, sv), (wo, so), (wu, su), (wd, sd) = mats
+    x_attn, x_o, x_up, x_down = xs
+    y_qkv, y_o, y_up, y_down = ys
+    if dependent:
+        x_o, x_up, x_down = y_qkv[0], y_o, y_up
+    return ops.GemvChain([(x_attn, [(wq, sq, y_qkv[0]), (wk, sk, y_qkv[1]), (wv, sv, y_qkv[2])], False),
+                          (x_o, [(wo, so, y_o)], dependent), (x_up, [(wu, su, y_up)], dependent),
+                          (x_down, [(wd, sd, y_down)], dependent)])
+
+
 def bench_decode_set(args, dev, host):
     import torch
 
@@ -160,23 +181,33 @@ def bench_decode_set(args, dev, host):
     copies = rotated(dev, [(w, s) for _, _, w, s in host], R)
     xs = (host[0][1].to(dev), host[3][1].to(dev), host[4][1].to(dev), host[5][1].to(dev))
     ys = step_buffers(dev, 1)
-    steps = [make_step(ops, xs, copies[r], ys) for r in range(R)]
+    chains = [make_chain(ops, xs, copies[r], ys) for r in range(R)]
     step_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l in synth.DECODE_SET)
 
     for i in range(max(args.warmup, R)):          # eager warm-up, also before any capture
-        steps[i % R]()
+        chains[i % R].launch()
     torch.cuda.synchronize()
     T = Timer()
-    g_all = T.capture(lambda: [s() for s in steps])
+    g_all = T.capture(lambda: [c.launch() for c in chains])
     tail = args.steps % R
-    g_tail = T.capture(lambda: [steps[r]() for r in range(tail)]) if tail else None
+    g_tail = T.capture(lambda: [chains[r].launch() for r in range(tail)]) if tail else None
     T.time_replays([g_all] * max(1, args.warmup // R))
     graphs = [g_all] * (args.steps // R) + ([g_tail] if g_tail is not None else [])
     ms = T.time_replays(graphs)
     ms_per_step = ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Each launch of the step alone: a graph of that launch over the R copies.
+    def timed(fn, reps=5):
+        g = T.capture(lambda: [fn(r) for r in range(R)])
+        T.time_replays([g])
+        t = T.time_replays([g] * reps) / (reps * R)
+        del g
+        return {"us_per_step": round(t * 1e3, 2), "GB/s": round(step_bytes / (t * 1e-3) / 1e9, 1)}
+
+    # The engine's launch structure: q|k|v grouped, o, up, down (four launches).
+    steps = [make_step(ops, xs, copies[r], ys) for r in range(R)]
+    engine = {"launches": 4, **timed(lambda r: steps[r]())}
+    # Each of those launches alone: a graph of that launch over the R copies.
     L = synth.DECODE_SET
     launches = {}
     groups = [("qkv_grouped", [0, 1, 2]), ("o_proj", [3]), ("up_proj", [4]), ("down_proj", [5])]
@@ -193,31 +224,35 @@ def bench_decode_set(args, dev, host):
         b = sum(synth.linear_bytes(1, L[i].N, L[i].K) for i in idx)
         launches[name] = {"N": sum(L[i].N for i in idx), "K": L[idx[0]].K, "bytes": b,
                           "us": round(t * 1e3, 2), "GB/s": round(b / (t * 1e-3) / 1e9, 1)}
+        del g
+
     # The six matrices as six separate launches (the reference's launch structure).
     def six(r):
         for i, l in enumerate(L):
             xi = xs[0] if i < 3 else xs[{3: 1, 4: 2, 5: 3}[i]]
             yi = ys[0][i] if i < 3 else ys[{3: 1, 4: 2, 5: 3}[i]]
             ops.linear_fp8_w8a16(xi, *copies[r][i], out=yi)
-    g6 = T.capture(lambda: [six(r) for r in range(R)])
-    T.time_replays([g6])
-    t6 = T.time_replays([g6] * 5) / (5 * R)
-    separate = {"launches": 6, "us_per_step": round(t6 * 1e3, 2),
-                "GB/s": round(step_bytes / (t6 * 1e-3) / 1e9, 1)}
+    separate = {"launches": 6, **timed(six)}
+    # The dependent chain: each phase waits for and reads the previous phase's output.
+    dep = [make_chain(ops, xs, copies[r], ys, dependent=True) for r in range(R)]
+    for c in dep:
+        c.launch()
+    torch.cuda.synchronize()
+    dependent = {"launches": 1, **timed(lambda r: dep[r].launch())}
 
-    n_launch = len(groups)
-    traffic = sum(MEASURED_TRAFFIC.values()) // len(MEASURED_TRAFFIC)
+    traffic = MEASURED_TRAFFIC.get("chain")
     roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per launch (x2.0 / x1.0 copy "
-                                  "calibration), profiles/gemv_m1_config1_decode_set.md",
-                "kernel": "gemv_fp8_m1_kernel (every launch of the step)",
-                "launches_per_step": n_launch,
-                "per_launch_bytes_avg": step_bytes // n_launch,
-                "per_launch_us_avg": round(ms_per_step * 1e3 / n_launch, 3)}
-    del copies, steps, g_all, g_tail, g6
+                                  "calibration), profiles/gemv_chain_config1_decode_set.md",
+                "kernel": "gemv_chain_kernel (one launch per step)",
+                "launches_per_step": 1,
+                "per_launch_bytes_avg": step_bytes,
+                "per_launch_us_avg": round(ms_per_step * 1e3, 3)}
+    del copies, chains, steps, dep, g_all, g_tail
     return dict(value=value, ms_per_step=ms_per_step, step_bytes=step_bytes, copies=R,
-                roofline=roofline, launches=launches, separate=separate)
+                roofline=roofline, launches=launches, engine=engine, separate=separate,
+                dependent=dependent)
 
 
 def steady(T, graph, seconds=0.3):
@@ -328,20 +363,38 @@ def bench_decode_stream(dev, reps=5):
                 lin, w, s, y = c[1]
                 ops.linear_fp8_w8a16(act(lin.K, lin.act), w, s, out=y)
 
+    # The same GEMVs as one chain launch (a phase per launch above, each on its own activation).
+    phases = []
+    for c in calls:
+        if c[0] == "grouped":
+            phases.append((act(c[1], "normal"), [(w, s, y) for (w, s), y in zip(c[2], c[3])], False))
+        else:
+            lin, w, s, y = c[1]
+            phases.append((act(lin.K, lin.act), [(w, s, y)], False))
+    chain = ops.GemvChain(phases)
+
     run()
+    chain.launch()
     torch.cuda.synchronize()
     T = Timer()
-    g = T.capture(run)
-    T.time_replays([g])
-    ms = T.time_replays([g] * reps) / reps
-    gbs = total_bytes / (ms * 1e-3) / 1e9
+
+    def timed(fn):
+        g = T.capture(fn)
+        T.time_replays([g])
+        ms = T.time_replays([g] * reps) / reps
+        del g
+        gbs = total_bytes / (ms * 1e-3) / 1e9
+        return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "tok_per_s_ceiling": round(1e3 / ms, 1)}
+
+    one = timed(chain.launch)
+    sep = timed(run)
     n_gemv = sum(len(l[2]) for l in layers)
     n_launch = len(calls)
-    del calls, g
-    return {"workload": "config4_42layer_decode_stream", "gemvs": n_gemv, "launches": n_launch,
-            "bytes": total_bytes, "weight_bytes": weight_bytes, "ms": round(ms, 4),
-            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "tok_per_s_ceiling": round(1e3 / ms, 1)}
+    del calls, chain, phases
+    return {"workload": "config4_42layer_decode_stream", "gemvs": n_gemv, "bytes": total_bytes,
+            "weight_bytes": weight_bytes, "launch": f"one GEMV chain launch of {n_launch} phases", **one,
+            "separate_launches": {"launches": n_launch, **sep}}
 
 
 def bench_mlp_block(dev, reps=5):
@@ -516,11 +569,14 @@ def main():
                    "weight_copies_rotated": d["copies"],
                    "operands": "W e4m3 [N,K] (converted exactly to bf16) + f32 per-row scale, x bf16, "
                                "f32 accumulation, y bf16",
-                   "launch": "HIP graph; per step: q|k|v grouped, o, up, down (4 launches)"},
+                   "launch": "HIP graph; per step one GEMV chain launch: phases q|k|v grouped, o, up, "
+                             "down, each on its own config-1 activation"},
         "roofline": d["roofline"],
         "cpu_baseline": cpu,
+        "engine_four_launches": d["engine"],
         "launches": d["launches"],
         "six_separate_launches": d["separate"],
+        "chain_dependent": d["dependent"],
         **extras,
         "wall_s": round(time.time() - t0, 1),
     }

@@ -113,6 +113,47 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                                  const nmi_linear_group* groups, int ngroups, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/*
+ * GEMV chain (M = 1): a sequence of GEMVs in one launch.  A chain is a list of phases, each a
+ * grouped GEMV of one activation vector x [K] (bf16) against up to NMI_MAX_GROUPS e4m3
+ * matrices, computed as nmi_linear_fp8_w8a16_grouped computes it (same per-row results up to
+ * float32 summation order).  A phase with wait_prev = 1 reads its x only after the previous
+ * phase has completed, so x may be that phase's output: the order of dependent launches on one
+ * stream, with the weight loads of the waiting phase issued while the previous one drains.
+ * Phases with wait_prev = 0 (x ready before the launch) stream back to back with no launch
+ * boundary between them.  Replaces a sequence of per-projection gemv_fp8 launches
+ * (ops/gemv.cuh:92-104 at model/attention_block.cuh:400-402,409, model/mlp_block.cuh:142-148,
+ * model/mamba_block.cuh:476-481,508-509); the reference has no chained form.
+ *   nmi_gemv_chain_create   validates the phases as nmi_linear_fp8_w8a16_grouped would (M = 1),
+ *                           plans the work split and the grid for the current device and copies
+ *                           the plan to device memory (hipMalloc + hipMemcpy: call it outside
+ *                           graph capture, once per set of pointers).
+ *   nmi_gemv_chain_launch   one kernel launch; workspace: 256-byte aligned, at least
+ *                           nmi_gemv_chain_workspace_bytes(nphases) bytes, zero-filled before its
+ *                           first use (every launch leaves it zero again).  Launches that may
+ *                           overlap in time need distinct workspaces.  Capturable in a HIP graph.
+ *   nmi_gemv_chain_destroy  frees the plan.
+ * The launch is a persistent grid of at most the workgroups that are resident at once, whose
+ * workgroups wait on each other's phases: run it with no other long-running kernel sharing the
+ * device (another chain on a concurrent stream may hold the slots a waiting phase needs).  A
+ * wait never hangs: after 0.2 s it gives up, the outputs are invalid and the 32-bit word at
+ * byte offset nmi_gemv_chain_workspace_bytes(nphases) - 128 is set non-zero (and stays so until
+ * the caller clears it).
+ */
+#define NMI_MAX_CHAIN_PHASES 4096
+typedef struct nmi_gemv_phase {
+    const void* x_bf16;   /* [K] bf16 */
+    int K;
+    int ngroups;
+    int wait_prev;        /* 1: read x only after the previous phase has completed */
+    nmi_linear_group groups[NMI_MAX_GROUPS];
+} nmi_gemv_phase;
+typedef struct nmi_gemv_chain nmi_gemv_chain;
+int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_chain** out);
+size_t nmi_gemv_chain_workspace_bytes(int nphases);
+int nmi_gemv_chain_launch(const nmi_gemv_chain* chain, void* workspace, size_t workspace_bytes, void* stream);
+int nmi_gemv_chain_destroy(nmi_gemv_chain* chain);
+
 /* Workspace bytes the kernels can use for M rows, total_n output rows (the sum over groups)
  * and K on the current device; 0 when the selected kernel needs none (the GEMV, the default
  * 4x4x4 skinny kernel, which splits K inside the workgroup only, and M < 512).  For M >= 512

@@ -39,6 +39,10 @@ SIGNATURES = {
     "nmi_alloc_reset": ([], _i),
     "nmi_alloc_stats": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
     "nmi_sync": ([], _i),
+    "nmi_gemv_chain_create": ([_vp, _i, ctypes.POINTER(_vp)], _i),
+    "nmi_gemv_chain_workspace_bytes": ([_i], _sz),
+    "nmi_gemv_chain_launch": ([_vp, _vp, _sz, _vp], _i),
+    "nmi_gemv_chain_destroy": ([_vp], _i),
 }
 
 MAX_GROUPS = 4
@@ -48,6 +52,12 @@ class LinearGroup(ctypes.Structure):
     """nmi_linear_group of include/nmi_fp8_linear.h."""
     _fields_ = [("w_e4m3", _vp), ("ldw", _i64), ("w_scale", _vp), ("y_bf16", _vp), ("ldy", _i64),
                 ("N", _i)]
+
+
+class GemvPhase(ctypes.Structure):
+    """nmi_gemv_phase of include/nmi_fp8_linear.h."""
+    _fields_ = [("x_bf16", _vp), ("K", _i), ("ngroups", _i), ("wait_prev", _i),
+                ("groups", LinearGroup * MAX_GROUPS)]
 
 
 _lib = None

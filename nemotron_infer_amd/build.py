@@ -40,7 +40,8 @@ HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}"
 
 
 def _run(cmd):
-    r = subprocess.run(cmd, capture_output=True, text=True)
+    # one compile or link step takes well under a minute; a step that runs for 15 minutes is stuck
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         raise RuntimeError("build step failed:\n  " + " ".join(cmd) + "\n" + r.stdout + r.stderr)
     return r

@@ -209,6 +209,95 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                     static_cast<hipStream_t>(stream), fn);
 }
 
+// GEMV chain: the planned phase table lives in device memory for the handle's lifetime.
+struct nmi_gemv_chain {
+    ChainPhase* dev = nullptr;
+    int nphases = 0;
+    int total_items = 0;
+    int grid = 0;
+    size_t lds_bytes = 0;
+    int device = -1;
+};
+
+int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_chain** out) {
+    const char* fn = "nmi_gemv_chain_create";
+    if (!out) return fail(NMI_ERR_INVALID_ARG, "%s: out is NULL", fn);
+    *out = nullptr;
+    if (!phases || nphases < 1 || nphases > NMI_MAX_CHAIN_PHASES)
+        return fail(NMI_ERR_INVALID_ARG, "%s: nphases=%d must be in [1, %d]", fn, nphases, NMI_MAX_CHAIN_PHASES);
+    std::vector<ChainPhase> host((size_t)nphases);
+    int64_t items = 0;
+    for (int p = 0; p < nphases; ++p) {
+        const nmi_gemv_phase& P = phases[p];
+        if (P.ngroups < 1 || P.ngroups > NMI_MAX_GROUPS)
+            return fail(NMI_ERR_INVALID_ARG, "%s: phase %d: ngroups=%d must be in [1, %d]", fn, p, P.ngroups,
+                        NMI_MAX_GROUPS);
+        ChainPhase& ph = host[(size_t)p];
+        ph = ChainPhase{};
+        ph.x = static_cast<const uint16_t*>(P.x_bf16);
+        ph.K = P.K;
+        ph.ngroups = P.ngroups;
+        ph.wait = P.wait_prev ? 1 : 0;
+        for (int i = 0; i < P.ngroups; ++i) {
+            const nmi_linear_group& G = P.groups[i];
+            int rc = check_linear(P.x_bf16, P.K, G.w_e4m3, G.ldw, G.w_scale, G.y_bf16, G.ldy, 1, G.N, P.K, fn);
+            if (rc) return rc;
+            ph.g[i] = GemvGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
+                                static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0};
+            items += (G.N + 3) / 4;                   // upper bound of the work items (4 rows each)
+        }
+    }
+    if (items >= ((int64_t)1 << 30)) return fail(NMI_ERR_INVALID_ARG, "%s: too many rows in total", fn);
+    size_t lds = 0;
+    const int total = gemv_chain_plan(host.data(), nphases, &lds);
+    auto* c = new nmi_gemv_chain;
+    c->nphases = nphases;
+    c->total_items = total;
+    c->lds_bytes = lds;
+    hipError_t e = hipGetDevice(&c->device);
+    if (e == hipSuccess) e = gemv_chain_grid(lds, total, &c->grid);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->dev), host.size() * sizeof(ChainPhase));
+    if (e == hipSuccess)
+        e = hipMemcpy(c->dev, host.data(), host.size() * sizeof(ChainPhase), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (c->dev) (void)hipFree(c->dev);
+        delete c;
+        return hip_status(e, fn);
+    }
+    *out = c;
+    return NMI_OK;
+}
+
+size_t nmi_gemv_chain_workspace_bytes(int nphases) {
+    if (nphases < 1 || nphases > NMI_MAX_CHAIN_PHASES) return 0;
+    return gemv_chain_counter_bytes(nphases);                 // a multiple of 256 bytes
+}
+
+int nmi_gemv_chain_launch(const nmi_gemv_chain* chain, void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "nmi_gemv_chain_launch";
+    if (!chain || !chain->dev) return fail(NMI_ERR_INVALID_ARG, "%s: invalid chain", fn);
+    if (!workspace || !aligned(workspace, 256))
+        return fail(NMI_ERR_ALIGNMENT, "%s: workspace must be non-NULL and 256-byte aligned", fn);
+    if (workspace_bytes < nmi_gemv_chain_workspace_bytes(chain->nphases)) {
+        set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes,
+                       nmi_gemv_chain_workspace_bytes(chain->nphases));
+        return NMI_ERR_WORKSPACE;
+    }
+    int dev = -1;
+    if (hipGetDevice(&dev) == hipSuccess && dev != chain->device)
+        return fail(NMI_ERR_INVALID_ARG, "%s: chain was created on device %d, current is %d", fn, chain->device, dev);
+    return hip_status(launch_gemv_chain(chain->dev, chain->nphases, chain->total_items, chain->grid, chain->lds_bytes,
+                                        static_cast<uint32_t*>(workspace), static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+int nmi_gemv_chain_destroy(nmi_gemv_chain* chain) {
+    if (!chain) return NMI_OK;
+    const hipError_t e = chain->dev ? hipFree(chain->dev) : hipSuccess;
+    delete chain;
+    return hip_status(e, "nmi_gemv_chain_destroy");
+}
+
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) {
     if (M < 1 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
     if (M > 16) return gemm_workspace_bytes(M);       // stream-K partials of the GEMM
@@ -264,6 +353,7 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s4.t")) t.s4_t = value;
     else if (!std::strcmp(knob, "s4.u")) t.s4_u = value;
     else if (!std::strcmp(knob, "gemm.sk")) t.gemm_sk = value;
+    else if (!std::strcmp(knob, "chain.wgs")) t.chain_wgs = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

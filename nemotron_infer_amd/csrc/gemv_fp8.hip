@@ -383,6 +383,234 @@ hipError_t launch_t(int t, int p, const Mode& md, GemvArgs& a, hipStream_t strea
 
 int pow2_pieces(int need) { return need <= 2 ? 2 : (need <= 4 ? 4 : 8); }
 
+// ---------------------------------------------------------------------------------------
+// GEMV chain: the GEMVs of a decode step (phases, each a grouped GEMV sharing one x) in one
+// launch.  Work items (T * 4 / ks rows of one group each) are numbered in phase order; the grid
+// is at most the number of workgroups that fit on the device at once, and workgroup b takes
+// items b, b + G, b + 2G, ... in order.  An item of a waiting phase issues its first weight
+// loads, then waits until the previous phase has completed (its x may be that phase's output),
+// then stages x and finishes its rows.  The weight stream of the next phase therefore starts
+// while the current one drains, and the step pays one launch.  Deadlock-free when all G
+// workgroups are resident together (G is sized so): the lowest unfinished item belongs to a
+// running workgroup whose earlier items are done, and it waits only on lower items.
+//
+// Completion is counted only for phases that a later phase waits on, and without one contended
+// address (device-scope atomics on one cache line serialize at a few ns each): such an item,
+// once its stores have completed (s_waitcnt), adds 1 to stripe (local index % kChainStripes) of
+// its phase, each stripe on its own 128-byte line; the item completing a stripe adds 1 to the
+// phase's done line, which the waiters poll.  Other items store and go on.  Every workgroup
+// leaving the loop adds 1 to its exit stripe (blockIdx % kChainStripes), the one completing a
+// stripe to the exit-done line, and the one completing that re-arms every line: the counters
+// are zero again when the launch ends.  A wait that has not ended after 0.2 s gives up (wrong
+// outputs, never a hang) and sets the error word, which is left set.  Outputs of a signalling
+// phase are stored, and x / residuals of a waiting phase are loaded, at device scope (coherent
+// across the XCDs' L2 caches).
+__device__ __forceinline__ uint32_t* chain_line(uint32_t* ctr, int p, int line) {
+    return ctr + ((int64_t)p * (kChainStripes + 1) + line) * kChainLineWords;
+}
+
+// Pointers read from the phase table carry no address space; the chain kernel converts them to
+// global-memory pointers so that its loads and stores are global (not FLAT) instructions.
+#define NMI_GLOBAL __attribute__((address_space(1)))
+template <class E>
+__device__ __forceinline__ NMI_GLOBAL E* global_ptr(E* p) {
+    return (NMI_GLOBAL E*)p;
+}
+
+__device__ __forceinline__ uint4 load_stream16_g(const NMI_GLOBAL uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const NMI_GLOBAL u32x4*>(p));
+    return uint4{v.x, v.y, v.z, v.w};
+}
+
+// The phase table is written before the launch and never by a kernel: read through the constant
+// address space, its uniform fields are scalar loads (as generic memory, next to the kernel's
+// own stores, the compiler would read it with vector loads and wait for them together with the
+// weight loads in flight).
+#define NMI_CONST __attribute__((address_space(4)))
+
+// 16 bytes per lane from global memory straight into LDS (64 lanes: 1 KiB at lds_addr, in lane
+// order), with no register staging; the plain form, or at device scope (sc1) for an earlier
+// phase's output.  The compiler does not track these loads: completion is waited for with an
+// explicit vmcnt.
+__device__ __forceinline__ void dma16_lds(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_lds_device(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc1" ::"v"(off), "s"(base), "s"(lds_addr)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ int chain_stripes(int nitems) { return nitems < kChainStripes ? nitems : kChainStripes; }
+
+template <int T, int P>
+__global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __restrict__ phases, int nphases,
+                                                          int total_items, uint32_t* __restrict__ ctr) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    extern __shared__ uint4 xs[];                  // [half][window rounded up to 64 chunks]
+    __shared__ float partial[kWaves][kWaves * T];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const uint32_t xs_addr = (uint32_t)(uintptr_t)(lds_void*)xs;
+    uint32_t* err = ctr + (int64_t)(gemv_chain_counter_lines(nphases) - 1) * kChainLineWords;
+    const NMI_CONST ChainPhase* tab = (const NMI_CONST ChainPhase*)phases;
+    int p = 0;
+    for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
+        while (p + 1 < nphases && tab[p + 1].item_begin <= item) ++p;
+        const NMI_CONST ChainPhase& ph = tab[p];
+        const int local = item - ph.item_begin;
+        int gi = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxGroups; ++i)
+            if (i < ph.ngroups && local >= ph.g[i].wg_begin) gi = i;
+        const NMI_CONST GemvGroup& grp = ph.g[gi];
+        const NMI_GLOBAL uint8_t* gW = global_ptr(grp.W);
+        const int ks = ph.ks;                      // waves splitting K: 1, 2 or 4
+        const int g = wave / ks, q = wave % ks;
+        const int rows_per_wg = (kWaves / ks) * T;
+        const int row_base = (local - grp.wg_begin) * rows_per_wg + g * T;
+        const int C = ph.K >> 4, window = ph.window;
+        const int wpad = (window + 63) & ~63;      // LDS chunks per half
+        const bool coherent_in = p > 0 && ph.wait, coherent_out = ph.signal;
+
+        const NMI_GLOBAL uint8_t* wrow[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) wrow[t] = gW + (int64_t)min(row_base + t, grp.N - 1) * grp.ldw;
+        float a0[T], a1[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) a0[t] = a1[t] = 0.f;
+        for (int w0 = 0; w0 < C; w0 += window) {
+            const int wc = min(window, C - w0);
+            const int cb = w0 + (q * wc) / ks;
+            const int ce = w0 + ((q + 1) * wc) / ks;
+            const int clast = max(ce - 1, cb);
+            int c0 = cb + lane;
+            // 1. this window's first batch of weights (independent of earlier phases)
+            uint4 wv[T][P];
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int i = 0; i < P; ++i)
+                    wv[t][i] = load_stream16_g(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
+            // 2. x may be the previous phase's output: wait for that phase (first window only)
+            if (w0 == 0 && p > 0 && ph.wait) {
+                if (tid == 0) {
+                    const uint32_t need = (uint32_t)chain_stripes(tab[p - 1].nitems);
+                    const uint32_t* done = chain_line(ctr, p - 1, kChainStripes);
+                    const uint64_t t_end = wall_clock64() + 20000000ull;   // 0.2 s at 100 MHz
+                    while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+                        if (wall_clock64() > t_end) {
+                            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                    }
+                }
+                __syncthreads();
+            } else if (w0 != 0) {
+                __syncthreads();                   // the previous window has been consumed
+            }
+            // 3. stage x by LDS DMA (two 16-byte halves per chunk, as the one-launch kernel): job
+            //    (half h, 64-chunk block b) has lane l load piece 2 (64 b + l) + h; lanes past the
+            //    window load a valid piece into an unread pad slot of the block
+            const uint8_t* xw = reinterpret_cast<const uint8_t*>(ph.x) + (int64_t)w0 * 32;
+            const int jobs = 2 * ((wc + 63) >> 6);
+            for (int j = wave; j < jobs; j += kWaves) {
+                const int h = j & 1, s0 = (j >> 1) << 6;
+                const uint32_t off = (uint32_t)min(2 * (s0 + lane) + h, 2 * wc - 1) * 16;
+                const uint32_t dst = xs_addr + (uint32_t)(h * wpad + s0) * 16;
+                if (coherent_in) dma16_lds_device(xw, off, dst);
+                else dma16_lds(xw, off, dst);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            // 4. consume; further batches when a lane's slice exceeds P chunks per row
+            for (;;) {
+#pragma unroll
+                for (int i = 0; i < P; ++i) {
+                    const int c = c0 + 64 * i;
+                    if (c < ce) {
+                        const uint4 lo4 = xs[c - w0], hi4 = xs[wpad + c - w0];
+#pragma unroll
+                        for (int t = 0; t < T; ++t) dot16(wv[t][i], lo4, hi4, a0[t], a1[t]);
+                    }
+                }
+                c0 += 64 * P;
+                if (c0 - lane >= ce) break;         // uniform across the wave
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int i = 0; i < P; ++i)
+                        wv[t][i] = load_stream16_g(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
+            }
+        }
+        // wave sums (16-lane DPP rows, then 0 + 1 + 2 + 3), then the K slices in order q = 0..ks-1
+        float sums[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) sums[t] = wave_sum(a0[t] + a1[t]);
+        if (lane == 0) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) partial[q][g * T + t] = sums[t];
+        }
+        __syncthreads();                           // also: every wave is done reading xs
+        if (q == 0 && lane < T) {
+            const int t = lane;
+            float v = partial[0][g * T + t];
+            for (int qq = 1; qq < ks; ++qq) v += partial[qq][g * T + t];
+            const int row = row_base + t;
+            if (row < grp.N) {
+                uint16_t res = 0;
+                if (grp.epi.kind == kEpiResidual) {
+                    const NMI_GLOBAL uint16_t* rp = global_ptr(grp.epi.res) + row;
+                    res = coherent_in ? __hip_atomic_load(rp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *rp;
+                }
+                const uint16_t out = epilogue(v, global_ptr(grp.s)[row], grp.epi.kind, res);
+                NMI_GLOBAL uint16_t* yp = global_ptr(grp.y) + row;
+                if (coherent_out) __hip_atomic_store(yp, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else *yp = out;
+            }
+        }
+        // completion (counted when a later phase waits on this one): the stores have completed,
+        // then the count
+        if (ph.signal) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0) {
+                const int n = ph.nitems;
+                const int stripe = local % kChainStripes;
+                const uint32_t v = __hip_atomic_fetch_add(chain_line(ctr, p, stripe), 1u, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+                if (v + 1 == (uint32_t)((n - stripe + kChainStripes - 1) / kChainStripes))
+                    __hip_atomic_fetch_add(chain_line(ctr, p, kChainStripes), 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+    // exit count, after this workgroup's own counts have landed; the last workgroup out re-arms
+    // the counters (nothing reads them any more)
+    if (wave == 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+        int rearm = 0;
+        if (lane == 0) {
+            const int G = (int)gridDim.x;
+            const int stripe = (int)blockIdx.x % kChainStripes;
+            const uint32_t v = __hip_atomic_fetch_add(chain_line(ctr, nphases, stripe), 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+            if (v + 1 == (uint32_t)((G - stripe + kChainStripes - 1) / kChainStripes)) {
+                const uint32_t d = __hip_atomic_fetch_add(chain_line(ctr, nphases, kChainStripes), 1u,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                rearm = d + 1 == (uint32_t)chain_stripes(G);
+            }
+        }
+        if (__builtin_amdgcn_readfirstlane(rearm)) {
+            const int lines = (nphases + 1) * (kChainStripes + 1);
+            for (int l = lane; l < lines; l += 64)
+                __hip_atomic_store(ctr + (int64_t)l * kChainLineWords, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 }  // namespace
 
 bool gemv_norm_supported(int M, int K) {
@@ -437,6 +665,57 @@ hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, con
         case 2: return launch_t<2>(t, p, md, a, stream);
         default: return launch_t<4>(t, p, md, a, stream);
     }
+}
+
+namespace {
+constexpr int kChainT = 4;       // rows per wave in the chain kernel
+constexpr int kChainP = 4;       // 16-byte chunks per lane per row per batch
+}  // namespace
+
+int gemv_chain_plan(ChainPhase* phases, int nphases, size_t* lds_bytes) {
+    int items = 0;
+    int wmax = 1;
+    for (int p = 0; p < nphases; ++p) {
+        ChainPhase& ph = phases[p];
+        const int C = ph.K >> 4;
+        ph.ks = C <= 64 * 4 ? 1 : (C <= 2 * 64 * 4 ? 2 : 4);   // about 3-4 chunks per lane per row
+        ph.window = C < kMaxWindowChunks ? C : kMaxWindowChunks;
+        wmax = ph.window > wmax ? ph.window : wmax;
+        const int rows_per_wg = (kWaves / ph.ks) * kChainT;
+        ph.item_begin = items;
+        int n = 0;
+        for (int i = 0; i < ph.ngroups; ++i) {
+            ph.g[i].wg_begin = n;
+            n += (ph.g[i].N + rows_per_wg - 1) / rows_per_wg;
+        }
+        ph.nitems = n;
+        items += n;
+    }
+    for (int p = 0; p < nphases; ++p) phases[p].signal = p + 1 < nphases && phases[p + 1].wait;
+    *lds_bytes = (size_t)((wmax + 63) & ~63) * 2 * sizeof(uint4);
+    return items;
+}
+
+hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid) {
+    const DeviceInfo& dev = device_info();
+    int per_cu = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, gemv_chain_kernel<kChainT, kChainP>, 256, lds_bytes);
+    if (e != hipSuccess) return e;
+    // Measured on the config-1 set: 4 workgroups per CU stream faster than the 5 that fit.
+    const int cap = tuning().chain_wgs >= 1 ? tuning().chain_wgs : 4;
+    if (cap < per_cu) per_cu = cap;
+    if (per_cu < 1) return hipErrorInvalidConfiguration;
+    const int64_t resident = (int64_t)per_cu * dev.num_cu;
+    *grid = (int)(total_items < resident ? total_items : resident);
+    return hipSuccess;
+}
+
+hipError_t launch_gemv_chain(const ChainPhase* phases, int nphases, int total_items, int grid, size_t lds_bytes,
+                             uint32_t* ctr, hipStream_t stream) {
+    hipLaunchKernelGGL((gemv_chain_kernel<kChainT, kChainP>), dim3(grid), dim3(256), lds_bytes, stream,
+                       phases, nphases, total_items, ctr);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,

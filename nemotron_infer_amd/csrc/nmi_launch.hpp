@@ -40,6 +40,7 @@ struct Tuning {
     int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
+    int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 4, or fewer if fewer are resident)
 };
 Tuning& tuning();
 
@@ -104,6 +105,45 @@ hipError_t launch_rmsnorm(const uint16_t* x, int64_t ldx, const Norm& norm, uint
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);
+
+// One phase of a GEMV chain (M = 1): the grouped GEMV of x [K] against up to kMaxGroups
+// matrices.  gemv_chain_plan fills ks, window, item_begin, nitems, signal and each group's
+// wg_begin (first work item of the group, relative to the phase); wait = 1 makes the phase wait
+// until the previous one has completed before reading x (x may be that phase's output).
+struct ChainPhase {
+    const uint16_t* x;
+    int K;
+    int ks;             // waves splitting K (1, 2 or 4)
+    int window;         // x chunks staged per window
+    int item_begin;     // first work item of the phase
+    int nitems;
+    int ngroups;
+    int wait;
+    int signal;         // the next phase waits: completions of this one are counted
+    GemvGroup g[kMaxGroups];
+};
+// Fills the derived fields of phases[0..n) and returns the number of work items; *lds_bytes
+// receives the dynamic LDS the launch needs.
+int gemv_chain_plan(ChainPhase* phases, int nphases, size_t* lds_bytes);
+// Counter workspace of a chain: per phase kChainStripes stripe counters and one done counter,
+// then kChainStripes exit counters and one exit-done counter, each on its own 128-byte line;
+// the last line (an even number of lines: a multiple of 256 bytes) holds the error word; zero
+// at rest.
+constexpr int kChainStripes = 8;
+constexpr int kChainLineWords = 32;
+constexpr int gemv_chain_counter_lines(int nphases) {
+    return ((nphases + 1) * (kChainStripes + 1) + 2) & ~1;
+}
+inline size_t gemv_chain_counter_bytes(int nphases) {
+    return (size_t)gemv_chain_counter_lines(nphases) * kChainLineWords * sizeof(uint32_t);
+}
+// Workgroups of the launch: the items, at most as many as are resident at once on the current
+// device (the workgroups wait on each other's items) and at most 4 per CU (tuning knob
+// chain.wgs sets that cap).
+hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid);
+// phases: the planned table in device memory; ctr: gemv_chain_counter_bytes(nphases) bytes.
+hipError_t launch_gemv_chain(const ChainPhase* phases, int nphases, int total_items, int grid, size_t lds_bytes,
+                             uint32_t* ctr, hipStream_t stream);
 
 // Prefill GEMM.  Given a workspace of at least gemm_workspace_bytes(M) bytes whose first 64 KiB
 // (the flag region) are zero -- every launch leaves them zero again -- the DMA-fed kernel splits

@@ -186,6 +186,69 @@ def mlp_forward_fp8(x: torch.Tensor, norm_w: torch.Tensor, up_w: torch.Tensor, u
     return out
 
 
+class GemvChain:
+    """The GEMVs of a decode step in one launch (nmi_gemv_chain_*; M = 1).
+
+    phases: a list of (x, groups, wait_prev): x a [K] (or [1, K]) bf16 tensor, groups a list of
+    up to four (w, s, y) -- w [N, K] e4m3 codes (uint8), s [N] float32, y [N] bf16 output -- and
+    wait_prev whether the phase reads x only after the previous phase has completed (x may be an
+    earlier phase's output).  The plan holds raw pointers: the tensors are kept referenced here
+    and must not be reallocated while the chain is in use.  The chain owns its zero-filled
+    counter workspace; launches go on torch's current stream and are graph-capturable."""
+
+    def __init__(self, phases):
+        L = _lib.lib()
+        n = len(phases)
+        arr = (_lib.GemvPhase * n)()
+        self._keep = []
+        dev = None
+        for i, (x, groups, wait_prev) in enumerate(phases):
+            x1 = x.reshape(-1)
+            if x1.dtype != torch.bfloat16 or not x1.is_contiguous():
+                raise ValueError("x must be a contiguous bf16 vector")
+            if not 1 <= len(groups) <= _lib.MAX_GROUPS:
+                raise ValueError(f"1..{_lib.MAX_GROUPS} groups per phase")
+            K = x1.numel()
+            arr[i].x_bf16 = x1.data_ptr()
+            arr[i].K = K
+            arr[i].ngroups = len(groups)
+            arr[i].wait_prev = 1 if wait_prev else 0
+            for j, (w, sc, y) in enumerate(groups):
+                w = _check_w(w)
+                y1 = y.reshape(-1)
+                arr[i].groups[j] = _lib.LinearGroup(w.data_ptr(), w.stride(0), sc.data_ptr(), y1.data_ptr(),
+                                                    y1.numel(), w.shape[0])
+                self._keep += [w, sc, y1]
+            self._keep.append(x1)
+            dev = x1.device
+        h = ctypes.c_void_p()
+        _lib.check(L.nmi_gemv_chain_create(arr, n, ctypes.byref(h)), "nmi_gemv_chain_create")
+        self._h = h
+        self.nphases = n
+        nbytes = L.nmi_gemv_chain_workspace_bytes(n)
+        self._ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+
+    def launch(self):
+        L = _lib.lib()
+        _lib.check(L.nmi_gemv_chain_launch(self._h, self._ws.data_ptr(), self._ws.numel(), _stream()),
+                   "nmi_gemv_chain_launch")
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _lib.lib().nmi_gemv_chain_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def workspace(self) -> torch.Tensor:
+        return self._ws
+
+
 def decode_e4m3(codes: torch.Tensor, scale: float):
     """Device decode of uint8 codes through the kernels' conversion helpers.
     Returns (f32 values, f32 values * scale, bf16 values)."""

@@ -180,3 +180,56 @@ def test_binding_block_entries_validate():
         B.rmsnorm(FAKE + 2, FAKE, FAKE, 1)
     with pytest.raises(RuntimeError, match="M=0"):
         B.mlp_forward_fp8(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0)
+
+
+def test_gemv_chain_workspace_bytes():
+    """Per phase 9 counter lines of 128 B, 9 exit lines, then the error line; an even number of
+    lines (a multiple of 256 B)."""
+    L = _lib.lib()
+    for n in (1, 2, 3, 4, 84, 4096):
+        lines = (n + 1) * 9 + 1
+        lines += lines % 2
+        assert L.nmi_gemv_chain_workspace_bytes(n) == lines * 128, n
+        assert L.nmi_gemv_chain_workspace_bytes(n) % 256 == 0
+    assert L.nmi_gemv_chain_workspace_bytes(0) == 0
+    assert L.nmi_gemv_chain_workspace_bytes(4097) == 0
+
+
+def _phase(x=FAKE, K=64, group=(FAKE, 64, FAKE, FAKE, 8, 8), ngroups=1, wait=0):
+    """A phase of ngroups copies of one group (ngroups may exceed the array to test the bound)."""
+    ph = _lib.GemvPhase()
+    ph.x_bf16, ph.K, ph.ngroups, ph.wait_prev = x, K, ngroups, wait
+    for i in range(min(ngroups, _lib.MAX_GROUPS)):
+        ph.groups[i] = _lib.LinearGroup(*group)
+    return ph
+
+
+@pytest.mark.parametrize("phase,code", [
+    (dict(x=0), _lib.NMI_ERR_INVALID_ARG),                                       # NULL x
+    (dict(K=72), _lib.NMI_ERR_INVALID_ARG),                                      # K % 16
+    (dict(ngroups=0), _lib.NMI_ERR_INVALID_ARG),                                 # no group
+    (dict(ngroups=5), _lib.NMI_ERR_INVALID_ARG),                                 # > 4 groups
+    (dict(group=(FAKE + 8, 64, FAKE, FAKE, 8, 8)), _lib.NMI_ERR_ALIGNMENT),      # W misaligned
+    (dict(group=(FAKE, 64, FAKE, FAKE, 8, 0)), _lib.NMI_ERR_INVALID_ARG),        # N = 0
+    (dict(x=FAKE + 2), _lib.NMI_ERR_ALIGNMENT),                                  # x misaligned
+])
+def test_gemv_chain_rejects_bad_phases(phase, code):
+    """A bad second phase is rejected on the host, before any device call."""
+    L = _lib.lib()
+    arr = (_lib.GemvPhase * 2)(_phase(), _phase(**phase))
+    h = ctypes.c_void_p()
+    assert L.nmi_gemv_chain_create(arr, 2, ctypes.byref(h)) == code
+    assert not h.value
+    assert L.nmi_last_error().decode().startswith("nmi_gemv_chain_create")
+
+
+def test_gemv_chain_handle_errors():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    arr = (_lib.GemvPhase * 1)(_phase())
+    assert L.nmi_gemv_chain_create(arr, 0, ctypes.byref(h)) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_gemv_chain_create(arr, 4097, ctypes.byref(h)) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_gemv_chain_create(None, 1, ctypes.byref(h)) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_gemv_chain_create(arr, 1, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_gemv_chain_launch(None, FAKE, 4096, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_gemv_chain_destroy(None) == _lib.NMI_OK
