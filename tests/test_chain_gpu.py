@@ -10,6 +10,7 @@
   phase): results and re-armed counters stay right over repeated launches.
 * The same with one workgroup per CU (tuning knob chain.wgs = 1), so that every workgroup runs
   many items of several phases in turn.
+* Independent phases with K beyond one x window (several windows per work item).
 * Graph replays (with eager work between them) equal the eager launch; every launch leaves the
   counter workspace zero (which includes the error word a timed-out wait would set).
 * Parity with the oracle (fp32 dequant-then-F.linear, rounded once).
@@ -137,6 +138,29 @@ def test_phase_without_wait_finishing_first(chain_wgs):
         r3 = ops.linear_fp8_w8a16(r2.view(1, -1), *w3).view(-1)
         for i, (y, r) in enumerate(((y0, r0), (y1[:8], r1), (y2, r2), (y3, r3))):
             assert torch.equal(y.view(torch.int16), r.view(torch.int16)), (rep, i)
+
+
+def test_long_k_phases_take_several_windows(chain_wgs):
+    """Independent phases whose K exceeds one x window (K = 20480: two windows of 1024 chunks)
+    next to short ones, byte-identical to separate launches."""
+    announce("chain_long_k", chain_wgs)
+    shapes = [(96, 20480), (100, 3136), (40, 16400), (8, 64)]
+    ws = [_w(N, K, 600 + i, "log_uniform") for i, (N, K) in enumerate(shapes)]
+    xs = [_x(K, 610 + i) for i, (_, K) in enumerate(shapes)]
+    ys = [torch.empty(N, dtype=torch.bfloat16, device=DEV) for N, _ in shapes]
+    chain = ops.GemvChain([(x, [(*w, y)], False) for x, w, y in zip(xs, ws, ys)])
+    for rep in range(2):
+        for y in ys:
+            y.fill_(5.0)
+        chain.launch()
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(chain.workspace) == 0
+        for i, (x, (w, s), y) in enumerate(zip(xs, ws, ys)):
+            r = ops.linear_fp8_w8a16(x.view(1, -1), w, s).view(-1)
+            assert torch.equal(y.view(torch.int16), r.view(torch.int16)), (rep, shapes[i])
+    xb = xs[0].view(torch.int16).cpu().numpy().view(np.uint16)[None]
+    assert_parity(bits(ys[0].view(1, -1)), oracle_bits(xb, ws[0][0].cpu().numpy(), ws[0][1].cpu().numpy()),
+                  "K = 20480 vs oracle")
 
 
 def test_chain_graph_replays():
