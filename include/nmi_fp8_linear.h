@@ -223,11 +223,14 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
                         int inter, float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "skinny.path",
- * "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path"); 0 restores the
- * automatic choice.  Process-wide, not thread-safe against concurrent launches; results
- * do not depend on them beyond float32 summation order.  No counterpart in the reference
- * (its launch shapes are compile-time constants, ops/gemv.cuh:100-103).
+ * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "gemm.sk",
+ * "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
+ * "chain.wgs": workgroups per CU of a GEMV chain created afterwards, "chain.wait_us": bound of a
+ * chain's waits in microseconds); 0 restores the automatic choice.  Process-wide, not
+ * thread-safe against concurrent launches; results do not depend on them beyond float32
+ * summation order (except chain.wait_us, whose bound a correct chain never reaches).  No
+ * counterpart in the reference (its launch shapes are compile-time constants,
+ * ops/gemv.cuh:100-103).
  */
 int nmi_tuning_set(const char* knob, int value);
 

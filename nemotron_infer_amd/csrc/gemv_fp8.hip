@@ -401,10 +401,11 @@ int pow2_pieces(int need) { return need <= 2 ? 2 : (need <= 4 ? 4 : 8); }
 // phase's done line, which the waiters poll.  Other items store and go on.  Every workgroup
 // leaving the loop adds 1 to its exit stripe (blockIdx % kChainStripes), the one completing a
 // stripe to the exit-done line, and the one completing that re-arms every line: the counters
-// are zero again when the launch ends.  A wait that has not ended after 0.2 s gives up (wrong
-// outputs, never a hang) and sets the error word, which is left set.  Outputs of a signalling
-// phase are stored, and x / residuals of a waiting phase are loaded, at device scope (coherent
-// across the XCDs' L2 caches).
+// are zero again when the launch ends.  A wait that has not ended after 0.2 s (tuning knob
+// chain.wait_us) gives up (wrong outputs, never a hang) and sets the error word, which is left
+// set.  Outputs of a signalling
+// phase are stored, and x of a waiting phase is loaded, at device scope (coherent across the
+// XCDs' L2 caches).
 __device__ __forceinline__ uint32_t* chain_line(uint32_t* ctr, int p, int line) {
     return ctr + ((int64_t)p * (kChainStripes + 1) + line) * kChainLineWords;
 }
@@ -445,7 +446,8 @@ __device__ __forceinline__ int chain_stripes(int nitems) { return nitems < kChai
 
 template <int T, int P>
 __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __restrict__ phases, int nphases,
-                                                          int total_items, uint32_t* __restrict__ ctr) {
+                                                          int total_items, uint32_t* __restrict__ ctr,
+                                                          uint64_t wait_ticks) {
     typedef __attribute__((address_space(3))) void lds_void;
     extern __shared__ uint4 xs[];                  // [half][window rounded up to 64 chunks]
     __shared__ float partial[kWaves][kWaves * T];
@@ -498,7 +500,7 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __res
                 if (tid == 0) {
                     const uint32_t need = (uint32_t)chain_stripes(tab[p - 1].nitems);
                     const uint32_t* done = chain_line(ctr, p - 1, kChainStripes);
-                    const uint64_t t_end = wall_clock64() + 20000000ull;   // 0.2 s at 100 MHz
+                    const uint64_t t_end = wall_clock64() + wait_ticks;   // wall clock: 100 MHz
                     while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
                         if (wall_clock64() > t_end) {
                             __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -560,12 +562,8 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __res
             for (int qq = 1; qq < ks; ++qq) v += partial[qq][g * T + t];
             const int row = row_base + t;
             if (row < grp.N) {
-                uint16_t res = 0;
-                if (grp.epi.kind == kEpiResidual) {
-                    const NMI_GLOBAL uint16_t* rp = global_ptr(grp.epi.res) + row;
-                    res = coherent_in ? __hip_atomic_load(rp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *rp;
-                }
-                const uint16_t out = epilogue(v, global_ptr(grp.s)[row], grp.epi.kind, res);
+                // plain epilogue: a chain group has no fused relu^2 or residual
+                const uint16_t out = epilogue(v, global_ptr(grp.s)[row], kEpiNone, 0);
                 NMI_GLOBAL uint16_t* yp = global_ptr(grp.y) + row;
                 if (coherent_out) __hip_atomic_store(yp, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 else *yp = out;
@@ -713,8 +711,10 @@ hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid) {
 
 hipError_t launch_gemv_chain(const ChainPhase* phases, int nphases, int total_items, int grid, size_t lds_bytes,
                              uint32_t* ctr, hipStream_t stream) {
+    // the bound of a wait: 0.2 s, or tuning knob chain.wait_us (microseconds) when set
+    const uint64_t wait_ticks = tuning().chain_wait_us > 0 ? (uint64_t)tuning().chain_wait_us * 100u : 20000000ull;
     hipLaunchKernelGGL((gemv_chain_kernel<kChainT, kChainP>), dim3(grid), dim3(256), lds_bytes, stream,
-                       phases, nphases, total_items, ctr);
+                       phases, nphases, total_items, ctr, wait_ticks);
     return hipGetLastError();
 }
 

@@ -41,6 +41,7 @@ struct Tuning {
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
     int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 4, or fewer if fewer are resident)
+    int chain_wait_us = 0; // GEMV chain: bound of a wait in microseconds (0: 200000)
 };
 Tuning& tuning();
 

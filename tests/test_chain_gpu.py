@@ -11,6 +11,8 @@
 * The same with one workgroup per CU (tuning knob chain.wgs = 1), so that every workgroup runs
   many items of several phases in turn.
 * Independent phases with K beyond one x window (several windows per work item).
+* A forced timeout (wait bound of 1 us) completes, sets the error word and re-arms the counters;
+  the chain is right again with the bound restored.
 * Graph replays (with eager work between them) equal the eager launch; every launch leaves the
   counter workspace zero (which includes the error word a timed-out wait would set).
 * Parity with the oracle (fp32 dequant-then-F.linear, rounded once).
@@ -161,6 +163,35 @@ def test_long_k_phases_take_several_windows(chain_wgs):
     xb = xs[0].view(torch.int16).cpu().numpy().view(np.uint16)[None]
     assert_parity(bits(ys[0].view(1, -1)), oracle_bits(xb, ws[0][0].cpu().numpy(), ws[0][1].cpu().numpy()),
                   "K = 20480 vs oracle")
+
+
+def test_wait_bound_sets_the_error_word():
+    """Failure handling, forced from the host: with the wait bound at 1 us (tuning knob
+    chain.wait_us) the waiting phases give up instead of waiting; the launch still completes (no
+    hang, no fault) and the error word at byte offset workspace_bytes - 128 is set and left set.
+    With the bound restored, the same chain (error word cleared by the caller) is right again."""
+    announce("chain_wait_bound")
+    x0, ws, ys, phases = _dependent_case([3136, 12544, 3136, 12544, 3136], 91)
+    chain = ops.GemvChain(phases)
+    err_at = chain.workspace.numel() - 128
+    try:
+        _lib.tuning_set("chain.wait_us", 1)
+        chain.launch()
+        torch.cuda.synchronize()
+        words = chain.workspace.view(torch.int32)
+        assert int(words[err_at // 4]) != 0, "no wait gave up with a 1 us bound"
+        assert torch.count_nonzero(words[: err_at // 4]) == 0, "counters not re-armed after the timeouts"
+    finally:
+        _lib.tuning_set("chain.wait_us", 0)
+    chain.workspace.zero_()
+    chain.launch()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(chain.workspace) == 0
+    x = x0
+    for i, (w, s) in enumerate(ws):
+        r = ops.linear_fp8_w8a16(x.view(1, -1), w, s).view(-1)
+        assert torch.equal(ys[i].view(torch.int16), r.view(torch.int16)), f"phase {i}"
+        x = r
 
 
 def test_chain_graph_replays():
