@@ -209,9 +209,9 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                     static_cast<hipStream_t>(stream), fn);
 }
 
-// GEMV chain: the planned phase table lives in device memory for the handle's lifetime.
+// GEMV chain: the planned work items live in device memory for the handle's lifetime.
 struct nmi_gemv_chain {
-    ChainPhase* dev = nullptr;
+    ChainItem* dev = nullptr;               // the work items, one record each
     int nphases = 0;
     int total_items = 0;
     int grid = 0;
@@ -256,9 +256,11 @@ int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_ch
     c->lds_bytes = lds;
     hipError_t e = hipGetDevice(&c->device);
     if (e == hipSuccess) e = gemv_chain_grid(lds, total, &c->grid);
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->dev), host.size() * sizeof(ChainPhase));
+    std::vector<ChainItem> table((size_t)total);
+    gemv_chain_items(host.data(), nphases, table.data());
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->dev), table.size() * sizeof(ChainItem));
     if (e == hipSuccess)
-        e = hipMemcpy(c->dev, host.data(), host.size() * sizeof(ChainPhase), hipMemcpyHostToDevice);
+        e = hipMemcpy(c->dev, table.data(), table.size() * sizeof(ChainItem), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         if (c->dev) (void)hipFree(c->dev);
         delete c;

@@ -445,7 +445,7 @@ __device__ __forceinline__ void dma16_lds_device(const void* base, uint32_t off,
 __device__ __forceinline__ int chain_stripes(int nitems) { return nitems < kChainStripes ? nitems : kChainStripes; }
 
 template <int T, int P>
-__global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __restrict__ phases, int nphases,
+__global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainItem* __restrict__ items, int nphases,
                                                           int total_items, uint32_t* __restrict__ ctr,
                                                           uint64_t wait_ticks) {
     typedef __attribute__((address_space(3))) void lds_void;
@@ -456,29 +456,22 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __res
     const int lane = tid & 63;
     const uint32_t xs_addr = (uint32_t)(uintptr_t)(lds_void*)xs;
     uint32_t* err = ctr + (int64_t)(gemv_chain_counter_lines(nphases) - 1) * kChainLineWords;
-    const NMI_CONST ChainPhase* tab = (const NMI_CONST ChainPhase*)phases;
-    int p = 0;
+    const NMI_CONST ChainItem* tab = (const NMI_CONST ChainItem*)items;
     for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
-        while (p + 1 < nphases && tab[p + 1].item_begin <= item) ++p;
-        const NMI_CONST ChainPhase& ph = tab[p];
-        const int local = item - ph.item_begin;
-        int gi = 0;
-#pragma unroll
-        for (int i = 1; i < kMaxGroups; ++i)
-            if (i < ph.ngroups && local >= ph.g[i].wg_begin) gi = i;
-        const NMI_CONST GemvGroup& grp = ph.g[gi];
-        const NMI_GLOBAL uint8_t* gW = global_ptr(grp.W);
-        const int ks = ph.ks;                      // waves splitting K: 1, 2 or 4
+        const NMI_CONST ChainItem& it = tab[item];
+        const int ks = it.ks;                      // waves splitting K: 1, 2 or 4
         const int g = wave / ks, q = wave % ks;
-        const int rows_per_wg = (kWaves / ks) * T;
-        const int row_base = (local - grp.wg_begin) * rows_per_wg + g * T;
-        const int C = ph.K >> 4, window = ph.window;
+        const int row0 = g * T;                    // this wave's first row within the item
+        const int rows = it.rows;
+        const int64_t ldw = it.ldw;
+        const int C = it.K >> 4, window = it.window;
         const int wpad = (window + 63) & ~63;      // LDS chunks per half
-        const bool coherent_in = p > 0 && ph.wait, coherent_out = ph.signal;
+        const bool wait = it.flags & kChainWait, signal = it.flags & kChainSignal;
+        const NMI_GLOBAL uint8_t* gW = global_ptr(it.w);
 
         const NMI_GLOBAL uint8_t* wrow[T];
 #pragma unroll
-        for (int t = 0; t < T; ++t) wrow[t] = gW + (int64_t)min(row_base + t, grp.N - 1) * grp.ldw;
+        for (int t = 0; t < T; ++t) wrow[t] = gW + (int64_t)min(row0 + t, rows - 1) * ldw;
         float a0[T], a1[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) a0[t] = a1[t] = 0.f;
@@ -496,10 +489,10 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __res
                 for (int i = 0; i < P; ++i)
                     wv[t][i] = load_stream16_g(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
             // 2. x may be the previous phase's output: wait for that phase (first window only)
-            if (w0 == 0 && p > 0 && ph.wait) {
+            if (w0 == 0 && wait) {
                 if (tid == 0) {
-                    const uint32_t need = (uint32_t)chain_stripes(tab[p - 1].nitems);
-                    const uint32_t* done = chain_line(ctr, p - 1, kChainStripes);
+                    const uint32_t need = (uint32_t)it.wait_need;
+                    const uint32_t* done = chain_line(ctr, it.phase - 1, kChainStripes);
                     const uint64_t t_end = wall_clock64() + wait_ticks;   // wall clock: 100 MHz
                     while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
                         if (wall_clock64() > t_end) {
@@ -516,13 +509,13 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __res
             // 3. stage x by LDS DMA (two 16-byte halves per chunk, as the one-launch kernel): job
             //    (half h, 64-chunk block b) has lane l load piece 2 (64 b + l) + h; lanes past the
             //    window load a valid piece into an unread pad slot of the block
-            const uint8_t* xw = reinterpret_cast<const uint8_t*>(ph.x) + (int64_t)w0 * 32;
+            const uint8_t* xw = reinterpret_cast<const uint8_t*>(it.x) + (int64_t)w0 * 32;
             const int jobs = 2 * ((wc + 63) >> 6);
             for (int j = wave; j < jobs; j += kWaves) {
                 const int h = j & 1, s0 = (j >> 1) << 6;
                 const uint32_t off = (uint32_t)min(2 * (s0 + lane) + h, 2 * wc - 1) * 16;
                 const uint32_t dst = xs_addr + (uint32_t)(h * wpad + s0) * 16;
-                if (coherent_in) dma16_lds_device(xw, off, dst);
+                if (wait) dma16_lds_device(xw, off, dst);
                 else dma16_lds(xw, off, dst);
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -560,27 +553,25 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainPhase* __res
             const int t = lane;
             float v = partial[0][g * T + t];
             for (int qq = 1; qq < ks; ++qq) v += partial[qq][g * T + t];
-            const int row = row_base + t;
-            if (row < grp.N) {
+            const int row = row0 + t;
+            if (row < rows) {
                 // plain epilogue: a chain group has no fused relu^2 or residual
-                const uint16_t out = epilogue(v, global_ptr(grp.s)[row], kEpiNone, 0);
-                NMI_GLOBAL uint16_t* yp = global_ptr(grp.y) + row;
-                if (coherent_out) __hip_atomic_store(yp, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint16_t out = epilogue(v, global_ptr(it.s)[row], kEpiNone, 0);
+                NMI_GLOBAL uint16_t* yp = global_ptr(it.y) + row;
+                if (signal) __hip_atomic_store(yp, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 else *yp = out;
             }
         }
         // completion (counted when a later phase waits on this one): the stores have completed,
         // then the count
-        if (ph.signal) {
+        if (signal) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             if (tid == 0) {
-                const int n = ph.nitems;
-                const int stripe = local % kChainStripes;
-                const uint32_t v = __hip_atomic_fetch_add(chain_line(ctr, p, stripe), 1u, __ATOMIC_RELAXED,
+                const uint32_t v = __hip_atomic_fetch_add(chain_line(ctr, it.phase, it.stripe), 1u, __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_AGENT);
-                if (v + 1 == (uint32_t)((n - stripe + kChainStripes - 1) / kChainStripes))
-                    __hip_atomic_fetch_add(chain_line(ctr, p, kChainStripes), 1u, __ATOMIC_RELAXED,
+                if (v + 1 == (uint32_t)it.stripe_items)
+                    __hip_atomic_fetch_add(chain_line(ctr, it.phase, kChainStripes), 1u, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
             }
         }
@@ -694,6 +685,35 @@ int gemv_chain_plan(ChainPhase* phases, int nphases, size_t* lds_bytes) {
     return items;
 }
 
+void gemv_chain_items(const ChainPhase* planned, int nphases, ChainItem* out) {
+    int k = 0;
+    for (int p = 0; p < nphases; ++p) {
+        const ChainPhase& ph = planned[p];
+        const int rows_per_item = (kWaves / ph.ks) * kChainT;
+        int local = 0;
+        for (int gi = 0; gi < ph.ngroups; ++gi) {
+            const GemvGroup& grp = ph.g[gi];
+            for (int r0 = 0; r0 < grp.N; r0 += rows_per_item, ++local, ++k) {
+                ChainItem& it = out[k];
+                it.w = grp.W + (int64_t)r0 * grp.ldw;
+                it.x = ph.x;
+                it.y = grp.y + r0;
+                it.s = grp.s + r0;
+                it.ldw = grp.ldw;
+                it.rows = grp.N - r0 < rows_per_item ? grp.N - r0 : rows_per_item;
+                it.K = ph.K;
+                it.ks = ph.ks;
+                it.window = ph.window;
+                it.phase = p;
+                it.flags = (p > 0 && ph.wait ? kChainWait : 0) | (ph.signal ? kChainSignal : 0);
+                it.wait_need = p > 0 ? (planned[p - 1].nitems < kChainStripes ? planned[p - 1].nitems : kChainStripes) : 0;
+                it.stripe = local % kChainStripes;
+                it.stripe_items = (ph.nitems - it.stripe + kChainStripes - 1) / kChainStripes;
+            }
+        }
+    }
+}
+
 hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid) {
     const DeviceInfo& dev = device_info();
     int per_cu = 0;
@@ -709,12 +729,12 @@ hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid) {
     return hipSuccess;
 }
 
-hipError_t launch_gemv_chain(const ChainPhase* phases, int nphases, int total_items, int grid, size_t lds_bytes,
+hipError_t launch_gemv_chain(const ChainItem* items, int nphases, int total_items, int grid, size_t lds_bytes,
                              uint32_t* ctr, hipStream_t stream) {
     // the bound of a wait: 0.2 s, or tuning knob chain.wait_us (microseconds) when set
     const uint64_t wait_ticks = tuning().chain_wait_us > 0 ? (uint64_t)tuning().chain_wait_us * 100u : 20000000ull;
     hipLaunchKernelGGL((gemv_chain_kernel<kChainT, kChainP>), dim3(grid), dim3(256), lds_bytes, stream,
-                       phases, nphases, total_items, ctr, wait_ticks);
+                       items, nphases, total_items, ctr, wait_ticks);
     return hipGetLastError();
 }
 

@@ -126,6 +126,29 @@ struct ChainPhase {
 // Fills the derived fields of phases[0..n) and returns the number of work items; *lds_bytes
 // receives the dynamic LDS the launch needs.
 int gemv_chain_plan(ChainPhase* phases, int nphases, size_t* lds_bytes);
+// One work item of a planned chain, everything its workgroup needs in one 80-byte record (read
+// with scalar loads and no dependent lookups: walking a phase table per item cost about 10% of
+// the chain's streaming rate): the item's rows of one group.
+struct ChainItem {
+    const uint8_t* w;       // first weight row of the item
+    const uint16_t* x;      // the phase's activations [K]
+    uint16_t* y;            // output of the item's first row
+    const float* s;         // scale of the item's first row
+    int64_t ldw;
+    int rows;               // rows of the item that exist (the last item of a group may be short)
+    int K;
+    int ks;                 // waves splitting K (1, 2, 4)
+    int window;             // x chunks per LDS window
+    int phase;
+    int flags;              // kChainWait | kChainSignal
+    int wait_need;          // done count of the previous phase that completes it
+    int stripe;             // completion stripe of the item
+    int stripe_items;       // items of the phase in that stripe
+};
+static_assert(sizeof(ChainItem) == 80, "one 80-byte record per item");
+enum : int { kChainWait = 1, kChainSignal = 2 };
+// The items of planned phases[0..n) in order (out: the count gemv_chain_plan returned).
+void gemv_chain_items(const ChainPhase* planned, int nphases, ChainItem* out);
 // Counter workspace of a chain: per phase kChainStripes stripe counters and one done counter,
 // then kChainStripes exit counters and one exit-done counter, each on its own 128-byte line;
 // the last line (an even number of lines: a multiple of 256 bytes) holds the error word; zero
@@ -142,8 +165,8 @@ inline size_t gemv_chain_counter_bytes(int nphases) {
 // device (the workgroups wait on each other's items) and at most 4 per CU (tuning knob
 // chain.wgs sets that cap).
 hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid);
-// phases: the planned table in device memory; ctr: gemv_chain_counter_bytes(nphases) bytes.
-hipError_t launch_gemv_chain(const ChainPhase* phases, int nphases, int total_items, int grid, size_t lds_bytes,
+// items: the item table in device memory; ctr: gemv_chain_counter_bytes(nphases) bytes.
+hipError_t launch_gemv_chain(const ChainItem* items, int nphases, int total_items, int grid, size_t lds_bytes,
                              uint32_t* ctr, hipStream_t stream);
 
 // Prefill GEMM.  Given a workspace of at least gemm_workspace_bytes(M) bytes whose first 64 KiB
