@@ -119,6 +119,18 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
     const int C = args.K >> 4;              // 16-byte weight chunks per row
     const int window = XG ? C : args.window;
 
+    // The epilogue operands of this lane (lane t * MR + m stores row row_base + t of activation
+    // row m), loaded before everything else: they arrive with the weights instead of after them,
+    // and the residual is read before any store (y may be the residual).
+    const int st_t = lane / MR, st_m = lane % MR, st_row = row_base + st_t;
+    const bool st_lane = lane < T * MR && st_row < grp.N && st_m < args.M && (KS == 1 || q == 0);
+    float st_s = 0.f;
+    uint16_t st_res = 0;
+    if (st_lane) {
+        st_s = grp.s[st_row];
+        if (grp.epi.kind == kEpiResidual) st_res = grp.epi.res[(int64_t)st_m * grp.epi.ldres + st_row];
+    }
+
     // Row t of this wave; rows past N read row N-1 (in bounds) and never store.
     const uint8_t* __restrict__ wrow[T];
 #pragma unroll
@@ -303,13 +315,7 @@ __global__ __launch_bounds__(256) void gemv_fp8_m1_kernel(const GemvArgs args) {
 #pragma unroll
             for (int m = 0; m < MR; ++m)
                 if (lane == t * MR + m) v = sums[t][m];
-        const int t = lane / MR, m = lane % MR;
-        const int row = row_base + t;
-        if (row < grp.N && m < args.M) {
-            const int64_t o = (int64_t)m * grp.epi.ldres + row;
-            grp.y[(int64_t)m * grp.ldy + row] =
-                epilogue(v, grp.s[row], grp.epi.kind, grp.epi.kind == kEpiResidual ? grp.epi.res[o] : 0);
-        }
+        if (st_lane) grp.y[(int64_t)st_m * grp.ldy + st_row] = epilogue(v, st_s, grp.epi.kind, st_res);
     }
 }
 
@@ -469,6 +475,10 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainItem* __rest
         const bool wait = it.flags & kChainWait, signal = it.flags & kChainSignal;
         const NMI_GLOBAL uint8_t* gW = global_ptr(it.w);
 
+        // this lane's row scale (lane t < T of a K-slice-0 wave), issued before the weights so that
+        // it has arrived with them
+        float sc = 0.f;
+        if (q == 0 && lane < T && row0 + lane < rows) sc = global_ptr(it.s)[row0 + lane];
         const NMI_GLOBAL uint8_t* wrow[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) wrow[t] = gW + (int64_t)min(row0 + t, rows - 1) * ldw;
@@ -556,7 +566,7 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainItem* __rest
             const int row = row0 + t;
             if (row < rows) {
                 // plain epilogue: a chain group has no fused relu^2 or residual
-                const uint16_t out = epilogue(v, global_ptr(it.s)[row], kEpiNone, 0);
+                const uint16_t out = epilogue(v, sc, kEpiNone, 0);
                 NMI_GLOBAL uint16_t* yp = global_ptr(it.y) + row;
                 if (signal) __hip_atomic_store(yp, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 else *yp = out;
