@@ -133,6 +133,9 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
  *                           first use (every launch leaves it zero again).  Launches that may
  *                           overlap in time need distinct workspaces.  Capturable in a HIP graph.
  *   nmi_gemv_chain_destroy  frees the plan.
+ * Buffers: a phase's output may overlap another phase's x or output only when every phase after
+ * the earlier of the two, up to the later, has wait_prev = 1 (a phase without it may run at the
+ * same time as the phases before it).
  * The launch is a persistent grid of at most the workgroups that are resident at once, whose
  * workgroups wait on each other's phases: run it with no other long-running kernel sharing the
  * device (another chain on a concurrent stream may hold the slots a waiting phase needs).  A
