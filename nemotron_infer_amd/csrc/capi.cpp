@@ -182,7 +182,7 @@ int nmi_linear_fp8_w8a16_ws(const void* x_bf16, int64_t ldx, const void* w_e4m3,
     if (rc) return rc;
     if (workspace && !aligned(workspace, 256))
         return fail(NMI_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", fn);
-    GemvGroup g{static_cast<const uint8_t*>(w_e4m3), ldw, w_scale, static_cast<uint16_t*>(y_bf16), ldy, N, 0, 0};
+    GemvGroup g{static_cast<const uint8_t*>(w_e4m3), ldw, w_scale, static_cast<uint16_t*>(y_bf16), ldy, N, 0, 0, Epi{}};
     return dispatch(static_cast<const uint16_t*>(x_bf16), ldx, M, K, &g, 1, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream), fn);
 }
@@ -203,7 +203,7 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
         int rc = check_linear(x_bf16, ldx, G.w_e4m3, G.ldw, G.w_scale, G.y_bf16, G.ldy, M, G.N, K, fn);
         if (rc) return rc;
         g[i] = GemvGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
-                         static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0};
+                         static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0, Epi{}};
     }
     return dispatch(static_cast<const uint16_t*>(x_bf16), ldx, M, K, g, ngroups, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream), fn);
@@ -243,7 +243,7 @@ int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_ch
             int rc = check_linear(P.x_bf16, P.K, G.w_e4m3, G.ldw, G.w_scale, G.y_bf16, G.ldy, 1, G.N, P.K, fn);
             if (rc) return rc;
             ph.g[i] = GemvGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
-                                static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0};
+                                static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0, Epi{}};
             items += (G.N + 3) / 4;                   // upper bound of the work items (4 rows each)
         }
     }

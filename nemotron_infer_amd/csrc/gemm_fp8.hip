@@ -742,7 +742,9 @@ constexpr size_t kDmaPartialBytes = (size_t)256 * 256 * sizeof(float);   // one 
 // 16 bytes per lane from base + off to LDS [lds_addr + 16 lane].  Inline asm so that the
 // compiler does not track the LDS write (it would wait for every outstanding DMA before any
 // LDS read); completion is waited for with an explicit vmcnt before the barrier that
-// publishes the stage.
+// publishes the stage.  m0 is set in the statement and listed as clobbered; the compiler warns
+// that it may not preserve a reserved register across it, and no compiler-generated code of
+// this file uses m0 (checked in its assembly), so nothing lives there to be lost.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
                  : "memory", "m0");
@@ -1053,7 +1055,6 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         // Stream-K as in the 8-wave kernel: per-XCD problems, each workgroup a contiguous range
         // of (tile, k tile) steps walked backwards; the workgroup holding a tile's last k tile
         // finishes it with the partials of the others (slot = their workgroup id).
-        constexpr int ACC = TN * TM * 16;
         const int g = (int)blockIdx.x;
         const int Gx = (int)gridDim.x >> 3;
         const int xcd = g & 7, v = g >> 3;

@@ -438,7 +438,9 @@ __device__ __forceinline__ uint4 load_stream16_g(const NMI_GLOBAL uint8_t* p) {
 // 16 bytes per lane from global memory straight into LDS (64 lanes: 1 KiB at lds_addr, in lane
 // order), with no register staging; the plain form, or at device scope (sc1) for an earlier
 // phase's output.  The compiler does not track these loads: completion is waited for with an
-// explicit vmcnt.
+// explicit vmcnt.  m0 is set in the statement and listed as clobbered; the compiler warns that it
+// may not preserve a reserved register across it, and no compiler-generated code of this file
+// uses m0 (checked in its assembly), so nothing lives there to be lost.
 __device__ __forceinline__ void dma16_lds(const void* base, uint32_t off, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
                  : "memory", "m0");
@@ -505,7 +507,7 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainItem* __rest
                     const uint32_t* done = chain_line(ctr, it.phase - 1, kChainStripes);
                     const uint64_t t_end = wall_clock64() + wait_ticks;   // wall clock: 100 MHz
                     while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-                        if (wall_clock64() > t_end) {
+                        if ((uint64_t)wall_clock64() > t_end) {
                             __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             break;
                         }
@@ -755,7 +757,7 @@ hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* gro
 
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream) {
-    GemvGroup g{W, ldw, s, y, N, N, 0, 0};
+    GemvGroup g{W, ldw, s, y, N, N, 0, 0, Epi{}};
     return launch_gemv_m1_grouped(x, K, &g, 1, stream);
 }
 
