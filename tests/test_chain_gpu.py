@@ -10,7 +10,8 @@
   phase): results and re-armed counters stay right over repeated launches.
 * The same with one workgroup per CU (tuning knob chain.wgs = 1), so that every workgroup runs
   many items of several phases in turn.
-* Independent phases with K beyond one x window (several windows per work item).
+* Independent phases with K beyond one x window (several windows per work item); phases of four
+  groups with ragged and single-row groups.
 * A forced timeout (wait bound of 1 us) completes, sets the error word and re-arms the counters;
   the chain is right again with the bound restored.
 * Graph replays (with eager work between them) equal the eager launch; every launch leaves the
@@ -163,6 +164,37 @@ def test_long_k_phases_take_several_windows(chain_wgs):
     xb = xs[0].view(torch.int16).cpu().numpy().view(np.uint16)[None]
     assert_parity(bits(ys[0].view(1, -1)), oracle_bits(xb, ws[0][0].cpu().numpy(), ws[0][1].cpu().numpy()),
                   "K = 20480 vs oracle")
+
+
+def test_four_group_phases_and_single_rows(chain_wgs):
+    """Phases of the maximum four groups with ragged N (1, 3, 17, 200 rows), a dependent phase
+    reading the first group's output, and a single-row phase: each group byte-identical to its
+    own launch."""
+    announce("chain_groups", chain_wgs)
+    K0 = 256
+    g0 = [_w(N, K0, 700 + i, "log_uniform") for i, N in enumerate((1, 3, 17, 200))]
+    x0 = _x(K0, 710)
+    y0 = [torch.empty(w.shape[0], dtype=torch.bfloat16, device=DEV) for w, _ in g0]
+    w1 = _w(64, 200, 711, "log_uniform")        # reads group 3's output (200 values)
+    y1 = torch.empty(64, dtype=torch.bfloat16, device=DEV)
+    w2 = _w(1, 1024, 712)                       # one row, independent x
+    x2 = _x(1024, 713)
+    y2 = torch.empty(1, dtype=torch.bfloat16, device=DEV)
+    chain = ops.GemvChain([(x0, [(w, s, y) for (w, s), y in zip(g0, y0)], False),
+                           (y0[3], [(*w1, y1)], True), (x2, [(*w2, y2)], False)])
+    for rep in range(3):
+        for y in y0 + [y1, y2]:
+            y.fill_(9.0)
+        chain.launch()
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(chain.workspace) == 0
+        for i, ((w, s), y) in enumerate(zip(g0, y0)):
+            r = ops.linear_fp8_w8a16(x0.view(1, -1), w, s).view(-1)
+            assert torch.equal(y.view(torch.int16), r.view(torch.int16)), (rep, i)
+        r1 = ops.linear_fp8_w8a16(y0[3].view(1, -1), *w1).view(-1)
+        assert torch.equal(y1.view(torch.int16), r1.view(torch.int16)), rep
+        r2 = ops.linear_fp8_w8a16(x2.view(1, -1), *w2).view(-1)
+        assert torch.equal(y2.view(torch.int16), r2.view(torch.int16)), rep
 
 
 def test_wait_bound_sets_the_error_word():
