@@ -167,15 +167,15 @@ def test_long_k_phases_take_several_windows(chain_wgs):
 
 
 def test_four_group_phases_and_single_rows(chain_wgs):
-    """Phases of the maximum four groups with ragged N (1, 3, 17, 200 rows), a dependent phase
+    """Phases of the maximum four groups with ragged N (1, 3, 17, 208 rows), a dependent phase
     reading the first group's output, and a single-row phase: each group byte-identical to its
     own launch."""
     announce("chain_groups", chain_wgs)
     K0 = 256
-    g0 = [_w(N, K0, 700 + i, "log_uniform") for i, N in enumerate((1, 3, 17, 200))]
+    g0 = [_w(N, K0, 700 + i, "log_uniform") for i, N in enumerate((1, 3, 17, 208))]
     x0 = _x(K0, 710)
     y0 = [torch.empty(w.shape[0], dtype=torch.bfloat16, device=DEV) for w, _ in g0]
-    w1 = _w(64, 200, 711, "log_uniform")        # reads group 3's output (200 values)
+    w1 = _w(64, 208, 711, "log_uniform")        # reads group 3's output (208 values)
     y1 = torch.empty(64, dtype=torch.bfloat16, device=DEV)
     w2 = _w(1, 1024, 712)                       # one row, independent x
     x2 = _x(1024, 713)
