@@ -53,8 +53,8 @@ ROTATION_BYTES = 1 << 30
 # script (scaled by a 256 MiB copy): the chain launch (profiles/gemv_chain_config1_decode_set.md)
 # and the four engine-structured launches (profiles/gemv_m1_config1_decode_set.md).  Re-measured
 # when the GEMV kernels change; reported as roofline.traffic next to the algorithmic bytes.
-MEASURED_TRAFFIC = {"chain": 118934566, "qkv_grouped": 22734903, "o_proj": 16316522, "up_proj": 39600751,
-                    "down_proj": 39770208}
+MEASURED_TRAFFIC = {"chain": 119086873, "qkv_grouped": 22735927, "o_proj": 16326761, "up_proj": 39600623,
+                    "down_proj": 39772640}
 
 
 def log(*a):
