@@ -1040,14 +1040,17 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
 
     if constexpr (!SK) {
         // One tile per workgroup, XCD-ordered: workgroup g runs on XCD g % 8, which takes the
-        // consecutive tiles [x * per_xcd, (x + 1) * per_xcd).
+        // consecutive tiles [x * per_xcd, (x + 1) * per_xcd) in column-band order (m fastest),
+        // so an XCD's tiles share few W column bands and less of W, the larger operand at
+        // these shapes, is fetched into each XCD's L2 (measured +2.5% on up_proj and q|k|v
+        // against n-fastest order).
         const int g = (int)blockIdx.x;
         const int local = g >> 3;
         const int tile = (g & 7) * a.per_xcd + local;
         if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
-        const int tm = tile / a.tiles_n;
-        m0 = tm * 256;
-        n0 = (tile - tm * a.tiles_n) * 256;
+        const int tn = tile / a.tiles_m;
+        m0 = (tile - tn * a.tiles_m) * 256;
+        n0 = tn * 256;
         zero_acc();
         run(0, KT);
         store();
