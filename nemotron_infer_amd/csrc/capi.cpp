@@ -354,6 +354,7 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s4.ks")) t.s4_ks = value;
     else if (!std::strcmp(knob, "s4.t")) t.s4_t = value;
     else if (!std::strcmp(knob, "s4.u")) t.s4_u = value;
+    else if (!std::strcmp(knob, "s4.dma")) t.s4_dma = value;
     else if (!std::strcmp(knob, "gemm.sk")) t.gemm_sk = value;
     else if (!std::strcmp(knob, "chain.wgs")) t.chain_wgs = value;
     else if (!std::strcmp(knob, "chain.wait_us")) t.chain_wait_us = value;

@@ -435,21 +435,6 @@ __device__ __forceinline__ uint4 load_stream16_g(const NMI_GLOBAL uint8_t* p) {
 // weight loads in flight).
 #define NMI_CONST __attribute__((address_space(4)))
 
-// 16 bytes per lane from global memory straight into LDS (64 lanes: 1 KiB at lds_addr, in lane
-// order), with no register staging; the plain form, or at device scope (sc1) for an earlier
-// phase's output.  The compiler does not track these loads: completion is waited for with an
-// explicit vmcnt.  m0 is set in the statement and listed as clobbered; the compiler warns that it
-// may not preserve a reserved register across it, and no compiler-generated code of this file
-// uses m0 (checked in its assembly), so nothing lives there to be lost.
-__device__ __forceinline__ void dma16_lds(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma16_lds_device(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc1" ::"v"(off), "s"(base), "s"(lds_addr)
-                 : "memory", "m0");
-}
-
 __device__ __forceinline__ int chain_stripes(int nitems) { return nitems < kChainStripes ? nitems : kChainStripes; }
 
 template <int T, int P>

@@ -166,4 +166,19 @@ __device__ __forceinline__ uint4 load16(const void* p) {
     return *reinterpret_cast<const uint4*>(p);
 }
 
+// 16 bytes per lane from global memory straight into LDS (64 lanes: 1 KiB at lds_addr, in lane
+// order), with no register staging; the plain form, or at device scope (sc1) for an earlier
+// phase's output.  The compiler does not track these loads: completion is waited for with an
+// explicit vmcnt.  m0 is set in the statement and listed as clobbered; the compiler warns that it
+// may not preserve a reserved register across it, and no compiler-generated code of the files that
+// use it uses m0 (checked in their assembly), so nothing lives there to be lost.
+__device__ __forceinline__ void dma16_lds(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_lds_device(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc1" ::"v"(off), "s"(base), "s"(lds_addr)
+                 : "memory", "m0");
+}
+
 }  // namespace nmi

@@ -39,6 +39,7 @@ struct Tuning {
     int s4_ks = 0;         // 4x4x4 skinny kernel: waves splitting K (1, 2, 4)
     int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
+    int s4_dma = 0;        // 4x4x4 skinny kernel: 0 pipelined form where it applies, 2 windowed form
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
     int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 4, or fewer if fewer are resident)
     int chain_wait_us = 0; // GEMV chain: bound of a wait in microseconds (0: 200000)

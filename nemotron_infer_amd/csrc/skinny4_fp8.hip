@@ -46,6 +46,80 @@ __device__ __forceinline__ bf16x4 as_bf16x4(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(bf16x4, uint2{lo, hi});
 }
 
+// The end of both forms: the 16 MFMA blocks of a lane group summed across lanes, the KS waves'
+// partials summed in order through LDS, then the scale, one bf16 rounding and the epilogue.
+template <int KS, int T, int G>
+__device__ __forceinline__ void skinny4_finish(f32x4 (&acc)[T][G], f32x4 (&partial)[KS > 1 ? KS : 1][kWaves / KS][T][G][4],
+                                               const GemvGroup& grp, int M, int row_base, int q, int gw, int lane,
+                                               int li) {
+    // Sum the 16 blocks (lanes with equal lane % 4) in a fixed order: xor 4, 8, 16, 32.
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[t][g][r];
+                v += __shfl_xor(v, 4);
+                v += __shfl_xor(v, 8);
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                acc[t][g][r] = v;
+            }
+    // Lane li (block 0) holds D[r][li] = rows 4 t + r, activation row 4 g + li.
+    if constexpr (KS > 1) {
+        if (lane < 4) {
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int g = 0; g < G; ++g) partial[q][gw][t][g][li] = acc[t][g];
+        }
+        __syncthreads();
+        if (q != 0) return;
+        if (lane < 4) {
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    f32x4 v = partial[0][gw][t][g][li];
+#pragma unroll
+                    for (int qq = 1; qq < KS; ++qq) {
+                        const f32x4 p = partial[qq][gw][t][g][li];
+                        v = f32x4{v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w};
+                    }
+                    acc[t][g] = v;
+                }
+        }
+    }
+    if (lane < 4) {
+        // residuals first (clamped in bounds), then the stores
+        uint16_t rres[T][G][4];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    rres[t][g][r] = grp.epi.kind == kEpiResidual
+                                        ? grp.epi.res[(int64_t)min(4 * g + li, M - 1) * grp.epi.ldres +
+                                                      min(row_base + 4 * t + r, grp.N - 1)]
+                                        : 0;
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int m = 4 * g + li;
+                if (m >= M) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = row_base + 4 * t + r;
+                    if (n < grp.N)
+                        grp.y[(int64_t)m * grp.ldy + n] = epilogue(acc[t][g][r], grp.s[n], grp.epi.kind, rres[t][g][r]);
+                }
+            }
+    }
+}
+
 // KS: waves splitting K; T: row groups (4 rows each) per wave; U: chunks per lane per batch;
 // G: groups of 4 activation rows (M <= 4 G).
 template <int KS, int T, int U, int G>
@@ -167,81 +241,201 @@ __global__ __launch_bounds__(256) void skinny4_fp8_kernel(const Skinny4Args a) {
         }
     }
 
-    // Sum the 16 blocks (lanes with equal lane % 4) in a fixed order: xor 4, 8, 16, 32.
+    skinny4_finish<KS, T, G>(acc, partial, grp, M, row_base, q, gw, lane, li);
+}
+
+// Waits until at most N vector memory loads of this wave are outstanding and every LDS access
+// has completed, then s_barrier.  Loads complete in issue order, so N = the loads issued after
+// the ones that must have landed.
+template <int N>
+__device__ __forceinline__ void wait_loads_barrier() {
+    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Pipelined form.  The same lane layout, products, reduction and epilogue; K is walked in
+// windows of 16 U KS chunks, one batch of U chunks per lane for each of the KS waves splitting a
+// window, and the x windows are staged by LDS DMA (no register staging) into two buffers, so
+// that the weights and activations of window w + 1 are in flight while window w is multiplied.
+// Buffer layout: [4 G rows m][2 halves h][kS words] of 16 bytes; word c of row (m, h) holds
+// x[m][16 (w0 + c) + 8 h .. + 8].  kS == 2 (mod 16): the 16 lanes (blk 4p..4p+3, li 0..3) of a
+// quarter of one 16-byte read fall in distinct bank groups.  Rows m >= M hold copies of row M - 1
+// (their products land only in outputs that are not stored); words past the end of K hold zeros
+// (their weight chunks are clamped copies of the row's last chunk).
+template <int KS, int T, int U, int G>
+__global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    extern __shared__ uint4 xw[];
+    constexpr int kRowGroups = kWaves / KS;
+    constexpr int kRowsPerWave = 4 * T;
+    constexpr int kRowsPerWG = kRowGroups * kRowsPerWave;
+    constexpr int kWin = 16 * U * KS;                  // chunks per window
+    constexpr int kS = kWin + 2;                       // words per (m, h) row of a buffer
+    constexpr int kBuf = 4 * G * 2 * kS;               // words per buffer
+    constexpr int kBlk = kWin < 64 ? kWin : 64;        // chunks per DMA instruction
+    constexpr int kBlkPerRow = kWin / kBlk;
+    constexpr int kJobs = 4 * G * 2 * kBlkPerRow;      // DMA instructions per window
+    __shared__ f32x4 partial[KS > 1 ? KS : 1][kRowGroups][T][G][4];
+
+    int gi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < a.ngroups && (int)blockIdx.x >= a.g[i].wg_begin) gi = i;
+    const GemvGroup grp = a.g[gi];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int gw = wave / KS;
+    const int q = wave % KS;
+    const int blk = lane >> 2;
+    const int li = lane & 3;
+    const int row_base = ((int)blockIdx.x - grp.wg_begin) * kRowsPerWG + gw * kRowsPerWave;
+    const int M = a.M;
+    const int C = a.K >> 4;
+    const int nw = (C + kWin - 1) / kWin;
+    const uint32_t xw_addr = (uint32_t)(uintptr_t)(lds_void*)xw;
+
+    const uint8_t* __restrict__ wrow[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) wrow[t] = grp.W + (int64_t)min(row_base + 4 * t + li, grp.N - 1) * grp.ldw;
+
+    f32x4 acc[T][G];
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = acc[t][g][r];
-                v += __shfl_xor(v, 4);
-                v += __shfl_xor(v, 8);
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
-                acc[t][g][r] = v;
+        for (int g = 0; g < G; ++g) acc[t][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // x window w into buffer b: job j = (row r = (m, h), block) has lane l copy chunk
+    // 64 block + l of the row; lanes past the end of K write zeros instead
+    auto stage = [&](int w, int b) {
+        const int w0 = w * kWin;
+        const int wc = min(kWin, C - w0);
+        for (int j = wave; j < kJobs; j += kWaves) {
+            const int r = j / kBlkPerRow;
+            const int c = (j - r * kBlkPerRow) * kBlk + lane;
+            const int m = min(r >> 1, M - 1);
+            const int word = b * kBuf + r * kS + c - lane;
+            if (lane < kBlk) {
+                if (c < wc)
+                    dma16_lds(a.x, (uint32_t)(((int64_t)m * a.ldx + (int64_t)(w0 + c) * 16 + 8 * (r & 1)) * 2),
+                              xw_addr + (uint32_t)word * 16);
+                else
+                    xw[word + lane] = uint4{0, 0, 0, 0};
             }
-    // Lane li (block 0) holds D[r][li] = rows 4 t + r, activation row 4 g + li.
-    if constexpr (KS > 1) {
-        if (lane < 4) {
-#pragma unroll
-            for (int t = 0; t < T; ++t)
-#pragma unroll
-                for (int g = 0; g < G; ++g) partial[q][gw][t][g][li] = acc[t][g];
         }
-        __syncthreads();
-        if (q != 0) return;
-        if (lane < 4) {
-#pragma unroll
-            for (int t = 0; t < T; ++t)
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    f32x4 v = partial[0][gw][t][g][li];
-#pragma unroll
-                    for (int qq = 1; qq < KS; ++qq) {
-                        const f32x4 p = partial[qq][gw][t][g][li];
-                        v = f32x4{v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w};
-                    }
-                    acc[t][g] = v;
-                }
-        }
-    }
-    if (lane < 4) {
-        // residuals first (clamped in bounds), then the stores
-        uint16_t rres[T][G][4];
+    };
+    // this wave's batch of window w: lane 4 blk + li loads chunk (window slice q) + blk + 16 u of
+    // row 4 t + li.  Issued as explicit instructions: the compiler's own wait counts would merge
+    // the paths into the loop (with and without a next window in flight) and wait for the next
+    // window's loads too; completion is waited for by wait_loads_barrier and pinned by pin().
+    auto load_w = [&](u32x4 (&wv)[T][U], int w) {
+        const int cb = w * kWin + q * 16 * U + blk;
 #pragma unroll
         for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                asm volatile("global_load_dwordx4 %0, %1, off nt"
+                             : "=v"(wv[t][u])
+                             : "v"(wrow[t] + (int64_t)min(cb + 16 * u, C - 1) * 16)
+                             : "memory");
+    };
+    // after a wait: the registers are read only from here on
+    auto pin = [&](u32x4 (&wv)[T][U]) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int u = 0; u < U; ++u) asm volatile("" : "+v"(wv[t][u]));
+    };
+    auto consume = [&](const u32x4 (&wv)[T][U], int b) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int cl = q * 16 * U + blk + 16 * u;
+            uint4 xb[G][2];
 #pragma unroll
             for (int g = 0; g < G; ++g)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    rres[t][g][r] = grp.epi.kind == kEpiResidual
-                                        ? grp.epi.res[(int64_t)min(4 * g + li, M - 1) * grp.epi.ldres +
-                                                      min(row_base + 4 * t + r, grp.N - 1)]
-                                        : 0;
+                for (int h = 0; h < 2; ++h) xb[g][h] = xw[b * kBuf + ((4 * g + li) * 2 + h) * kS + cl];
 #pragma unroll
-        for (int t = 0; t < T; ++t)
+            for (int t = 0; t < T; ++t) {
+                const u32x4 w = wv[t][u];
+                const uint2 p0 = e4m3x4_to_bf16(w[0]), p1 = e4m3x4_to_bf16(w[1]);
+                const uint2 p2 = e4m3x4_to_bf16(w[2]), p3 = e4m3x4_to_bf16(w[3]);
+                const bf16x4 A0 = as_bf16x4(p0.x, p0.y), A1 = as_bf16x4(p1.x, p1.y);
+                const bf16x4 A2 = as_bf16x4(p2.x, p2.y), A3 = as_bf16x4(p3.x, p3.y);
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const int m = 4 * g + li;
-                if (m >= M) continue;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int n = row_base + 4 * t + r;
-                    if (n < grp.N)
-                        grp.y[(int64_t)m * grp.ldy + n] = epilogue(acc[t][g][r], grp.s[n], grp.epi.kind, rres[t][g][r]);
+                for (int g = 0; g < G; ++g) {
+                    acc[t][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A0, as_bf16x4(xb[g][0].x, xb[g][0].y), acc[t][g], 0, 0, 0);
+                    acc[t][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A1, as_bf16x4(xb[g][0].z, xb[g][0].w), acc[t][g], 0, 0, 0);
+                    acc[t][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A2, as_bf16x4(xb[g][1].x, xb[g][1].y), acc[t][g], 0, 0, 0);
+                    acc[t][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A3, as_bf16x4(xb[g][1].z, xb[g][1].w), acc[t][g], 0, 0, 0);
                 }
             }
+        }
+    };
+
+    // Two windows in flight: (wa, buffer 0) holds the even windows, (wb, buffer 1) the odd ones.
+    // Each window's x DMA is issued before its weights, so waiting until only the next window's
+    // weight loads are outstanding covers this window's weights and both windows' x.
+    u32x4 wa[T][U], wb[T][U];
+    stage(0, 0);
+    load_w(wa, 0);
+    if (nw > 1) {
+        stage(1, 1);
+        load_w(wb, 1);
     }
+    for (int w = 0;; w += 2) {
+        if (w + 1 < nw) wait_loads_barrier<T * U>();
+        else wait_loads_barrier<0>();
+        pin(wa);
+        consume(wa, 0);
+        if (w + 1 >= nw) break;
+        asm volatile("s_barrier" ::: "memory");        // every wave is done reading buffer 0
+        if (w + 2 < nw) {
+            stage(w + 2, 0);
+            load_w(wa, w + 2);
+            wait_loads_barrier<T * U>();
+        } else {
+            wait_loads_barrier<0>();
+        }
+        pin(wb);
+        consume(wb, 1);
+        if (w + 2 >= nw) break;
+        asm volatile("s_barrier" ::: "memory");        // every wave is done reading buffer 1
+        if (w + 3 < nw) {
+            stage(w + 3, 1);
+            load_w(wb, w + 3);
+        }
+    }
+
+    skinny4_finish<KS, T, G>(acc, partial, grp, M, row_base, q, gw, lane, li);
 }
 
+// Dynamic LDS of the pipelined form: two windows of 4 G x 2 rows of 16 U KS + 2 words (the
+// static partial sums take at most 2 KiB of the 160 KiB).
+constexpr size_t dma_lds_bytes(int KS, int U, int G) { return 2 * (size_t)(8 * G) * (16 * U * KS + 2) * 16; }
+constexpr size_t kDmaLdsMax = 156 * 1024;
+
 template <int KS, int T, int U, int G>
-hipError_t launch_cfg(Skinny4Args& a, hipStream_t stream) {
+hipError_t launch_cfg(Skinny4Args& a, bool dma, hipStream_t stream) {
     constexpr int rows_per_wg = (kWaves / KS) * 4 * T;
     int wgs = 0;
     for (int i = 0; i < a.ngroups; ++i) {
         a.g[i].wg_begin = wgs;
         wgs += (a.g[i].N + rows_per_wg - 1) / rows_per_wg;
+    }
+    if constexpr (dma_lds_bytes(KS, U, G) <= kDmaLdsMax) {
+        if (dma) {
+            constexpr size_t lds = dma_lds_bytes(KS, U, G);
+            constexpr auto kernel = &skinny4_dma_kernel<KS, T, U, G>;
+            if constexpr (lds > 64 * 1024) {
+                static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (attr != hipSuccess) return attr;
+            }
+            hipLaunchKernelGGL(kernel, dim3(wgs), dim3(256), lds, stream, a);
+            return hipGetLastError();
+        }
     }
     const size_t lds = ((size_t)a.M * 4 * a.xs_stride + 1) * sizeof(uint2);
     hipLaunchKernelGGL((skinny4_fp8_kernel<KS, T, U, G>), dim3(wgs), dim3(256), lds, stream, a);
@@ -249,24 +443,24 @@ hipError_t launch_cfg(Skinny4Args& a, hipStream_t stream) {
 }
 
 template <int KS, int T, int U>
-hipError_t launch_g(int M, Skinny4Args& a, hipStream_t stream) {
-    if (M <= 4) return launch_cfg<KS, T, U, 1>(a, stream);
-    if (M <= 8) return launch_cfg<KS, T, U, 2>(a, stream);
-    return launch_cfg<KS, T, U, 4>(a, stream);
+hipError_t launch_g(int M, Skinny4Args& a, bool dma, hipStream_t stream) {
+    if (M <= 4) return launch_cfg<KS, T, U, 1>(a, dma, stream);
+    if (M <= 8) return launch_cfg<KS, T, U, 2>(a, dma, stream);
+    return launch_cfg<KS, T, U, 4>(a, dma, stream);
 }
 
 template <int KS, int T>
-hipError_t launch_u(int u, int M, Skinny4Args& a, hipStream_t stream) {
+hipError_t launch_u(int u, int M, Skinny4Args& a, bool dma, hipStream_t stream) {
     switch (u) {
-        case 2: return launch_g<KS, T, 2>(M, a, stream);
-        case 4: return launch_g<KS, T, 4>(M, a, stream);
-        default: return launch_g<KS, T, 8>(M, a, stream);
+        case 2: return launch_g<KS, T, 2>(M, a, dma, stream);
+        case 4: return launch_g<KS, T, 4>(M, a, dma, stream);
+        default: return launch_g<KS, T, 8>(M, a, dma, stream);
     }
 }
 
 template <int KS>
-hipError_t launch_t(int t, int u, int M, Skinny4Args& a, hipStream_t stream) {
-    return t == 2 ? launch_u<KS, 2>(u, M, a, stream) : launch_u<KS, 1>(u, M, a, stream);
+hipError_t launch_t(int t, int u, int M, Skinny4Args& a, bool dma, hipStream_t stream) {
+    return t == 2 ? launch_u<KS, 2>(u, M, a, dma, stream) : launch_u<KS, 1>(u, M, a, dma, stream);
 }
 
 }  // namespace
@@ -293,6 +487,25 @@ hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, 
     // start in different 64-byte bank groups.
     a.xs_stride = ((a.window + 5) & ~7) + 2;
     const Tuning& tn = tuning();
+    // The pipelined form needs 16-byte x rows (LDS DMA) with 32-bit byte offsets.
+    const bool dma_ok = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ldx & 7) == 0 &&
+                        (int64_t)M * ldx * 2 < ((int64_t)1 << 32);
+    if (dma_ok && tn.s4_dma != 2) {
+        // one batch of U chunks per lane per window; KS = 1 and T = 1 keep the most workgroups
+        // and the LDS to two windows of 64 (M > 4) or 128 chunks (measured on config 2: K split
+        // between waves widens the window and halves the workgroups per CU)
+        int ks = 1, t = 1, u = M > 4 ? 4 : 8;
+        if (tn.s4_ks == 1 || tn.s4_ks == 2 || tn.s4_ks == 4) ks = tn.s4_ks;
+        if (tn.s4_t == 1 || tn.s4_t == 2) t = tn.s4_t;
+        if (tn.s4_u == 2 || tn.s4_u == 4 || tn.s4_u == 8) u = tn.s4_u;
+        if (dma_lds_bytes(ks, u, (M + 3) / 4) <= kDmaLdsMax) {
+            switch (ks) {
+                case 1: return launch_t<1>(t, u, M, a, true, stream);
+                case 2: return launch_t<2>(t, u, M, a, true, stream);
+                default: return launch_t<4>(t, u, M, a, true, stream);
+            }
+        }
+    }
     // K split inside the workgroup so that a lane has 2-8 chunks per window; T = 2 when there
     // are enough rows to keep ~3 workgroups per CU.
     const int slice = a.window;
@@ -305,9 +518,9 @@ hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, 
     int u = per_lane <= 2 ? 2 : (per_lane <= 4 ? 4 : 8);
     if (tn.s4_u == 2 || tn.s4_u == 4 || tn.s4_u == 8) u = tn.s4_u;
     switch (ks) {
-        case 1: return launch_t<1>(t, u, M, a, stream);
-        case 2: return launch_t<2>(t, u, M, a, stream);
-        default: return launch_t<4>(t, u, M, a, stream);
+        case 1: return launch_t<1>(t, u, M, a, false, stream);
+        case 2: return launch_t<2>(t, u, M, a, false, stream);
+        default: return launch_t<4>(t, u, M, a, false, stream);
     }
 }
 

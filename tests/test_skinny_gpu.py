@@ -21,7 +21,8 @@ from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_t
 
 pytestmark = pytest.mark.gpu
 
-KNOBS = ("skinny.ks", "skinny.kg", "skinny.u", "m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u")
+KNOBS = ("skinny.ks", "skinny.kg", "skinny.u", "m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u",
+         "s4.dma")
 
 
 @pytest.fixture(autouse=True)
@@ -64,17 +65,18 @@ def test_fixtures_all_m(name, use_ws, path):
 
 @pytest.mark.parametrize("M", list(range(1, 17)))
 def test_every_m_ragged(M):
-    """Ragged N (not a multiple of 4, 16 or 64) and K (not a multiple of 64), both kernels and
-    both workspace modes."""
+    """Ragged N (not a multiple of 4, 16 or 64) and K (not a multiple of 64), both kernels (the
+    4x4x4 one in both forms) and both workspace modes."""
     _lib.tuning_set("m1.path", 2)
     for N, K in [(37, 208), (1000, 3136), (130, 12544 + 16)]:
         x, w, s = _case(M, N, K, 17 * M + N + K)
         ref = oracle_bits(x, w, s)
-        for path in (0, 1):
+        for path, dma in ((0, 0), (0, 2), (1, 0)):
             _lib.tuning_set("skinny.path", path)
+            _lib.tuning_set("s4.dma", dma)
             for use_ws in (False, True):
-                announce("skinny_ragged", M, N, K, path, use_ws)
-                assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} path={path} ws={use_ws}")
+                announce("skinny_ragged", M, N, K, path, dma, use_ws)
+                assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} path={path} dma={dma} ws={use_ws}")
 
 
 @pytest.mark.parametrize("ksw", [1, 2, 4])
@@ -96,30 +98,34 @@ def test_every_schedule(ksw, u, kg):
 @pytest.mark.parametrize("ks", [1, 2, 4])
 @pytest.mark.parametrize("t", [1, 2])
 @pytest.mark.parametrize("u", [2, 4, 8])
-def test_s4_every_schedule(ks, t, u):
+@pytest.mark.parametrize("dma", [0, 2])
+def test_s4_every_schedule(ks, t, u, dma):
     """Each (waves splitting K, row groups per wave, chunks per lane) instantiation of the 4x4x4
-    kernel for M in {2, 5, 8, 16} (1, 2 and 4 groups of activation rows), with several LDS
-    windows (K = 3136 at M = 16: 64-chunk windows) and N not a multiple of the rows per
-    workgroup."""
+    kernel, in both forms (dma 0: pipelined, two LDS-DMA windows in flight, where its LDS fits;
+    dma 2: the windowed form), for M in {2, 5, 8, 16} (1, 2 and 4 groups of activation rows),
+    with several LDS windows (odd and even window counts, partial last windows) and N not a
+    multiple of the rows per workgroup."""
     _lib.tuning_set("s4.ks", ks)
     _lib.tuning_set("s4.t", t)
     _lib.tuning_set("s4.u", u)
-    for M, N, K in [(2, 300, 3136), (5, 77, 5120), (8, 130, 1040), (16, 264, 3136)]:
-        announce("s4_schedule", ks, t, u, M, N, K)
+    _lib.tuning_set("s4.dma", dma)
+    for M, N, K in [(2, 300, 3136), (5, 77, 5120), (8, 130, 1040), (16, 264, 3136), (13, 72, 208)]:
+        announce("s4_schedule", ks, t, u, dma, M, N, K)
         x, w, s = _case(M, N, K, 100 * ks + 10 * t + u + M)
         assert_parity(_run(x, w, s, False), oracle_bits(x, w, s), f"ks={ks} t={t} u={u} M={M}")
 
 
 @pytest.mark.parametrize("M", [2, 4, 8, 16])
-@pytest.mark.parametrize("path", [0, 1])
-def test_config2_shapes(M, path):
-    """Config 2 (M in {2,4,8,16}, the six decode shapes, per-row log-uniform scales), both
-    kernels (the split-K one with its workspace)."""
+@pytest.mark.parametrize("path,dma", [(0, 0), (0, 2), (1, 0)])
+def test_config2_shapes(M, path, dma):
+    """Config 2 (M in {2,4,8,16}, the six decode shapes, per-row log-uniform scales) on the
+    4x4x4 kernel in both forms and on the split-K kernel (with its workspace)."""
     _lib.tuning_set("skinny.path", path)
+    _lib.tuning_set("s4.dma", dma)
     for lin in synth.DECODE_SET:
-        announce("skinny_config2", M, path, lin.name)
+        announce("skinny_config2", M, path, dma, lin.name)
         x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, act=lin.act)
-        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} path={path} {lin.name}")
+        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} path={path} dma={dma} {lin.name}")
 
 
 def test_workspace_rearmed_and_deterministic():
