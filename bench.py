@@ -2,7 +2,7 @@
 """bench.py -- fp8 (e4m3) W8A16 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--no-extras]
-                    [--only prefill|block]
+                    [--only prefill|block|skinny]
 
 Headline (``value``): BASELINE config 1, the decode-step GEMV set of one attention block and
 one MLP block at M = 1 (q 3136->5120, k/v 3136->1024, o 5120->3136, up 3136->12544,
@@ -68,7 +68,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
-    p.add_argument("--only", choices=["prefill", "block"],
+    p.add_argument("--only", choices=["prefill", "block", "skinny"],
                    help="run one extra leg alone and print its JSON record (for profiling that leg); "
                         "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
@@ -527,7 +527,10 @@ def main():
         torch.cuda.synchronize()
         del a, b
     if args.only:
-        leg = bench_prefill(dev) if args.only == "prefill" else bench_mlp_block(dev)
+        if args.only == "skinny":
+            leg = bench_skinny(dev, decode_inputs())
+        else:
+            leg = bench_prefill(dev) if args.only == "prefill" else bench_mlp_block(dev)
         print(json.dumps(leg), flush=True)
         return
     host = decode_inputs()

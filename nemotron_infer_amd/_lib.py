@@ -81,6 +81,11 @@ def lib():
             fn.argtypes = args
             fn.restype = res
         _lib = L
+        # NMI_TUNING="knob=value,knob=value": tuning knobs applied at load (for sweeps and
+        # profiles of one variant from an unchanged command line)
+        for item in filter(None, os.environ.get("NMI_TUNING", "").split(",")):
+            knob, _, value = item.partition("=")
+            tuning_set(knob.strip(), int(value))
     return _lib
 
 

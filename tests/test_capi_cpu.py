@@ -233,3 +233,17 @@ def test_gemv_chain_handle_errors():
     assert L.nmi_gemv_chain_create(arr, 1, None) == _lib.NMI_ERR_INVALID_ARG
     assert L.nmi_gemv_chain_launch(None, FAKE, 4096, None) == _lib.NMI_ERR_INVALID_ARG
     assert L.nmi_gemv_chain_destroy(None) == _lib.NMI_OK
+
+
+def test_tuning_knobs_from_environment():
+    """NMI_TUNING applies knobs when the library is loaded; an unknown knob fails loudly."""
+    import subprocess
+    import sys
+
+    code = "from nemotron_infer_amd import _lib; _lib.lib(); print('loaded')"
+    env = dict(os.environ, NMI_TUNING="s4.dma=2, s4.u=4")
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "loaded" in r.stdout, r.stderr
+    env["NMI_TUNING"] = "no.such.knob=1"
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "unknown knob 'no.such.knob'" in r.stderr
