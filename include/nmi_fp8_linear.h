@@ -229,6 +229,8 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
  * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "gemm.sk",
  * "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
  * "s4.dma": 2 selects the windowed form of the 4x4x4 skinny kernel instead of the pipelined one,
+ * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace
+ * nmi_linear_workspace_bytes then reports),
  * "chain.wgs": workgroups per CU of a GEMV chain created afterwards, "chain.wait_us": bound of a
  * chain's waits in microseconds); 0 restores the automatic choice.  Process-wide, not
  * thread-safe against concurrent launches; results do not depend on them beyond float32

@@ -121,7 +121,7 @@ hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGro
     switch (path) {
         case Path::Gemv: return launch_gemv_grouped(x, ldx, M, K, g, ng, st, norm);
         case Path::Skinny: return launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
-        case Path::Skinny4: return launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
+        case Path::Skinny4: return launch_skinny4_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
         case Path::Gemm: break;
     }
     hipError_t e = hipSuccess;
@@ -303,10 +303,12 @@ int nmi_gemv_chain_destroy(nmi_gemv_chain* chain) {
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) {
     if (M < 1 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
     if (M > 16) return gemm_workspace_bytes(M);       // stream-K partials of the GEMM
-    // only the split-K 16x16x32 kernel uses a workspace (selected with "skinny.path" = 1,
-    // or "m1.path" = 2 for M = 1)
-    if (!(tuning().skinny_path == 1 || (M == 1 && tuning().m1_path == 2))) return 0;
-    return skinny_workspace_bytes(M, K, total_n, device_info().num_cu);
+    // the split-K 16x16x32 kernel ("skinny.path" = 1, or "m1.path" = 2 for M = 1) and the K
+    // split of the 4x4x4 kernel's pipelined form use a workspace
+    const Path path = choose_path(M);
+    if (path == Path::Skinny) return skinny_workspace_bytes(M, K, total_n, device_info().num_cu);
+    if (path == Path::Skinny4) return skinny4_workspace_bytes(M, K, total_n, device_info().num_cu);
+    return 0;
 }
 
 int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
@@ -355,6 +357,7 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s4.t")) t.s4_t = value;
     else if (!std::strcmp(knob, "s4.u")) t.s4_u = value;
     else if (!std::strcmp(knob, "s4.dma")) t.s4_dma = value;
+    else if (!std::strcmp(knob, "s4.kg")) t.s4_kg = value;
     else if (!std::strcmp(knob, "gemm.sk")) t.gemm_sk = value;
     else if (!std::strcmp(knob, "chain.wgs")) t.chain_wgs = value;
     else if (!std::strcmp(knob, "chain.wait_us")) t.chain_wait_us = value;

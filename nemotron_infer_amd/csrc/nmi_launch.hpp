@@ -40,6 +40,7 @@ struct Tuning {
     int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
     int s4_dma = 0;        // 4x4x4 skinny kernel: 0 pipelined form where it applies, 2 windowed form
+    int s4_kg = 0;         // 4x4x4 skinny kernel: workgroups splitting K (> 1, with a workspace; 0, 1: none)
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
     int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 4, or fewer if fewer are resident)
     int chain_wait_us = 0; // GEMV chain: bound of a wait in microseconds (0: 200000)
@@ -89,9 +90,12 @@ size_t skinny_workspace_bytes(int M, int K, int64_t total_rows, int num_cu);
 hipError_t launch_skinny_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
                                  int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-// 2 <= M <= 16 on 4x4x4 MFMA with coalesced weight reads (no workspace).
+// 2 <= M <= 16 on 4x4x4 MFMA with coalesced weight reads.  With a workspace of at least
+// skinny4_workspace_bytes() bytes (zero-filled before its first use; every launch leaves it
+// re-armed; 0 = the schedule has no K split) K is also split between workgroups.
+size_t skinny4_workspace_bytes(int M, int K, int64_t total_rows, int num_cu);
 hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
-                                  int ngroups, hipStream_t stream);
+                                  int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // The GEMV kernel for 1 <= M <= 4 activation rows (x row stride ldx elements).  With norm.w
 // set (only where gemv_norm_supported(M, K)), x is the raw input and every workgroup applies

@@ -37,8 +37,22 @@ struct Skinny4Args {
     int window;          // chunks per LDS window
     int xs_stride;       // 8-byte words between (m, k group) rows of the LDS window
     int ngroups;
-    GemvGroup g[kMaxGroups];
+    GemvGroup g[kMaxGroups];  // wg_begin counts row blocks; ws_col is the group's first partial column
+    // K split between workgroups (pipelined form): workgroup b computes row block b / kgroups over
+    // chunks [cpg (b % kgroups), cpg (b % kgroups + 1)) and writes float32 partials to
+    // ws[kg][m][ws_ld]; the last of a row block's workgroups (arrival counter) adds them in
+    // K-group order and stores.  kgroups = 1: no split, no workspace.
+    int kgroups;
+    int cpg;
+    float* ws;
+    uint32_t* counters;      // one per row block; zero between launches
+    int ws_ld;               // sum of N over the groups
 };
+
+// Workspace of the K split: a fixed block of arrival counters, then the partials (the layout of
+// the split-K 16x16x32 kernel, so that either kernel may use a workspace the other has used).
+constexpr int kSplitCounterSlots = 16384;
+constexpr size_t kSplitCounterBytes = kSplitCounterSlots * sizeof(uint32_t);
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -118,6 +132,105 @@ __device__ __forceinline__ void skinny4_finish(f32x4 (&acc)[T][G], f32x4 (&parti
                 }
             }
     }
+}
+
+// The end of a K-split workgroup: the same cross-lane and cross-wave sums, then the partial
+// tile (agent-scope stores, visible to every XCD), the row block's arrival count, and in the
+// last workgroup to arrive the sum of the K groups' partials in order 0..kgroups-1, the scale, one
+// bf16 rounding and the epilogue.  Every word that crosses workgroups is written and read with
+// agent-scope operations only; the counter is re-armed by the last arrival.
+template <int KS, int T, int G>
+__device__ __forceinline__ void skinny4_finish_split(f32x4 (&acc)[T][G],
+                                                     f32x4 (&partial)[KS > 1 ? KS : 1][kWaves / KS][T][G][4],
+                                                     const Skinny4Args& a, const GemvGroup& grp, int rb_all, int kg,
+                                                     int rb_row0, int row_base, int q, int gw, int lane, int li,
+                                                     int tid) {
+    __shared__ uint32_t last_flag;
+    const int M = a.M;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[t][g][r];
+                v += __shfl_xor(v, 4);
+                v += __shfl_xor(v, 8);
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                acc[t][g][r] = v;
+            }
+    if constexpr (KS > 1) {
+        if (lane < 4) {
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int g = 0; g < G; ++g) partial[q][gw][t][g][li] = acc[t][g];
+        }
+        __syncthreads();
+        if (q == 0 && lane < 4) {
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    f32x4 v = partial[0][gw][t][g][li];
+#pragma unroll
+                    for (int qq = 1; qq < KS; ++qq) {
+                        const f32x4 p = partial[qq][gw][t][g][li];
+                        v = f32x4{v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w};
+                    }
+                    acc[t][g] = v;
+                }
+        }
+    }
+    if (q == 0 && lane < 4) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int m = 4 * g + li;
+            if (m >= M) continue;
+            float* dst = a.ws + ((int64_t)kg * M + m) * a.ws_ld + grp.ws_col;
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = row_base + 4 * t + r;
+                    if (n < grp.N) __hip_atomic_store(dst + n, acc[t][g][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);              // this wave's partial stores have completed
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev =
+            __hip_atomic_fetch_add(a.counters + rb_all, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = (prev == (uint32_t)(a.kgroups - 1)) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    // the row block's outputs: kWaves / KS * 4 T rows x M activation rows, spread over the threads;
+    // each issues its loads of up to 8 K groups at once, then adds them in order
+    constexpr int kRows = kWaves / KS * 4 * T;
+    for (int o = tid; o < kRows * M; o += 256) {
+        const int m = o / kRows;
+        const int n = rb_row0 + (o - m * kRows);
+        if (n >= grp.N) continue;
+        const float* src = a.ws + (int64_t)m * a.ws_ld + grp.ws_col + n;
+        const int64_t step = (int64_t)M * a.ws_ld;
+        float tsum = 0.f;
+        for (int k0 = 0; k0 < a.kgroups; k0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                v[j] = __hip_atomic_load(src + (int64_t)min(k0 + j, a.kgroups - 1) * step, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (k0 + j < a.kgroups) tsum += v[j];
+        }
+        const uint16_t res = grp.epi.kind == kEpiResidual ? grp.epi.res[(int64_t)m * grp.epi.ldres + n] : 0;
+        grp.y[(int64_t)m * grp.ldy + n] = epilogue(tsum, grp.s[n], grp.epi.kind, res);
+    }
+    if (tid == 0) __hip_atomic_store(a.counters + rb_all, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // KS: waves splitting K; T: row groups (4 rows each) per wave; U: chunks per lane per batch;
@@ -277,10 +390,12 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
     constexpr int kJobs = 4 * G * 2 * kBlkPerRow;      // DMA instructions per window
     __shared__ f32x4 partial[KS > 1 ? KS : 1][kRowGroups][T][G][4];
 
+    const int rb_all = (int)blockIdx.x / a.kgroups;   // row block over all groups
+    const int kg = (int)blockIdx.x - rb_all * a.kgroups;
     int gi = 0;
 #pragma unroll
     for (int i = 1; i < kMaxGroups; ++i)
-        if (i < a.ngroups && (int)blockIdx.x >= a.g[i].wg_begin) gi = i;
+        if (i < a.ngroups && rb_all >= a.g[i].wg_begin) gi = i;
     const GemvGroup grp = a.g[gi];
 
     const int tid = threadIdx.x;
@@ -290,10 +405,12 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
     const int q = wave % KS;
     const int blk = lane >> 2;
     const int li = lane & 3;
-    const int row_base = ((int)blockIdx.x - grp.wg_begin) * kRowsPerWG + gw * kRowsPerWave;
+    const int rb_row0 = (rb_all - grp.wg_begin) * kRowsPerWG;
+    const int row_base = rb_row0 + gw * kRowsPerWave;
     const int M = a.M;
-    const int C = a.K >> 4;
-    const int nw = (C + kWin - 1) / kWin;
+    const int c_begin = kg * a.cpg;                    // this workgroup's chunks [c_begin, c_end)
+    const int c_end = min(a.K >> 4, c_begin + a.cpg);
+    const int nw = (c_end - c_begin + kWin - 1) / kWin;
     const uint32_t xw_addr = (uint32_t)(uintptr_t)(lds_void*)xw;
 
     const uint8_t* __restrict__ wrow[T];
@@ -309,8 +426,8 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
     // x window w into buffer b: job j = (row r = (m, h), block) has lane l copy chunk
     // 64 block + l of the row; lanes past the end of K write zeros instead
     auto stage = [&](int w, int b) {
-        const int w0 = w * kWin;
-        const int wc = min(kWin, C - w0);
+        const int w0 = c_begin + w * kWin;
+        const int wc = min(kWin, c_end - w0);
         for (int j = wave; j < kJobs; j += kWaves) {
             const int r = j / kBlkPerRow;
             const int c = (j - r * kBlkPerRow) * kBlk + lane;
@@ -330,14 +447,14 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
     // the paths into the loop (with and without a next window in flight) and wait for the next
     // window's loads too; completion is waited for by wait_loads_barrier and pinned by pin().
     auto load_w = [&](u32x4 (&wv)[T][U], int w) {
-        const int cb = w * kWin + q * 16 * U + blk;
+        const int cb = c_begin + w * kWin + q * 16 * U + blk;
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 asm volatile("global_load_dwordx4 %0, %1, off nt"
                              : "=v"(wv[t][u])
-                             : "v"(wrow[t] + (int64_t)min(cb + 16 * u, C - 1) * 16)
+                             : "v"(wrow[t] + (int64_t)min(cb + 16 * u, c_end - 1) * 16)
                              : "memory");
     };
     // after a wait: the registers are read only from here on
@@ -408,7 +525,10 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
         }
     }
 
-    skinny4_finish<KS, T, G>(acc, partial, grp, M, row_base, q, gw, lane, li);
+    if (a.kgroups > 1)
+        skinny4_finish_split<KS, T, G>(acc, partial, a, grp, rb_all, kg, rb_row0, row_base, q, gw, lane, li, tid);
+    else
+        skinny4_finish<KS, T, G>(acc, partial, grp, M, row_base, q, gw, lane, li);
 }
 
 // Dynamic LDS of the pipelined form: two windows of 4 G x 2 rows of 16 U KS + 2 words (the
@@ -419,11 +539,14 @@ constexpr size_t kDmaLdsMax = 156 * 1024;
 template <int KS, int T, int U, int G>
 hipError_t launch_cfg(Skinny4Args& a, bool dma, hipStream_t stream) {
     constexpr int rows_per_wg = (kWaves / KS) * 4 * T;
-    int wgs = 0;
+    int blocks = 0, col = 0;
     for (int i = 0; i < a.ngroups; ++i) {
-        a.g[i].wg_begin = wgs;
-        wgs += (a.g[i].N + rows_per_wg - 1) / rows_per_wg;
+        a.g[i].wg_begin = blocks;
+        a.g[i].ws_col = col;
+        blocks += (a.g[i].N + rows_per_wg - 1) / rows_per_wg;
+        col += a.g[i].N;
     }
+    a.ws_ld = col;
     if constexpr (dma_lds_bytes(KS, U, G) <= kDmaLdsMax) {
         if (dma) {
             constexpr size_t lds = dma_lds_bytes(KS, U, G);
@@ -433,13 +556,17 @@ hipError_t launch_cfg(Skinny4Args& a, bool dma, hipStream_t stream) {
                                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
                 if (attr != hipSuccess) return attr;
             }
-            hipLaunchKernelGGL(kernel, dim3(wgs), dim3(256), lds, stream, a);
+            hipLaunchKernelGGL(kernel, dim3(blocks * a.kgroups), dim3(256), lds, stream, a);
             return hipGetLastError();
         }
     }
-    const size_t lds = ((size_t)a.M * 4 * a.xs_stride + 1) * sizeof(uint2);
-    hipLaunchKernelGGL((skinny4_fp8_kernel<KS, T, U, G>), dim3(wgs), dim3(256), lds, stream, a);
-    return hipGetLastError();
+    if constexpr (T <= 2) {
+        if (a.kgroups != 1) return hipErrorInvalidValue;
+        const size_t lds = ((size_t)a.M * 4 * a.xs_stride + 1) * sizeof(uint2);
+        hipLaunchKernelGGL((skinny4_fp8_kernel<KS, T, U, G>), dim3(blocks), dim3(256), lds, stream, a);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
 }
 
 template <int KS, int T, int U>
@@ -454,19 +581,92 @@ hipError_t launch_u(int u, int M, Skinny4Args& a, bool dma, hipStream_t stream) 
     switch (u) {
         case 2: return launch_g<KS, T, 2>(M, a, dma, stream);
         case 4: return launch_g<KS, T, 4>(M, a, dma, stream);
-        default: return launch_g<KS, T, 8>(M, a, dma, stream);
+        default:
+            if constexpr (T == 4) return launch_g<KS, T, 4>(M, a, dma, stream);   // T = 4 x U = 8: too many registers
+            else return launch_g<KS, T, 8>(M, a, dma, stream);
     }
 }
 
 template <int KS>
 hipError_t launch_t(int t, int u, int M, Skinny4Args& a, bool dma, hipStream_t stream) {
-    return t == 2 ? launch_u<KS, 2>(u, M, a, dma, stream) : launch_u<KS, 1>(u, M, a, dma, stream);
+    if constexpr (KS == 1)
+        if (t == 4 && dma) return launch_u<1, 4>(u, M, a, dma, stream);   // 4 row groups: pipelined form, KS = 1 only
+    return t >= 2 ? launch_u<KS, 2>(u, M, a, dma, stream) : launch_u<KS, 1>(u, M, a, dma, stream);
+}
+
+// Schedule of the 4x4x4 kernel for M activation rows, K, `rows` weight rows in all groups.
+struct S4Plan {
+    bool dma;       // pipelined form
+    int ks, t, u;
+    int kgroups;    // workgroups splitting K (pipelined form with a workspace)
+    int cpg;        // chunks per K group
+};
+
+S4Plan s4_plan(int M, int K, int64_t rows, int num_cu, bool dma_ok, bool split_ok) {
+    const Tuning& tn = tuning();
+    const int C = K >> 4;
+    S4Plan p{};
+    p.dma = dma_ok && tn.s4_dma != 2;
+    p.kgroups = 1;
+    p.cpg = C;
+    if (p.dma) {
+        // one batch of U chunks per lane per window; KS = 1 and T = 1 keep the most workgroups
+        // and the LDS to two windows of 64 (M > 4) or 128 chunks (measured on config 2: K split
+        // between waves widens the window and halves the workgroups per CU)
+        p.ks = 1, p.t = 1, p.u = M > 4 ? 4 : 8;
+        // K split between workgroups (s4.kg > 1 K groups; measured slower than no split at every
+        // config-2 shape, so not chosen automatically): row tiles of 2 row groups per wave share
+        // one 32-chunk x window
+        if (split_ok && tn.s4_kg > 1) {
+            int ks = 1, t = 2, u = 2;
+            if (tn.s4_ks == 1 || tn.s4_ks == 2 || tn.s4_ks == 4) ks = tn.s4_ks;
+            if (tn.s4_t == 1 || tn.s4_t == 2 || tn.s4_t == 4) t = tn.s4_t;
+            if (tn.s4_u == 2 || tn.s4_u == 4) u = tn.s4_u;
+            if (ks != 1 && t == 4) t = 2;
+            const int win = 16 * u * ks;
+            const int64_t rb = (rows + (kWaves / ks) * 4 * t - 1) / ((kWaves / ks) * 4 * t);
+            const int nwin = (C + win - 1) / win;
+            const int64_t kg = tn.s4_kg > nwin ? nwin : tn.s4_kg;
+            const int cpg = (int)(((C + kg - 1) / kg + win - 1) / win) * win;
+            const int kgroups = (C + cpg - 1) / cpg;
+            if (kgroups > 1 && rb + kMaxGroups <= kSplitCounterSlots &&
+                dma_lds_bytes(ks, u, (M + 3) / 4) <= kDmaLdsMax) {
+                p.ks = ks, p.t = t, p.u = u, p.kgroups = kgroups, p.cpg = cpg;
+                return p;
+            }
+        }
+        if (tn.s4_ks == 1 || tn.s4_ks == 2 || tn.s4_ks == 4) p.ks = tn.s4_ks;
+        if (tn.s4_t == 1 || tn.s4_t == 2 || tn.s4_t == 4) p.t = tn.s4_t;
+        if (tn.s4_u == 2 || tn.s4_u == 4 || tn.s4_u == 8) p.u = tn.s4_u;
+        if (p.ks != 1 && p.t == 4) p.t = 2;
+        if (dma_lds_bytes(p.ks, p.u, (M + 3) / 4) <= kDmaLdsMax) return p;
+        p.dma = false;
+    }
+    // windowed form: K split inside the workgroup so that a lane has 2-8 chunks per window; T = 2
+    // when there are enough rows to keep ~3 workgroups per CU
+    const int wmax = kStageBytes / (32 * M);
+    const int slice = C < wmax ? C : wmax;
+    p.ks = slice >= 16 * 8 * 4 ? 4 : (slice >= 16 * 8 * 2 ? 2 : 1);
+    if (tn.s4_ks == 1 || tn.s4_ks == 2 || tn.s4_ks == 4) p.ks = tn.s4_ks;
+    const int64_t wg_t1 = (rows + (int64_t)(kWaves / p.ks) * 4 - 1) / ((int64_t)(kWaves / p.ks) * 4);
+    p.t = (wg_t1 >= 6 * (int64_t)num_cu) ? 2 : 1;
+    if (tn.s4_t == 1 || tn.s4_t == 2) p.t = tn.s4_t;
+    const int per_lane = (slice / p.ks + 15) / 16;
+    p.u = per_lane <= 2 ? 2 : (per_lane <= 4 ? 4 : 8);
+    if (tn.s4_u == 2 || tn.s4_u == 4 || tn.s4_u == 8) p.u = tn.s4_u;
+    return p;
 }
 
 }  // namespace
 
+size_t skinny4_workspace_bytes(int M, int K, int64_t total_rows, int num_cu) {
+    const S4Plan p = s4_plan(M, K, total_rows, num_cu, true, true);
+    if (!p.dma || p.kgroups <= 1) return 0;
+    return kSplitCounterBytes + (size_t)p.kgroups * M * total_rows * sizeof(float);
+}
+
 hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
-                                  int ngroups, hipStream_t stream) {
+                                  int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     const DeviceInfo& dev = device_info();
     Skinny4Args a{};
     a.x = x;
@@ -480,47 +680,29 @@ hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, 
         rows += groups[i].N;
     }
     const int C = K >> 4;
-    // x window: 2 M w 16-byte pieces <= 2048 (8 per thread) and M x 32 w bytes <= 32 KiB.
+    // windowed form: x window of 2 M w 16-byte pieces <= 2048 (8 per thread) and M x 32 w bytes
+    // <= 32 KiB; (m, kg) rows padded to a stride of 2 mod 8 words (the 4 activation rows one read
+    // touches start in different 64-byte bank groups)
     const int wmax = kStageBytes / (32 * M);
     a.window = C < wmax ? C : wmax;
-    // (m, kg) rows padded to a stride of 2 mod 8 words: the 4 activation rows one read touches
-    // start in different 64-byte bank groups.
     a.xs_stride = ((a.window + 5) & ~7) + 2;
-    const Tuning& tn = tuning();
-    // The pipelined form needs 16-byte x rows (LDS DMA) with 32-bit byte offsets.
+    // the pipelined form needs 16-byte x rows (LDS DMA) with 32-bit byte offsets
     const bool dma_ok = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ldx & 7) == 0 &&
                         (int64_t)M * ldx * 2 < ((int64_t)1 << 32);
-    if (dma_ok && tn.s4_dma != 2) {
-        // one batch of U chunks per lane per window; KS = 1 and T = 1 keep the most workgroups
-        // and the LDS to two windows of 64 (M > 4) or 128 chunks (measured on config 2: K split
-        // between waves widens the window and halves the workgroups per CU)
-        int ks = 1, t = 1, u = M > 4 ? 4 : 8;
-        if (tn.s4_ks == 1 || tn.s4_ks == 2 || tn.s4_ks == 4) ks = tn.s4_ks;
-        if (tn.s4_t == 1 || tn.s4_t == 2) t = tn.s4_t;
-        if (tn.s4_u == 2 || tn.s4_u == 4 || tn.s4_u == 8) u = tn.s4_u;
-        if (dma_lds_bytes(ks, u, (M + 3) / 4) <= kDmaLdsMax) {
-            switch (ks) {
-                case 1: return launch_t<1>(t, u, M, a, true, stream);
-                case 2: return launch_t<2>(t, u, M, a, true, stream);
-                default: return launch_t<4>(t, u, M, a, true, stream);
-            }
-        }
+    const size_t need = skinny4_workspace_bytes(M, K, rows, dev.num_cu);
+    const bool split_ok = workspace != nullptr && need > 0 && workspace_bytes >= need &&
+                          (reinterpret_cast<uintptr_t>(workspace) & 15) == 0;
+    const S4Plan p = s4_plan(M, K, rows, dev.num_cu, dma_ok, split_ok);
+    a.kgroups = p.kgroups;
+    a.cpg = p.cpg;
+    if (p.kgroups > 1) {
+        a.counters = static_cast<uint32_t*>(workspace);
+        a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kSplitCounterBytes);
     }
-    // K split inside the workgroup so that a lane has 2-8 chunks per window; T = 2 when there
-    // are enough rows to keep ~3 workgroups per CU.
-    const int slice = a.window;
-    int ks = slice >= 16 * 8 * 4 ? 4 : (slice >= 16 * 8 * 2 ? 2 : 1);
-    if (tn.s4_ks == 1 || tn.s4_ks == 2 || tn.s4_ks == 4) ks = tn.s4_ks;
-    const int64_t wg_t1 = (rows + (int64_t)(kWaves / ks) * 4 - 1) / ((int64_t)(kWaves / ks) * 4);
-    int t = (wg_t1 >= 6 * (int64_t)dev.num_cu) ? 2 : 1;
-    if (tn.s4_t == 1 || tn.s4_t == 2) t = tn.s4_t;
-    const int per_lane = (slice / ks + 15) / 16;
-    int u = per_lane <= 2 ? 2 : (per_lane <= 4 ? 4 : 8);
-    if (tn.s4_u == 2 || tn.s4_u == 4 || tn.s4_u == 8) u = tn.s4_u;
-    switch (ks) {
-        case 1: return launch_t<1>(t, u, M, a, false, stream);
-        case 2: return launch_t<2>(t, u, M, a, false, stream);
-        default: return launch_t<4>(t, u, M, a, false, stream);
+    switch (p.ks) {
+        case 1: return launch_t<1>(p.t, p.u, M, a, p.dma, stream);
+        case 2: return launch_t<2>(p.t, p.u, M, a, p.dma, stream);
+        default: return launch_t<4>(p.t, p.u, M, a, p.dma, stream);
     }
 }
 

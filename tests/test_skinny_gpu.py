@@ -22,7 +22,7 @@ from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_t
 pytestmark = pytest.mark.gpu
 
 KNOBS = ("skinny.ks", "skinny.kg", "skinny.u", "m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u",
-         "s4.dma")
+         "s4.dma", "s4.kg")
 
 
 @pytest.fixture(autouse=True)
@@ -250,4 +250,40 @@ def test_gemv_kernel_small_m(ks, t, p):
             assert_parity(_run(x, w, s, False), oracle_bits(x, w, s), f"ks={ks} t={t} p={p} M={M} N={N} K={K}")
     finally:
         for k in ("gemv.ks", "gemv.t", "gemv.p"):
+            _lib.tuning_set(k, 0)
+
+
+@pytest.mark.parametrize("M", [1, 3, 5, 8, 13, 16])
+@pytest.mark.parametrize("kg,t,u", [(0, 0, 0), (2, 0, 0), (5, 2, 2), (3, 1, 4), (7, 4, 2), (4, 2, 4)])
+def test_s4_k_split(M, kg, t, u):
+    """The pipelined form's K split between workgroups (s4.kg > 1; float32 partials in the
+    workspace; the last workgroup of a row block adds them in K-group order): forced K-group
+    counts and the automatic schedule (no split), 1, 2 and 4 row groups per wave, a grouped call with ragged N, K ranges whose last
+    window or last group is partial, and K too short to split. Against the oracle; repeated
+    calls bit-identical; the workspace's counters read back zero."""
+    _lib.tuning_set("m1.path", 3)                    # M = 1 on the 4x4x4 kernel too
+    _lib.tuning_set("s4.kg", kg)
+    _lib.tuning_set("s4.t", t)
+    _lib.tuning_set("s4.u", u)
+    try:
+        K = 3136
+        x = synth.make_act(M, K, 500 + M, "cpu")
+        ws_host = [synth.make_weight(N, K, 510 + i, "cpu", scales="log_uniform") for i, N in enumerate((37, 300, 1000))]
+        xb = x.view(torch.int16).numpy().view(np.uint16)
+        announce("s4_split_grouped", M, kg, t, u)
+        outs = [bits(y) for y in ops.linear_fp8_w8a16_grouped(x.to(DEV), [(w.to(DEV), s.to(DEV)) for w, s in ws_host])]
+        again = [bits(y) for y in ops.linear_fp8_w8a16_grouped(x.to(DEV), [(w.to(DEV), s.to(DEV)) for w, s in ws_host])]
+        for (w, s), y, y2 in zip(ws_host, outs, again):
+            assert np.array_equal(y, y2)
+            assert_parity(y, oracle_bits(xb, w.numpy(), s.numpy()), f"grouped M={M} kg={kg} t={t} u={u}")
+        for N, K2 in [(130, 12544 + 16), (1000, 5120), (48, 208)]:
+            announce("s4_split", M, kg, t, u, N, K2)
+            xs, w, s = _case(M, N, K2, 520 + M + N)
+            assert_parity(_run(xs, w, s, True), oracle_bits(xs, w, s), f"M={M} N={N} K={K2} kg={kg} t={t} u={u}")
+        torch.cuda.synchronize()
+        ws = ops._WORKSPACE.get(0)
+        if ws is not None:
+            assert not ws[: 4 * 16384].cpu().numpy().any(), "arrival counters not re-armed"
+    finally:
+        for k in ("m1.path", "s4.kg"):
             _lib.tuning_set(k, 0)
