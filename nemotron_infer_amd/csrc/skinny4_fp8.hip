@@ -19,7 +19,13 @@
 // * The 16 blocks hold partial sums over different chunks; they are added across lanes at
 //   the end (xor 4, 8, 16, 32, a fixed order), KS waves of a workgroup split K and their
 //   partials are summed in order through LDS, then the per-row scale and one bf16 rounding.
-// * x [M, window] is staged per workgroup in LDS as [m][k group (4)][chunk] 8-byte words.
+// * Two forms stage x [M, window] per workgroup in LDS:
+//   - pipelined (skinny4_dma_kernel, the default): windows of exactly one batch per wave,
+//     staged by LDS DMA into two buffers, so the next window's weights and x are in flight
+//     while this one is multiplied; optionally (s4.kg > 1, with a workspace) K is also split
+//     between workgroups, whose float32 partials the last one of a row block adds in order;
+//   - windowed (skinny4_fp8_kernel, s4.dma = 2): x staged through registers as
+//     [m][k group (4)][chunk] 8-byte words, each window's weights loaded after it is staged.
 #include "nmi_device.hpp"
 #include "nmi_launch.hpp"
 
