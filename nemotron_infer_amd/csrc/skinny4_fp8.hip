@@ -620,6 +620,9 @@ S4Plan s4_plan(int M, int K, int64_t rows, int num_cu, bool dma_ok, bool split_o
         // and the LDS to two windows of 64 (M > 4) or 128 chunks (measured on config 2: K split
         // between waves widens the window and halves the workgroups per CU)
         p.ks = 1, p.t = 1, p.u = M > 4 ? 4 : 8;
+        // M > 8: two row groups per wave once one group would give more than ~3 workgroups per
+        // CU (config 2 at M = 16: up_proj 27.1 -> 23.5 us; the smaller shapes lose workgroups)
+        if (M > 8 && (rows + 15) / 16 >= 3 * (int64_t)num_cu) p.t = 2;
         // K split between workgroups (s4.kg > 1 K groups; measured slower than no split at every
         // config-2 shape, so not chosen automatically): row tiles of 2 row groups per wave share
         // one 32-chunk x window
