@@ -287,3 +287,32 @@ def test_s4_k_split(M, kg, t, u):
     finally:
         for k in ("m1.path", "s4.kg"):
             _lib.tuning_set(k, 0)
+
+
+@pytest.mark.parametrize("M", [3, 5, 16])
+@pytest.mark.parametrize("dma,kg", [(0, 0), (2, 0), (0, 3)])
+def test_s4_strided_operands(M, dma, kg):
+    """ldx > K, ldw > K, ldy > N (slices of wider buffers) through the 4x4x4 kernel in both forms
+    and with the K split: the DMA offsets and the loads follow the strides, and nothing outside
+    the output slice is written."""
+    N, K = 200, 3136
+    _lib.tuning_set("s4.dma", dma)
+    _lib.tuning_set("s4.kg", kg)
+    announce("s4_strided", M, dma, kg)
+    x, w, s = _case(M, N, K, 900 + M, scales="log_uniform")
+    xbig = torch.zeros((M, K + 64), dtype=torch.bfloat16, device=DEV)
+    xbig[:, 32:32 + K] = x_to_dev(x)
+    wbig = torch.zeros((N, K + 48), dtype=torch.uint8, device=DEV)
+    wbig[:, 16:16 + K] = w_to_dev(w)
+    ybig = torch.full((M, N + 40), 7.0, dtype=torch.bfloat16, device=DEV)
+    sd = s_to_dev(s)
+    L = _lib.lib()
+    nbytes = L.nmi_linear_workspace_bytes(M, N, K)
+    ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=DEV)
+    xv, wv, yv = xbig[:, 32:], wbig[:, 16:], ybig[:, 8:]
+    _lib.check(L.nmi_linear_fp8_w8a16_ws(xv.data_ptr(), xbig.stride(0), wv.data_ptr(), wbig.stride(0), sd.data_ptr(),
+                                         yv.data_ptr(), ybig.stride(0), M, N, K, ws.data_ptr(), nbytes, None), "ws")
+    torch.cuda.synchronize()
+    assert_parity(bits(ybig[:, 8:8 + N]), oracle_bits(x, w, s), f"strided M={M} dma={dma} kg={kg}")
+    assert torch.all(ybig[:, :8] == 7.0) and torch.all(ybig[:, 8 + N:] == 7.0)
+    assert not ws[: 4 * 16384].cpu().numpy().any()
