@@ -77,8 +77,9 @@ int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, in
                          void* stream);
 
 /*
- * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the skinny kernel
- * (2 <= M <= 16, split-K variant) split K between workgroups, and the prefill GEMM (M >= 512)
+ * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the skinny kernels
+ * (2 <= M <= 16: the split-K 16x16x32 variant, or the 4x4x4 kernel's K split when the tuning
+ * knob s4.kg > 1 selects it) split K between workgroups, and the prefill GEMM (M >= 512)
  * split the k tiles of a few large tiles between all CUs (stream-K: fp32 partial tiles and
  * per-workgroup flags in the workspace; used when the 256 x 256 tiles cover at most half of
  * the CUs, e.g. N = 3136 at M = 2048).
@@ -159,7 +160,9 @@ int nmi_gemv_chain_destroy(nmi_gemv_chain* chain);
 
 /* Workspace bytes the kernels can use for M rows, total_n output rows (the sum over groups)
  * and K on the current device; 0 when the selected kernel needs none (the GEMV, the default
- * 4x4x4 skinny kernel, which splits K inside the workgroup only, and M < 512).  For M >= 512
+ * 4x4x4 skinny kernel, which splits K inside the workgroup only, and M < 512).  With the 4x4x4
+ * kernel's K split (s4.kg > 1): 64 KiB of arrival counters and the fp32 partials,
+ * s4.kg x M x total_n x 4 bytes (fewer K groups when K has fewer windows).  For M >= 512
  * about 64 MiB: a 64 KiB flag region and one 256 x 256 fp32 partial tile per CU. */
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K);
 
