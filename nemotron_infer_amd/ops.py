@@ -19,12 +19,49 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _check_w(w: torch.Tensor) -> torch.Tensor:
+def _check_w(w: torch.Tensor, K: int | None = None) -> torch.Tensor:
+    """e4m3 weights [N, K] as uint8 codes; rows must be contiguous (stride(-1) == 1)."""
     if w.dtype == torch.float8_e4m3fn:
-        return w.view(torch.uint8)
-    if w.dtype != torch.uint8:
+        w = w.view(torch.uint8)
+    elif w.dtype != torch.uint8:
         raise TypeError(f"weights must be float8_e4m3fn or uint8 codes, got {w.dtype}")
+    if w.dim() != 2 or w.stride(-1) != 1:
+        raise ValueError(f"weights must be a 2-D [N, K] matrix with contiguous rows (shape {tuple(w.shape)}, "
+                         f"strides {w.stride()})")
+    if K is not None and w.shape[1] != K:
+        raise ValueError(f"weights have K = {w.shape[1]}, activations K = {K}")
     return w
+
+
+def _check_s(s: torch.Tensor, N: int) -> torch.Tensor:
+    """Per-row scales: contiguous float32 [N]."""
+    if s.dtype != torch.float32:
+        raise TypeError(f"w_scale must be float32, got {s.dtype}")
+    if s.dim() != 1 or s.numel() != N or not s.is_contiguous():
+        raise ValueError(f"w_scale must be a contiguous float32 vector of N = {N} values (shape {tuple(s.shape)})")
+    return s
+
+
+def _check_out(y: torch.Tensor, M: int, N: int, name: str = "out") -> torch.Tensor:
+    """An output buffer: contiguous bf16 holding exactly [M, N] (or [N] when M == 1), returned
+    as a 2-D view.  Anything else raises: a strided or copied view would silently receive
+    the wrong elements or lose the results."""
+    if y.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {y.dtype}")
+    ok_shape = tuple(y.shape) == (M, N) or (M == 1 and tuple(y.shape) == (N,))
+    if not ok_shape or not y.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous bf16 tensor of shape ({M}, {N}) "
+                         f"(got shape {tuple(y.shape)}, strides {y.stride()})")
+    return y.view(M, N)
+
+
+def _check_device(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"tensors must be on a GPU, got {dev}")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}, got {t.device}")
 
 
 _WORKSPACE: dict[int, torch.Tensor] = {}
@@ -57,18 +94,16 @@ def _as_2d(x: torch.Tensor):
 def linear_fp8_w8a16(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
                      out: torch.Tensor | None = None, use_workspace: bool = True) -> torch.Tensor:
     """y[M, N] = bf16_rne((x[M, K] . e4m3(W[N, K])^T) * w_scale[N]) on the GPU."""
-    w = _check_w(w)
     squeeze = x.dim() == 1
     x2 = _as_2d(x)
-    if w_scale.dtype != torch.float32:
-        raise TypeError("w_scale must be float32")
-    if w.stride(-1) != 1 or not w_scale.is_contiguous():
-        raise ValueError("W rows and w_scale must be contiguous in the last dimension")
     M, K = x2.shape
+    w = _check_w(w, K)
     N = w.shape[0]
+    _check_s(w_scale, N)
     if out is None:
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    y2 = out.view(M, N) if squeeze and out.dim() == 1 else out
+        out = torch.empty((N,) if squeeze else (M, N), dtype=torch.bfloat16, device=x.device)
+    y2 = _check_out(out, M, N)
+    _check_device(x2, w, w_scale, y2)
     L = _lib.lib()
     ws = workspace(x.device, L.nmi_linear_workspace_bytes(M, N, K)) if use_workspace else None
     rc = L.nmi_linear_fp8_w8a16_ws(
@@ -76,7 +111,7 @@ def linear_fp8_w8a16(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
         y2.data_ptr(), y2.stride(0), M, N, K,
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream())
     _lib.check(rc, "nmi_linear_fp8_w8a16_ws")
-    return out[0] if squeeze and out.dim() == 2 else out
+    return out
 
 
 def linear_fp8_w8a16_grouped(x: torch.Tensor, weights, outs=None, use_workspace: bool = True):
@@ -89,10 +124,14 @@ def linear_fp8_w8a16_grouped(x: torch.Tensor, weights, outs=None, use_workspace:
         raise ValueError(f"1..{_lib.MAX_GROUPS} groups")
     if outs is None:
         outs = [torch.empty((M, w.shape[0]), dtype=torch.bfloat16, device=x.device) for w, _ in weights]
+    if len(outs) != n:
+        raise ValueError(f"{n} weight groups but {len(outs)} outputs")
     arr = (_lib.LinearGroup * n)()
     for i, ((w, s), y) in enumerate(zip(weights, outs)):
-        w = _check_w(w)
-        y2 = y.view(M, -1)
+        w = _check_w(w, K)
+        _check_s(s, w.shape[0])
+        y2 = _check_out(y, M, w.shape[0], f"outs[{i}]")
+        _check_device(x2, w, s, y2)
         arr[i] = _lib.LinearGroup(w.data_ptr(), w.stride(0), s.data_ptr(), y2.data_ptr(), y2.stride(0),
                                   w.shape[0])
     L = _lib.lib()
@@ -107,11 +146,19 @@ def linear_fp8_w8a16_grouped(x: torch.Tensor, weights, outs=None, use_workspace:
 
 def gemv_fp8(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
              out: torch.Tensor | None = None) -> torch.Tensor:
-    """M = 1 GEMV (ops/gemv.cuh:92-104 semantics): y[N] = bf16((W . x) * s)."""
+    """M = 1 GEMV (ops/gemv.cuh:92-104 semantics): y[N] = bf16((W . x) * s).  x is a contiguous
+    bf16 [K] vector, W [N, K] with row stride K."""
     w = _check_w(w)
     N, K = w.shape
+    if w.stride(0) != K:
+        raise ValueError("gemv_fp8 takes W with row stride K (use linear_fp8_w8a16 for strided rows)")
+    if x.dtype != torch.bfloat16 or x.numel() != K or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous bf16 vector of K = {K} values (shape {tuple(x.shape)})")
+    _check_s(w_scale, N)
     if out is None:
         out = torch.empty((N,), dtype=torch.bfloat16, device=x.device)
+    _check_out(out, 1, N)
+    _check_device(x, w, w_scale, out)
     rc = _lib.lib().nmi_gemv_fp8(x.data_ptr(), w.data_ptr(), w_scale.data_ptr(), out.data_ptr(),
                                  N, K, _stream())
     _lib.check(rc, "nmi_gemv_fp8")
@@ -122,15 +169,21 @@ def gemm_fp8_w8a16(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
                    out: torch.Tensor | None = None, use_workspace: bool = True) -> torch.Tensor:
     """Prefill GEMM on bf16 MFMA for any M (ops/gemm.cuh:325-403 replacement).  With the
     per-device workspace the large-tile kernels may split K between workgroups (stream-K)."""
-    w = _check_w(w)
-    M, K = x.shape
+    if x.dim() != 2:
+        raise ValueError("x must be a 2-D [M, K] bf16 matrix")
+    x2 = _as_2d(x)
+    M, K = x2.shape
+    w = _check_w(w, K)
     N = w.shape[0]
+    _check_s(w_scale, N)
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    y2 = _check_out(out, M, N)
+    _check_device(x2, w, w_scale, y2)
     L = _lib.lib()
     ws = workspace(x.device, L.nmi_linear_workspace_bytes(M, N, K)) if use_workspace else None
-    rc = L.nmi_gemm_fp8_w8a16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
-                              w_scale.data_ptr(), out.data_ptr(), out.stride(0), M, N, K,
+    rc = L.nmi_gemm_fp8_w8a16(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0),
+                              w_scale.data_ptr(), y2.data_ptr(), y2.stride(0), M, N, K,
                               None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
                               _stream())
     _lib.check(rc, "nmi_gemm_fp8_w8a16")
@@ -144,8 +197,12 @@ def rmsnorm_bf16(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5,
     if not x2.is_contiguous() or w.dtype != torch.float32 or not w.is_contiguous():
         raise ValueError("x must be contiguous bf16 and w contiguous float32")
     M, K = x2.shape
+    if tuple(w.shape) != (K,):
+        raise ValueError(f"w must hold K = {K} values")
     if out is None:
         out = torch.empty_like(x)
+    _check_out(out, M, K) if x.dim() == 2 else _check_out(out, 1, K)
+    _check_device(x2, w, out)
     rc = _lib.lib().nmi_rmsnorm_bf16(x2.data_ptr(), w.data_ptr(), out.data_ptr(), M, K, eps, _stream())
     _lib.check(rc, "nmi_rmsnorm_bf16")
     return out
@@ -164,11 +221,20 @@ def mlp_forward_fp8(x: torch.Tensor, norm_w: torch.Tensor, up_w: torch.Tensor, u
     x2 = _as_2d(x)
     if not x2.is_contiguous():
         raise ValueError("x must be contiguous")
-    up_w, down_w = _check_w(up_w), _check_w(down_w)
     M, hidden = x2.shape
+    up_w = _check_w(up_w, hidden)
     inter = up_w.shape[0]
+    down_w = _check_w(down_w, inter)
+    if down_w.shape[0] != hidden:
+        raise ValueError(f"down_proj has {down_w.shape[0]} rows, hidden size is {hidden}")
+    _check_s(up_s, inter)
+    _check_s(down_s, hidden)
+    if norm_w.dtype != torch.float32 or tuple(norm_w.shape) != (hidden,) or not norm_w.is_contiguous():
+        raise ValueError(f"norm_w must be a contiguous float32 vector of {hidden} values")
     if out is None:
         out = torch.empty_like(x)
+    _check_out(out, M, hidden) if x.dim() == 2 else _check_out(out, 1, hidden)
+    _check_device(x2, norm_w, up_w, up_s, down_w, down_s, out)
     L = _lib.lib()
     ws = None
     if use_workspace:
@@ -203,9 +269,10 @@ class GemvChain:
         self._keep = []
         dev = None
         for i, (x, groups, wait_prev) in enumerate(phases):
-            x1 = x.reshape(-1)
-            if x1.dtype != torch.bfloat16 or not x1.is_contiguous():
-                raise ValueError("x must be a contiguous bf16 vector")
+            if x.dtype != torch.bfloat16 or not x.is_contiguous() or not (
+                    x.dim() == 1 or (x.dim() == 2 and x.shape[0] == 1)):
+                raise ValueError(f"phase {i}: x must be a contiguous bf16 [K] (or [1, K]) vector")
+            x1 = x.view(-1)
             if not 1 <= len(groups) <= _lib.MAX_GROUPS:
                 raise ValueError(f"1..{_lib.MAX_GROUPS} groups per phase")
             K = x1.numel()
@@ -214,8 +281,10 @@ class GemvChain:
             arr[i].ngroups = len(groups)
             arr[i].wait_prev = 1 if wait_prev else 0
             for j, (w, sc, y) in enumerate(groups):
-                w = _check_w(w)
-                y1 = y.reshape(-1)
+                w = _check_w(w, K)
+                _check_s(sc, w.shape[0])
+                y1 = _check_out(y, 1, w.shape[0], f"phase {i} group {j} y").view(-1)
+                _check_device(x1, w, sc, y1)
                 arr[i].groups[j] = _lib.LinearGroup(w.data_ptr(), w.stride(0), sc.data_ptr(), y1.data_ptr(),
                                                     y1.numel(), w.shape[0])
                 self._keep += [w, sc, y1]

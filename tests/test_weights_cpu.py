@@ -147,3 +147,25 @@ def test_layer_count_stops_at_first_gap(ckpt_dir):
     gap = {k: v for k, v in t.items() if not k.startswith("backbone.layers.1.")}
     ck = weights.load_checkpoint(raw=gap, device="cpu")
     assert ck.nlayers == 1 and ck.layers[0]["type"] == "mamba"
+
+
+def test_shape_links_are_checked(ckpt_dir):
+    """Projections must chain: q/k/v/up/in_proj read the hidden size, o/down/out_proj write it,
+    down reads up's rows, o reads q's rows; a per-tensor scale holds one value."""
+    _, t = ckpt_dir
+    bad = dict(t)
+    bad["backbone.layers.2.mixer.down_proj.weight"], _ = _fp8((HID, 128), 30, 1e-4)   # down K != up N
+    with pytest.raises(ValueError, match="layer 2 .*down dim 1"):
+        weights.load_checkpoint(raw=bad, device="cpu")
+    bad = dict(t)
+    bad["backbone.layers.1.mixer.k_proj.weight"], _ = _fp8((16, HID + 16), 31, 1e-4)   # k K != hidden
+    with pytest.raises(ValueError, match="layer 1 .*k dim 1"):
+        weights.load_checkpoint(raw=bad, device="cpu")
+    bad = dict(t)
+    bad["backbone.layers.0.mixer.in_proj.weight_scale"] = torch.tensor([1e-4, 2e-4])
+    with pytest.raises(ValueError, match="weight_scale"):
+        weights.load_checkpoint(raw=bad, device="cpu")
+    bad = dict(t)
+    bad["backbone.layers.2.mixer.up_proj.weight"] = bad["backbone.layers.2.mixer.up_proj.weight"].reshape(-1)
+    with pytest.raises(ValueError, match="2-D"):
+        weights.load_checkpoint(raw=bad, device="cpu")
