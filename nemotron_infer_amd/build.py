@@ -9,7 +9,9 @@ Produces
 Every HIP translation unit is compiled with ``--offload-arch=gfx950`` and with packed-fp32
 code generation disabled (``-Xclang -target-feature -Xclang -packed-fp32-ops``).  The build
 always recompiles (it is also the "does it build" check) and replaces outputs atomically.
-CMakeLists.txt at the repository root describes the same build for CMake users.
+CMakeLists.txt at the repository root builds the same two artefacts with the same flags
+(``cmake -S . -B build -G Ninja && cmake --build build``; tests/test_cmake_build.py checks that
+both builds export the same symbols).
 """
 from __future__ import annotations
 
