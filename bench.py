@@ -2,35 +2,33 @@
 """bench.py -- fp8 (e4m3) W8A16 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--no-extras]
-                    [--only prefill|block|skinny]
+                    [--only stream|decode|prefill|block|skinny]
 
-Headline (``value``): BASELINE config 1, the decode-step GEMV set of one attention block and
-one MLP block at M = 1 (q 3136->5120, k/v 3136->1024, o 5120->3136, up 3136->12544,
-down 12544->3136), each GEMV on its own seeded activation as config 1 defines them.  A step is
-one GEMV chain launch (nmi_gemv_chain): phases q|k|v (grouped: they share one input, as
-model/attention_block.cuh:400-402 runs them), o, up, down, replayed from a HIP graph.  A step's
-algorithmic bytes are sum(N*K + 4N + 2K + 2N) over the six matrices = 117,427,456 B.  Weights
-rotate over ten copies (1.17 GB > the 256 MB Infinity Cache + L2), so every step streams W
-from HBM.  ``value`` = bytes per step / time per step (GB/s).
-
-Reported beside it on the same line: ``engine_four_launches`` (q|k|v grouped, o, up, down as
-four GEMV launches, the launch structure of the engine's blocks, where attention and the MLP's
-relu^2 separate the GEMVs), ``launches`` (each of those launches alone), ``six_separate_launches``
-(the reference's launch structure) and ``chain_dependent`` (one chain launch in which o reads
-q's output, up o's and down up's, each phase waiting for the previous one).
+Headline (``value``): BASELINE config 4, the full decode-step weight stream at M = 1 -- 4
+attention layers (q|k|v grouped: they share one normed input, model/attention_block.cuh:400-402;
+then o), 17 MLP layers (up, down) and 21 Mamba layers (in_proj with ragged N = 14690, out_proj
+with K = 6272): 92 GEMVs over 2.87 GB of e4m3 weights, each GEMV on its own seeded activation.
+A step is one GEMV chain launch (nmi_gemv_chain, 84 phases) replayed from a HIP graph; the
+stream is larger than the 256 MB Infinity Cache, so every step reads W from HBM.  A step's
+algorithmic bytes are sum(N*K + 4N + 2K + 2N) over the 92 matrices = 2,877,242,812 B; ``value``
+= bytes per step / time per step (GB/s); the north star's target is >= 80% of 8 TB/s on it.
 
 ``roofline`` -- the chain kernel (one launch per step): algorithmic bytes per launch over the
 launch duration, both from the timed region (graph replay, HIP events on the replay stream);
-HBM-bound, peak 8 TB/s.
+HBM-bound, peak 8 TB/s; ``traffic`` -- HBM bytes per launch from rocprofv3 FETCH_SIZE /
+WRITE_SIZE (profiles/gemv_chain_config4_decode_stream.md).  Beside it: the same GEMVs as 84
+separate launches, and as a dependent chain (every phase waits for its predecessor).
 
-Also reported (same line): ``prefill_gemm`` (config 3, M = 2048, TFLOP/s against 2.5 PFLOP/s
-dense bf16 MFMA; steady state: timed after 0.3 s of untimed replays), ``skinny`` (config 2, M in {2,4,8,16}, same four launches per step),
-``decode_stream`` (config 4, the 42-layer weight stream: one 84-phase chain launch, and as 84
-launches), ``mlp_block`` (the fp8
+Also reported (same line): ``decode_set`` (config 1, one attention and one MLP block at M = 1,
+ten rotated weight copies: one chain launch per step, the engine's four launches, each launch
+alone, six separate launches, the dependent chain), ``prefill_gemm`` (config 3, M = 2048,
+TFLOP/s against 2.5 PFLOP/s dense bf16 MFMA; steady state: timed after 0.3 s of untimed
+replays), ``skinny`` (config 2, M in {2,4,8,16}, four launches per step), ``mlp_block`` (the fp8
 MLP block, decode and prefill, fused against the reference's five-launch structure) and
-``cpu_baseline``:
-the torch CPU reference path (fp32 dequant then F.linear, oracle/linear.py) on a bounded
-sample of config 1, on this host's cores.
+``cpu_baseline``: the torch CPU reference path (per call: fp32 dequant of W, then F.linear in
+fp32, bf16 rounding -- tools/ref_full_model.py:44-49,137, restated in oracle/linear.py) on a
+bounded sample of config 4's layers on this host's cores, with the matmul-only time (W
+dequantized once, outside the timed region) and config 1 and config 3 samples beside it.
 """
 from __future__ import annotations
 
@@ -49,12 +47,11 @@ METRIC = "fp8 W8A16 GEMV achieved HBM GB/s (% of peak) at M=1; prefill GEMM TFLO
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 ROTATION_BYTES = 1 << 30
-# HBM bytes per launch of the config-1 step, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
-# script (scaled by a 256 MiB copy): the chain launch (profiles/gemv_chain_config1_decode_set.md)
-# and the four engine-structured launches (profiles/gemv_m1_config1_decode_set.md).  Re-measured
-# when the GEMV kernels change; reported as roofline.traffic next to the algorithmic bytes.
-MEASURED_TRAFFIC = {"chain": 119086873, "qkv_grouped": 22735927, "o_proj": 16326761, "up_proj": 39600623,
-                    "down_proj": 39772640}
+# HBM bytes per launch of the headline (config 4 as one chain launch), from rocprofv3
+# FETCH_SIZE / WRITE_SIZE runs of `bench.py --only stream` scaled by a 256 MiB copy
+# (profiles/gemv_chain_config4_decode_stream.md).  Re-measured when the GEMV kernels change;
+# reported as roofline.traffic next to the algorithmic bytes.  None until measured.
+MEASURED_TRAFFIC = {"chain_config4": 2904229512}
 
 
 def log(*a):
@@ -68,7 +65,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
-    p.add_argument("--only", choices=["prefill", "block", "skinny"],
+    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny"],
                    help="run one extra leg alone and print its JSON record (for profiling that leg); "
                         "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
@@ -184,17 +181,14 @@ def bench_decode_set(args, dev, host):
     chains = [make_chain(ops, xs, copies[r], ys) for r in range(R)]
     step_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l in synth.DECODE_SET)
 
-    for i in range(max(args.warmup, R)):          # eager warm-up, also before any capture
+    for i in range(2 * R):                        # eager warm-up, also before any capture
         chains[i % R].launch()
     torch.cuda.synchronize()
     T = Timer()
     g_all = T.capture(lambda: [c.launch() for c in chains])
-    tail = args.steps % R
-    g_tail = T.capture(lambda: [chains[r].launch() for r in range(tail)]) if tail else None
-    T.time_replays([g_all] * max(1, args.warmup // R))
-    graphs = [g_all] * (args.steps // R) + ([g_tail] if g_tail is not None else [])
-    ms = T.time_replays(graphs)
-    ms_per_step = ms / args.steps
+    T.time_replays([g_all] * 2)
+    reps = 20
+    ms_per_step = T.time_replays([g_all] * reps) / (reps * R)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     def timed(fn, reps=5):
@@ -233,26 +227,19 @@ def bench_decode_set(args, dev, host):
             yi = ys[0][i] if i < 3 else ys[{3: 1, 4: 2, 5: 3}[i]]
             ops.linear_fp8_w8a16(xi, *copies[r][i], out=yi)
     separate = {"launches": 6, **timed(six)}
-    # The dependent chain: each phase waits for and reads the previous phase's output.
+    # The dependent chain: each phase waits for and reads the previous phase's output (a launch
+    # per phase, ordered by the stream).
     dep = [make_chain(ops, xs, copies[r], ys, dependent=True) for r in range(R)]
     for c in dep:
         c.launch()
     torch.cuda.synchronize()
-    dependent = {"launches": 1, **timed(lambda r: dep[r].launch())}
-
-    traffic = MEASURED_TRAFFIC.get("chain")
-    roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per launch (x2.0 / x1.0 copy "
-                                  "calibration), profiles/gemv_chain_config1_decode_set.md",
-                "kernel": "gemv_chain_kernel (one launch per step)",
-                "launches_per_step": 1,
-                "per_launch_bytes_avg": step_bytes,
-                "per_launch_us_avg": round(ms_per_step * 1e3, 3)}
-    del copies, chains, steps, dep, g_all, g_tail
-    return dict(value=value, ms_per_step=ms_per_step, step_bytes=step_bytes, copies=R,
-                roofline=roofline, launches=launches, engine=engine, separate=separate,
-                dependent=dependent)
+    dependent = {"launches": dep[0].launches, **timed(lambda r: dep[r].launch())}
+    del copies, chains, steps, dep, g_all
+    return {"workload": "config1_decode_gemv_set_m1", "bytes_per_step": step_bytes, "weight_copies_rotated": R,
+            "chain_one_launch": {"launches": 1, "us_per_step": round(ms_per_step * 1e3, 2),
+                                 "GB/s": round(value, 1), "frac": round(value / HBM_PEAK_GBS, 4)},
+            "engine_four_launches": engine, "launches": launches, "six_separate_launches": separate,
+            "chain_dependent": dependent}
 
 
 def steady(T, graph, seconds=0.3):
@@ -325,76 +312,70 @@ def bench_skinny(dev, host, reps=20):
     return {"workload": "config2_skinny_decode_set", "launches_per_step": 4, "results": res}
 
 
-def bench_decode_stream(dev, reps=5):
+def bench_decode_stream(args, dev):
+    """Config 4 (the headline): the 84-phase chain launch per step, timed over args.steps
+    replays after args.warmup; beside it the same GEMVs as separate launches and as a dependent
+    chain."""
     import torch
 
     from nemotron_infer_amd import ops, synth
 
     layers = synth.decode_stream_layers()
-    acts = {}
-    calls = []
-    total_bytes = weight_bytes = 0
-
-    def act(K, kind):
-        if (K, kind) not in acts:
-            acts[(K, kind)] = synth.make_act(1, K, 41000 + K, dev, kind=kind)
-        return acts[(K, kind)]
-
-    for li, kind, lins in layers:
-        mats = []
-        for j, lin in enumerate(lins):
-            w, s = synth.make_weight(lin.N, lin.K, 40000 + 10 * li + j, dev)
-            mats.append((lin, w, s, torch.empty((1, lin.N), dtype=torch.bfloat16, device=dev)))
-            total_bytes += synth.linear_bytes(1, lin.N, lin.K)
-            weight_bytes += lin.N * lin.K
-        if kind == "attn":
-            q, k, v, o = mats
-            calls.append(("grouped", q[0].K, [(q[1], q[2]), (k[1], k[2]), (v[1], v[2])], [q[3], k[3], v[3]]))
-            calls.append(("single", o))
-        else:
-            for m in mats:
-                calls.append(("single", m))
+    phases, calls, total_bytes, weight_bytes, _ = synth.decode_stream_chain(dev)
 
     def run():
         for c in calls:
             if c[0] == "grouped":
-                ops.linear_fp8_w8a16_grouped(act(c[1], "normal"), c[2], outs=c[3])
+                ops.linear_fp8_w8a16_grouped(c[1], c[2], outs=c[3])
             else:
-                lin, w, s, y = c[1]
-                ops.linear_fp8_w8a16(act(lin.K, lin.act), w, s, out=y)
+                ops.linear_fp8_w8a16(c[1], c[2], c[3], out=c[4])
 
-    # The same GEMVs as one chain launch (a phase per launch above, each on its own activation).
-    phases = []
-    for c in calls:
-        if c[0] == "grouped":
-            phases.append((act(c[1], "normal"), [(w, s, y) for (w, s), y in zip(c[2], c[3])], False))
-        else:
-            lin, w, s, y = c[1]
-            phases.append((act(lin.K, lin.act), [(w, s, y)], False))
     chain = ops.GemvChain(phases)
-
     run()
-    chain.launch()
+    for _ in range(max(1, args.warmup)):          # eager warm-up, also before any capture
+        chain.launch()
     torch.cuda.synchronize()
     T = Timer()
+    # graphs of up to 20 launches, replayed to make exactly args.steps launches
+    per_g = min(20, args.steps)
+    g = T.capture(lambda: [chain.launch() for _ in range(per_g)])
+    tail = args.steps % per_g
+    g_tail = T.capture(lambda: [chain.launch() for _ in range(tail)]) if tail else None
+    T.time_replays([g] * max(1, args.warmup // per_g))
+    ms = T.time_replays([g] * (args.steps // per_g) + ([g_tail] if g_tail is not None else []))
+    ms_per_step = ms / args.steps
+    value = total_bytes / (ms_per_step * 1e-3) / 1e9
 
-    def timed(fn):
-        g = T.capture(fn)
-        T.time_replays([g])
-        ms = T.time_replays([g] * reps) / reps
-        del g
-        gbs = total_bytes / (ms * 1e-3) / 1e9
-        return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "tok_per_s_ceiling": round(1e3 / ms, 1)}
+    def timed(fn, reps=5):
+        gg = T.capture(fn)
+        T.time_replays([gg])
+        t = T.time_replays([gg] * reps) / reps
+        del gg
+        gbs = total_bytes / (t * 1e-3) / 1e9
+        return {"ms": round(t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "tok_per_s_ceiling": round(1e3 / t, 1)}
 
-    one = timed(chain.launch)
     sep = timed(run)
+    dep_chain = ops.GemvChain([(x, grp, i > 0) for i, (x, grp, _) in enumerate(phases)])
+    dep_chain.launch()
+    torch.cuda.synchronize()
+    dep = timed(dep_chain.launch)
+    roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC["chain_config4"],
+                "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per launch of `bench.py --only stream` "
+                                  "(x2.0 / x1.0 copy calibration), profiles/gemv_chain_config4_decode_stream.md",
+                "kernel": "gemv_stream_kernel (chain form, one launch per step)",
+                "launches_per_step": 1, "per_launch_bytes_avg": total_bytes,
+                "per_launch_us_avg": round(ms_per_step * 1e3, 2)}
     n_gemv = sum(len(l[2]) for l in layers)
-    n_launch = len(calls)
-    del calls, chain, phases
-    return {"workload": "config4_42layer_decode_stream", "gemvs": n_gemv, "bytes": total_bytes,
-            "weight_bytes": weight_bytes, "launch": f"one GEMV chain launch of {n_launch} phases", **one,
-            "separate_launches": {"launches": n_launch, **sep}}
+    out = dict(value=value, ms_per_step=ms_per_step, step_bytes=total_bytes, weight_bytes=weight_bytes,
+               gemvs=n_gemv, phases=len(phases), roofline=roofline,
+               tok_per_s_ceiling=round(1e3 / ms_per_step, 1),
+               separate_launches={"launches": len(calls), **sep},
+               dependent_chain={"launches": dep_chain.launches, **dep})
+    del calls, chain, dep_chain, phases, g, g_tail
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_mlp_block(dev, reps=5):
@@ -465,42 +446,85 @@ def bench_mlp_block(dev, reps=5):
                               "steps": "rmsnorm; stream-K flag clear; up GEMM + relu^2; down GEMM (stream-K) + residual"}}
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
 def cpu_baseline(host, seconds):
     """The reference's CPU path (tools/ref_full_model.py:44-49,137, restated in
-    oracle/linear.py): fp32 dequant of W, F.linear in fp32, bf16 rounding -- on config 1's
-    bytes, for about ``seconds`` of work, with torch's intra-op threads on this host."""
+    oracle/linear.py): per call, fp32 dequant of W, F.linear in fp32, bf16 rounding -- with
+    torch's intra-op threads on this host.  Timed on a bounded sample of config 4 (one Mamba, one
+    MLP and one attention layer: 14 % of its bytes; ``value``, GB/s), plus the matmul-only time
+    of the same sample (W dequantized once, outside the timed region), config 1's six matrices,
+    and one config-3 prefill GEMM (up_proj at M = 2048)."""
     import numpy as np
     import torch
 
     from nemotron_infer_amd import synth
     from oracle import linear as olin
 
-    data = [(x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy()) for _, x, w, s in host]
-    step_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l, *_ in host)
     threads = torch.get_num_threads()
-    olin.linear_fp8_w8a16(*data[0])          # warm-up
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
-        for x, w, s in data:
-            olin.linear_fp8_w8a16(x, w, s)
-        steps += 1
-        if time.perf_counter() - t0 >= seconds and steps >= 2:
-            break
-    dt = time.perf_counter() - t0
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
+    budget = seconds / 4.0
+
+    def loop(fn, budget_s, min_iters=2):
+        fn()                                       # warm-up
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            fn()
+            n += 1
+            if time.perf_counter() - t0 >= budget_s and n >= min_iters:
                 break
-    except OSError:
-        pass
-    return {"value": round(step_bytes * steps / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port", "ms_per_step": round(dt / steps * 1e3, 1),
-            "sample": f"config 1 decode set (6 GEMVs, M=1), {steps} steps in {dt:.1f} s: "
-                      f"torch CPU fp32 dequant + F.linear + bf16 round (oracle/linear.py), "
-                      f"{threads} threads of os.cpu_count()={os.cpu_count()} ({model})"}
+        return (time.perf_counter() - t0) / n
+
+    # config 4 sample: one layer of each kind, on the CPU, same generator as the GPU stream
+    sample = []
+    for li, kind, lins in synth.decode_stream_layers():
+        if (kind, li) in (("mamba", 0), ("mlp", 1), ("attn", 41)):
+            for j, lin in enumerate(lins):
+                w, s = synth.make_weight(lin.N, lin.K, 40000 + 10 * li + j, "cpu")
+                x = synth.make_act(1, lin.K, 41000 + lin.K, "cpu", kind=lin.act)
+                sample.append((x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy(), lin))
+    sbytes = sum(synth.linear_bytes(1, l.N, l.K) for *_, l in sample)
+    t_ref = loop(lambda: [olin.linear_fp8_w8a16(x, w, s) for x, w, s, _ in sample], budget)
+    deq = [(torch.from_numpy(olin.bf16_to_f32(x)).view(1, -1),
+            torch.from_numpy(olin.dequant_f32(w, s))) for x, w, s, _ in sample]
+    t_mm = loop(lambda: [torch.nn.functional.linear(x, w) for x, w in deq], budget)
+    del deq
+    # config 1: the six matrices, per call dequant
+    c1 = [(x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy()) for _, x, w, s in host]
+    c1_bytes = sum(synth.linear_bytes(1, l.N, l.K) for l, *_ in host)
+    t_c1 = loop(lambda: [olin.linear_fp8_w8a16(x, w, s) for x, w, s in c1], budget)
+    # config 3: one prefill GEMM (up_proj, M = 2048), per call dequant and matmul only
+    lin = synth.PREFILL_SET[0]
+    M = synth.PREFILL_M
+    w3, s3 = synth.make_weight(lin.N, lin.K, 3000, "cpu")
+    x3 = synth.make_act(M, lin.K, 3100, "cpu", outlier_frac=0.001).float()
+    w3t = w3.view(torch.float8_e4m3fn)
+    w3d = w3t.float() * s3[:, None]
+    t_c3_mm = loop(lambda: torch.nn.functional.linear(x3, w3d), budget / 2, min_iters=1)
+    t_c3 = loop(lambda: torch.nn.functional.linear(x3, w3t.float() * s3[:, None]), budget / 2, min_iters=1)
+    fl3 = synth.linear_flops(M, lin.N, lin.K)
+    where = f"{threads} threads of os.cpu_count()={os.cpu_count()} ({_cpu_model()})"
+    return {"value": round(sbytes / t_ref / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"config 4 layers 0 (Mamba), 1 (MLP), 41 (attention): 8 GEMVs, {sbytes} B per pass, "
+                      f"{t_ref * 1e3:.1f} ms per pass: torch CPU per-call fp32 dequant + F.linear + bf16 round "
+                      f"(oracle/linear.py), {where}",
+            "matmul_only": {"value": round(sbytes / t_mm / 1e9, 3), "unit": "GB/s",
+                            "ms_per_pass": round(t_mm * 1e3, 2),
+                            "note": "same sample, W dequantized once outside the timed region, F.linear fp32"},
+            "config1": {"value": round(c1_bytes / t_c1 / 1e9, 3), "unit": "GB/s", "ms_per_step": round(t_c1 * 1e3, 1)},
+            "config3_prefill_up_proj": {"M": M, "N": lin.N, "K": lin.K,
+                                        "per_call_dequant": {"ms": round(t_c3 * 1e3, 1),
+                                                             "TFLOP/s": round(fl3 / t_c3 / 1e12, 3)},
+                                        "matmul_only": {"ms": round(t_c3_mm * 1e3, 1),
+                                                        "TFLOP/s": round(fl3 / t_c3_mm / 1e12, 3)}}}
 
 
 def main():
@@ -529,24 +553,29 @@ def main():
     if args.only:
         if args.only == "skinny":
             leg = bench_skinny(dev, decode_inputs())
+        elif args.only == "stream":
+            leg = bench_decode_stream(args, dev)
+            leg = {k: v for k, v in leg.items()}
+        elif args.only == "decode":
+            leg = bench_decode_set(args, dev, decode_inputs())
         else:
             leg = bench_prefill(dev) if args.only == "prefill" else bench_mlp_block(dev)
         print(json.dumps(leg), flush=True)
         return
+    log("decode stream (config 4, headline) ...")
+    d = bench_decode_stream(args, dev)
+    log(f"decode stream: {d['value']:.1f} GB/s, {d['ms_per_step'] * 1e3:.1f} us/step")
     host = decode_inputs()
-    log("decode set (config 1) ...")
-    d = bench_decode_set(args, dev, host)
-    log(f"decode set: {d['value']:.1f} GB/s, {d['ms_per_step'] * 1e3:.2f} us/step")
     extras = {}
     if not args.no_extras:
+        log("decode set (config 1) ...")
+        extras["decode_set"] = bench_decode_set(args, dev, host)
+        log(f"decode set: {extras['decode_set']['chain_one_launch']}")
         log("prefill GEMM (config 3) ...")
         extras["prefill_gemm"] = bench_prefill(dev)
         log(f"prefill: {extras['prefill_gemm']['tflops']} TFLOP/s")
         log("skinny M (config 2) ...")
         extras["skinny"] = bench_skinny(dev, host)
-        log("decode stream (config 4) ...")
-        extras["decode_stream"] = bench_decode_stream(dev)
-        log(f"stream: {extras['decode_stream']['GB/s']} GB/s")
         log("mlp block ...")
         extras["mlp_block"] = bench_mlp_block(dev)
         log(f"mlp block: {extras['mlp_block']['decode_m1']}")
@@ -566,20 +595,19 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,0.02) weights -> e4m3 per-tensor scale; bf16 N(0,1) / relu^2 activations)",
-        "config": {"workload": "config1_decode_gemv_set_m1",
-                   "shapes": {l.name: [l.N, l.K] for l in synth.DECODE_SET},
-                   "M": 1, "bytes_per_step": d["step_bytes"],
-                   "weight_copies_rotated": d["copies"],
+        "config": {"workload": "config4_42layer_decode_stream",
+                   "layers": {"attention": 4, "mlp": 17, "mamba": 21}, "gemvs": d["gemvs"],
+                   "phases_per_launch": d["phases"], "M": 1, "bytes_per_step": d["step_bytes"],
+                   "weight_bytes": d["weight_bytes"],
                    "operands": "W e4m3 [N,K] (converted exactly to bf16) + f32 per-row scale, x bf16, "
                                "f32 accumulation, y bf16",
-                   "launch": "HIP graph; per step one GEMV chain launch: phases q|k|v grouped, o, up, "
-                             "down, each on its own config-1 activation"},
+                   "launch": "HIP graph; per step one GEMV chain launch of 84 phases (q|k|v grouped, o; up, "
+                             "down; in_proj, out_proj per layer), each on its own activation"},
         "roofline": d["roofline"],
         "cpu_baseline": cpu,
-        "engine_four_launches": d["engine"],
-        "launches": d["launches"],
-        "six_separate_launches": d["separate"],
-        "chain_dependent": d["dependent"],
+        "tok_per_s_ceiling": d["tok_per_s_ceiling"],
+        "separate_launches": d["separate_launches"],
+        "dependent_chain": d["dependent_chain"],
         **extras,
         "wall_s": round(time.time() - t0, 1),
     }

@@ -115,34 +115,27 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                                  size_t workspace_bytes, void* stream);
 
 /*
- * GEMV chain (M = 1): a sequence of GEMVs in one launch.  A chain is a list of phases, each a
- * grouped GEMV of one activation vector x [K] (bf16) against up to NMI_MAX_GROUPS e4m3
- * matrices, computed as nmi_linear_fp8_w8a16_grouped computes it (same per-row results up to
- * float32 summation order).  A phase with wait_prev = 1 reads its x only after the previous
- * phase has completed, so x may be that phase's output: the order of dependent launches on one
- * stream, with the weight loads of the waiting phase issued while the previous one drains.
- * Phases with wait_prev = 0 (x ready before the launch) stream back to back with no launch
- * boundary between them.  Replaces a sequence of per-projection gemv_fp8 launches
- * (ops/gemv.cuh:92-104 at model/attention_block.cuh:400-402,409, model/mlp_block.cuh:142-148,
- * model/mamba_block.cuh:476-481,508-509); the reference has no chained form.
+ * GEMV chain (M = 1): a sequence of GEMVs with as few launches as the dependencies allow.  A
+ * chain is a list of phases, each a grouped GEMV of one activation vector x [K] (bf16) against
+ * up to NMI_MAX_GROUPS e4m3 matrices, computed exactly as nmi_linear_fp8_w8a16(_grouped) computes
+ * it at M = 1 (the same per-row results, bit for bit).  Phases with wait_prev = 0 (x ready before
+ * the launch) stream back to back in one kernel launch; a phase with wait_prev = 1 reads its x
+ * only after the previous phase has completed, so x may be that phase's output: it starts a new
+ * launch on the same stream (stream order is the synchronisation).  Replaces a sequence of
+ * per-projection gemv_fp8 launches (ops/gemv.cuh:92-104 at model/attention_block.cuh:400-402,409,
+ * model/mlp_block.cuh:142-148, model/mamba_block.cuh:476-481,508-509); the reference has no
+ * chained form.
  *   nmi_gemv_chain_create   validates the phases as nmi_linear_fp8_w8a16_grouped would (M = 1),
- *                           plans the work split and the grid for the current device and copies
+ *                           plans the work split and the grids for the current device and copies
  *                           the plan to device memory (hipMalloc + hipMemcpy: call it outside
  *                           graph capture, once per set of pointers).
- *   nmi_gemv_chain_launch   one kernel launch; workspace: 256-byte aligned, at least
- *                           nmi_gemv_chain_workspace_bytes(nphases) bytes, zero-filled before its
- *                           first use (every launch leaves it zero again).  Launches that may
- *                           overlap in time need distinct workspaces.  Capturable in a HIP graph.
+ *   nmi_gemv_chain_launch   one kernel launch per run of phases up to the next waiting phase,
+ *                           asynchronous on `stream`; capturable in a HIP graph.  workspace /
+ *                           workspace_bytes are accepted for compatibility and never accessed
+ *                           (NULL / 0 is fine).
  *   nmi_gemv_chain_destroy  frees the plan.
- * Buffers: a phase's output may overlap another phase's x or output only when every phase after
- * the earlier of the two, up to the later, has wait_prev = 1 (a phase without it may run at the
- * same time as the phases before it).
- * The launch is a persistent grid of at most the workgroups that are resident at once, whose
- * workgroups wait on each other's phases: run it with no other long-running kernel sharing the
- * device (another chain on a concurrent stream may hold the slots a waiting phase needs).  A
- * wait never hangs: after 0.2 s it gives up, the outputs are invalid and the 32-bit word at
- * byte offset nmi_gemv_chain_workspace_bytes(nphases) - 128 is set non-zero (and stays so until
- * the caller clears it).
+ * Buffers: a phase's output may overlap another phase's x or output only when a waiting phase
+ * lies between the two (phases of one launch may run at the same time).
  */
 #define NMI_MAX_CHAIN_PHASES 4096
 typedef struct nmi_gemv_phase {
@@ -154,7 +147,7 @@ typedef struct nmi_gemv_phase {
 } nmi_gemv_phase;
 typedef struct nmi_gemv_chain nmi_gemv_chain;
 int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_chain** out);
-size_t nmi_gemv_chain_workspace_bytes(int nphases);
+size_t nmi_gemv_chain_workspace_bytes(int nphases);     /* 0: no launch writes a workspace */
 int nmi_gemv_chain_launch(const nmi_gemv_chain* chain, void* workspace, size_t workspace_bytes, void* stream);
 int nmi_gemv_chain_destroy(nmi_gemv_chain* chain);
 
@@ -229,15 +222,15 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
                         int inter, float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "gemm.sk",
+ * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg": schedule of the multi-row
+ * GEMV kernel (M = 2, or M = 1 with "gemv.multirow" = 1), "gemv.t" = 4 also 4 rows per step for
+ * the M = 1 stream kernel, "gemv.wgs": its workgroups per CU (1, 2), "gemm.tile", "gemm.sk",
  * "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
  * "s4.dma": 2 selects the windowed form of the 4x4x4 skinny kernel instead of the pipelined one,
  * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace
- * nmi_linear_workspace_bytes then reports),
- * "chain.wgs": workgroups per CU of a GEMV chain created afterwards, "chain.wait_us": bound of a
- * chain's waits in microseconds); 0 restores the automatic choice.  Process-wide, not
- * thread-safe against concurrent launches; results do not depend on them beyond float32
- * summation order (except chain.wait_us, whose bound a correct chain never reaches).  No
+ * nmi_linear_workspace_bytes then reports), "chain.wgs": workgroups per CU of a GEMV chain
+ * created afterwards); 0 restores the automatic choice.  Process-wide, not thread-safe against
+ * concurrent launches; results do not depend on them beyond float32 summation order.  No
  * counterpart in the reference (its launch shapes are compile-time constants,
  * ops/gemv.cuh:100-103).
  */

@@ -209,13 +209,19 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                     static_cast<hipStream_t>(stream), fn);
 }
 
-// GEMV chain: the planned work items live in device memory for the handle's lifetime.
+// GEMV chain: the planned phase table and per-wave step counts live in device memory for the
+// handle's lifetime; one launch per segment (a run of phases up to the next one that waits).
+struct ChainSegment {
+    int p0, nphases;                        // phases of the segment
+    int total_rg;                           // its row groups
+    int grid;
+    size_t steps_off;                       // its waves' step counts in wave_steps
+};
 struct nmi_gemv_chain {
-    ChainItem* dev = nullptr;               // the work items, one record each
+    StreamPhase* dev = nullptr;             // the phase table
+    int* wave_steps = nullptr;              // steps of each wave, segment by segment
+    std::vector<ChainSegment> seg;
     int nphases = 0;
-    int total_items = 0;
-    int grid = 0;
-    size_t lds_bytes = 0;
     int device = -1;
 };
 
@@ -225,44 +231,54 @@ int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_ch
     *out = nullptr;
     if (!phases || nphases < 1 || nphases > NMI_MAX_CHAIN_PHASES)
         return fail(NMI_ERR_INVALID_ARG, "%s: nphases=%d must be in [1, %d]", fn, nphases, NMI_MAX_CHAIN_PHASES);
-    std::vector<ChainPhase> host((size_t)nphases);
-    int64_t items = 0;
+    std::vector<StreamPhase> host((size_t)nphases);
+    std::vector<ChainSegment> seg;
+    int64_t rgs = 0;
     for (int p = 0; p < nphases; ++p) {
         const nmi_gemv_phase& P = phases[p];
         if (P.ngroups < 1 || P.ngroups > NMI_MAX_GROUPS)
             return fail(NMI_ERR_INVALID_ARG, "%s: phase %d: ngroups=%d must be in [1, %d]", fn, p, P.ngroups,
                         NMI_MAX_GROUPS);
-        ChainPhase& ph = host[(size_t)p];
-        ph = ChainPhase{};
+        StreamPhase& ph = host[(size_t)p];
+        ph = StreamPhase{};
         ph.x = static_cast<const uint16_t*>(P.x_bf16);
         ph.K = P.K;
         ph.ngroups = P.ngroups;
-        ph.wait = P.wait_prev ? 1 : 0;
         for (int i = 0; i < P.ngroups; ++i) {
             const nmi_linear_group& G = P.groups[i];
             int rc = check_linear(P.x_bf16, P.K, G.w_e4m3, G.ldw, G.w_scale, G.y_bf16, G.ldy, 1, G.N, P.K, fn);
             if (rc) return rc;
-            ph.g[i] = GemvGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
-                                static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0, Epi{}};
-            items += (G.N + 3) / 4;                   // upper bound of the work items (4 rows each)
+            ph.g[i] = StreamGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
+                                  static_cast<uint16_t*>(G.y_bf16), nullptr, G.N, 0, kEpiNone, 0};
+            rgs += (G.N + kStreamChainT - 1) / kStreamChainT;
         }
+        if (p == 0 || P.wait_prev) seg.push_back(ChainSegment{p, 0, 0, 0, 0});
+        ++seg.back().nphases;
     }
-    if (items >= ((int64_t)1 << 30)) return fail(NMI_ERR_INVALID_ARG, "%s: too many rows in total", fn);
-    size_t lds = 0;
-    const int total = gemv_chain_plan(host.data(), nphases, &lds);
+    if (rgs >= ((int64_t)1 << 30)) return fail(NMI_ERR_INVALID_ARG, "%s: too many rows in total", fn);
+    hipError_t e = hipSuccess;
+    std::vector<int> steps;
+    for (ChainSegment& sg : seg) {
+        sg.total_rg = stream_chain_plan(host.data() + sg.p0, sg.nphases);
+        if (e == hipSuccess) e = stream_chain_grid(sg.total_rg, &sg.grid);
+        if (e != hipSuccess) break;
+        sg.steps_off = steps.size();
+        steps.resize(steps.size() + (size_t)sg.grid * 4);
+        stream_chain_wave_steps(host.data() + sg.p0, sg.nphases, sg.grid * 4, steps.data() + sg.steps_off);
+    }
     auto* c = new nmi_gemv_chain;
     c->nphases = nphases;
-    c->total_items = total;
-    c->lds_bytes = lds;
-    hipError_t e = hipGetDevice(&c->device);
-    if (e == hipSuccess) e = gemv_chain_grid(lds, total, &c->grid);
-    std::vector<ChainItem> table((size_t)total);
-    gemv_chain_items(host.data(), nphases, table.data());
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->dev), table.size() * sizeof(ChainItem));
+    c->seg = seg;
+    if (e == hipSuccess) e = hipGetDevice(&c->device);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->dev), host.size() * sizeof(StreamPhase));
     if (e == hipSuccess)
-        e = hipMemcpy(c->dev, table.data(), table.size() * sizeof(ChainItem), hipMemcpyHostToDevice);
+        e = hipMemcpy(c->dev, host.data(), host.size() * sizeof(StreamPhase), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->wave_steps), steps.size() * sizeof(int));
+    if (e == hipSuccess)
+        e = hipMemcpy(c->wave_steps, steps.data(), steps.size() * sizeof(int), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         if (c->dev) (void)hipFree(c->dev);
+        if (c->wave_steps) (void)hipFree(c->wave_steps);
         delete c;
         return hip_status(e, fn);
     }
@@ -271,31 +287,31 @@ int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_ch
 }
 
 size_t nmi_gemv_chain_workspace_bytes(int nphases) {
-    if (nphases < 1 || nphases > NMI_MAX_CHAIN_PHASES) return 0;
-    return gemv_chain_counter_bytes(nphases);                 // a multiple of 256 bytes
+    (void)nphases;
+    return 0;                                                 // no launch of a chain writes one
 }
 
 int nmi_gemv_chain_launch(const nmi_gemv_chain* chain, void* workspace, size_t workspace_bytes, void* stream) {
     const char* fn = "nmi_gemv_chain_launch";
+    (void)workspace;
+    (void)workspace_bytes;
     if (!chain || !chain->dev) return fail(NMI_ERR_INVALID_ARG, "%s: invalid chain", fn);
-    if (!workspace || !aligned(workspace, 256))
-        return fail(NMI_ERR_ALIGNMENT, "%s: workspace must be non-NULL and 256-byte aligned", fn);
-    if (workspace_bytes < nmi_gemv_chain_workspace_bytes(chain->nphases)) {
-        set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes,
-                       nmi_gemv_chain_workspace_bytes(chain->nphases));
-        return NMI_ERR_WORKSPACE;
-    }
     int dev = -1;
     if (hipGetDevice(&dev) == hipSuccess && dev != chain->device)
         return fail(NMI_ERR_INVALID_ARG, "%s: chain was created on device %d, current is %d", fn, chain->device, dev);
-    return hip_status(launch_gemv_chain(chain->dev, chain->nphases, chain->total_items, chain->grid, chain->lds_bytes,
-                                        static_cast<uint32_t*>(workspace), static_cast<hipStream_t>(stream)),
-                      fn);
+    for (const ChainSegment& sg : chain->seg) {
+        const hipError_t e = launch_gemv_stream_chain(chain->dev + sg.p0, chain->wave_steps + sg.steps_off, sg.nphases,
+                                                      sg.total_rg, sg.grid, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_status(e, fn);
+    }
+    return NMI_OK;
 }
 
 int nmi_gemv_chain_destroy(nmi_gemv_chain* chain) {
     if (!chain) return NMI_OK;
-    const hipError_t e = chain->dev ? hipFree(chain->dev) : hipSuccess;
+    hipError_t e = chain->dev ? hipFree(chain->dev) : hipSuccess;
+    const hipError_t e2 = chain->wave_steps ? hipFree(chain->wave_steps) : hipSuccess;
+    if (e == hipSuccess) e = e2;
     delete chain;
     return hip_status(e, "nmi_gemv_chain_destroy");
 }
@@ -360,7 +376,8 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s4.kg")) t.s4_kg = value;
     else if (!std::strcmp(knob, "gemm.sk")) t.gemm_sk = value;
     else if (!std::strcmp(knob, "chain.wgs")) t.chain_wgs = value;
-    else if (!std::strcmp(knob, "chain.wait_us")) t.chain_wait_us = value;
+    else if (!std::strcmp(knob, "gemv.wgs")) t.gemv_wgs = value;
+    else if (!std::strcmp(knob, "gemv.multirow")) t.gemv_multirow = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

@@ -389,223 +389,19 @@ hipError_t launch_t(int t, int p, const Mode& md, GemvArgs& a, hipStream_t strea
 
 int pow2_pieces(int need) { return need <= 2 ? 2 : (need <= 4 ? 4 : 8); }
 
-// ---------------------------------------------------------------------------------------
-// GEMV chain: the GEMVs of a decode step (phases, each a grouped GEMV sharing one x) in one
-// launch.  Work items (T * 4 / ks rows of one group each) are numbered in phase order; the grid
-// is at most the number of workgroups that fit on the device at once, and workgroup b takes
-// items b, b + G, b + 2G, ... in order.  An item of a waiting phase issues its first weight
-// loads, then waits until the previous phase has completed (its x may be that phase's output),
-// then stages x and finishes its rows.  The weight stream of the next phase therefore starts
-// while the current one drains, and the step pays one launch.  Deadlock-free when all G
-// workgroups are resident together (G is sized so): the lowest unfinished item belongs to a
-// running workgroup whose earlier items are done, and it waits only on lower items.
-//
-// Completion is counted only for phases that a later phase waits on, and without one contended
-// address (device-scope atomics on one cache line serialize at a few ns each): such an item,
-// once its stores have completed (s_waitcnt), adds 1 to stripe (local index % kChainStripes) of
-// its phase, each stripe on its own 128-byte line; the item completing a stripe adds 1 to the
-// phase's done line, which the waiters poll.  Other items store and go on.  Every workgroup
-// leaving the loop adds 1 to its exit stripe (blockIdx % kChainStripes), the one completing a
-// stripe to the exit-done line, and the one completing that re-arms every line: the counters
-// are zero again when the launch ends.  A wait that has not ended after 0.2 s (tuning knob
-// chain.wait_us) gives up (wrong outputs, never a hang) and sets the error word, which is left
-// set.  Outputs of a signalling
-// phase are stored, and x of a waiting phase is loaded, at device scope (coherent across the
-// XCDs' L2 caches).
-__device__ __forceinline__ uint32_t* chain_line(uint32_t* ctr, int p, int line) {
-    return ctr + ((int64_t)p * (kChainStripes + 1) + line) * kChainLineWords;
-}
-
-// Pointers read from the phase table carry no address space; the chain kernel converts them to
-// global-memory pointers so that its loads and stores are global (not FLAT) instructions.
-#define NMI_GLOBAL __attribute__((address_space(1)))
-template <class E>
-__device__ __forceinline__ NMI_GLOBAL E* global_ptr(E* p) {
-    return (NMI_GLOBAL E*)p;
-}
-
-__device__ __forceinline__ uint4 load_stream16_g(const NMI_GLOBAL uint8_t* p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const NMI_GLOBAL u32x4*>(p));
-    return uint4{v.x, v.y, v.z, v.w};
-}
-
-// The phase table is written before the launch and never by a kernel: read through the constant
-// address space, its uniform fields are scalar loads (as generic memory, next to the kernel's
-// own stores, the compiler would read it with vector loads and wait for them together with the
-// weight loads in flight).
-#define NMI_CONST __attribute__((address_space(4)))
-
-__device__ __forceinline__ int chain_stripes(int nitems) { return nitems < kChainStripes ? nitems : kChainStripes; }
-
-template <int T, int P>
-__global__ __launch_bounds__(256) void gemv_chain_kernel(const ChainItem* __restrict__ items, int nphases,
-                                                          int total_items, uint32_t* __restrict__ ctr,
-                                                          uint64_t wait_ticks) {
-    typedef __attribute__((address_space(3))) void lds_void;
-    extern __shared__ uint4 xs[];                  // [half][window rounded up to 64 chunks]
-    __shared__ float partial[kWaves][kWaves * T];
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-    const uint32_t xs_addr = (uint32_t)(uintptr_t)(lds_void*)xs;
-    uint32_t* err = ctr + (int64_t)(gemv_chain_counter_lines(nphases) - 1) * kChainLineWords;
-    const NMI_CONST ChainItem* tab = (const NMI_CONST ChainItem*)items;
-    for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
-        const NMI_CONST ChainItem& it = tab[item];
-        const int ks = it.ks;                      // waves splitting K: 1, 2 or 4
-        const int g = wave / ks, q = wave % ks;
-        const int row0 = g * T;                    // this wave's first row within the item
-        const int rows = it.rows;
-        const int64_t ldw = it.ldw;
-        const int C = it.K >> 4, window = it.window;
-        const int wpad = (window + 63) & ~63;      // LDS chunks per half
-        const bool wait = it.flags & kChainWait, signal = it.flags & kChainSignal;
-        const NMI_GLOBAL uint8_t* gW = global_ptr(it.w);
-
-        // this lane's row scale (lane t < T of a K-slice-0 wave), issued before the weights so that
-        // it has arrived with them
-        float sc = 0.f;
-        if (q == 0 && lane < T && row0 + lane < rows) sc = global_ptr(it.s)[row0 + lane];
-        const NMI_GLOBAL uint8_t* wrow[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) wrow[t] = gW + (int64_t)min(row0 + t, rows - 1) * ldw;
-        float a0[T], a1[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) a0[t] = a1[t] = 0.f;
-        for (int w0 = 0; w0 < C; w0 += window) {
-            const int wc = min(window, C - w0);
-            const int cb = w0 + (q * wc) / ks;
-            const int ce = w0 + ((q + 1) * wc) / ks;
-            const int clast = max(ce - 1, cb);
-            int c0 = cb + lane;
-            // 1. this window's first batch of weights (independent of earlier phases)
-            uint4 wv[T][P];
-#pragma unroll
-            for (int t = 0; t < T; ++t)
-#pragma unroll
-                for (int i = 0; i < P; ++i)
-                    wv[t][i] = load_stream16_g(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
-            // 2. x may be the previous phase's output: wait for that phase (first window only)
-            if (w0 == 0 && wait) {
-                if (tid == 0) {
-                    const uint32_t need = (uint32_t)it.wait_need;
-                    const uint32_t* done = chain_line(ctr, it.phase - 1, kChainStripes);
-                    const uint64_t t_end = wall_clock64() + wait_ticks;   // wall clock: 100 MHz
-                    while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-                        if ((uint64_t)wall_clock64() > t_end) {
-                            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(2);
-                    }
-                }
-                __syncthreads();
-            } else if (w0 != 0) {
-                __syncthreads();                   // the previous window has been consumed
-            }
-            // 3. stage x by LDS DMA (two 16-byte halves per chunk, as the one-launch kernel): job
-            //    (half h, 64-chunk block b) has lane l load piece 2 (64 b + l) + h; lanes past the
-            //    window load a valid piece into an unread pad slot of the block
-            const uint8_t* xw = reinterpret_cast<const uint8_t*>(it.x) + (int64_t)w0 * 32;
-            const int jobs = 2 * ((wc + 63) >> 6);
-            for (int j = wave; j < jobs; j += kWaves) {
-                const int h = j & 1, s0 = (j >> 1) << 6;
-                const uint32_t off = (uint32_t)min(2 * (s0 + lane) + h, 2 * wc - 1) * 16;
-                const uint32_t dst = xs_addr + (uint32_t)(h * wpad + s0) * 16;
-                if (wait) dma16_lds_device(xw, off, dst);
-                else dma16_lds(xw, off, dst);
-            }
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            // 4. consume; further batches when a lane's slice exceeds P chunks per row
-            for (;;) {
-#pragma unroll
-                for (int i = 0; i < P; ++i) {
-                    const int c = c0 + 64 * i;
-                    if (c < ce) {
-                        const uint4 lo4 = xs[c - w0], hi4 = xs[wpad + c - w0];
-#pragma unroll
-                        for (int t = 0; t < T; ++t) dot16(wv[t][i], lo4, hi4, a0[t], a1[t]);
-                    }
-                }
-                c0 += 64 * P;
-                if (c0 - lane >= ce) break;         // uniform across the wave
-#pragma unroll
-                for (int t = 0; t < T; ++t)
-#pragma unroll
-                    for (int i = 0; i < P; ++i)
-                        wv[t][i] = load_stream16_g(wrow[t] + (int64_t)min(c0 + 64 * i, clast) * 16);
-            }
-        }
-        // wave sums (16-lane DPP rows, then 0 + 1 + 2 + 3), then the K slices in order q = 0..ks-1
-        float sums[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) sums[t] = wave_sum(a0[t] + a1[t]);
-        if (lane == 0) {
-#pragma unroll
-            for (int t = 0; t < T; ++t) partial[q][g * T + t] = sums[t];
-        }
-        __syncthreads();                           // also: every wave is done reading xs
-        if (q == 0 && lane < T) {
-            const int t = lane;
-            float v = partial[0][g * T + t];
-            for (int qq = 1; qq < ks; ++qq) v += partial[qq][g * T + t];
-            const int row = row0 + t;
-            if (row < rows) {
-                // plain epilogue: a chain group has no fused relu^2 or residual
-                const uint16_t out = epilogue(v, sc, kEpiNone, 0);
-                NMI_GLOBAL uint16_t* yp = global_ptr(it.y) + row;
-                if (signal) __hip_atomic_store(yp, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else *yp = out;
-            }
-        }
-        // completion (counted when a later phase waits on this one): the stores have completed,
-        // then the count
-        if (signal) {
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (tid == 0) {
-                const uint32_t v = __hip_atomic_fetch_add(chain_line(ctr, it.phase, it.stripe), 1u, __ATOMIC_RELAXED,
-                                                          __HIP_MEMORY_SCOPE_AGENT);
-                if (v + 1 == (uint32_t)it.stripe_items)
-                    __hip_atomic_fetch_add(chain_line(ctr, it.phase, kChainStripes), 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-    }
-    // exit count, after this workgroup's own counts have landed; the last workgroup out re-arms
-    // the counters (nothing reads them any more)
-    if (wave == 0) {
-        __builtin_amdgcn_s_waitcnt(0);
-        int rearm = 0;
-        if (lane == 0) {
-            const int G = (int)gridDim.x;
-            const int stripe = (int)blockIdx.x % kChainStripes;
-            const uint32_t v = __hip_atomic_fetch_add(chain_line(ctr, nphases, stripe), 1u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-            if (v + 1 == (uint32_t)((G - stripe + kChainStripes - 1) / kChainStripes)) {
-                const uint32_t d = __hip_atomic_fetch_add(chain_line(ctr, nphases, kChainStripes), 1u,
-                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                rearm = d + 1 == (uint32_t)chain_stripes(G);
-            }
-        }
-        if (__builtin_amdgcn_readfirstlane(rearm)) {
-            const int lines = (nphases + 1) * (kChainStripes + 1);
-            for (int l = lane; l < lines; l += 64)
-                __hip_atomic_store(ctr + (int64_t)l * kChainLineWords, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-}
-
 }  // namespace
 
 bool gemv_norm_supported(int M, int K) {
+    if (M == 1 && tuning().gemv_multirow == 0) return gemv_stream_supported(K);
     const int C = K >> 4;
     return (M == 1 || M == 2) && 2 * C <= 256 * (8 / M);
 }
 
 hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
                                int ngroups, hipStream_t stream, const Norm& norm) {
+    // M = 1: the stream kernel (gemv_stream.hip), unless tuning knob gemv.multirow selects this one
+    if (M == 1 && tuning().gemv_multirow == 0 && gemv_stream_supported(K))
+        return launch_gemv_stream(x, K, groups, ngroups, stream, norm);
     const DeviceInfo& dev = device_info();
     if (norm.w && !gemv_norm_supported(M, K)) return hipErrorInvalidValue;
     GemvArgs a{};
@@ -651,88 +447,6 @@ hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, con
         case 2: return launch_t<2>(t, p, md, a, stream);
         default: return launch_t<4>(t, p, md, a, stream);
     }
-}
-
-namespace {
-constexpr int kChainT = 4;       // rows per wave in the chain kernel
-constexpr int kChainP = 4;       // 16-byte chunks per lane per row per batch
-}  // namespace
-
-int gemv_chain_plan(ChainPhase* phases, int nphases, size_t* lds_bytes) {
-    int items = 0;
-    int wmax = 1;
-    for (int p = 0; p < nphases; ++p) {
-        ChainPhase& ph = phases[p];
-        const int C = ph.K >> 4;
-        ph.ks = C <= 64 * 4 ? 1 : (C <= 2 * 64 * 4 ? 2 : 4);   // about 3-4 chunks per lane per row
-        ph.window = C < kMaxWindowChunks ? C : kMaxWindowChunks;
-        wmax = ph.window > wmax ? ph.window : wmax;
-        const int rows_per_wg = (kWaves / ph.ks) * kChainT;
-        ph.item_begin = items;
-        int n = 0;
-        for (int i = 0; i < ph.ngroups; ++i) {
-            ph.g[i].wg_begin = n;
-            n += (ph.g[i].N + rows_per_wg - 1) / rows_per_wg;
-        }
-        ph.nitems = n;
-        items += n;
-    }
-    for (int p = 0; p < nphases; ++p) phases[p].signal = p + 1 < nphases && phases[p + 1].wait;
-    *lds_bytes = (size_t)((wmax + 63) & ~63) * 2 * sizeof(uint4);
-    return items;
-}
-
-void gemv_chain_items(const ChainPhase* planned, int nphases, ChainItem* out) {
-    int k = 0;
-    for (int p = 0; p < nphases; ++p) {
-        const ChainPhase& ph = planned[p];
-        const int rows_per_item = (kWaves / ph.ks) * kChainT;
-        int local = 0;
-        for (int gi = 0; gi < ph.ngroups; ++gi) {
-            const GemvGroup& grp = ph.g[gi];
-            for (int r0 = 0; r0 < grp.N; r0 += rows_per_item, ++local, ++k) {
-                ChainItem& it = out[k];
-                it.w = grp.W + (int64_t)r0 * grp.ldw;
-                it.x = ph.x;
-                it.y = grp.y + r0;
-                it.s = grp.s + r0;
-                it.ldw = grp.ldw;
-                it.rows = grp.N - r0 < rows_per_item ? grp.N - r0 : rows_per_item;
-                it.K = ph.K;
-                it.ks = ph.ks;
-                it.window = ph.window;
-                it.phase = p;
-                it.flags = (p > 0 && ph.wait ? kChainWait : 0) | (ph.signal ? kChainSignal : 0);
-                it.wait_need = p > 0 ? (planned[p - 1].nitems < kChainStripes ? planned[p - 1].nitems : kChainStripes) : 0;
-                it.stripe = local % kChainStripes;
-                it.stripe_items = (ph.nitems - it.stripe + kChainStripes - 1) / kChainStripes;
-            }
-        }
-    }
-}
-
-hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid) {
-    const DeviceInfo& dev = device_info();
-    int per_cu = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, gemv_chain_kernel<kChainT, kChainP>, 256, lds_bytes);
-    if (e != hipSuccess) return e;
-    // Measured on the config-1 set: 4 workgroups per CU stream faster than the 5 that fit.
-    const int cap = tuning().chain_wgs >= 1 ? tuning().chain_wgs : 4;
-    if (cap < per_cu) per_cu = cap;
-    if (per_cu < 1) return hipErrorInvalidConfiguration;
-    const int64_t resident = (int64_t)per_cu * dev.num_cu;
-    *grid = (int)(total_items < resident ? total_items : resident);
-    return hipSuccess;
-}
-
-hipError_t launch_gemv_chain(const ChainItem* items, int nphases, int total_items, int grid, size_t lds_bytes,
-                             uint32_t* ctr, hipStream_t stream) {
-    // the bound of a wait: 0.2 s, or tuning knob chain.wait_us (microseconds) when set
-    const uint64_t wait_ticks = tuning().chain_wait_us > 0 ? (uint64_t)tuning().chain_wait_us * 100u : 20000000ull;
-    hipLaunchKernelGGL((gemv_chain_kernel<kChainT, kChainP>), dim3(grid), dim3(256), lds_bytes, stream,
-                       items, nphases, total_items, ctr, wait_ticks);
-    return hipGetLastError();
 }
 
 hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,

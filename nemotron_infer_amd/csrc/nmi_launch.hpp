@@ -26,7 +26,7 @@ const DeviceInfo& device_info();
 // correctness.
 struct Tuning {
     int gemv_ks = 0;       // M = 1 GEMV: waves of a workgroup that split K (1, 2, 4)
-    int gemv_t = 0;        // M = 1 GEMV: weight rows per wave (1, 2, 4)
+    int gemv_t = 0;        // M = 1 GEMV: weight rows per wave (1, 2, 4; the stream kernel: 2, or 4)
     int gemv_p = 0;        // M = 1 GEMV: 16-byte chunks per lane per row per batch (2, 3, 4)
     int gemv_xg = 0;       // M = 1 GEMV: 1 reads x from global memory instead of LDS
     int gemm_tile = 0;     // GEMM tile variant id (see gemm_fp8.hip)
@@ -42,8 +42,9 @@ struct Tuning {
     int s4_dma = 0;        // 4x4x4 skinny kernel: 0 pipelined form where it applies, 2 windowed form
     int s4_kg = 0;         // 4x4x4 skinny kernel: workgroups splitting K (> 1, with a workspace; 0, 1: none)
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
-    int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 4, or fewer if fewer are resident)
-    int chain_wait_us = 0; // GEMV chain: bound of a wait in microseconds (0: 200000)
+    int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 2, or fewer if fewer are resident)
+    int gemv_wgs = 0;      // M = 1 stream GEMV: workgroups per CU at most (1, 2; 0: 1)
+    int gemv_multirow = 0; // M = 1: 1 runs the multi-row GEMV kernel (gemv_fp8.hip) instead of the stream kernel
 };
 Tuning& tuning();
 
@@ -112,67 +113,58 @@ hipError_t launch_rmsnorm(const uint16_t* x, int64_t ldx, const Norm& norm, uint
 hipError_t launch_gemv_m1(const uint16_t* x, const uint8_t* W, int64_t ldw, const float* s,
                           uint16_t* y, int N, int K, hipStream_t stream);
 
-// One phase of a GEMV chain (M = 1): the grouped GEMV of x [K] against up to kMaxGroups
-// matrices.  gemv_chain_plan fills ks, window, item_begin, nitems, signal and each group's
-// wg_begin (first work item of the group, relative to the phase); wait = 1 makes the phase wait
-// until the previous one has completed before reading x (x may be that phase's output).
-struct ChainPhase {
+// The M = 1 stream GEMV (gemv_stream.hip).  A phase is a grouped GEMV of one x [K] against up to
+// kMaxGroups matrices; rows go 2 or 4 at a time ("row groups", numbered across all phases; 4 in
+// chains, kStreamChainT), K in slices of at most 256 16-byte chunks.  Single launches carry one
+// phase in the kernel arguments and stage x in LDS (K <= 16 * kStreamMaxLdsChunks); chains keep
+// a table of phases in device memory and read x per step from global memory.
+constexpr int kStreamChainT = 4;
+constexpr int kStreamMaxLdsChunks = 2048;
+struct StreamGroup {
+    const uint8_t* W;
+    int64_t ldw;
+    const float* s;
+    uint16_t* y;
+    const uint16_t* res;    // residual [N] (epi == kEpiResidual)
+    int N;
+    int rg_begin;           // first row group of the group within its phase
+    int epi;                // kEpiNone / kEpiRelu2 / kEpiResidual
+    int pad;
+};
+static_assert(sizeof(StreamGroup) == 56, "56-byte group record");
+struct StreamPhase {
     const uint16_t* x;
     int K;
-    int ks;             // waves splitting K (1, 2 or 4)
-    int window;         // x chunks staged per window
-    int item_begin;     // first work item of the phase
-    int nitems;
+    int C;                  // chunks (K / 16)
+    int S;                  // slices
+    int sw;                 // chunks per slice (the last slice may be shorter)
     int ngroups;
-    int wait;
-    int signal;         // the next phase waits: completions of this one are counted
-    GemvGroup g[kMaxGroups];
+    int g_begin, g_end;     // row groups of the phase, numbered across its launch
+    StreamGroup g[kMaxGroups];
 };
-// Fills the derived fields of phases[0..n) and returns the number of work items; *lds_bytes
-// receives the dynamic LDS the launch needs.
-int gemv_chain_plan(ChainPhase* phases, int nphases, size_t* lds_bytes);
-// One work item of a planned chain, everything its workgroup needs in one 80-byte record (read
-// with scalar loads and no dependent lookups: walking a phase table per item cost about 10% of
-// the chain's streaming rate): the item's rows of one group.
-struct ChainItem {
-    const uint8_t* w;       // first weight row of the item
-    const uint16_t* x;      // the phase's activations [K]
-    uint16_t* y;            // output of the item's first row
-    const float* s;         // scale of the item's first row
-    int64_t ldw;
-    int rows;               // rows of the item that exist (the last item of a group may be short)
-    int K;
-    int ks;                 // waves splitting K (1, 2, 4)
-    int window;             // x chunks per LDS window
-    int phase;
-    int flags;              // kChainWait | kChainSignal
-    int wait_need;          // done count of the previous phase that completes it
-    int stripe;             // completion stripe of the item
-    int stripe_items;       // items of the phase in that stripe
+struct StreamArgs {
+    StreamPhase one;            // single launches
+    const StreamPhase* tab;     // chains: the launch's phases
+    const int* wave_steps;      // chains: steps of each wave of the grid
+    const float* norm_w;        // single launches: fused RMSNorm weight (nullptr: none)
+    float eps;
+    int nphases;
+    int total_rg;
+    int xs_half;                // LDS chunks per x half (single launches)
 };
-static_assert(sizeof(ChainItem) == 80, "one 80-byte record per item");
-enum : int { kChainWait = 1, kChainSignal = 2 };
-// The items of planned phases[0..n) in order (out: the count gemv_chain_plan returned).
-void gemv_chain_items(const ChainPhase* planned, int nphases, ChainItem* out);
-// Counter workspace of a chain: per phase kChainStripes stripe counters and one done counter,
-// then kChainStripes exit counters and one exit-done counter, each on its own 128-byte line;
-// the last line (an even number of lines: a multiple of 256 bytes) holds the error word; zero
-// at rest.
-constexpr int kChainStripes = 8;
-constexpr int kChainLineWords = 32;
-constexpr int gemv_chain_counter_lines(int nphases) {
-    return ((nphases + 1) * (kChainStripes + 1) + 2) & ~1;
-}
-inline size_t gemv_chain_counter_bytes(int nphases) {
-    return (size_t)gemv_chain_counter_lines(nphases) * kChainLineWords * sizeof(uint32_t);
-}
-// Workgroups of the launch: the items, at most as many as are resident at once on the current
-// device (the workgroups wait on each other's items) and at most 4 per CU (tuning knob
-// chain.wgs sets that cap).
-hipError_t gemv_chain_grid(size_t lds_bytes, int total_items, int* grid);
-// items: the item table in device memory; ctr: gemv_chain_counter_bytes(nphases) bytes.
-hipError_t launch_gemv_chain(const ChainItem* items, int nphases, int total_items, int grid, size_t lds_bytes,
-                             uint32_t* ctr, hipStream_t stream);
+// Single launch (one phase) on the stream kernel; norm.w applies the RMSNorm to x while staging.
+bool gemv_stream_supported(int K);
+hipError_t launch_gemv_stream(const uint16_t* x, int K, const GemvGroup* groups, int ngroups, hipStream_t stream,
+                              const Norm& norm = Norm{});
+// Chains: one launch per run of phases up to the next phase that waits for its predecessor.
+// stream_chain_plan fills the slices and row groups of a run's phases and returns its row
+// groups; stream_chain_grid sizes its grid (at most 2 workgroups per CU, or tuning knob
+// chain.wgs); stream_chain_wave_steps gives each of its nw waves' step counts.
+int stream_chain_plan(StreamPhase* phases, int nphases);
+void stream_chain_wave_steps(const StreamPhase* phases, int nphases, int nw, int* out);
+hipError_t stream_chain_grid(int total_rg, int* grid);
+hipError_t launch_gemv_stream_chain(const StreamPhase* tab, const int* wave_steps, int nphases, int total_rg, int grid,
+                                    hipStream_t stream);
 
 // Prefill GEMM.  Given a workspace of at least gemm_workspace_bytes(M) bytes whose first 64 KiB
 // (the flag region) are zero -- every launch leaves them zero again -- the DMA-fed kernel splits

@@ -253,21 +253,21 @@ def mlp_forward_fp8(x: torch.Tensor, norm_w: torch.Tensor, up_w: torch.Tensor, u
 
 
 class GemvChain:
-    """The GEMVs of a decode step in one launch (nmi_gemv_chain_*; M = 1).
+    """The GEMVs of a decode step with as few launches as the dependencies allow
+    (nmi_gemv_chain_*; M = 1).
 
     phases: a list of (x, groups, wait_prev): x a [K] (or [1, K]) bf16 tensor, groups a list of
     up to four (w, s, y) -- w [N, K] e4m3 codes (uint8), s [N] float32, y [N] bf16 output -- and
     wait_prev whether the phase reads x only after the previous phase has completed (x may be an
-    earlier phase's output).  The plan holds raw pointers: the tensors are kept referenced here
-    and must not be reallocated while the chain is in use.  The chain owns its zero-filled
-    counter workspace; launches go on torch's current stream and are graph-capturable."""
+    earlier phase's output; the phase then starts a new launch).  The plan holds raw pointers:
+    the tensors are kept referenced here and must not be reallocated while the chain is in use.
+    Launches go on torch's current stream and are graph-capturable."""
 
     def __init__(self, phases):
         L = _lib.lib()
         n = len(phases)
         arr = (_lib.GemvPhase * n)()
         self._keep = []
-        dev = None
         for i, (x, groups, wait_prev) in enumerate(phases):
             if x.dtype != torch.bfloat16 or not x.is_contiguous() or not (
                     x.dim() == 1 or (x.dim() == 2 and x.shape[0] == 1)):
@@ -289,18 +289,14 @@ class GemvChain:
                                                     y1.numel(), w.shape[0])
                 self._keep += [w, sc, y1]
             self._keep.append(x1)
-            dev = x1.device
         h = ctypes.c_void_p()
         _lib.check(L.nmi_gemv_chain_create(arr, n, ctypes.byref(h)), "nmi_gemv_chain_create")
         self._h = h
         self.nphases = n
-        nbytes = L.nmi_gemv_chain_workspace_bytes(n)
-        self._ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        self.launches = 1 + sum(1 for _, _, w in phases[1:] if w)
 
     def launch(self):
-        L = _lib.lib()
-        _lib.check(L.nmi_gemv_chain_launch(self._h, self._ws.data_ptr(), self._ws.numel(), _stream()),
-                   "nmi_gemv_chain_launch")
+        _lib.check(_lib.lib().nmi_gemv_chain_launch(self._h, None, 0, _stream()), "nmi_gemv_chain_launch")
 
     def close(self):
         if getattr(self, "_h", None) is not None and self._h.value:
@@ -312,10 +308,6 @@ class GemvChain:
             self.close()
         except Exception:
             pass
-
-    @property
-    def workspace(self) -> torch.Tensor:
-        return self._ws
 
 
 def decode_e4m3(codes: torch.Tensor, scale: float):

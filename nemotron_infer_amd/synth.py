@@ -128,3 +128,43 @@ def make_act(M: int, K: int, seed: int, device="cpu", kind: str = "normal",
         idx = torch.randperm(M * K, generator=g, device=device)[:n_out]
         z.view(-1)[idx] *= 50.0
     return z.to(torch.bfloat16)
+
+
+def decode_stream_chain(device, wait_prev: bool = False):
+    """Config 4 as the GEMV chain the bench times: one phase per launch of the engine's decode
+    step -- an attention layer's q|k|v grouped (they share the normed input) then o, an MLP
+    layer's up then down, a Mamba layer's in_proj (ragged N = 14690) then out_proj (K = 6272) --
+    84 phases in layer order.  Weights are seeded per layer and projection; every phase reads its
+    own activation, shared by phases of the same (K, kind).  wait_prev makes every phase after
+    the first wait for its predecessor (the dependent form; the activations stay independent).
+
+    Returns (phases, calls, total_bytes, weight_bytes, acts): phases as ops.GemvChain takes them;
+    calls the same work as separate launches, ("grouped", x, [(w, s)], [y]) or
+    ("single", x, w, s, y); acts the activations by (K, kind)."""
+    acts = {}
+
+    def act(K, kind):
+        if (K, kind) not in acts:
+            acts[(K, kind)] = make_act(1, K, 41000 + K, device, kind=kind)
+        return acts[(K, kind)]
+
+    phases, calls = [], []
+    total_bytes = weight_bytes = 0
+    for li, kind, lins in decode_stream_layers():
+        mats = []
+        for j, lin in enumerate(lins):
+            w, s = make_weight(lin.N, lin.K, 40000 + 10 * li + j, device)
+            mats.append((lin, w, s, torch.empty((1, lin.N), dtype=torch.bfloat16, device=device)))
+            total_bytes += linear_bytes(1, lin.N, lin.K)
+            weight_bytes += lin.N * lin.K
+        groups = [mats[:3], mats[3:]] if kind == "attn" else [[m] for m in mats]
+        for grp in groups:
+            x = act(grp[0][0].K, grp[0][0].act)
+            wait = wait_prev and len(phases) > 0
+            phases.append((x, [(w, s, y) for _, w, s, y in grp], wait))
+            if len(grp) > 1:
+                calls.append(("grouped", x, [(w, s) for _, w, s, _ in grp], [y for _, _, _, y in grp]))
+            else:
+                _, w, s, y = grp[0]
+                calls.append(("single", x, w, s, y))
+    return phases, calls, total_bytes, weight_bytes, acts

@@ -116,7 +116,7 @@ def bf16_ulp(a: np.ndarray) -> np.ndarray:
 
 def parity(y_bits: np.ndarray, ref_bits: np.ndarray, ulp_tol: float = 2.0,
            rel_l2_tol: float = 1e-3, floor_frac: float = 2.0 ** -8, flip_frac: float = 0.01,
-           mag: np.ndarray | None = None):
+           mag: np.ndarray | None = None, rel_l2_all_tol: float | None = None):
     """Compare a bf16 result with the bf16-rounded oracle.
 
     * max |y - ref| <= ``ulp_tol`` bf16 ulp taken at ``max(|ref|, floor_frac * rms(ref))``
@@ -129,9 +129,10 @@ def parity(y_bits: np.ndarray, ref_bits: np.ndarray, ulp_tol: float = 2.0,
       <= ``rel_l2_tol`` (every systematic error -- a dropped term, a wrong scale or index --
       shows there);
     * NaN positions must agree exactly.
-    Also returned: ``rel_l2_all``, the plain rel_l2 over every element (one flip on an element
-    that dominates ||ref|| -- e.g. with per-row scales spread over two decades -- can alone
-    exceed 1e-3).
+    Also returned: ``rel_l2_all``, the plain rel_l2 over every element, which must be
+    <= ``rel_l2_all_tol`` when one is given.  Gate it wherever the scales are per tensor; with
+    per-row scales spread over two decades (log-uniform) one rounding flip on an element that
+    dominates ||ref|| can alone exceed 1e-3, so those cases rely on the flip-exempt rel_l2.
 
     ``mag`` (optional, float, shape of ``ref``) replaces |ref| as the magnitude at which ulps
     are taken: for a rounded sum such as a residual add, the larger summand, since a one-ulp
@@ -157,6 +158,7 @@ def parity(y_bits: np.ndarray, ref_bits: np.ndarray, ulp_tol: float = 2.0,
     rel = float(np.linalg.norm(big) / denom) if denom > 0 else float(np.linalg.norm(big))
     max_ulp = float(ulps.max()) if ulps.size else 0.0
     n_flip = int(np.count_nonzero(flip))
-    ok = (nan_ok and rel <= rel_l2_tol and max_ulp <= ulp_tol and n_flip <= flip_frac * r.size)
+    ok = (nan_ok and rel <= rel_l2_tol and max_ulp <= ulp_tol and n_flip <= flip_frac * r.size
+          and (rel_l2_all_tol is None or rel_all <= rel_l2_all_tol))
     return dict(ok=ok, rel_l2=rel, rel_l2_all=rel_all, max_ulp=max_ulp, nan_ok=nan_ok, n=int(r.size),
                 n_diff=int(np.count_nonzero(d)), n_flip=n_flip)

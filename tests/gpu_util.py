@@ -42,7 +42,20 @@ def oracle_bits(x_bits, codes, s) -> np.ndarray:
     return linear.linear_fp8_w8a16(x_bits, codes, s)
 
 
-def assert_parity(y_bits, ref_bits, label="", **kw):
+# Outputs of at least this many elements are also gated on rel_l2 over all elements: below it a
+# single legitimate rounding flip (the oracle's own float32 summation order differs) on one
+# large element can reach 1e-3 by itself (one flip of 2^-8 |y| on an element at 4 rms gives
+# 0.016 / sqrt(n)).
+STRICT_MIN_ELEMENTS = 2048
+
+
+def assert_parity(y_bits, ref_bits, label="", per_row_scales=False, **kw):
+    """The parity gate of oracle.linear.parity, plus rel_l2 over all elements <= 1e-3 on outputs
+    of at least STRICT_MIN_ELEMENTS elements, unless the case has per-row scales spread over
+    decades (log-uniform), where one rounding flip on a dominant element can exceed that alone
+    and the flip-exempt rel_l2 is the systematic-error gate."""
+    if not per_row_scales and np.asarray(ref_bits).size >= STRICT_MIN_ELEMENTS:
+        kw.setdefault("rel_l2_all_tol", 1e-3)
     r = linear.parity(y_bits, ref_bits, **kw)
     assert r["ok"], f"{label}: {r}"
     return r

@@ -52,7 +52,7 @@ def test_skinny_config2(M):
         announce("skinny", M, lin.name, lin.N, lin.K)
         x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, scales="log_uniform", act=lin.act)
         y = bits(ops.linear_fp8_w8a16(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
-        assert_parity(y, oracle_bits(x, w, s), f"M={M} {lin.name}")
+        assert_parity(y, oracle_bits(x, w, s), f"M={M} {lin.name}", per_row_scales=True)
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 37, 16), (100, 130, 80), (130, 257, 208), (1, 300, 3136),
@@ -62,7 +62,7 @@ def test_ragged_shapes(M, N, K):
     x, w, s = _case(M, N, K, M * 131 + N * 7 + K, scales="log_uniform")
     for fn in (ops.gemm_fp8_w8a16, ops.linear_fp8_w8a16):
         y = bits(fn(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
-        assert_parity(y, oracle_bits(x, w, s), f"{fn.__name__} M={M} N={N} K={K}")
+        assert_parity(y, oracle_bits(x, w, s), f"{fn.__name__} M={M} N={N} K={K}", per_row_scales=True)
 
 
 def test_strided_operands():
@@ -85,7 +85,7 @@ def test_strided_operands():
               else L.nmi_linear_fp8_w8a16(*args, None))
         _lib.check(rc, entry)
         torch.cuda.synchronize()
-        assert_parity(bits(ybig[:, 8:8 + N]), oracle_bits(x, w, s), f"strided {entry}")
+        assert_parity(bits(ybig[:, 8:8 + N]), oracle_bits(x, w, s), f"strided {entry}", per_row_scales=True)
         assert torch.all(ybig[:, :8] == 7.0) and torch.all(ybig[:, 8 + N:] == 7.0)
 
 
@@ -106,7 +106,7 @@ def test_every_tile_variant(tile, _gemm_tile_reset):
         announce("gemm_tile", tile, M, N, K)
         x, w, s = _case(M, N, K, tile * 1000 + M + N + K, scales="log_uniform")
         y = bits(ops.gemm_fp8_w8a16(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
-        assert_parity(y, oracle_bits(x, w, s), f"tile={tile} M={M} N={N} K={K}")
+        assert_parity(y, oracle_bits(x, w, s), f"tile={tile} M={M} N={N} K={K}", per_row_scales=True)
     # y with an odd row stride and a 2-byte offset: the 8-byte store path must switch off
     M, N, K = 300, 260, 320
     x, w, s = _case(M, N, K, 4242 + tile, scales="log_uniform")
@@ -117,7 +117,7 @@ def test_every_tile_variant(tile, _gemm_tile_reset):
     _lib.check(_lib.lib().nmi_gemm_fp8_w8a16(xd.data_ptr(), K, wd.data_ptr(), K, sd.data_ptr(), yv.data_ptr(),
                                              ybig.stride(0), M, N, K, None, 0, None), "strided y")
     torch.cuda.synchronize()
-    assert_parity(bits(ybig[:, 1:1 + N]), oracle_bits(x, w, s), f"tile={tile} strided y")
+    assert_parity(bits(ybig[:, 1:1 + N]), oracle_bits(x, w, s), f"tile={tile} strided y", per_row_scales=True)
     assert torch.all(ybig[:, 0] == 5.0) and torch.all(ybig[:, 1 + N:] == 5.0)
 
 
@@ -172,7 +172,7 @@ def test_stream_k_forced_on_small_problems(tile, _sk_reset):
         torch.cuda.synchronize()
         assert torch.count_nonzero(ws[:64 * 1024]) == 0, "flag region not re-armed"
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
-        assert_parity(bits(y1), oracle_bits(x, w, s), f"stream-K tile={tile} M={M} N={N} K={K}")
+        assert_parity(bits(y1), oracle_bits(x, w, s), f"stream-K tile={tile} M={M} N={N} K={K}", per_row_scales=True)
 
 
 def test_stream_k_large_matches_oracle_and_replays_in_a_graph(_sk_reset):
@@ -228,7 +228,7 @@ def test_dma_kernel_forms(sk, _sk_reset):
         torch.cuda.synchronize()
         assert torch.count_nonzero(ws[:64 * 1024]) == 0, "flag region not re-armed"
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
-        assert_parity(bits(y1), oracle_bits(x, w, s), f"dma sk={sk} M={M} N={N} K={K}")
+        assert_parity(bits(y1), oracle_bits(x, w, s), f"dma sk={sk} M={M} N={N} K={K}", per_row_scales=True)
 
 
 def test_dma_kernel_forms_agree_on_config3(_sk_reset):

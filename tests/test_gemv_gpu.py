@@ -21,7 +21,7 @@ FIXTURES = ["kat_gemv_n64_k3136", "tiny_m4_n8_k16", "ragged_m3_n37_k208",
             "skinny_m16_n48_k3136", "special_nan_zero"]
 
 
-GEMV_KNOBS = ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg")
+GEMV_KNOBS = ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemv.wgs", "gemv.multirow")
 
 
 @pytest.fixture(autouse=True)
@@ -118,14 +118,66 @@ def test_gemv_real_shapes(label, N, K, act):
     assert r["n"] == N
 
 
+# K values that exercise every slice layout of the stream kernel: one partial chunk group
+# (16, 48), exactly 256 chunks (4096), 257 chunks (two slices of 129), the decode shapes (one,
+# two and four slices of 196 / 160 chunks), 20000 (five slices), the LDS limit (32768, eight
+# slices) and K past it (40000: the multi-row kernel takes over)
+STREAM_K = [16, 48, 1024, 3136, 4096, 4112, 5120, 6272, 12544, 20000, 32768, 40000]
+
+
+@pytest.mark.parametrize("K", STREAM_K)
+@pytest.mark.parametrize("wgs", [0, 1])
+def test_stream_gemv_slices(K, wgs):
+    """The M = 1 stream kernel against the oracle at every slice layout, with row counts that
+    leave a half row group (odd N), a single row and fewer row groups than waves, per-row
+    log-uniform scales (a wrong scale index shows), and both grid caps (tuning knob gemv.wgs)."""
+    _lib.tuning_set("gemv.wgs", wgs)
+    for N in (1, 3, 37, 1000):
+        announce("stream_gemv", K, N, wgs)
+        x, w, s = _case(N, K, 11 * N + K, scales="log_uniform")
+        y = bits(ops.gemv_fp8(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
+        assert_parity(y, oracle_bits(x, w, s), f"stream K={K} N={N} wgs={wgs}", per_row_scales=True)
+
+
+def test_stream_gemv_matches_grouped_and_strided():
+    """Grouped launch (q|k|v sharing x) == three separate launches bit for bit, and strided
+    weight rows (ldw > K) and strided outputs (ldy > N) give the same bits as contiguous ones."""
+    K = 3136
+    x, _, _ = _case(8, K, 3)
+    xd = x_to_dev(x)
+    groups = [_case(N, K, 40 + N, scales="log_uniform")[1:] for N in (5120, 1024, 1000)]
+    wd = [(w_to_dev(w), s_to_dev(s)) for w, s in groups]
+    announce("stream_grouped", K)
+    ys = ops.linear_fp8_w8a16_grouped(xd, wd)
+    for (w, s), yg, (wh, sh) in zip(wd, ys, groups):
+        yone = ops.linear_fp8_w8a16(xd, w, s)
+        assert np.array_equal(bits(yg).reshape(-1), bits(yone).reshape(-1))
+        assert_parity(bits(yone), oracle_bits(x, wh, sh), "grouped", per_row_scales=True)
+    # strided rows and outputs through the C ABI
+    w, s = wd[2]
+    N = w.shape[0]
+    wpad = torch.zeros((N, K + 64), dtype=torch.uint8, device=DEV)
+    wpad[:, :K] = w
+    ypad = torch.full((1, 2 * N + 8), float("nan"), dtype=torch.bfloat16, device=DEV)
+    L = _lib.lib()
+    announce("stream_strided", N, K)
+    _lib.check(L.nmi_linear_fp8_w8a16(xd.data_ptr(), K, wpad.data_ptr(), K + 64, s.data_ptr(),
+                                      ypad.data_ptr(), 2 * N + 8, 1, N, K, None), "strided")
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(ypad)[0, :N], bits(ys[2]).reshape(-1))
+    assert np.all(np.isnan(ypad[0, N:].float().cpu().numpy()))         # nothing past N written
+
+
 @pytest.mark.parametrize("ks", [1, 2, 4])
 @pytest.mark.parametrize("t", [1, 2, 4])
 @pytest.mark.parametrize("p", [2, 3, 4])
 def test_gemv_every_schedule(ks, t, p):
-    """Every (K-split waves, rows per wave, chunks per lane) instantiation with x from LDS and
-    from global memory, against the oracle: K beyond one LDS window (K = 20000 -> 1250 chunks >
-    the 1024-chunk window), slices longer than one batch (K = 12544 at ks = 1), short K (one
-    partial chunk group) and N not a multiple of the rows per workgroup."""
+    """The multi-row GEMV kernel (M = 2 and, with tuning knob gemv.multirow = 1, M = 1): every
+    (K-split waves, rows per wave, chunks per lane) instantiation with x from LDS and from
+    global memory, against the oracle: K beyond one LDS window (K = 20000 -> 1250 chunks > the
+    1024-chunk window), slices longer than one batch (K = 12544 at ks = 1), short K (one partial
+    chunk group) and N not a multiple of the rows per workgroup."""
+    _lib.tuning_set("gemv.multirow", 1)
     _lib.tuning_set("gemv.ks", ks)
     _lib.tuning_set("gemv.t", t)
     _lib.tuning_set("gemv.p", p)
@@ -135,7 +187,7 @@ def test_gemv_every_schedule(ks, t, p):
             announce("gemv_schedule", ks, t, p, xg, N, K)
             x, w, s = _case(N, K, 7 * N + K, scales="log_uniform")
             y = bits(ops.gemv_fp8(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
-            assert_parity(y, oracle_bits(x, w, s), f"ks={ks} t={t} p={p} xg={xg} N={N} K={K}")
+            assert_parity(y, oracle_bits(x, w, s), f"ks={ks} t={t} p={p} xg={xg} N={N} K={K}", per_row_scales=True)
 
 
 # ------------------------------------------------------------------------------- properties
@@ -158,7 +210,7 @@ def test_row_slices_match_full_call():
                                           1, r1 - r0, K, None), "slice")
     torch.cuda.synchronize()
     assert np.array_equal(bits(full), bits(sliced))
-    assert_parity(bits(full)[0], oracle_bits(x, w, s), "in_proj full")
+    assert_parity(bits(full)[0], oracle_bits(x, w, s), "in_proj full", per_row_scales=True)
 
 
 def test_power_of_two_linearity_full_size():
