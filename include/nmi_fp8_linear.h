@@ -222,6 +222,22 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
                         int inter, float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * nmi_mlp_forward_fp8 without any allocation: the same block and result (bit for bit), with
+ * the transient buffers in a file-scope device array of nmi_mlp_noalloc_scratch_bytes() bytes
+ * (4 MiB) that each GPU the library runs on holds until the process ends.  No counterpart in
+ * the reference: for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Calls no hipMalloc / hipFree.  Needs
+ * nmi_mlp_workspace_bytes(M, hidden, inter) <= the array's size (hidden 3136, inter 12544:
+ * M <= 133), else NMI_ERR_WORKSPACE.  Every call on a GPU shares that GPU's array: calls that
+ * may overlap in time on one GPU (other streams, other threads) race.  Same argument
+ * requirements as nmi_mlp_forward_fp8.
+ */
+size_t nmi_mlp_noalloc_scratch_bytes(void);
+int nmi_mlp_forward_fp8_noalloc(const void* input_bf16, const float* norm_w, const void* up_w_e4m3,
+                                const float* up_scale, const void* down_w_e4m3, const float* down_scale,
+                                void* out_bf16, int M, int hidden, int inter, float eps, void* stream);
+
+/*
  * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg": schedule of the multi-row
  * GEMV kernel (M = 2, or M = 1 with "gemv.multirow" = 1), "gemv.t" = 4 also 4 rows per step for
  * the M = 1 stream kernel, "gemv.wgs": its workgroups per CU (1, 2), "gemm.tile", "gemm.sk",
