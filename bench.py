@@ -65,7 +65,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
-    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny"],
+    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn"],
                    help="run one extra leg alone and print its JSON record (for profiling that leg); "
                         "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
@@ -446,6 +446,76 @@ def bench_mlp_block(dev, reps=5):
                               "steps": "rmsnorm; stream-K flag clear; up GEMM + relu^2; down GEMM (stream-K) + residual"}}
 
 
+def bench_attn_decode(dev, reps=5):
+    """The fp8 attention block at decode (attn_decode_fp8; 40 query heads, 8 KV heads of 128)
+    at cache lengths S, weights and caches rotated over copies totalling > 1 GB: the block
+    (q|k|v GEMV with the RMSNorm, SDPA split [+ combine], o GEMV + residual) against the
+    reference's launch structure on this library's kernels (rmsnorm, q, k, v, SDPA, o, add);
+    and the SDPA kernel(s) alone, priced on the K/V bytes they read."""
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    H, HQ, HKV, D = synth.HIDDEN, 40, 8, 128
+    mats = [synth.make_weight(r, c, 9000 + i, dev)
+            for i, (r, c) in enumerate([(HQ * D, H), (HKV * D, H), (HKV * D, H), (H, HQ * D)])]
+    nw = (1.0 + 0.1 * torch.randn(H, generator=torch.Generator(device=dev).manual_seed(9010), device=dev)).float()
+    wbytes = sum(synth.linear_bytes(1, w.shape[0], w.shape[1]) for w, _ in mats)
+    x = synth.make_act(1, H, 9011, dev)
+    out = torch.empty_like(x)
+    T = Timer()
+    res = {}
+    for S in (1024, 4096, 32768):
+        cap = S + 1
+        kv_bytes = 2 * HKV * S * D * 2
+        R = max(2, math.ceil(ROTATION_BYTES / (wbytes + 2 * kv_bytes)))
+        g = torch.Generator(device=dev).manual_seed(9100 + S)
+        caches = [(torch.randn((HKV, cap, D), generator=g, device=dev).to(torch.bfloat16),
+                   torch.randn((HKV, cap, D), generator=g, device=dev).to(torch.bfloat16)) for _ in range(R)]
+        copies = [[(w.clone(), sc.clone()) for w, sc in mats] for _ in range(R)]
+        q = torch.empty((HQ, D), dtype=torch.bfloat16, device=dev)
+        kn = torch.empty((HKV, D), dtype=torch.bfloat16, device=dev)
+        vn = torch.empty_like(kn)
+        o = torch.empty_like(q)
+        h = torch.empty_like(x)
+        att = torch.empty_like(x)
+
+        def block(r):
+            (qw, qs), (kw, ks), (vw, vs), (ow, os_) = copies[r]
+            ops.attn_decode_fp8(x, nw, qw, qs, kw, ks, vw, vs, ow, os_, *caches[r], S, out=out)
+
+        def separate(r):
+            (qw, qs), (kw, ks), (vw, vs), (ow, os_) = copies[r]
+            ops.rmsnorm_bf16(x, nw, out=h)
+            ops.linear_fp8_w8a16(h, qw, qs, out=q.view(1, -1))
+            ops.linear_fp8_w8a16(h, kw, ks, out=kn.view(1, -1))
+            ops.linear_fp8_w8a16(h, vw, vs, out=vn.view(1, -1))
+            ops.sdpa_decode_bf16(q, *caches[r], kn, vn, S, out=o)
+            ops.linear_fp8_w8a16(o.view(1, -1), ow, os_, out=att)
+            torch.add(x, att, out=out)
+
+        def sdpa(r):
+            ops.sdpa_decode_bf16(q, *caches[r], kn, vn, S, out=o)
+
+        row = {"kv_bytes": kv_bytes, "weight_copies_rotated": R}
+        for name, fn, nbytes in (("block", block, wbytes + kv_bytes), ("separate_7_launches", separate,
+                                                                        wbytes + kv_bytes),
+                                 ("sdpa_only", sdpa, kv_bytes)):
+            for r in range(R):
+                fn(r)
+            torch.cuda.synchronize()
+            gr = T.capture(lambda: [fn(r) for r in range(R)])
+            T.time_replays([gr])
+            t = T.time_replays([gr] * reps) / (reps * R)
+            row[name] = {"us": round(t * 1e3, 2), "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1)}
+            del gr
+        res[f"S={S}"] = row
+        del caches, copies
+        torch.cuda.empty_cache()
+    return {"workload": "attn_decode_fp8 block (hidden 3136, 40 q heads, 8 KV heads, head 128)",
+            "weight_bytes": wbytes, **res}
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -558,6 +628,8 @@ def main():
             leg = {k: v for k, v in leg.items()}
         elif args.only == "decode":
             leg = bench_decode_set(args, dev, decode_inputs())
+        elif args.only == "attn":
+            leg = bench_attn_decode(dev)
         else:
             leg = bench_prefill(dev) if args.only == "prefill" else bench_mlp_block(dev)
         print(json.dumps(leg), flush=True)
@@ -579,6 +651,9 @@ def main():
         log("mlp block ...")
         extras["mlp_block"] = bench_mlp_block(dev)
         log(f"mlp block: {extras['mlp_block']['decode_m1']}")
+        log("attention decode block ...")
+        extras["attn_decode"] = bench_attn_decode(dev)
+        log(f"attention decode: {extras['attn_decode']['S=4096']}")
     torch.cuda.empty_cache()
     log("cpu baseline ...")
     cpu = cpu_baseline(host, args.cpu_seconds)

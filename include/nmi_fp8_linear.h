@@ -9,7 +9,7 @@
  * with float32 accumulation and a single bf16 rounding.  All pointers are device pointers
  * (hipMalloc / torch CUDA tensors) unless stated otherwise.  `stream` is a hipStream_t passed
  * as void* (NULL = the null stream).  No entry point allocates device memory (except nmi_alloc,
- * and nmi_mlp_forward_fp8 called without a workspace), synchronizes the device (except
+ * and the block and SDPA entries called without a workspace), synchronizes the device (except
  * nmi_sync), or retains pointers after it returns; launches are asynchronous on `stream`.
  *
  * Return value: NMI_OK (0) on success; a negative NMI_ERR_* for argument errors detected on
@@ -236,6 +236,48 @@ size_t nmi_mlp_noalloc_scratch_bytes(void);
 int nmi_mlp_forward_fp8_noalloc(const void* input_bf16, const float* norm_w, const void* up_w_e4m3,
                                 const float* up_scale, const void* down_w_e4m3, const float* down_scale,
                                 void* out_bf16, int M, int hidden, int inter, float eps, void* stream);
+
+/*
+ * Attention decode, one query token per head against the KV cache
+ * (replaces sdpa_decode_bf16<128>, nemotron_infer/csrc/include/ops/attention/
+ * sdpa_decode.cuh:267-285, kernels :57-180):
+ *   o[h] = bf16( softmax(q[h] . K[kv(h), 0:S_cache]^T / sqrt(128)) . V[kv(h), 0:S_cache] ),
+ *   kv(h) = h / (n_heads / n_kv_heads), float32 arithmetic; then K[kv, S_cache] = k_new[kv] and
+ *   V[kv, S_cache] = v_new[kv].  As in the reference the query attends the S_cache cached
+ *   positions only (the new token's K/V are stored after), and S_cache == 0 gives o = 0.
+ * q, o [n_heads, 128]; k_new, v_new [n_kv_heads, 128]; caches [n_kv_heads, cache_cap, 128],
+ * all bf16.  Head dim 128; 1 <= n_heads / n_kv_heads <= 6; 0 <= S_cache < cache_cap.
+ * workspace: nmi_sdpa_decode_workspace_bytes(n_heads, n_kv_heads, S_cache) bytes (0 when the
+ * positions are not split; the fp32 partials otherwise), 16-byte aligned, no initialisation;
+ * NULL takes it from the bump allocator.  q, the caches, k_new and v_new 16-byte aligned, o
+ * 4-byte aligned.
+ */
+size_t nmi_sdpa_decode_workspace_bytes(int n_heads, int n_kv_heads, int S_cache);
+int nmi_sdpa_decode_bf16(const void* q_bf16, void* k_cache_bf16, void* v_cache_bf16, void* o_bf16,
+                         const void* k_new_bf16, const void* v_new_bf16, int S_cache, int cache_cap, int n_heads,
+                         int n_kv_heads, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The fp8 attention block at decode (replaces attention_block_decode_fp8<HIDDEN, H_Q, H_KV, 128>,
+ * nemotron_infer/csrc/include/model/attention_block.cuh:371-414; binding attn_decode_fp8,
+ * csrc/include/binding.cu:189-199):
+ *   h = rmsnorm(input) (bf16); q, k_new, v_new = bf16 linears of h (e4m3 weights, per-row
+ *   scales); o = nmi_sdpa_decode_bf16(q, caches, k_new, v_new, S_cache); out = bf16(input +
+ *   bf16(o . o_w^T * o_s)).  NoPE (no rotary), as the reference.  The caches receive this token's
+ *   K/V at position S_cache.
+ * input, out [1, hidden] bf16 (out may be input); q_w [n_heads*128, hidden], k_w and v_w
+ * [n_kv_heads*128, hidden], o_w [hidden, n_heads*128] e4m3 with float32 scales of their row
+ * counts.  Launches: the q|k|v GEMV (RMSNorm applied while staging), the SDPA kernel(s), the o
+ * GEMV with the residual add in its stores.
+ * workspace: nmi_attn_decode_workspace_bytes(hidden, n_heads, n_kv_heads, S_cache) bytes,
+ * 16-byte aligned, no initialisation; NULL takes it from the bump allocator.
+ */
+size_t nmi_attn_decode_workspace_bytes(int hidden, int n_heads, int n_kv_heads, int S_cache);
+int nmi_attn_decode_fp8(const void* input_bf16, const float* norm_w, const void* q_w_e4m3, const float* q_scale,
+                        const void* k_w_e4m3, const float* k_scale, const void* v_w_e4m3, const float* v_scale,
+                        const void* o_w_e4m3, const float* o_scale, void* k_cache_bf16, void* v_cache_bf16,
+                        int S_cache, int cache_cap, void* out_bf16, int hidden, int n_heads, int n_kv_heads,
+                        float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg": schedule of the multi-row

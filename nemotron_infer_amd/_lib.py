@@ -34,6 +34,10 @@ SIGNATURES = {
     "nmi_mlp_workspace_bytes": ([_i, _i, _i], _sz),
     "nmi_mlp_forward_fp8": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp], _i),
     "nmi_mlp_noalloc_scratch_bytes": ([], _sz),
+    "nmi_sdpa_decode_workspace_bytes": ([_i, _i, _i], _sz),
+    "nmi_sdpa_decode_bf16": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp], _i),
+    "nmi_attn_decode_workspace_bytes": ([_i, _i, _i, _i], _sz),
+    "nmi_attn_decode_fp8": ([_vp] * 12 + [_i, _i, _vp, _i, _i, _i, _f, _vp, _sz, _vp], _i),
     "nmi_mlp_forward_fp8_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp], _i),
     "nmi_tuning_set": ([ctypes.c_char_p, _i], _i),
     "nmi_alloc": ([_sz, ctypes.POINTER(_vp)], _i),

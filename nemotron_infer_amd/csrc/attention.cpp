@@ -1,0 +1,189 @@
+// attention.cpp -- extern "C" entries of the attention decode path (declared in
+// include/nmi_fp8_linear.h): the SDPA decode op and the fp8 attention decode block.
+//
+// The reference's attention_block_decode_fp8 (nemotron_infer/csrc/include/model/
+// attention_block.cuh:371-414) runs eight launches over bump-allocated buffers: rmsnorm, three
+// gemv_fp8 (q, k, v), the two kernels of sdpa_decode_bf16, gemv_fp8 (o) and a residual add.
+// Here: one grouped q|k|v GEMV that applies the RMSNorm while staging its input, the SDPA split
+// kernel (which also appends K/V to the caches), its combine kernel when the positions are
+// split, and the o GEMV with the residual add in its stores -- three or four launches.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "nmi_fp8_linear.h"
+#include "nmi_launch.hpp"
+
+using namespace nmi;
+
+namespace {
+
+int fail(int code, const char* msg) {
+    set_last_error("%s", msg);
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return NMI_OK;
+    set_last_error("%s: %s (hipError %d)", what, hipGetErrorString(e), (int)e);
+    return (int)e;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Shape checks shared by the op and the block; 0 or an NMI_ERR_* with the message set.
+int check_sdpa_shape(const char* fn, int S_cache, int cache_cap, int n_heads, int n_kv) {
+    if (n_kv < 1 || n_heads < n_kv || n_heads % n_kv != 0 || n_heads / n_kv > kSdpaMaxGroup) {
+        set_last_error("%s: n_heads=%d n_kv_heads=%d (need n_heads a multiple of n_kv_heads, at most %d query "
+                       "heads per KV head)",
+                       fn, n_heads, n_kv, kSdpaMaxGroup);
+        return NMI_ERR_INVALID_ARG;
+    }
+    if (S_cache < 0 || cache_cap <= S_cache) {
+        set_last_error("%s: S_cache=%d cache_cap=%d (need 0 <= S_cache < cache_cap: the new token is stored at "
+                       "position S_cache)",
+                       fn, S_cache, cache_cap);
+        return NMI_ERR_INVALID_ARG;
+    }
+    return NMI_OK;
+}
+
+// Block workspace: q [H*128], k_new, v_new [H_KV*128], o [H*128], normed [hidden] (when the
+// RMSNorm is not fused into the q|k|v GEMV), then the SDPA partials.
+struct AttnLayout {
+    size_t q, k, v, o, normed, part, total;
+};
+
+AttnLayout attn_layout(int hidden, int n_heads, int n_kv, int S_cache) {
+    AttnLayout L{};
+    const size_t qb = round256((size_t)n_heads * kSdpaHead * 2), kb = round256((size_t)n_kv * kSdpaHead * 2);
+    L.q = 0;
+    L.k = L.q + qb;
+    L.v = L.k + kb;
+    L.o = L.v + kb;
+    L.normed = L.o + qb;
+    L.part = L.normed + round256((size_t)hidden * 2);
+    L.total = L.part + round256(sdpa_decode_workspace_bytes(n_heads, S_cache, n_kv));
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nmi_sdpa_decode_workspace_bytes(int n_heads, int n_kv_heads, int S_cache) {
+    if (n_kv_heads < 1 || n_heads < 1 || S_cache < 0) return 0;
+    return sdpa_decode_workspace_bytes(n_heads, S_cache, n_kv_heads);
+}
+
+int nmi_sdpa_decode_bf16(const void* q_bf16, void* k_cache_bf16, void* v_cache_bf16, void* o_bf16,
+                         const void* k_new_bf16, const void* v_new_bf16, int S_cache, int cache_cap, int n_heads,
+                         int n_kv_heads, void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "nmi_sdpa_decode_bf16";
+    if (!q_bf16 || !k_cache_bf16 || !v_cache_bf16 || !o_bf16 || !k_new_bf16 || !v_new_bf16)
+        return fail(NMI_ERR_INVALID_ARG, "nmi_sdpa_decode_bf16: NULL pointer argument");
+    int rc = check_sdpa_shape(fn, S_cache, cache_cap, n_heads, n_kv_heads);
+    if (rc != NMI_OK) return rc;
+    if (!aligned(q_bf16, 16) || !aligned(k_cache_bf16, 16) || !aligned(v_cache_bf16, 16) || !aligned(k_new_bf16, 16) ||
+        !aligned(v_new_bf16, 16) || !aligned(o_bf16, 4))
+        return fail(NMI_ERR_ALIGNMENT,
+                    "nmi_sdpa_decode_bf16: q, the caches, k_new and v_new must be 16-byte aligned, o 4-byte aligned");
+    const size_t need = sdpa_decode_workspace_bytes(n_heads, S_cache, n_kv_heads);
+    if (need) {
+        if (workspace) {
+            if (!aligned(workspace, 16))
+                return fail(NMI_ERR_ALIGNMENT, "nmi_sdpa_decode_bf16: workspace must be 16-byte aligned");
+            if (workspace_bytes < need) {
+                set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
+                return NMI_ERR_WORKSPACE;
+            }
+        } else {
+            rc = nmi_alloc(need, &workspace);
+            if (rc != NMI_OK) return rc;
+        }
+    }
+    return hip_status(launch_sdpa_decode(static_cast<const uint16_t*>(q_bf16), static_cast<uint16_t*>(k_cache_bf16),
+                                         static_cast<uint16_t*>(v_cache_bf16), static_cast<const uint16_t*>(k_new_bf16),
+                                         static_cast<const uint16_t*>(v_new_bf16), static_cast<uint16_t*>(o_bf16),
+                                         S_cache, cache_cap, n_heads, n_kv_heads, workspace,
+                                         static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+size_t nmi_attn_decode_workspace_bytes(int hidden, int n_heads, int n_kv_heads, int S_cache) {
+    if (hidden < 16 || n_heads < 1 || n_kv_heads < 1 || S_cache < 0) return 0;
+    return attn_layout(hidden, n_heads, n_kv_heads, S_cache).total;
+}
+
+int nmi_attn_decode_fp8(const void* input_bf16, const float* norm_w, const void* q_w_e4m3, const float* q_scale,
+                        const void* k_w_e4m3, const float* k_scale, const void* v_w_e4m3, const float* v_scale,
+                        const void* o_w_e4m3, const float* o_scale, void* k_cache_bf16, void* v_cache_bf16,
+                        int S_cache, int cache_cap, void* out_bf16, int hidden, int n_heads, int n_kv_heads,
+                        float eps, void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "nmi_attn_decode_fp8";
+    if (!input_bf16 || !norm_w || !q_w_e4m3 || !q_scale || !k_w_e4m3 || !k_scale || !v_w_e4m3 || !v_scale ||
+        !o_w_e4m3 || !o_scale || !k_cache_bf16 || !v_cache_bf16 || !out_bf16)
+        return fail(NMI_ERR_INVALID_ARG, "nmi_attn_decode_fp8: NULL pointer argument");
+    if (hidden < 16 || hidden % 16 != 0) {
+        set_last_error("%s: hidden=%d (need a positive multiple of 16)", fn, hidden);
+        return NMI_ERR_INVALID_ARG;
+    }
+    int rc = check_sdpa_shape(fn, S_cache, cache_cap, n_heads, n_kv_heads);
+    if (rc != NMI_OK) return rc;
+    if (!aligned(input_bf16, 16) || !aligned(norm_w, 16) || !aligned(q_w_e4m3, 16) || !aligned(k_w_e4m3, 16) ||
+        !aligned(v_w_e4m3, 16) || !aligned(o_w_e4m3, 16) || !aligned(k_cache_bf16, 16) || !aligned(v_cache_bf16, 16))
+        return fail(NMI_ERR_ALIGNMENT,
+                    "nmi_attn_decode_fp8: input, norm_w, the weights and the caches must be 16-byte aligned");
+    if (!aligned(q_scale, 4) || !aligned(k_scale, 4) || !aligned(v_scale, 4) || !aligned(o_scale, 4) ||
+        !aligned(out_bf16, 2))
+        return fail(NMI_ERR_ALIGNMENT, "nmi_attn_decode_fp8: misaligned scale or output");
+    const AttnLayout lay = attn_layout(hidden, n_heads, n_kv_heads, S_cache);
+    if (workspace) {
+        if (!aligned(workspace, 16))
+            return fail(NMI_ERR_ALIGNMENT, "nmi_attn_decode_fp8: workspace must be 16-byte aligned");
+        if (workspace_bytes < lay.total) {
+            set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, lay.total);
+            return NMI_ERR_WORKSPACE;
+        }
+    } else {
+        rc = nmi_alloc(lay.total, &workspace);   // as the reference's allocate_tensor calls
+        if (rc != NMI_OK) return rc;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char* base = static_cast<char*>(workspace);
+    uint16_t* q = reinterpret_cast<uint16_t*>(base + lay.q);
+    uint16_t* kn = reinterpret_cast<uint16_t*>(base + lay.k);
+    uint16_t* vn = reinterpret_cast<uint16_t*>(base + lay.v);
+    uint16_t* ot = reinterpret_cast<uint16_t*>(base + lay.o);
+    const uint16_t* in = static_cast<const uint16_t*>(input_bf16);
+    const int QD = n_heads * kSdpaHead, KD = n_kv_heads * kSdpaHead;
+
+    // q|k|v of the normed input, one grouped launch
+    GemvGroup qkv[3] = {
+        {static_cast<const uint8_t*>(q_w_e4m3), hidden, q_scale, q, QD, QD, 0, 0, Epi{}},
+        {static_cast<const uint8_t*>(k_w_e4m3), hidden, k_scale, kn, KD, KD, 0, 0, Epi{}},
+        {static_cast<const uint8_t*>(v_w_e4m3), hidden, v_scale, vn, KD, KD, 0, 0, Epi{}},
+    };
+    const Norm norm{norm_w, eps};
+    hipError_t e;
+    if (choose_path(1) == Path::Gemv && gemv_norm_supported(1, hidden)) {
+        e = dispatch_linear(in, hidden, 1, hidden, qkv, 3, nullptr, 0, st, norm);
+    } else {
+        uint16_t* normed = reinterpret_cast<uint16_t*>(base + lay.normed);
+        e = launch_rmsnorm(in, hidden, norm, normed, hidden, 1, hidden, st);
+        if (e == hipSuccess) e = dispatch_linear(normed, hidden, 1, hidden, qkv, 3, nullptr, 0, st);
+    }
+    if (e != hipSuccess) return hip_status(e, fn);
+    // attention over the cached positions, then K/V of this token appended at S_cache
+    e = launch_sdpa_decode(q, static_cast<uint16_t*>(k_cache_bf16), static_cast<uint16_t*>(v_cache_bf16), kn, vn, ot,
+                           S_cache, cache_cap, n_heads, n_kv_heads, base + lay.part, st);
+    if (e != hipSuccess) return hip_status(e, fn);
+    // out = bf16(input + bf16(o_proj(ot)))
+    GemvGroup og{static_cast<const uint8_t*>(o_w_e4m3), QD, o_scale, static_cast<uint16_t*>(out_bf16), hidden, hidden,
+                 0, 0, Epi{kEpiResidual, in, hidden}};
+    return hip_status(dispatch_linear(ot, QD, 1, QD, &og, 1, nullptr, 0, st), fn);
+}
+
+}  // extern "C"

@@ -45,6 +45,7 @@ struct Tuning {
     int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 2, or fewer if fewer are resident)
     int gemv_wgs = 0;      // M = 1 stream GEMV: workgroups per CU at most (1, 2; 0: 1)
     int gemv_multirow = 0; // M = 1: 1 runs the multi-row GEMV kernel (gemv_fp8.hip) instead of the stream kernel
+    int sdpa_chunk = 0;    // attention decode: positions per split (0: kSdpaMinChunk, capped by the grid size)
 };
 Tuning& tuning();
 
@@ -173,6 +174,19 @@ hipError_t launch_gemv_stream_chain(const StreamPhase* tab, const int* wave_step
 // one tile per workgroup.  launch_sk_flags_clear zeroes the flag region (one small kernel, safe
 // under graph capture).
 size_t gemm_workspace_bytes(int M);
+// Attention decode (sdpa_decode.hip): q [H, 128] against the caches [H_KV, cap, 128] over
+// positions [0, S), then K_new / V_new appended at position S; H / H_KV in 1..kSdpaMaxGroup.
+// The workspace (sdpa_decode_workspace_bytes) holds the fp32 partials of split launches.
+constexpr int kSdpaHead = 128;
+constexpr int kSdpaMaxGroup = 6;
+constexpr int kSdpaMinChunk = 64;
+constexpr int kSdpaMaxSplits = 256;
+void sdpa_decode_plan(int S, int n_kv, int* nsplit, int* chunk);
+size_t sdpa_decode_workspace_bytes(int n_heads, int S, int n_kv);
+hipError_t launch_sdpa_decode(const uint16_t* q, uint16_t* k_cache, uint16_t* v_cache, const uint16_t* k_new,
+                              const uint16_t* v_new, uint16_t* o, int S, int cap, int n_heads, int n_kv,
+                              void* workspace, hipStream_t stream);
+
 hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream);
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,

@@ -236,19 +236,111 @@ def mlp_forward_fp8(x: torch.Tensor, norm_w: torch.Tensor, up_w: torch.Tensor, u
     _check_out(out, M, hidden) if x.dim() == 2 else _check_out(out, 1, hidden)
     _check_device(x2, norm_w, up_w, up_s, down_w, down_s, out)
     L = _lib.lib()
-    ws = None
-    if use_workspace:
-        need = L.nmi_mlp_workspace_bytes(M, hidden, inter)
-        idx = x.device.index or 0
-        ws = _BLOCK_WS.get(idx)
-        if ws is None or ws.numel() < need:
-            ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=x.device)
-            _BLOCK_WS[idx] = ws
+    ws = _block_ws(x.device, L.nmi_mlp_workspace_bytes(M, hidden, inter)) if use_workspace else None
     rc = L.nmi_mlp_forward_fp8(x2.data_ptr(), norm_w.data_ptr(), up_w.data_ptr(), up_s.data_ptr(),
                                down_w.data_ptr(), down_s.data_ptr(), out.data_ptr(), M, hidden, inter, eps,
                                None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
                                _stream())
     _lib.check(rc, "nmi_mlp_forward_fp8")
+    return out
+
+
+def _block_ws(device: torch.device, need: int) -> torch.Tensor:
+    idx = device.index or 0
+    ws = _BLOCK_WS.get(idx)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=device)
+        _BLOCK_WS[idx] = ws
+    return ws
+
+
+def _check_bf16(t: torch.Tensor, shape, name: str) -> None:
+    if t.dtype != torch.bfloat16 or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous bf16 tensor of shape {tuple(shape)}, "
+                         f"got {t.dtype} {tuple(t.shape)}")
+
+
+def _check_caches(k_cache: torch.Tensor, v_cache: torch.Tensor, S_cache: int):
+    if k_cache.dim() != 3 or k_cache.shape[2] != 128:
+        raise ValueError(f"k_cache must be [n_kv_heads, cache_cap, 128], got {tuple(k_cache.shape)}")
+    n_kv, cap, _ = k_cache.shape
+    _check_bf16(k_cache, (n_kv, cap, 128), "k_cache")
+    _check_bf16(v_cache, (n_kv, cap, 128), "v_cache")
+    if not 0 <= S_cache < cap:
+        raise ValueError(f"S_cache={S_cache} must be in [0, cache_cap={cap})")
+    return n_kv, cap
+
+
+def sdpa_decode_bf16(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k_new: torch.Tensor,
+                     v_new: torch.Tensor, S_cache: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention decode (ops/attention/sdpa_decode.cuh:267-285): q [H, 128] against the caches
+    [H_KV, cap, 128] over positions [0, S_cache), then k_new / v_new [H_KV, 128] stored at
+    position S_cache.  Returns o [H, 128] bf16."""
+    n_kv, cap = _check_caches(k_cache, v_cache, S_cache)
+    if q.dim() != 2 or q.shape[1] != 128:
+        raise ValueError(f"q must be [n_heads, 128], got {tuple(q.shape)}")
+    H = q.shape[0]
+    _check_bf16(q, (H, 128), "q")
+    _check_bf16(k_new, (n_kv, 128), "k_new")
+    _check_bf16(v_new, (n_kv, 128), "v_new")
+    if out is None:
+        out = torch.empty_like(q)
+    _check_bf16(out, (H, 128), "out")
+    _check_device(q, k_cache, v_cache, k_new, v_new, out)
+    L = _lib.lib()
+    need = L.nmi_sdpa_decode_workspace_bytes(H, n_kv, S_cache)
+    ws = _block_ws(q.device, need) if need else None
+    rc = L.nmi_sdpa_decode_bf16(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                                k_new.data_ptr(), v_new.data_ptr(), S_cache, cap, H, n_kv,
+                                None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream())
+    _lib.check(rc, "nmi_sdpa_decode_bf16")
+    return out
+
+
+def attn_decode_fp8(x: torch.Tensor, norm_w: torch.Tensor, q_w, q_s, k_w, k_s, v_w, v_s, o_w, o_s,
+                    k_cache: torch.Tensor, v_cache: torch.Tensor, S_cache: int, out: torch.Tensor | None = None,
+                    eps: float = 1e-5, use_workspace: bool = True) -> torch.Tensor:
+    """The fp8 attention block at decode (model/attention_block.cuh:371-414):
+    out = x + o_proj(sdpa_decode(q_proj(h), caches, S_cache)), h = rmsnorm(x), with this token's
+    k_proj(h) / v_proj(h) stored in the caches at position S_cache.  x, out [1, hidden] (or
+    [hidden]) bf16; weights e4m3 [rows, cols] with per-row float32 scales; caches
+    [n_kv_heads, cap, 128] bf16."""
+    x2 = _as_2d(x)
+    if x2.shape[0] != 1 or not x2.is_contiguous() or x2.dtype != torch.bfloat16:
+        raise ValueError("x must be one contiguous bf16 row")
+    hidden = x2.shape[1]
+    n_kv, cap = _check_caches(k_cache, v_cache, S_cache)
+    q_w = _check_w(q_w, hidden)
+    if q_w.shape[0] % 128:
+        raise ValueError(f"q_proj has {q_w.shape[0]} rows, not a multiple of the head dim 128")
+    H = q_w.shape[0] // 128
+    k_w, v_w = _check_w(k_w, hidden), _check_w(v_w, hidden)
+    for name, w in (("k_proj", k_w), ("v_proj", v_w)):
+        if w.shape[0] != n_kv * 128:
+            raise ValueError(f"{name} has {w.shape[0]} rows, the caches hold {n_kv} heads of 128")
+    o_w = _check_w(o_w, H * 128)
+    if o_w.shape[0] != hidden:
+        raise ValueError(f"o_proj has {o_w.shape[0]} rows, hidden size is {hidden}")
+    _check_s(q_s, H * 128)
+    _check_s(k_s, n_kv * 128)
+    _check_s(v_s, n_kv * 128)
+    _check_s(o_s, hidden)
+    if norm_w.dtype != torch.float32 or tuple(norm_w.shape) != (hidden,) or not norm_w.is_contiguous():
+        raise ValueError(f"norm_w must be a contiguous float32 vector of {hidden} values")
+    if out is None:
+        out = torch.empty_like(x)
+    _check_out(out, 1, hidden)
+    _check_device(x2, norm_w, q_w, q_s, k_w, k_s, v_w, v_s, o_w, o_s, k_cache, v_cache, out)
+    L = _lib.lib()
+    ws = None
+    if use_workspace:
+        ws = _block_ws(x.device, L.nmi_attn_decode_workspace_bytes(hidden, H, n_kv, S_cache))
+    rc = L.nmi_attn_decode_fp8(x2.data_ptr(), norm_w.data_ptr(), q_w.data_ptr(), q_s.data_ptr(), k_w.data_ptr(),
+                               k_s.data_ptr(), v_w.data_ptr(), v_s.data_ptr(), o_w.data_ptr(), o_s.data_ptr(),
+                               k_cache.data_ptr(), v_cache.data_ptr(), S_cache, cap, out.data_ptr(), hidden, H, n_kv,
+                               eps, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+                               _stream())
+    _lib.check(rc, "nmi_attn_decode_fp8")
     return out
 
 

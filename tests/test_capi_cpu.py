@@ -114,7 +114,7 @@ def test_out_of_scope_entries_fail_loudly():
     from nemotron_infer_amd.csrc import binding as B
 
     with pytest.raises(NotImplementedError, match="not part of this build"):
-        B.attn_decode_fp8(*([0] * 15))
+        B.attn_forward_fp8(*([0] * 15))
     with pytest.raises(NotImplementedError):
         B.mlp_forward(*([0] * 6))
     with pytest.raises(NotImplementedError):
@@ -180,6 +180,69 @@ def test_binding_block_entries_validate():
         B.rmsnorm(FAKE + 2, FAKE, FAKE, 1)
     with pytest.raises(RuntimeError, match="M=0"):
         B.mlp_forward_fp8(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0)
+
+
+def test_sdpa_and_attention_workspace_bytes():
+    L = _lib.lib()
+    # one split (no partials) up to 64 positions; fp32 (m, l, o[128]) per (head, split) beyond
+    assert L.nmi_sdpa_decode_workspace_bytes(40, 8, 0) == 0
+    assert L.nmi_sdpa_decode_workspace_bytes(40, 8, 64) == 0
+    assert L.nmi_sdpa_decode_workspace_bytes(40, 8, 65) == 40 * 2 * 130 * 4
+    assert L.nmi_sdpa_decode_workspace_bytes(40, 8, 4096) == 40 * 32 * 130 * 4
+    assert L.nmi_sdpa_decode_workspace_bytes(40, 0, 10) == 0
+    base = 2 * 10240 + 2 * 2048 + ((3136 * 2 + 255) // 256) * 256
+    assert L.nmi_attn_decode_workspace_bytes(3136, 40, 8, 10) == base
+    assert L.nmi_attn_decode_workspace_bytes(3136, 40, 8, 4096) == base + 40 * 32 * 130 * 4
+    assert L.nmi_attn_decode_workspace_bytes(8, 40, 8, 10) == 0
+
+
+@pytest.mark.parametrize("S,cap,H,H_KV,offs,code", [
+    (-1, 8, 40, 8, {}, _lib.NMI_ERR_INVALID_ARG),
+    (8, 8, 40, 8, {}, _lib.NMI_ERR_INVALID_ARG),          # no room for the new token
+    (0, 8, 40, 6, {}, _lib.NMI_ERR_INVALID_ARG),          # 40 % 6
+    (0, 8, 56, 8, {}, _lib.NMI_ERR_INVALID_ARG),          # 7 query heads per KV head
+    (0, 8, 40, 0, {}, _lib.NMI_ERR_INVALID_ARG),
+    (0, 8, 40, 8, {0: 8}, _lib.NMI_ERR_ALIGNMENT),        # q
+    (0, 8, 40, 8, {1: 8}, _lib.NMI_ERR_ALIGNMENT),        # k_cache
+    (0, 8, 40, 8, {5: 2}, _lib.NMI_ERR_ALIGNMENT),        # v_new
+    (0, 8, 40, 8, {3: 1}, _lib.NMI_ERR_ALIGNMENT),        # o
+    (100, 128, 40, 8, {"ws_bytes": 16}, _lib.NMI_ERR_WORKSPACE),
+])
+def test_sdpa_rejects_bad_arguments(S, cap, H, H_KV, offs, code):
+    L = _lib.lib()
+    ptrs = [FAKE + offs.get(i, 0) for i in range(6)]
+    rc = L.nmi_sdpa_decode_bf16(*ptrs, S, cap, H, H_KV, FAKE, offs.get("ws_bytes", 1 << 20), None)
+    assert rc == code
+    assert L.nmi_last_error().decode().startswith("nmi_sdpa_decode_bf16")
+    ptrs[2] = 0
+    assert L.nmi_sdpa_decode_bf16(*ptrs, 0, 8, 40, 8, None, 0, None) == _lib.NMI_ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("hidden,S,cap,offs,code", [
+    (3136, 0, 0, {}, _lib.NMI_ERR_INVALID_ARG),
+    (3144, 0, 8, {}, _lib.NMI_ERR_INVALID_ARG),            # hidden % 16
+    (3136, 0, 8, {0: 2}, _lib.NMI_ERR_ALIGNMENT),          # input
+    (3136, 0, 8, {8: 8}, _lib.NMI_ERR_ALIGNMENT),          # o_w
+    (3136, 0, 8, {10: 8}, _lib.NMI_ERR_ALIGNMENT),         # k_cache
+    (3136, 0, 8, {9: 2}, _lib.NMI_ERR_ALIGNMENT),          # o_s
+    (3136, 0, 8, {"ws": 8}, _lib.NMI_ERR_ALIGNMENT),
+    (3136, 0, 8, {"ws_bytes": 64}, _lib.NMI_ERR_WORKSPACE),
+])
+def test_attn_decode_rejects_bad_arguments(hidden, S, cap, offs, code):
+    L = _lib.lib()
+    ptrs = [FAKE + offs.get(i, 0) for i in range(12)]
+    out = FAKE + offs.get(12, 0)
+    rc = L.nmi_attn_decode_fp8(*ptrs, S, cap, out, hidden, 40, 8, 1e-5, FAKE + offs.get("ws", 0),
+                               offs.get("ws_bytes", 1 << 20), None)
+    assert rc == code
+    assert L.nmi_last_error().decode().startswith("nmi_attn_decode_fp8")
+
+
+def test_binding_attn_decode_validates():
+    from nemotron_infer_amd.csrc import binding as B
+
+    with pytest.raises(RuntimeError, match="S_cache=5 cache_cap=5"):
+        B.attn_decode_fp8(*([FAKE] * 12), 5, 5, FAKE)
 
 
 def test_gemv_chain_workspace_bytes():

@@ -212,7 +212,7 @@ def test_block_norm_fusion_limits(hidden, Ms):
         assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (hidden, M)
 
 
-@pytest.mark.parametrize("M", [1, 3, 64])
+@pytest.mark.parametrize("M", [1, 3, 64, 520])
 def test_block_in_place_and_bump_allocator(M):
     announce("mlp_block_inplace_alloc", M)
     dev = _dev(*_weights(HIDDEN, INTER))
