@@ -65,7 +65,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
-    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn"],
+    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn", "mamba", "engine"],
                    help="run one extra leg alone and print its JSON record (for profiling that leg); "
                         "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
@@ -516,6 +516,143 @@ def bench_attn_decode(dev, reps=5):
             "weight_bytes": wbytes, **res}
 
 
+def _mamba_layer(dev, seed):
+    """Real-model Mamba-2 layer (hidden 3136, 96 heads of 80, 8 groups, state 128): fp8 in_proj
+    [17504, 3136] and out_proj [3136, 7680], float32 parameters and states."""
+    import torch
+
+    from nemotron_infer_amd import synth
+
+    H, P, G, N, hid = 96, 80, 8, 128, synth.HIDDEN
+    inter, conv_dim = H * P, H * P + 2 * G * N
+    g = torch.Generator(device=dev).manual_seed(seed)
+    f = dict(device=dev, dtype=torch.float32)
+    return dict(norm=1.0 + 0.1 * torch.randn(hid, generator=g, **f),
+                inp=synth.make_weight(inter + conv_dim + H, hid, seed + 1, dev),
+                out=synth.make_weight(hid, inter, seed + 2, dev),
+                conv_w=0.3 * torch.randn((conv_dim, 4), generator=g, **f),
+                conv_b=0.1 * torch.randn(conv_dim, generator=g, **f),
+                A_log=torch.rand(H, generator=g, **f) * 2.5 - 1.0,
+                D=torch.randn(H, generator=g, **f),
+                dt_bias=0.5 * torch.randn(H, generator=g, **f),
+                gnorm_w=1.0 + 0.1 * torch.randn(inter, generator=g, **f),
+                conv_state=torch.zeros((1, conv_dim, 3), **f),
+                ssm_state=torch.zeros((1, H, P, N), **f))
+
+
+def _mamba_args(L):
+    return (L["norm"], *L["inp"], L["conv_w"], L["conv_b"], L["A_log"], L["D"], L["dt_bias"], L["gnorm_w"],
+            *L["out"], L["conv_state"], L["ssm_state"])
+
+
+def bench_mamba_decode(dev, reps=5):
+    """The fp8 Mamba-2 block at decode (mamba_decode_fp8), layers rotated over copies totalling
+    > 1 GB: the block (4 launches) against the reference's launch structure on this library's
+    kernels (rmsnorm, in_proj, mixer, out_proj, add: 6 launches; the reference has 12, counting
+    its three in_proj slices and three split copies)."""
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    H, P, G = 96, 80, 8
+    L0 = _mamba_layer(dev, 9500)
+    wbytes = sum(synth.linear_bytes(1, w.shape[0], w.shape[1]) for w, _ in (L0["inp"], L0["out"]))
+    state_bytes = 2 * (L0["ssm_state"].numel() * 4 + L0["conv_state"].numel() * 4)
+    R = max(2, math.ceil(ROTATION_BYTES / wbytes))
+    layers = [L0] + [{k: (tuple(t.clone() for t in v) if isinstance(v, tuple) else v.clone()) for k, v in L0.items()}
+                     for _ in range(R - 1)]
+    x = synth.make_act(1, synth.HIDDEN, 9501, dev)
+    out = torch.empty_like(x)
+    h = torch.empty_like(x)
+    proj = torch.empty((1, L0["inp"][0].shape[0]), dtype=torch.bfloat16, device=dev)
+    mix = torch.empty_like(x)
+
+    def blk(r):
+        ops.mamba_decode_fp8(x, *_mamba_args(layers[r]), H, P, G, out=out)
+
+    def separate(r):
+        Lr = layers[r]
+        ops.rmsnorm_bf16(x, Lr["norm"], out=h)
+        ops.linear_fp8_w8a16(h, *Lr["inp"], out=proj)
+        _, g = ops.mamba_mixer_decode(proj, Lr["conv_w"], Lr["conv_b"], Lr["A_log"], Lr["D"], Lr["dt_bias"],
+                                      Lr["gnorm_w"], Lr["conv_state"], Lr["ssm_state"], H, P, G)
+        ops.linear_fp8_w8a16(g, *Lr["out"], out=mix)
+        torch.add(x, mix, out=out)
+
+    T = Timer()
+    res = {"weight_bytes": wbytes, "state_bytes_read_written": state_bytes, "weight_copies_rotated": R}
+    for name, fn in (("block_4_launches", blk), ("separate_6_launches", separate)):
+        for r in range(R):
+            fn(r)
+        torch.cuda.synchronize()
+        g = T.capture(lambda: [fn(r) for r in range(R)])
+        T.time_replays([g])
+        t = T.time_replays([g] * reps) / (reps * R)
+        res[name] = {"us": round(t * 1e3, 2), "GB/s": round((wbytes + state_bytes) / (t * 1e-3) / 1e9, 1)}
+        del g
+    return {"workload": "mamba_decode_fp8 block (hidden 3136, 96 heads x 80, 8 groups, state 128)", **res}
+
+
+def bench_engine_decode(dev, s_cache=1024, reps=5):
+    """A whole decode step of the 42-layer stack through the three block entries, in the
+    engine's order (engine.py:252-265; config 4's layer pattern at the real model's Mamba
+    dimensions): 21 mamba_decode_fp8, 17 mlp_forward_fp8, 4 attn_decode_fp8 at S_cache
+    positions, each reading the previous layer's output.  One HIP graph per step."""
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    H, P, G, hid = 96, 80, 8, synth.HIDDEN
+    HQ, HKV, D = 40, 8, 128
+    kinds = [k for _, k, _ in synth.decode_stream_layers()]
+    layers = []
+    wbytes = 0
+    for i, kind in enumerate(kinds):
+        if kind == "mamba":
+            L = _mamba_layer(dev, 20000 + 10 * i)
+            wbytes += sum(synth.linear_bytes(1, w.shape[0], w.shape[1]) for w, _ in (L["inp"], L["out"]))
+        elif kind == "mlp":
+            L = dict(norm=1.0 + 0.1 * torch.randn(hid, device=dev),
+                     up=synth.make_weight(synth.INTER, hid, 20000 + 10 * i, dev),
+                     down=synth.make_weight(hid, synth.INTER, 20001 + 10 * i, dev))
+            wbytes += synth.linear_bytes(1, synth.INTER, hid) + synth.linear_bytes(1, hid, synth.INTER)
+        else:
+            mats = [synth.make_weight(r, c, 20000 + 10 * i + j, dev)
+                    for j, (r, c) in enumerate([(HQ * D, hid), (HKV * D, hid), (HKV * D, hid), (hid, HQ * D)])]
+            g = torch.Generator(device=dev).manual_seed(20005 + 10 * i)
+            L = dict(norm=1.0 + 0.1 * torch.randn(hid, device=dev), mats=mats,
+                     kc=torch.randn((HKV, s_cache + 1, D), generator=g, device=dev).to(torch.bfloat16),
+                     vc=torch.randn((HKV, s_cache + 1, D), generator=g, device=dev).to(torch.bfloat16))
+            wbytes += sum(synth.linear_bytes(1, w.shape[0], w.shape[1]) for w, _ in mats)
+        layers.append((kind, L))
+    bufs = [synth.make_act(1, hid, 20999, dev), torch.empty((1, hid), dtype=torch.bfloat16, device=dev)]
+
+    def step():
+        cur, nxt = bufs
+        for kind, L in layers:
+            if kind == "mamba":
+                ops.mamba_decode_fp8(cur, *_mamba_args(L), H, P, G, out=nxt)
+            elif kind == "mlp":
+                ops.mlp_forward_fp8(cur, L["norm"], *L["up"], *L["down"], out=nxt)
+            else:
+                (qw, qs), (kw, ks), (vw, vs), (ow, os_) = L["mats"]
+                ops.attn_decode_fp8(cur, L["norm"], qw, qs, kw, ks, vw, vs, ow, os_, L["kc"], L["vc"], s_cache, out=nxt)
+            cur, nxt = nxt, cur
+
+    step()
+    torch.cuda.synchronize()
+    T = Timer()
+    g = T.capture(step)
+    T.time_replays([g])
+    t = T.time_replays([g] * reps) / reps
+    del g, layers
+    torch.cuda.empty_cache()
+    return {"workload": "42-layer decode step through the block entries (21 Mamba, 17 MLP, 4 attention; "
+                        f"S_cache {s_cache})", "launches": 21 * 4 + 17 * 2 + 4 * 4, "weight_bytes": wbytes,
+            "us_per_token": round(t * 1e3, 1), "tok_per_s": round(1e3 / t, 1),
+            "weight_GB/s": round(wbytes / (t * 1e-3) / 1e9, 1)}
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -630,6 +767,10 @@ def main():
             leg = bench_decode_set(args, dev, decode_inputs())
         elif args.only == "attn":
             leg = bench_attn_decode(dev)
+        elif args.only == "mamba":
+            leg = bench_mamba_decode(dev)
+        elif args.only == "engine":
+            leg = bench_engine_decode(dev)
         else:
             leg = bench_prefill(dev) if args.only == "prefill" else bench_mlp_block(dev)
         print(json.dumps(leg), flush=True)
@@ -654,6 +795,12 @@ def main():
         log("attention decode block ...")
         extras["attn_decode"] = bench_attn_decode(dev)
         log(f"attention decode: {extras['attn_decode']['S=4096']}")
+        log("mamba decode block ...")
+        extras["mamba_decode"] = bench_mamba_decode(dev)
+        log(f"mamba decode: {extras['mamba_decode']['block_4_launches']}")
+        log("42-layer decode step through the blocks ...")
+        extras["engine_decode_step"] = bench_engine_decode(dev)
+        log(f"engine decode step: {extras['engine_decode_step']['us_per_token']} us")
     torch.cuda.empty_cache()
     log("cpu baseline ...")
     cpu = cpu_baseline(host, args.cpu_seconds)

@@ -280,9 +280,54 @@ int nmi_attn_decode_fp8(const void* input_bf16, const float* norm_w, const void*
                         float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The fp8 Mamba-2 block at decode, one token per sequence (replaces
+ * mamba_block_decode_fp8<HIDDEN, H, P, N, G, 4>, nemotron_infer/csrc/include/model/
+ * mamba_block.cuh:436-515; binding mamba_decode_fp8, csrc/include/binding.cu:162-175):
+ *   h = rmsnorm(input) (bf16); proj = [z | xBC | dt] = in_proj(h) (bf16, one GEMV over all
+ *   n_heads*head_dim + conv_dim + n_heads rows); the causal conv1d step with SiLU on xBC
+ *   (conv_state [batch, conv_dim, 3] updated); the SSM step on x, B, C (ssm_state
+ *   [batch, n_heads, head_dim, d_state] updated) giving y (bf16); the gated RMSNorm of y with
+ *   gate z over n_groups groups (bf16); out = bf16(input + bf16(out_proj(...))).
+ *   conv_dim = n_heads*head_dim + 2*n_groups*d_state; states float32, as the reference.
+ * input, out [batch, hidden] bf16 (out may be input); in_proj_w [n_heads*head_dim + conv_dim +
+ * n_heads, hidden] and out_proj_w [hidden, n_heads*head_dim] e4m3 with float32 per-row scales;
+ * conv_w [conv_dim, 4], conv_b [conv_dim], A_log, D, dt_bias [n_heads], gnorm_w
+ * [n_heads*head_dim] float32.  Supported: d_state 128, conv_k 4, n_groups dividing n_heads
+ * with groups of at most 2048 values, head_dim <= 128.  The reference's GEMV path computes batch
+ * row 0 only; this entry computes every row (the linears dispatch on M = batch).
+ * workspace: nmi_mamba_decode_workspace_bytes(batch, hidden, n_heads, head_dim, n_groups,
+ * d_state) bytes, 16-byte aligned, no initialisation; NULL takes it from the bump allocator.
+ */
+/*
+ * The mixer of the Mamba-2 block at decode, between its projections (replaces the op calls
+ * causal_conv1d_decode_bf16, ssm_decode_bf16 and rmsnorm_gated_bf16 of
+ * mamba_block.cuh:476-509, kernels ops/mamba2/causal_conv1d.cuh:391-459,
+ * ops/mamba2/ssm.cuh:46-130, ops/reduce.cuh:383-500): from proj = [z | xBC | dt]
+ * ([batch, proj_ld] bf16, the in_proj output), the conv step (conv_state updated), the SSM step
+ * (ssm_state updated) giving y [batch, n_heads*head_dim] bf16, and the gated RMSNorm of y with
+ * gate z giving g [batch, n_heads*head_dim] bf16 (out_proj's input).  Same shapes and
+ * requirements as nmi_mamba_decode_fp8; proj, y, g, conv_w, gnorm_w and ssm_state 16-byte
+ * aligned, proj_ld a multiple of 8.  Two launches.
+ */
+int nmi_mamba_mixer_decode(const void* proj_bf16, int64_t proj_ld, const float* conv_w, const float* conv_b,
+                           const float* A_log, const float* D, const float* dt_bias, const float* gnorm_w,
+                           float* conv_state, float* ssm_state, void* y_bf16, void* g_bf16, int batch, int n_heads,
+                           int head_dim, int n_groups, int d_state, int conv_k, float eps, void* stream);
+size_t nmi_mamba_decode_workspace_bytes(int batch, int hidden, int n_heads, int head_dim, int n_groups,
+                                        int d_state);
+int nmi_mamba_decode_fp8(const void* input_bf16, const float* norm_w, const void* in_proj_w_e4m3,
+                         const float* in_proj_scale, const float* conv_w, const float* conv_b, const float* A_log,
+                         const float* D, const float* dt_bias, const float* gnorm_w, const void* out_proj_w_e4m3,
+                         const float* out_proj_scale, float* conv_state, float* ssm_state, void* out_bf16, int batch,
+                         int hidden, int n_heads, int head_dim, int n_groups, int d_state, int conv_k, float eps,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg": schedule of the multi-row
  * GEMV kernel (M = 2, or M = 1 with "gemv.multirow" = 1), "gemv.t" = 4 also 4 rows per step for
- * the M = 1 stream kernel, "gemv.wgs": its workgroups per CU (1, 2), "gemm.tile", "gemm.sk",
+ * the M = 1 stream kernel, "gemv.wgs": its workgroups per CU (1, 2), "gemv.grid": its exact
+ * workgroup count, "gemv.balance": 2 keeps the plain grid instead of one whose waves get equal row
+ * counts, "sdpa.chunk": cache positions per workgroup of the attention decode, "gemm.tile", "gemm.sk",
  * "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
  * "s4.dma": 2 selects the windowed form of the 4x4x4 skinny kernel instead of the pipelined one,
  * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace

@@ -37,6 +37,9 @@ SIGNATURES = {
     "nmi_sdpa_decode_workspace_bytes": ([_i, _i, _i], _sz),
     "nmi_sdpa_decode_bf16": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp], _i),
     "nmi_attn_decode_workspace_bytes": ([_i, _i, _i, _i], _sz),
+    "nmi_mamba_decode_workspace_bytes": ([_i] * 6, _sz),
+    "nmi_mamba_mixer_decode": ([_vp, _i64] + [_vp] * 10 + [_i] * 6 + [_f, _vp], _i),
+    "nmi_mamba_decode_fp8": ([_vp] * 15 + [_i] * 7 + [_f, _vp, _sz, _vp], _i),
     "nmi_attn_decode_fp8": ([_vp] * 12 + [_i, _i, _vp, _i, _i, _i, _f, _vp, _sz, _vp], _i),
     "nmi_mlp_forward_fp8_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp], _i),
     "nmi_tuning_set": ([ctypes.c_char_p, _i], _i),

@@ -379,6 +379,8 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "gemv.wgs")) t.gemv_wgs = value;
     else if (!std::strcmp(knob, "gemv.multirow")) t.gemv_multirow = value;
     else if (!std::strcmp(knob, "sdpa.chunk")) t.sdpa_chunk = value;
+    else if (!std::strcmp(knob, "gemv.grid")) t.gemv_grid = value;
+    else if (!std::strcmp(knob, "gemv.balance")) t.gemv_balance = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

@@ -441,7 +441,15 @@ hipError_t launch_gemv_stream(const uint16_t* x, int K, const GemvGroup* groups,
     const int per_cu = tn.gemv_wgs >= 1 && tn.gemv_wgs <= 2 ? tn.gemv_wgs : 1;
     const int64_t want = ((int64_t)nrg * ph.S + 3 * kWaves - 1) / (3 * kWaves);
     const int64_t cap = (int64_t)per_cu * dev.num_cu;
-    const int grid = (int)(want < 1 ? 1 : (want < cap ? want : cap));
+    int grid = (int)(want < 1 ? 1 : (want < cap ? want : cap));
+    if (tn.gemv_balance != 2) {
+        // as few waves as keep the most row groups per wave, so that no wave ends a round early
+        // (measured: 1-6% faster on five of the six decode shapes, 1% slower on up_proj)
+        const int64_t per_wave = ((int64_t)nrg + (int64_t)grid * kWaves - 1) / ((int64_t)grid * kWaves);
+        const int64_t waves = ((int64_t)nrg + per_wave - 1) / per_wave;
+        grid = (int)((waves + kWaves - 1) / kWaves);
+    }
+    if (tn.gemv_grid > 0) grid = tn.gemv_grid;
     // x pieces (8 activations) per thread: 2 C pieces over 256 threads
     const int need = (2 * ph.C + 255) / 256;
     const int xpc = need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 8 ? 8 : 16));

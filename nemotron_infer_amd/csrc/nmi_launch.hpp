@@ -46,6 +46,8 @@ struct Tuning {
     int gemv_wgs = 0;      // M = 1 stream GEMV: workgroups per CU at most (1, 2; 0: 1)
     int gemv_multirow = 0; // M = 1: 1 runs the multi-row GEMV kernel (gemv_fp8.hip) instead of the stream kernel
     int sdpa_chunk = 0;    // attention decode: positions per split (0: kSdpaMinChunk, capped by the grid size)
+    int gemv_grid = 0;     // M = 1 stream GEMV (single launches): explicit workgroup count
+    int gemv_balance = 0;  // M = 1 stream GEMV (single launches): 2 turns off the grid sizing that makes row groups divide evenly
 };
 Tuning& tuning();
 
@@ -186,6 +188,30 @@ size_t sdpa_decode_workspace_bytes(int n_heads, int S, int n_kv);
 hipError_t launch_sdpa_decode(const uint16_t* q, uint16_t* k_cache, uint16_t* v_cache, const uint16_t* k_new,
                               const uint16_t* v_new, uint16_t* o, int S, int cap, int n_heads, int n_kv,
                               void* workspace, hipStream_t stream);
+
+// Mamba-2 mixer at decode (mamba_decode.hip): conv1d step + SiLU, SSM state update and
+// output, gated RMSNorm, for `batch` sequences of one token.  Shapes: H heads of P, G groups,
+// state size kMambaDState, conv width kMambaConvK (mamba_decode_supported).
+constexpr int kMambaDState = 128;
+constexpr int kMambaConvK = 4;
+struct MambaDecodeArgs {
+    const uint16_t* proj;   // [batch, proj_ld] bf16: z [inter] | xBC [conv_dim] | dt [H]
+    int64_t proj_ld;
+    const float* conv_w;    // [conv_dim, 4]
+    const float* conv_b;    // [conv_dim]
+    const float* A_log;     // [H]
+    const float* D;         // [H]
+    const float* dt_bias;   // [H]
+    const float* gnorm_w;   // [inter]
+    float* conv_state;      // [batch, conv_dim, 3]
+    float* ssm_state;       // [batch, H, P, 128]
+    uint16_t* y;            // [batch, inter] bf16: SSM output
+    uint16_t* g;            // [batch, inter] bf16: gated-norm output (out_proj's input)
+    int H, P, G, inter, conv_dim;
+    float eps;
+};
+bool mamba_decode_supported(int H, int P, int G, int d_state, int conv_k);
+hipError_t launch_mamba_decode_mixer(const MambaDecodeArgs& a, int batch, hipStream_t stream);
 
 hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream);
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,

@@ -344,6 +344,89 @@ def attn_decode_fp8(x: torch.Tensor, norm_w: torch.Tensor, q_w, q_s, k_w, k_s, v
     return out
 
 
+def _check_f32(t: torch.Tensor, shape, name: str) -> None:
+    if t.dtype != torch.float32 or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(shape)}, "
+                         f"got {t.dtype} {tuple(t.shape)}")
+
+
+def _mamba_params(n_heads, head_dim, n_groups, conv_w, conv_b, A_log, D, dt_bias, gnorm_w, conv_state, ssm_state,
+                  batch):
+    inter = n_heads * head_dim
+    conv_dim = inter + 2 * n_groups * 128
+    _check_f32(conv_w, (conv_dim, 4), "conv_w")
+    _check_f32(conv_b, (conv_dim,), "conv_b")
+    for name, t in (("A_log", A_log), ("D", D), ("dt_bias", dt_bias)):
+        _check_f32(t, (n_heads,), name)
+    _check_f32(gnorm_w, (inter,), "gnorm_w")
+    _check_f32(conv_state, (batch, conv_dim, 3), "conv_state")
+    _check_f32(ssm_state, (batch, n_heads, head_dim, 128), "ssm_state")
+    return inter, conv_dim
+
+
+def mamba_mixer_decode(proj: torch.Tensor, conv_w, conv_b, A_log, D, dt_bias, gnorm_w, conv_state, ssm_state,
+                       n_heads: int, head_dim: int, n_groups: int, eps: float = 1e-5):
+    """The Mamba-2 mixer between the projections at decode (nmi_mamba_mixer_decode): proj
+    [batch, >= PROJ] bf16 = [z | xBC | dt]; conv_state [batch, conv_dim, 3] and ssm_state
+    [batch, n_heads, head_dim, 128] float32, updated in place.  Returns (y, g), both
+    [batch, n_heads * head_dim] bf16: the SSM output and the gated-norm output."""
+    if proj.dim() != 2 or proj.dtype != torch.bfloat16 or proj.stride(-1) != 1:
+        raise ValueError("proj must be a 2-D bf16 tensor with contiguous rows")
+    batch = proj.shape[0]
+    inter, _ = _mamba_params(n_heads, head_dim, n_groups, conv_w, conv_b, A_log, D, dt_bias, gnorm_w, conv_state,
+                             ssm_state, batch)
+    y = torch.empty((batch, inter), dtype=torch.bfloat16, device=proj.device)
+    g = torch.empty_like(y)
+    _check_device(proj, conv_w, conv_b, A_log, D, dt_bias, gnorm_w, conv_state, ssm_state)
+    L = _lib.lib()
+    rc = L.nmi_mamba_mixer_decode(proj.data_ptr(), proj.stride(0), conv_w.data_ptr(), conv_b.data_ptr(),
+                                  A_log.data_ptr(), D.data_ptr(), dt_bias.data_ptr(), gnorm_w.data_ptr(),
+                                  conv_state.data_ptr(), ssm_state.data_ptr(), y.data_ptr(), g.data_ptr(), batch,
+                                  n_heads, head_dim, n_groups, 128, 4, eps, _stream())
+    _lib.check(rc, "nmi_mamba_mixer_decode")
+    return y, g
+
+
+def mamba_decode_fp8(x: torch.Tensor, norm_w: torch.Tensor, in_w, in_s, conv_w, conv_b, A_log, D, dt_bias, gnorm_w,
+                     out_w, out_s, conv_state, ssm_state, n_heads: int, head_dim: int, n_groups: int,
+                     out: torch.Tensor | None = None, eps: float = 1e-5, use_workspace: bool = True) -> torch.Tensor:
+    """The fp8 Mamba-2 block at decode (model/mamba_block.cuh:436-515): x, out [batch, hidden]
+    bf16; in_w [PROJ, hidden], out_w [hidden, n_heads * head_dim] e4m3 with per-row float32 scales;
+    the states are updated in place."""
+    x2 = _as_2d(x)
+    if not x2.is_contiguous() or x2.dtype != torch.bfloat16:
+        raise ValueError("x must be a contiguous bf16 tensor")
+    batch, hidden = x2.shape
+    inter, conv_dim = _mamba_params(n_heads, head_dim, n_groups, conv_w, conv_b, A_log, D, dt_bias, gnorm_w,
+                                    conv_state, ssm_state, batch)
+    in_w = _check_w(in_w, hidden)
+    if in_w.shape[0] != inter + conv_dim + n_heads:
+        raise ValueError(f"in_proj has {in_w.shape[0]} rows, expected {inter + conv_dim + n_heads}")
+    out_w = _check_w(out_w, inter)
+    if out_w.shape[0] != hidden:
+        raise ValueError(f"out_proj has {out_w.shape[0]} rows, hidden size is {hidden}")
+    _check_s(in_s, in_w.shape[0])
+    _check_s(out_s, hidden)
+    if norm_w.dtype != torch.float32 or tuple(norm_w.shape) != (hidden,) or not norm_w.is_contiguous():
+        raise ValueError(f"norm_w must be a contiguous float32 vector of {hidden} values")
+    if out is None:
+        out = torch.empty_like(x)
+    _check_out(out, batch, hidden) if x.dim() == 2 else _check_out(out, 1, hidden)
+    _check_device(x2, norm_w, in_w, in_s, conv_w, conv_b, A_log, D, dt_bias, gnorm_w, out_w, out_s, conv_state,
+                  ssm_state, out)
+    L = _lib.lib()
+    ws = None
+    if use_workspace:
+        ws = _block_ws(x.device, L.nmi_mamba_decode_workspace_bytes(batch, hidden, n_heads, head_dim, n_groups, 128))
+    rc = L.nmi_mamba_decode_fp8(x2.data_ptr(), norm_w.data_ptr(), in_w.data_ptr(), in_s.data_ptr(), conv_w.data_ptr(),
+                                conv_b.data_ptr(), A_log.data_ptr(), D.data_ptr(), dt_bias.data_ptr(),
+                                gnorm_w.data_ptr(), out_w.data_ptr(), out_s.data_ptr(), conv_state.data_ptr(),
+                                ssm_state.data_ptr(), out.data_ptr(), batch, hidden, n_heads, head_dim, n_groups, 128, 4,
+                                eps, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream())
+    _lib.check(rc, "nmi_mamba_decode_fp8")
+    return out
+
+
 class GemvChain:
     """The GEMVs of a decode step with as few launches as the dependencies allow
     (nmi_gemv_chain_*; M = 1).

@@ -245,6 +245,44 @@ def test_binding_attn_decode_validates():
         B.attn_decode_fp8(*([FAKE] * 12), 5, 5, FAKE)
 
 
+def test_mamba_decode_workspace_bytes_and_rejections():
+    L = _lib.lib()
+    proj_ld = 17504                                   # already a multiple of 8
+    r256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    want = r256(2 * proj_ld) + 2 * r256(2 * 7680) + r256(3136 * 2)
+    assert L.nmi_mamba_decode_workspace_bytes(1, 3136, 96, 80, 8, 128) == want
+    assert L.nmi_mamba_decode_workspace_bytes(0, 3136, 96, 80, 8, 128) == 0
+    ptrs = [FAKE] * 15
+
+    def call(*dims, ptrs=ptrs, ws=FAKE, ws_bytes=1 << 24):
+        return L.nmi_mamba_decode_fp8(*ptrs, *dims, 1e-5, ws, ws_bytes, None)
+
+    assert call(0, 3136, 96, 80, 8, 128, 4) == _lib.NMI_ERR_INVALID_ARG
+    assert call(1, 3136, 96, 80, 8, 64, 4) == _lib.NMI_ERR_INVALID_ARG     # d_state
+    assert call(1, 3136, 96, 80, 8, 128, 3) == _lib.NMI_ERR_INVALID_ARG    # conv_k
+    assert call(1, 3136, 96, 80, 7, 128, 4) == _lib.NMI_ERR_INVALID_ARG    # groups do not divide heads
+    assert call(1, 3136, 96, 136, 8, 128, 4) == _lib.NMI_ERR_INVALID_ARG   # head_dim > 128
+    assert call(1, 3136, 96, 80, 8, 128, 4, ws_bytes=64) == _lib.NMI_ERR_WORKSPACE
+    bad = list(ptrs)
+    bad[13] = FAKE + 4                                                     # ssm_state
+    assert call(1, 3136, 96, 80, 8, 128, 4, ptrs=bad) == _lib.NMI_ERR_ALIGNMENT
+    bad[13] = 0
+    assert call(1, 3136, 96, 80, 8, 128, 4, ptrs=bad) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_last_error().decode().startswith("nmi_mamba_decode_fp8")
+    # the mixer op
+    assert L.nmi_mamba_mixer_decode(FAKE, 17500, *([FAKE] * 10), 1, 96, 80, 8, 128, 4, 1e-5,
+                                    None) == _lib.NMI_ERR_INVALID_ARG          # proj_ld < PROJ
+    assert L.nmi_mamba_mixer_decode(FAKE + 8, 17504, *([FAKE] * 10), 1, 96, 80, 8, 128, 4, 1e-5,
+                                    None) == _lib.NMI_ERR_ALIGNMENT
+
+
+def test_binding_mamba_decode_validates():
+    from nemotron_infer_amd.csrc import binding as B
+
+    with pytest.raises(RuntimeError, match="batch=0"):
+        B.mamba_decode_fp8(*([FAKE] * 15), 0)
+
+
 def test_gemv_chain_workspace_bytes():
     """Chains synchronise through launch order only: no launch needs a workspace."""
     L = _lib.lib()

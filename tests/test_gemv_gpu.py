@@ -21,7 +21,7 @@ FIXTURES = ["kat_gemv_n64_k3136", "tiny_m4_n8_k16", "ragged_m3_n37_k208",
             "skinny_m16_n48_k3136", "special_nan_zero"]
 
 
-GEMV_KNOBS = ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemv.wgs", "gemv.multirow")
+GEMV_KNOBS = ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemv.wgs", "gemv.multirow", "gemv.grid", "gemv.balance")
 
 
 @pytest.fixture(autouse=True)
@@ -126,17 +126,20 @@ STREAM_K = [16, 48, 1024, 3136, 4096, 4112, 5120, 6272, 12544, 20000, 32768, 400
 
 
 @pytest.mark.parametrize("K", STREAM_K)
-@pytest.mark.parametrize("wgs", [0, 1])
-def test_stream_gemv_slices(K, wgs):
+@pytest.mark.parametrize("knobs", [{}, {"gemv.wgs": 2}, {"gemv.balance": 2}, {"gemv.grid": 3}])
+def test_stream_gemv_slices(K, knobs):
     """The M = 1 stream kernel against the oracle at every slice layout, with row counts that
     leave a half row group (odd N), a single row and fewer row groups than waves, per-row
-    log-uniform scales (a wrong scale index shows), and both grid caps (tuning knob gemv.wgs)."""
-    _lib.tuning_set("gemv.wgs", wgs)
+    log-uniform scales (a wrong scale index shows), and several grids: the default (sized so
+    that waves get equal row counts), two workgroups per CU, the plain capped grid, and three
+    workgroups walking everything."""
+    for k, v in knobs.items():
+        _lib.tuning_set(k, v)
     for N in (1, 3, 37, 1000):
-        announce("stream_gemv", K, N, wgs)
+        announce("stream_gemv", K, N, knobs)
         x, w, s = _case(N, K, 11 * N + K, scales="log_uniform")
         y = bits(ops.gemv_fp8(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
-        assert_parity(y, oracle_bits(x, w, s), f"stream K={K} N={N} wgs={wgs}", per_row_scales=True)
+        assert_parity(y, oracle_bits(x, w, s), f"stream K={K} N={N} {knobs}", per_row_scales=True)
 
 
 def test_stream_gemv_matches_grouped_and_strided():
