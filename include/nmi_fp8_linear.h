@@ -88,7 +88,14 @@ int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, in
  * the kernels run without the split (same results up to float32 summation order).  Two
  * launches that may run concurrently must not share a workspace.  The reference's blocks
  * likewise hand a workspace to their prefill GEMMs (model/mlp_block.cuh:133,156,160-161).
+ * Stream-K ordering: a contributor stores its partial tile, then releases its flag at device
+ * scope; the finisher polls the flag and acquires at device scope before reading the partial.
+ * The wait is bounded: if a flag never comes (a workgroup that never ran), the finisher gives
+ * up, leaves that partial out and sets the 32-bit error word at byte NMI_WS_ERROR_OFFSET of
+ * the workspace to 1.  After that the results of the launch are wrong and the workspace must be
+ * zero-filled again before its next use; the word stays set until then.
  */
+#define NMI_WS_ERROR_OFFSET 65532
 int nmi_linear_fp8_w8a16_ws(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
                             const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
                             void* workspace, size_t workspace_bytes, void* stream);

@@ -17,6 +17,7 @@ NMI_ERR_ALIGNMENT = -2
 NMI_ERR_UNSUPPORTED = -3
 NMI_ERR_WORKSPACE = -4
 NMI_ERR_ALLOC = -5
+NMI_WS_ERROR_OFFSET = 65532   # byte offset of the stream-K error word in a linear workspace
 
 # Every symbol the header declares, with its ctypes signature.
 _vp, _i, _i64, _sz, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float

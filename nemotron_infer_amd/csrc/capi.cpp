@@ -375,6 +375,8 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s4.dma")) t.s4_dma = value;
     else if (!std::strcmp(knob, "s4.kg")) t.s4_kg = value;
     else if (!std::strcmp(knob, "gemm.sk")) t.gemm_sk = value;
+    else if (!std::strcmp(knob, "gemm.sk_spin")) t.gemm_sk_spin = value;
+    else if (!std::strcmp(knob, "gemm.sk_lostflag")) t.gemm_sk_lostflag = value;
     else if (!std::strcmp(knob, "chain.wgs")) t.chain_wgs = value;
     else if (!std::strcmp(knob, "gemv.wgs")) t.gemv_wgs = value;
     else if (!std::strcmp(knob, "gemv.multirow")) t.gemv_multirow = value;

@@ -42,6 +42,8 @@ struct Tuning {
     int s4_dma = 0;        // 4x4x4 skinny kernel: 0 pipelined form where it applies, 2 windowed form
     int s4_kg = 0;         // 4x4x4 skinny kernel: workgroups splitting K (> 1, with a workspace; 0, 1: none)
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
+    int gemm_sk_spin = 0;  // GEMM stream-K: polls of a flag before the wait gives up (0: 2^26)
+    int gemm_sk_lostflag = 0;  // GEMM stream-K (tests): 1 = contributors do not raise their flags
     int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 2, or fewer if fewer are resident)
     int gemv_wgs = 0;      // M = 1 stream GEMV: workgroups per CU at most (1, 2; 0: 1)
     int gemv_multirow = 0; // M = 1: 1 runs the multi-row GEMV kernel (gemv_fp8.hip) instead of the stream kernel

@@ -342,3 +342,14 @@ def test_tuning_knobs_from_environment():
     env["NMI_TUNING"] = "no.such.knob=1"
     r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode != 0 and "unknown knob 'no.such.knob'" in r.stderr
+
+
+def test_workspace_error_offset_matches_the_header():
+    import re
+
+    hdr = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                            "nmi_fp8_linear.h")).read()
+    assert int(re.search(r"#define NMI_WS_ERROR_OFFSET (\d+)", hdr).group(1)) == _lib.NMI_WS_ERROR_OFFSET
+    L = _lib.lib()
+    for knob in ("gemm.sk_spin", "gemm.sk_lostflag", "gemv.grid", "gemv.balance", "sdpa.chunk"):
+        assert L.nmi_tuning_set(knob.encode(), 0) == 0, knob

@@ -177,8 +177,8 @@ def test_block_matches_oracle(M):
     ({"gemv.ks": 2, "gemv.t": 2, "gemv.p": 3}, [1, 2]),
     ({"gemv.ks": 4, "gemv.t": 1}, [1]),
     ({"gemv.xg": 1}, [1]),                           # the fused form always stages x in LDS
-    ({"gemm.tile": 8}, [600]),
-    ({"gemm.tile": 9}, [600]),
+    ({"gemm.tile": 20}, [600]),
+    ({"gemm.tile": 21}, [600]),
 ])
 def test_block_equals_composition_under_knobs(knobs, Ms):
     dev = _dev(*_weights(HIDDEN, INTER))
