@@ -65,7 +65,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
-    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn", "mamba", "engine"],
+    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn", "mamba", "engine", "prefill_attn"],
                    help="run one extra leg alone and print its JSON record (for profiling that leg); "
                         "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
@@ -516,6 +516,51 @@ def bench_attn_decode(dev, reps=5):
             "weight_bytes": wbytes, **res}
 
 
+def bench_attn_prefill(dev, reps=10):
+    """Causal attention over a prompt (sdpa_prefill, 40 query heads, 8 KV heads of 128) at
+    S = 512 / 2048 / 8192, priced on its causal flops (2 S (S + 1) / 2 x 128 x 2 per head for
+    Q.K^T and P.V), and the fp8 attention block attn_forward_fp8 at S = 2048."""
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    HQ, HKV, D = 40, 8, 128
+    T = Timer()
+    res = {}
+    for S in (512, 2048, 8192):
+        g = torch.Generator(device=dev).manual_seed(9300 + S)
+        qkv = torch.randn((S, (HQ + 2 * HKV) * D), generator=g, device=dev).to(torch.bfloat16)
+        q, k, v = qkv[:, :HQ * D], qkv[:, HQ * D:(HQ + HKV) * D], qkv[:, (HQ + HKV) * D:]
+        o = torch.empty((S, HQ * D), dtype=torch.bfloat16, device=dev)
+        ops.sdpa_prefill_bf16(q, k, v, HQ, HKV, out=o)
+        torch.cuda.synchronize()
+        gr = T.capture(lambda: [ops.sdpa_prefill_bf16(q, k, v, HQ, HKV, out=o) for _ in range(reps)])
+        steady(T, gr, 0.2)
+        t = T.time_replays([gr]) / reps
+        fl = 2 * 2 * (S * (S + 1) // 2) * D * HQ
+        res[f"sdpa_S={S}"] = {"us": round(t * 1e3, 1), "TFLOP/s": round(fl / (t * 1e-3) / 1e12, 1)}
+        del gr, qkv, o
+    S, hid = 2048, synth.HIDDEN
+    mats = [synth.make_weight(r, c, 9400 + i, dev)
+            for i, (r, c) in enumerate([(HQ * D, hid), (HKV * D, hid), (HKV * D, hid), (hid, HQ * D)])]
+    nw = 1.0 + 0.1 * torch.randn(hid, device=dev)
+    x = synth.make_act(S, hid, 9410, dev)
+    out = torch.empty_like(x)
+    kc = torch.empty((HKV, S, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    args = [t for m in mats for t in m]
+    ops.attn_forward_fp8(x, nw, *args, k_cache=kc, v_cache=vc, out=out)
+    torch.cuda.synchronize()
+    gr = T.capture(lambda: [ops.attn_forward_fp8(x, nw, *args, k_cache=kc, v_cache=vc, out=out) for _ in range(reps)])
+    steady(T, gr, 0.2)
+    t = T.time_replays([gr]) / reps
+    fl = sum(synth.linear_flops(S, w.shape[0], w.shape[1]) for w, _ in mats) + 2 * 2 * (S * (S + 1) // 2) * D * HQ
+    res["attn_forward_block_S=2048"] = {"us": round(t * 1e3, 1), "TFLOP/s": round(fl / (t * 1e-3) / 1e12, 1),
+                                        "launches": 8}
+    del gr
+    return {"workload": "causal attention prefill (40 q heads, 8 KV heads, head 128) and attn_forward_fp8", **res}
+
+
 def _mamba_layer(dev, seed):
     """Real-model Mamba-2 layer (hidden 3136, 96 heads of 80, 8 groups, state 128): fp8 in_proj
     [17504, 3136] and out_proj [3136, 7680], float32 parameters and states."""
@@ -769,6 +814,8 @@ def main():
             leg = bench_attn_decode(dev)
         elif args.only == "mamba":
             leg = bench_mamba_decode(dev)
+        elif args.only == "prefill_attn":
+            leg = bench_attn_prefill(dev)
         elif args.only == "engine":
             leg = bench_engine_decode(dev)
         else:
@@ -795,6 +842,9 @@ def main():
         log("attention decode block ...")
         extras["attn_decode"] = bench_attn_decode(dev)
         log(f"attention decode: {extras['attn_decode']['S=4096']}")
+        log("attention prefill ...")
+        extras["attn_prefill"] = bench_attn_prefill(dev)
+        log(f"attention prefill: {extras['attn_prefill']['sdpa_S=2048']}")
         log("mamba decode block ...")
         extras["mamba_decode"] = bench_mamba_decode(dev)
         log(f"mamba decode: {extras['mamba_decode']['block_4_launches']}")

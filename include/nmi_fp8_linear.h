@@ -287,6 +287,43 @@ int nmi_attn_decode_fp8(const void* input_bf16, const float* norm_w, const void*
                         float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Causal attention over a prompt (replaces sdpa_prefill_bf16<32, 128>,
+ * nemotron_infer/csrc/include/ops/attention/sdpa_prefill.cuh:364-395, kernel :224-320):
+ *   o[s, h] = bf16( softmax_{t <= s}(q[s, h] . k[t, kv(h)] / sqrt(128)) . v[t, kv(h)] ),
+ *   kv(h) = h / (n_heads / n_kv_heads), float32 softmax and sums.
+ * Token-major layouts (as the projections write them; the reference's kernel takes head-major
+ * [H, S, 128] and its block transposes around it): q, o [S, >= n_heads*128] with head h at
+ * column 128 h, k, v [S, >= n_kv_heads*128]; row strides ldq, ldk, ldv (multiples of 8) and ldo
+ * (multiple of 4) in elements.  q, k, v 16-byte aligned, o 8-byte aligned.
+ * workspace: nmi_sdpa_prefill_workspace_bytes(n_kv_heads, S) bytes (a transposed copy of v),
+ * 16-byte aligned; NULL takes it from the bump allocator.  Two launches.
+ */
+size_t nmi_sdpa_prefill_workspace_bytes(int n_kv_heads, int S);
+int nmi_sdpa_prefill_bf16(const void* q_bf16, int64_t ldq, const void* k_bf16, int64_t ldk, const void* v_bf16,
+                          int64_t ldv, void* o_bf16, int64_t ldo, int S, int n_heads, int n_kv_heads, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * The fp8 attention block over a prompt (replaces attention_block_forward_fp8<HIDDEN, H_Q, H_KV, 128>,
+ * nemotron_infer/csrc/include/model/attention_block.cuh:289-366; binding attn_forward_fp8,
+ * csrc/include/binding.cu:177-187):
+ *   h = rmsnorm(input) [S, hidden] (bf16); q, k, v = bf16 linears of h; o = causal attention
+ *   (nmi_sdpa_prefill_bf16); out = bf16(input + bf16(o . o_w^T * o_s)); when k_cache and v_cache
+ *   are both non-NULL, positions [0, S) of the caches [n_kv_heads, cache_cap, 128]
+ *   (cache_cap <= 0: S) receive k and v.  NoPE, as the reference.  The activations stay bf16
+ *   into every linear (the reference quantizes them to e4m3 first, attention_block.cuh:330-350).
+ * input, out [S, hidden] bf16 (out may be input); weights as nmi_attn_decode_fp8.
+ * workspace: nmi_attn_forward_workspace_bytes(S, hidden, n_heads, n_kv_heads) bytes, 256-byte
+ * aligned, no initialisation; NULL takes it from the bump allocator.
+ */
+size_t nmi_attn_forward_workspace_bytes(int S, int hidden, int n_heads, int n_kv_heads);
+int nmi_attn_forward_fp8(const void* input_bf16, const float* norm_w, const void* q_w_e4m3, const float* q_scale,
+                         const void* k_w_e4m3, const float* k_scale, const void* v_w_e4m3, const float* v_scale,
+                         const void* o_w_e4m3, const float* o_scale, void* out_bf16, int S, void* k_cache_bf16,
+                         void* v_cache_bf16, int cache_cap, int hidden, int n_heads, int n_kv_heads, float eps,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * The fp8 Mamba-2 block at decode, one token per sequence (replaces
  * mamba_block_decode_fp8<HIDDEN, H, P, N, G, 4>, nemotron_infer/csrc/include/model/
  * mamba_block.cuh:436-515; binding mamba_decode_fp8, csrc/include/binding.cu:162-175):

@@ -39,6 +39,10 @@ SIGNATURES = {
     "nmi_sdpa_decode_bf16": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp], _i),
     "nmi_attn_decode_workspace_bytes": ([_i, _i, _i, _i], _sz),
     "nmi_mamba_decode_workspace_bytes": ([_i] * 6, _sz),
+    "nmi_sdpa_prefill_workspace_bytes": ([_i, _i], _sz),
+    "nmi_sdpa_prefill_bf16": ([_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i, _i, _i, _vp, _sz, _vp], _i),
+    "nmi_attn_forward_workspace_bytes": ([_i] * 4, _sz),
+    "nmi_attn_forward_fp8": ([_vp] * 11 + [_i, _vp, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp], _i),
     "nmi_mamba_mixer_decode": ([_vp, _i64] + [_vp] * 10 + [_i] * 6 + [_f, _vp], _i),
     "nmi_mamba_decode_fp8": ([_vp] * 15 + [_i] * 7 + [_f, _vp, _sz, _vp], _i),
     "nmi_attn_decode_fp8": ([_vp] * 12 + [_i, _i, _vp, _i, _i, _i, _f, _vp, _sz, _vp], _i),

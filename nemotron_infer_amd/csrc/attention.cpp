@@ -69,9 +69,165 @@ AttnLayout attn_layout(int hidden, int n_heads, int n_kv, int S_cache) {
     return L;
 }
 
+// Prefill block workspace: the GEMMs' stream-K region (S >= 512), normed [S, hidden], q
+// [S, H*128], k and v [S, H_KV*128], o [S, H*128], V^T [H_KV, 128, ldvt].
+struct FwdLayout {
+    size_t gemm, normed, q, k, v, o, vt, total;
+};
+
+size_t gemm_region(int M) { return choose_path(M) == Path::Gemm ? round256(gemm_workspace_bytes(M)) : 0; }
+
+FwdLayout fwd_layout(int S, int hidden, int n_heads, int n_kv) {
+    FwdLayout L{};
+    const size_t QD = (size_t)n_heads * kSdpaHead, KD = (size_t)n_kv * kSdpaHead;
+    L.gemm = 0;
+    L.normed = L.gemm + gemm_region(S);
+    L.q = L.normed + round256((size_t)S * hidden * 2);
+    L.k = L.q + round256((size_t)S * QD * 2);
+    L.v = L.k + round256((size_t)S * KD * 2);
+    L.o = L.v + round256((size_t)S * KD * 2);
+    L.vt = L.o + round256((size_t)S * QD * 2);
+    L.total = L.vt + round256((size_t)n_kv * kSdpaHead * sdpa_prefill_vt_ld(S) * 2);
+    return L;
+}
+
+bool heads_ok(int n_heads, int n_kv) { return n_kv >= 1 && n_heads >= n_kv && n_heads % n_kv == 0; }
+
 }  // namespace
 
 extern "C" {
+
+size_t nmi_sdpa_prefill_workspace_bytes(int n_kv_heads, int S) {
+    if (n_kv_heads < 1 || S < 1) return 0;
+    return (size_t)n_kv_heads * kSdpaHead * sdpa_prefill_vt_ld(S) * 2;
+}
+
+int nmi_sdpa_prefill_bf16(const void* q_bf16, int64_t ldq, const void* k_bf16, int64_t ldk, const void* v_bf16,
+                          int64_t ldv, void* o_bf16, int64_t ldo, int S, int n_heads, int n_kv_heads, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    const char* fn = "nmi_sdpa_prefill_bf16";
+    if (!q_bf16 || !k_bf16 || !v_bf16 || !o_bf16)
+        return fail(NMI_ERR_INVALID_ARG, "nmi_sdpa_prefill_bf16: NULL pointer argument");
+    if (S < 1 || !heads_ok(n_heads, n_kv_heads) || ldq < (int64_t)n_heads * kSdpaHead ||
+        ldo < (int64_t)n_heads * kSdpaHead || ldk < (int64_t)n_kv_heads * kSdpaHead ||
+        ldv < (int64_t)n_kv_heads * kSdpaHead) {
+        set_last_error("%s: S=%d n_heads=%d n_kv_heads=%d ldq=%lld ldk=%lld ldv=%lld ldo=%lld (need S >= 1, n_heads a "
+                       "multiple of n_kv_heads, row strides of at least the heads' 128 columns)",
+                       fn, S, n_heads, n_kv_heads, (long long)ldq, (long long)ldk, (long long)ldv, (long long)ldo);
+        return NMI_ERR_INVALID_ARG;
+    }
+    if (!aligned(q_bf16, 16) || !aligned(k_bf16, 16) || !aligned(v_bf16, 16) || !aligned(o_bf16, 8) || ldq % 8 ||
+        ldk % 8 || ldv % 8 || ldo % 4)
+        return fail(NMI_ERR_ALIGNMENT,
+                    "nmi_sdpa_prefill_bf16: q, k, v must be 16-byte aligned with row strides multiple of 8 elements; "
+                    "o 8-byte aligned with a row stride multiple of 4");
+    const size_t need = nmi_sdpa_prefill_workspace_bytes(n_kv_heads, S);
+    if (workspace) {
+        if (!aligned(workspace, 16))
+            return fail(NMI_ERR_ALIGNMENT, "nmi_sdpa_prefill_bf16: workspace must be 16-byte aligned");
+        if (workspace_bytes < need) {
+            set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
+            return NMI_ERR_WORKSPACE;
+        }
+    } else {
+        const int rc = nmi_alloc(need, &workspace);
+        if (rc != NMI_OK) return rc;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint16_t* vt = static_cast<uint16_t*>(workspace);
+    hipError_t e = launch_kv_layout(static_cast<const uint16_t*>(k_bf16), ldk, static_cast<const uint16_t*>(v_bf16), ldv,
+                                    vt, S, n_kv_heads, nullptr, nullptr, 0, st);
+    if (e == hipSuccess)
+        e = launch_sdpa_prefill(static_cast<const uint16_t*>(q_bf16), ldq, static_cast<const uint16_t*>(k_bf16), ldk, vt,
+                                static_cast<uint16_t*>(o_bf16), ldo, S, n_heads, n_kv_heads, st);
+    return hip_status(e, fn);
+}
+
+size_t nmi_attn_forward_workspace_bytes(int S, int hidden, int n_heads, int n_kv_heads) {
+    if (S < 1 || hidden < 16 || !heads_ok(n_heads, n_kv_heads)) return 0;
+    return fwd_layout(S, hidden, n_heads, n_kv_heads).total;
+}
+
+int nmi_attn_forward_fp8(const void* input_bf16, const float* norm_w, const void* q_w_e4m3, const float* q_scale,
+                         const void* k_w_e4m3, const float* k_scale, const void* v_w_e4m3, const float* v_scale,
+                         const void* o_w_e4m3, const float* o_scale, void* out_bf16, int S, void* k_cache_bf16,
+                         void* v_cache_bf16, int cache_cap, int hidden, int n_heads, int n_kv_heads, float eps,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "nmi_attn_forward_fp8";
+    if (!input_bf16 || !norm_w || !q_w_e4m3 || !q_scale || !k_w_e4m3 || !k_scale || !v_w_e4m3 || !v_scale ||
+        !o_w_e4m3 || !o_scale || !out_bf16)
+        return fail(NMI_ERR_INVALID_ARG, "nmi_attn_forward_fp8: NULL pointer argument");
+    if (S < 1 || hidden < 16 || hidden % 16 != 0 || !heads_ok(n_heads, n_kv_heads)) {
+        set_last_error("%s: S=%d hidden=%d n_heads=%d n_kv_heads=%d (need S >= 1, hidden a positive multiple of 16, "
+                       "n_heads a multiple of n_kv_heads)",
+                       fn, S, hidden, n_heads, n_kv_heads);
+        return NMI_ERR_INVALID_ARG;
+    }
+    const bool caches = k_cache_bf16 && v_cache_bf16;
+    const int cap = cache_cap > 0 ? cache_cap : S;
+    if (caches && cap < S) {
+        set_last_error("%s: cache_cap=%d < S=%d", fn, cache_cap, S);
+        return NMI_ERR_INVALID_ARG;
+    }
+    if (!aligned(input_bf16, 16) || !aligned(norm_w, 16) || !aligned(q_w_e4m3, 16) || !aligned(k_w_e4m3, 16) ||
+        !aligned(v_w_e4m3, 16) || !aligned(o_w_e4m3, 16) ||
+        (caches && (!aligned(k_cache_bf16, 16) || !aligned(v_cache_bf16, 16))))
+        return fail(NMI_ERR_ALIGNMENT,
+                    "nmi_attn_forward_fp8: input, norm_w, the weights and the caches must be 16-byte aligned");
+    if (!aligned(q_scale, 4) || !aligned(k_scale, 4) || !aligned(v_scale, 4) || !aligned(o_scale, 4) ||
+        !aligned(out_bf16, 2))
+        return fail(NMI_ERR_ALIGNMENT, "nmi_attn_forward_fp8: misaligned scale or output");
+    const FwdLayout lay = fwd_layout(S, hidden, n_heads, n_kv_heads);
+    if (workspace) {
+        if (!aligned(workspace, 256))
+            return fail(NMI_ERR_ALIGNMENT, "nmi_attn_forward_fp8: workspace must be 256-byte aligned");
+        if (workspace_bytes < lay.total) {
+            set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, lay.total);
+            return NMI_ERR_WORKSPACE;
+        }
+    } else {
+        const int rc = nmi_alloc(lay.total, &workspace);   // as the reference's allocate_tensor calls
+        if (rc != NMI_OK) return rc;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char* base = static_cast<char*>(workspace);
+    const size_t gws = lay.normed - lay.gemm;
+    void* gemm_ws = gws ? base + lay.gemm : nullptr;
+    const int QD = n_heads * kSdpaHead, KD = n_kv_heads * kSdpaHead;
+    const uint16_t* in = static_cast<const uint16_t*>(input_bf16);
+    uint16_t* q = reinterpret_cast<uint16_t*>(base + lay.q);
+    uint16_t* k = reinterpret_cast<uint16_t*>(base + lay.k);
+    uint16_t* v = reinterpret_cast<uint16_t*>(base + lay.v);
+    uint16_t* o = reinterpret_cast<uint16_t*>(base + lay.o);
+    uint16_t* vt = reinterpret_cast<uint16_t*>(base + lay.vt);
+    hipError_t e = hipSuccess;
+    if (gws) e = launch_sk_flags_clear(gemm_ws, st);   // the workspace may hold anything
+    if (e != hipSuccess) return hip_status(e, fn);
+    // q, k, v of the normed input
+    GemvGroup qkv[3] = {
+        {static_cast<const uint8_t*>(q_w_e4m3), hidden, q_scale, q, QD, QD, 0, 0, Epi{}},
+        {static_cast<const uint8_t*>(k_w_e4m3), hidden, k_scale, k, KD, KD, 0, 0, Epi{}},
+        {static_cast<const uint8_t*>(v_w_e4m3), hidden, v_scale, v, KD, KD, 0, 0, Epi{}},
+    };
+    const Norm norm{norm_w, eps};
+    if (choose_path(S) == Path::Gemv && gemv_norm_supported(S, hidden)) {
+        e = dispatch_linear(in, hidden, S, hidden, qkv, 3, nullptr, 0, st, norm);
+    } else {
+        uint16_t* normed = reinterpret_cast<uint16_t*>(base + lay.normed);
+        e = launch_rmsnorm(in, hidden, norm, normed, hidden, S, hidden, st);
+        if (e == hipSuccess) e = dispatch_linear(normed, hidden, S, hidden, qkv, 3, gemm_ws, gws, st);
+    }
+    if (e != hipSuccess) return hip_status(e, fn);
+    // V^T (and the caches), causal attention
+    e = launch_kv_layout(k, KD, v, KD, vt, S, n_kv_heads, caches ? static_cast<uint16_t*>(k_cache_bf16) : nullptr,
+                         caches ? static_cast<uint16_t*>(v_cache_bf16) : nullptr, cap, st);
+    if (e == hipSuccess) e = launch_sdpa_prefill(q, QD, k, KD, vt, o, QD, S, n_heads, n_kv_heads, st);
+    if (e != hipSuccess) return hip_status(e, fn);
+    // out = bf16(input + bf16(o_proj(o)))
+    GemvGroup og{static_cast<const uint8_t*>(o_w_e4m3), QD, o_scale, static_cast<uint16_t*>(out_bf16), hidden, hidden,
+                 0, 0, Epi{kEpiResidual, in, hidden}};
+    return hip_status(dispatch_linear(o, QD, S, QD, &og, 1, gemm_ws, gws, st), fn);
+}
 
 size_t nmi_sdpa_decode_workspace_bytes(int n_heads, int n_kv_heads, int S_cache) {
     if (n_kv_heads < 1 || n_heads < 1 || S_cache < 0) return 0;

@@ -8,8 +8,8 @@
 // it never includes HIP headers.
 //
 // Built here: the fp8 linear hot path (linear_fp8, gemv_fp8), the fp8 MLP block
-// (mlp_forward_fp8), the fp8 attention and Mamba blocks at decode (attn_decode_fp8,
-// mamba_decode_fp8), rmsnorm, and the allocator/sync entries.  Reference entries outside that
+// (mlp_forward_fp8), the fp8 attention block (attn_forward_fp8, attn_decode_fp8), the fp8 Mamba
+// block at decode (mamba_decode_fp8), rmsnorm, and the allocator/sync entries.  Reference entries outside that
 // path exist with the reference's arity and raise NotImplementedError naming what is missing,
 // so a caller fails loudly instead of computing something else.
 #include <pybind11/pybind11.h>
@@ -44,7 +44,8 @@ const float* cf(uintptr_t p) { return reinterpret_cast<const float*>(p); }
 [[noreturn]] void not_built(const char* name) {
     std::string msg = std::string(name) +
                       " is not part of this build: nemotron_infer_amd implements the fp8 W8A16 linear hot "
-                      "path (linear_fp8, gemv_fp8), mlp_forward_fp8, attn_decode_fp8, mamba_decode_fp8 and rmsnorm only";
+                      "path (linear_fp8, gemv_fp8), mlp_forward_fp8, attn_forward_fp8, attn_decode_fp8, mamba_decode_fp8 "
+                      "and rmsnorm only";
     PyErr_SetString(PyExc_NotImplementedError, msg.c_str());
     throw py::error_already_set();
 }
@@ -130,6 +131,22 @@ PYBIND11_MODULE(binding, m) {
         py::arg("v_w"), py::arg("v_s"), py::arg("o_w"), py::arg("o_s"), py::arg("k_cache"), py::arg("v_cache"),
         py::arg("S_cache"), py::arg("cache_cap"), py::arg("out"));
 
+    // binding.cu:177-187 attn_forward_fp8(input, block_norm_w, q_w, q_s, k_w, k_s, v_w, v_s, o_w, o_s, out,
+    // S, k_cache, v_cache, cache_cap): caches written when both are non-zero (cache_cap <= 0: S).
+    m.def(
+        "attn_forward_fp8",
+        [](uintptr_t input, uintptr_t norm_w, uintptr_t q_w, uintptr_t q_s, uintptr_t k_w, uintptr_t k_s,
+           uintptr_t v_w, uintptr_t v_s, uintptr_t o_w, uintptr_t o_s, uintptr_t out, int S, uintptr_t k_cache,
+           uintptr_t v_cache, int cache_cap) {
+            check(nmi_attn_forward_fp8(cp(input), cf(norm_w), cp(q_w), cf(q_s), cp(k_w), cf(k_s), cp(v_w), cf(v_s),
+                                       cp(o_w), cf(o_s), mp(out), S, mp(k_cache), mp(v_cache), cache_cap, cfg::HIDDEN,
+                                       cfg::H_Q, cfg::H_KV, cfg::EPS, nullptr, 0, nullptr),
+                  "attn_forward_fp8");
+        },
+        py::arg("input"), py::arg("block_norm_w"), py::arg("q_w"), py::arg("q_s"), py::arg("k_w"), py::arg("k_s"),
+        py::arg("v_w"), py::arg("v_s"), py::arg("o_w"), py::arg("o_s"), py::arg("out"), py::arg("S"),
+        py::arg("k_cache"), py::arg("v_cache"), py::arg("cache_cap"));
+
     // binding.cu:162-175 mamba_decode_fp8(input, block_norm_w, in_proj_w, in_proj_wscale, conv1d_w,
     // conv1d_b, A_log, D, dt_bias, gnorm_w, out_proj_w, out_proj_wscale, conv_state, ssm_state, out,
     // B): states float32 [B, CONV_DIM, CONV_K - 1] and [B, H, P, N], updated in place.
@@ -171,7 +188,4 @@ PYBIND11_MODULE(binding, m) {
                                   uintptr_t, int, int, uintptr_t, uintptr_t) {
         not_built("mamba_forward_fp8");
     });
-    m.def("attn_forward_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
-                                 uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int, uintptr_t,
-                                 uintptr_t, int) { not_built("attn_forward_fp8"); });
 }

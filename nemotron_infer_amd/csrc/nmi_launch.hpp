@@ -215,6 +215,15 @@ struct MambaDecodeArgs {
 bool mamba_decode_supported(int H, int P, int G, int d_state, int conv_k);
 hipError_t launch_mamba_decode_mixer(const MambaDecodeArgs& a, int batch, hipStream_t stream);
 
+// Causal attention over a prompt (sdpa_prefill.hip), token-major q [S, ldq], k [S, ldk], o
+// [S, ldo] (head h at column 128 h), V through V^T [H_KV, 128, sdpa_prefill_vt_ld(S)] written by
+// launch_kv_layout (which also fills the KV caches [H_KV, cap, 128] when given).
+int64_t sdpa_prefill_vt_ld(int S);
+hipError_t launch_kv_layout(const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, uint16_t* vt, int S,
+                            int H_KV, uint16_t* k_cache, uint16_t* v_cache, int cap, hipStream_t stream);
+hipError_t launch_sdpa_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k, int64_t ldk, const uint16_t* vt,
+                               uint16_t* o, int64_t ldo, int S, int H, int H_KV, hipStream_t stream);
+
 hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream);
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,

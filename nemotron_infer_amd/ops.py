@@ -344,6 +344,82 @@ def attn_decode_fp8(x: torch.Tensor, norm_w: torch.Tensor, q_w, q_s, k_w, k_s, v
     return out
 
 
+def _check_rows(t: torch.Tensor, S: int, cols: int, name: str) -> None:
+    if t.dtype != torch.bfloat16 or t.dim() != 2 or t.shape[0] != S or t.shape[1] < cols or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a bf16 [S={S}, >= {cols}] tensor with contiguous rows, "
+                         f"got {t.dtype} {tuple(t.shape)} strides {t.stride()}")
+
+
+def sdpa_prefill_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, n_heads: int, n_kv_heads: int,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal attention over a prompt (ops/attention/sdpa_prefill.cuh:364-395), token-major: q
+    [S, >= n_heads * 128], k, v [S, >= n_kv_heads * 128] (row-strided views allowed).  Returns o
+    [S, n_heads * 128] bf16."""
+    S = q.shape[0]
+    _check_rows(q, S, n_heads * 128, "q")
+    _check_rows(k, S, n_kv_heads * 128, "k")
+    _check_rows(v, S, n_kv_heads * 128, "v")
+    if out is None:
+        out = torch.empty((S, n_heads * 128), dtype=torch.bfloat16, device=q.device)
+    _check_rows(out, S, n_heads * 128, "out")
+    _check_device(q, k, v, out)
+    L = _lib.lib()
+    need = L.nmi_sdpa_prefill_workspace_bytes(n_kv_heads, S)
+    ws = _block_ws(q.device, need)
+    rc = L.nmi_sdpa_prefill_bf16(q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
+                                 out.data_ptr(), out.stride(0), S, n_heads, n_kv_heads, ws.data_ptr(), ws.numel(),
+                                 _stream())
+    _lib.check(rc, "nmi_sdpa_prefill_bf16")
+    return out
+
+
+def attn_forward_fp8(x: torch.Tensor, norm_w: torch.Tensor, q_w, q_s, k_w, k_s, v_w, v_s, o_w, o_s,
+                     k_cache: torch.Tensor | None = None, v_cache: torch.Tensor | None = None,
+                     out: torch.Tensor | None = None, eps: float = 1e-5, use_workspace: bool = True) -> torch.Tensor:
+    """The fp8 attention block over a prompt (model/attention_block.cuh:289-366): x, out
+    [S, hidden] bf16; with k_cache and v_cache ([n_kv_heads, cap, 128] bf16) positions [0, S)
+    receive this prompt's k and v."""
+    x2 = _as_2d(x)
+    if not x2.is_contiguous() or x2.dtype != torch.bfloat16:
+        raise ValueError("x must be a contiguous bf16 tensor")
+    S, hidden = x2.shape
+    q_w, k_w, v_w = _check_w(q_w, hidden), _check_w(k_w, hidden), _check_w(v_w, hidden)
+    if q_w.shape[0] % 128 or k_w.shape[0] % 128 or k_w.shape[0] != v_w.shape[0]:
+        raise ValueError("q/k/v projections must have whole 128-row heads, k and v the same count")
+    H, n_kv = q_w.shape[0] // 128, k_w.shape[0] // 128
+    o_w = _check_w(o_w, H * 128)
+    if o_w.shape[0] != hidden:
+        raise ValueError(f"o_proj has {o_w.shape[0]} rows, hidden size is {hidden}")
+    _check_s(q_s, H * 128)
+    _check_s(k_s, n_kv * 128)
+    _check_s(v_s, n_kv * 128)
+    _check_s(o_s, hidden)
+    if norm_w.dtype != torch.float32 or tuple(norm_w.shape) != (hidden,) or not norm_w.is_contiguous():
+        raise ValueError(f"norm_w must be a contiguous float32 vector of {hidden} values")
+    cap = 0
+    if k_cache is not None or v_cache is not None:
+        if k_cache is None or v_cache is None:
+            raise ValueError("give both caches or neither")
+        if k_cache.dim() != 3 or k_cache.shape[0] != n_kv or k_cache.shape[2] != 128 or k_cache.shape[1] < S:
+            raise ValueError(f"k_cache must be [{n_kv}, cap >= {S}, 128], got {tuple(k_cache.shape)}")
+        cap = k_cache.shape[1]
+        _check_bf16(k_cache, (n_kv, cap, 128), "k_cache")
+        _check_bf16(v_cache, (n_kv, cap, 128), "v_cache")
+    if out is None:
+        out = torch.empty_like(x)
+    _check_out(out, S, hidden) if x.dim() == 2 else _check_out(out, 1, hidden)
+    _check_device(x2, norm_w, q_w, q_s, k_w, k_s, v_w, v_s, o_w, o_s, out)
+    L = _lib.lib()
+    ws = _block_ws(x.device, L.nmi_attn_forward_workspace_bytes(S, hidden, H, n_kv)) if use_workspace else None
+    rc = L.nmi_attn_forward_fp8(x2.data_ptr(), norm_w.data_ptr(), q_w.data_ptr(), q_s.data_ptr(), k_w.data_ptr(),
+                                k_s.data_ptr(), v_w.data_ptr(), v_s.data_ptr(), o_w.data_ptr(), o_s.data_ptr(),
+                                out.data_ptr(), S, None if k_cache is None else k_cache.data_ptr(),
+                                None if v_cache is None else v_cache.data_ptr(), cap, hidden, H, n_kv, eps,
+                                None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream())
+    _lib.check(rc, "nmi_attn_forward_fp8")
+    return out
+
+
 def _check_f32(t: torch.Tensor, shape, name: str) -> None:
     if t.dtype != torch.float32 or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
         raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(shape)}, "

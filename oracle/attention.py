@@ -1,6 +1,6 @@
-"""CPU oracle for nemotron_infer's attention decode -- TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for nemotron_infer's attention (decode and prefill) -- TEST INFRASTRUCTURE ONLY.
 
-Restates on the CPU what the reference's attention decode computes, so that the HIP kernels
+Restates on the CPU what the reference's attention computes, so that the HIP kernels
 can be checked against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg use it.  bf16 tensors are uint16 bit patterns, as in ``oracle.linear``.
 
@@ -20,6 +20,13 @@ can be checked against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and ``b
   out = bf16(input + bf16(o_proj(o))); returns out and the updated caches.  NoPE (no rotary;
   attention_block.cuh:8-10).  The projections are ``oracle.linear``'s; the RMSNorm and the add
   are ``oracle.block``'s.
+* ``sdpa_prefill`` -- ops/attention/sdpa_prefill.cuh:224-320: causal attention of every query
+  s over keys t <= s of its KV head, float64, rounded once to bf16; token-major q [S, H*D],
+  k, v [S, H_KV*D].
+* ``attn_forward_block_fp8`` -- model/attention_block.cuh:289-366 on bf16 activations (the
+  reference's e4m3 activation quantization into its GEMMs is not reproduced, as for every
+  linear of this build): rmsnorm -> q, k, v linears -> sdpa_prefill -> o linear -> residual
+  add; k and v are what the reference copies into the caches (:355-364).
 
 Pinned in tests/test_oracle_attention.py: ``sdpa_decode`` against torch's own
 ``F.scaled_dot_product_attention`` in float64 with the KV heads repeated (a library routine,
@@ -27,7 +34,9 @@ independent of this restatement), against closed forms (one cached position retu
 a zero query returns the mean of V; S == 0 returns 0) and with planted mistakes (a wrong KV-head
 mapping, attending the new token, a dropped 1/sqrt(D)) that those checks catch; the block
 against an independent float32 torch composition and against the closed forms o_w == 0 and
-S == 0 (both give out == input).
+S == 0 (both give out == input).  ``sdpa_prefill`` against torch's scaled_dot_product_attention
+with is_causal=True in float64 and the closed form of its first row (the value of position 0);
+a non-causal variant is caught.
 """
 from __future__ import annotations
 
@@ -97,3 +106,46 @@ def attn_decode_block_fp8(x_bits, norm_w, q_codes, q_s, k_codes, k_s, v_codes, v
     if return_stages:
         return out, kc, vc, dict(normed=h, q=q, k_new=kn, v_new=vn, o=o, attn=attn)
     return out, kc, vc
+
+
+def sdpa_prefill_f64(q_bits, k_bits, v_bits, n_kv: int, causal: bool = True) -> np.ndarray:
+    """float64 o [S, H*D] before rounding (token-major bf16 bits in)."""
+    q = _f64(q_bits)
+    K = _f64(k_bits)
+    V = _f64(v_bits)
+    S = q.shape[0]
+    H = q.shape[1] // HEAD
+    r = H // n_kv
+    out = np.zeros((S, H * HEAD), np.float64)
+    mask = np.tril(np.ones((S, S), bool)) if causal else np.ones((S, S), bool)
+    for h in range(H):
+        kv = h // r
+        qh = q[:, h * HEAD:(h + 1) * HEAD]
+        kh = K[:, kv * HEAD:(kv + 1) * HEAD]
+        vh = V[:, kv * HEAD:(kv + 1) * HEAD]
+        sc = (qh @ kh.T) / np.sqrt(HEAD)
+        sc = np.where(mask, sc, -np.inf)
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        out[:, h * HEAD:(h + 1) * HEAD] = (p @ vh) / p.sum(axis=1, keepdims=True)
+    return out
+
+
+def sdpa_prefill(q_bits, k_bits, v_bits, n_kv: int) -> np.ndarray:
+    return block.bf16_round_exact(sdpa_prefill_f64(q_bits, k_bits, v_bits, n_kv))
+
+
+def attn_forward_block_fp8(x_bits, norm_w, q_codes, q_s, k_codes, k_s, v_codes, v_s, o_codes, o_s, n_kv: int,
+                           eps: float = 1e-5, return_stages: bool = False):
+    """The block over a prompt: x [S, hidden] bf16 bits.  Returns out (+ the stages, whose k and
+    v are the cache contents)."""
+    x_bits = np.atleast_2d(np.asarray(x_bits, np.uint16))
+    h = block.rmsnorm_bf16(x_bits, norm_w, eps)
+    q = linear.linear_fp8_w8a16(h, q_codes, q_s)
+    k = linear.linear_fp8_w8a16(h, k_codes, k_s)
+    v = linear.linear_fp8_w8a16(h, v_codes, v_s)
+    o = sdpa_prefill(q, k, v, n_kv)
+    attn = linear.linear_fp8_w8a16(o, o_codes, o_s)
+    out = block.add_bf16(x_bits, attn)
+    if return_stages:
+        return out, dict(normed=h, q=q, k=k, v=v, o=o, attn=attn)
+    return out

@@ -114,7 +114,7 @@ def test_out_of_scope_entries_fail_loudly():
     from nemotron_infer_amd.csrc import binding as B
 
     with pytest.raises(NotImplementedError, match="not part of this build"):
-        B.attn_forward_fp8(*([0] * 15))
+        B.attn_forward(*([0] * 11))
     with pytest.raises(NotImplementedError):
         B.mlp_forward(*([0] * 6))
     with pytest.raises(NotImplementedError):

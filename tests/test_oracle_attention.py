@@ -160,3 +160,36 @@ def test_block_closed_forms_give_the_input():
     out, _, _ = attention.attn_decode_block_fp8(x, nw, *qw, *kw, *vw, *ow, kc, vc, 4, H_KV)
     assert not np.array_equal(out, x)
     assert np.array_equal(block.add_bf16(x, np.zeros_like(x)), x)
+
+
+# --------------------------------------------------------------------------------------
+# prefill (sdpa_prefill.cuh:224-320)
+# --------------------------------------------------------------------------------------
+def _prefill_case(S, H, H_KV, seed):
+    rng = np.random.default_rng(seed)
+    return (bf16(rng.standard_normal((S, H * D))), bf16(rng.standard_normal((S, H_KV * D))),
+            bf16(rng.standard_normal((S, H_KV * D))))
+
+
+@pytest.mark.parametrize("S,H,H_KV", [(1, 4, 2), (37, 10, 2), (130, 8, 8), (64, 6, 1)])
+def test_prefill_matches_torch_causal_sdpa(S, H, H_KV):
+    q, k, v = _prefill_case(S, H, H_KV, seed=S + H)
+    got = attention.sdpa_prefill_f64(q, k, v, H_KV)
+    qt = torch.from_numpy(val(q)).view(S, H, D).transpose(0, 1)[None]
+    kt = torch.from_numpy(val(k)).view(S, H_KV, D).transpose(0, 1)[None].repeat_interleave(H // H_KV, dim=1)
+    vt = torch.from_numpy(val(v)).view(S, H_KV, D).transpose(0, 1)[None].repeat_interleave(H // H_KV, dim=1)
+    ref = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)[0].transpose(0, 1).reshape(S, H * D).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_prefill_first_row_is_the_first_value():
+    q, k, v = _prefill_case(20, 10, 2, seed=5)
+    o = attention.sdpa_prefill(q, k, v, 2)
+    for h in range(10):
+        assert np.array_equal(o[0, h * D:(h + 1) * D], v[0, (h // 5) * D:(h // 5 + 1) * D])
+
+
+def test_planted_non_causal_prefill_is_caught():
+    q, k, v = _prefill_case(33, 4, 2, seed=6)
+    wrong = attention.sdpa_prefill_f64(q, k, v, 2, causal=False)
+    assert not np.allclose(wrong, attention.sdpa_prefill_f64(q, k, v, 2), rtol=1e-3, atol=1e-3)
