@@ -65,7 +65,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
-    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn", "mamba", "engine", "prefill_attn"],
+    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn", "mamba", "engine", "prefill_attn", "prefill_mamba"],
                    help="run one extra leg alone and print its JSON record (for profiling that leg); "
                         "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
@@ -590,6 +590,39 @@ def _mamba_args(L):
             *L["out"], L["conv_state"], L["ssm_state"])
 
 
+def bench_mamba_prefill(dev, reps=5):
+    """The fp8 Mamba-2 block over a prompt (mamba_forward_fp8) at S = 2048 with its final states:
+    block time and TFLOP/s of its two linears, and the conv + scan kernels' share (kernel trace)."""
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    H, P, G = 96, 80, 8
+    L = _mamba_layer(dev, 9600)
+    res = {}
+    for S in (512, 2048):
+        x = synth.make_act(S, synth.HIDDEN, 9601, dev)
+        out = torch.empty_like(x)
+        args = (L["norm"], *L["inp"], L["conv_w"], L["conv_b"], L["A_log"], L["D"], L["dt_bias"], L["gnorm_w"],
+                *L["out"])
+
+        def run():
+            ops.mamba_forward_fp8(x, *args, H, P, G, conv_state_out=L["conv_state"], ssm_state_out=L["ssm_state"],
+                                  out=out)
+
+        run()
+        torch.cuda.synchronize()
+        T = Timer()
+        g = T.capture(lambda: [run() for _ in range(reps)])
+        steady(T, g, 0.2)
+        t = T.time_replays([g]) / reps
+        fl = sum(synth.linear_flops(S, w.shape[0], w.shape[1]) for w, _ in (L["inp"], L["out"]))
+        res[f"S={S}"] = {"us": round(t * 1e3, 1), "linear_TFLOP/s_equiv": round(fl / (t * 1e-3) / 1e12, 1),
+                         "launches": 6}
+        del g
+    return {"workload": "mamba_forward_fp8 block (hidden 3136, 96 heads x 80, 8 groups, state 128)", **res}
+
+
 def bench_mamba_decode(dev, reps=5):
     """The fp8 Mamba-2 block at decode (mamba_decode_fp8), layers rotated over copies totalling
     > 1 GB: the block (4 launches) against the reference's launch structure on this library's
@@ -816,6 +849,8 @@ def main():
             leg = bench_mamba_decode(dev)
         elif args.only == "prefill_attn":
             leg = bench_attn_prefill(dev)
+        elif args.only == "prefill_mamba":
+            leg = bench_mamba_prefill(dev)
         elif args.only == "engine":
             leg = bench_engine_decode(dev)
         else:
@@ -845,6 +880,9 @@ def main():
         log("attention prefill ...")
         extras["attn_prefill"] = bench_attn_prefill(dev)
         log(f"attention prefill: {extras['attn_prefill']['sdpa_S=2048']}")
+        log("mamba prefill block ...")
+        extras["mamba_prefill"] = bench_mamba_prefill(dev)
+        log(f"mamba prefill: {extras['mamba_prefill']['S=2048']}")
         log("mamba decode block ...")
         extras["mamba_decode"] = bench_mamba_decode(dev)
         log(f"mamba decode: {extras['mamba_decode']['block_4_launches']}")

@@ -367,6 +367,29 @@ int nmi_mamba_decode_fp8(const void* input_bf16, const float* norm_w, const void
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The fp8 Mamba-2 block over prompts (replaces mamba_block_forward_fp8<HIDDEN, H, P, N, G, 4>,
+ * nemotron_infer/csrc/include/model/mamba_block.cuh:346-425; binding mamba_forward_fp8,
+ * csrc/include/binding.cu:147-160): input, out [batch * S, hidden] bf16 (batch sequences of S
+ * tokens; out may be input).  h = rmsnorm(input); proj = in_proj(h); per sequence the causal
+ * conv1d + SiLU from a zero state and the SSM scan from a zero state (the recurrence in float32,
+ * where the reference runs the chunked form with TF32 products); the gated RMSNorm; out =
+ * bf16(input + bf16(out_proj(...))).  When given, conv_state_out [batch, conv_dim, 3] and
+ * ssm_state_out [batch, n_heads, head_dim, d_state] (float32) receive each sequence's final
+ * states, for nmi_mamba_decode_fp8 to continue from.  Weights and supported shapes as
+ * nmi_mamba_decode_fp8.
+ * workspace: nmi_mamba_forward_workspace_bytes(batch, S, hidden, n_heads, head_dim, n_groups,
+ * d_state) bytes, 256-byte aligned, no initialisation; NULL takes it from the bump allocator.
+ */
+size_t nmi_mamba_forward_workspace_bytes(int batch, int S, int hidden, int n_heads, int head_dim, int n_groups,
+                                         int d_state);
+int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const void* in_proj_w_e4m3,
+                          const float* in_proj_scale, const float* conv_w, const float* conv_b, const float* A_log,
+                          const float* D, const float* dt_bias, const float* gnorm_w, const void* out_proj_w_e4m3,
+                          const float* out_proj_scale, void* out_bf16, int batch, int S, float* conv_state_out,
+                          float* ssm_state_out, int hidden, int n_heads, int head_dim, int n_groups, int d_state,
+                          int conv_k, float eps, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg": schedule of the multi-row
  * GEMV kernel (M = 2, or M = 1 with "gemv.multirow" = 1), "gemv.t" = 4 also 4 rows per step for
  * the M = 1 stream kernel, "gemv.wgs": its workgroups per CU (1, 2), "gemv.grid": its exact

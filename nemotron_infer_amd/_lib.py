@@ -40,6 +40,8 @@ SIGNATURES = {
     "nmi_attn_decode_workspace_bytes": ([_i, _i, _i, _i], _sz),
     "nmi_mamba_decode_workspace_bytes": ([_i] * 6, _sz),
     "nmi_sdpa_prefill_workspace_bytes": ([_i, _i], _sz),
+    "nmi_mamba_forward_workspace_bytes": ([_i] * 7, _sz),
+    "nmi_mamba_forward_fp8": ([_vp] * 13 + [_i, _i, _vp, _vp] + [_i] * 6 + [_f, _vp, _sz, _vp], _i),
     "nmi_sdpa_prefill_bf16": ([_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i, _i, _i, _vp, _sz, _vp], _i),
     "nmi_attn_forward_workspace_bytes": ([_i] * 4, _sz),
     "nmi_attn_forward_fp8": ([_vp] * 11 + [_i, _vp, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp], _i),

@@ -8,8 +8,8 @@
 // it never includes HIP headers.
 //
 // Built here: the fp8 linear hot path (linear_fp8, gemv_fp8), the fp8 MLP block
-// (mlp_forward_fp8), the fp8 attention block (attn_forward_fp8, attn_decode_fp8), the fp8 Mamba
-// block at decode (mamba_decode_fp8), rmsnorm, and the allocator/sync entries.  Reference entries outside that
+// (mlp_forward_fp8), the fp8 attention and Mamba blocks (attn_forward_fp8, attn_decode_fp8,
+// mamba_forward_fp8, mamba_decode_fp8), rmsnorm, and the allocator/sync entries.  Reference entries outside that
 // path exist with the reference's arity and raise NotImplementedError naming what is missing,
 // so a caller fails loudly instead of computing something else.
 #include <pybind11/pybind11.h>
@@ -44,8 +44,8 @@ const float* cf(uintptr_t p) { return reinterpret_cast<const float*>(p); }
 [[noreturn]] void not_built(const char* name) {
     std::string msg = std::string(name) +
                       " is not part of this build: nemotron_infer_amd implements the fp8 W8A16 linear hot "
-                      "path (linear_fp8, gemv_fp8), mlp_forward_fp8, attn_forward_fp8, attn_decode_fp8, mamba_decode_fp8 "
-                      "and rmsnorm only";
+                      "path (linear_fp8, gemv_fp8) and the fp8 blocks (mlp_forward_fp8, attn_forward_fp8, "
+                      "attn_decode_fp8, mamba_forward_fp8, mamba_decode_fp8) with rmsnorm only";
     PyErr_SetString(PyExc_NotImplementedError, msg.c_str());
     throw py::error_already_set();
 }
@@ -147,6 +147,26 @@ PYBIND11_MODULE(binding, m) {
         py::arg("v_w"), py::arg("v_s"), py::arg("o_w"), py::arg("o_s"), py::arg("out"), py::arg("S"),
         py::arg("k_cache"), py::arg("v_cache"), py::arg("cache_cap"));
 
+    // binding.cu:147-160 mamba_forward_fp8(input, block_norm_w, in_proj_w, in_proj_wscale, conv1d_w, conv1d_b,
+    // A_log, D, dt_bias, gnorm_w, out_proj_w, out_proj_wscale, out, B, S, conv_state_out, ssm_state_out):
+    // the final states are written when their pointers are non-zero.
+    m.def(
+        "mamba_forward_fp8",
+        [](uintptr_t input, uintptr_t norm_w, uintptr_t in_w, uintptr_t in_s, uintptr_t conv_w, uintptr_t conv_b,
+           uintptr_t A_log, uintptr_t D, uintptr_t dt_bias, uintptr_t gnorm_w, uintptr_t out_w, uintptr_t out_s,
+           uintptr_t out, int B, int S, uintptr_t conv_state_out, uintptr_t ssm_state_out) {
+            check(nmi_mamba_forward_fp8(cp(input), cf(norm_w), cp(in_w), cf(in_s), cf(conv_w), cf(conv_b), cf(A_log),
+                                        cf(D), cf(dt_bias), cf(gnorm_w), cp(out_w), cf(out_s), mp(out), B, S,
+                                        reinterpret_cast<float*>(conv_state_out),
+                                        reinterpret_cast<float*>(ssm_state_out), cfg::HIDDEN, cfg::H, cfg::P, cfg::G,
+                                        cfg::N, cfg::CONV_K, cfg::EPS, nullptr, 0, nullptr),
+                  "mamba_forward_fp8");
+        },
+        py::arg("input"), py::arg("block_norm_w"), py::arg("in_proj_w"), py::arg("in_proj_wscale"),
+        py::arg("conv1d_w"), py::arg("conv1d_b"), py::arg("A_log"), py::arg("D"), py::arg("dt_bias"),
+        py::arg("gnorm_w"), py::arg("out_proj_w"), py::arg("out_proj_wscale"), py::arg("out"), py::arg("B"),
+        py::arg("S"), py::arg("conv_state_out"), py::arg("ssm_state_out"));
+
     // binding.cu:162-175 mamba_decode_fp8(input, block_norm_w, in_proj_w, in_proj_wscale, conv1d_w,
     // conv1d_b, A_log, D, dt_bias, gnorm_w, out_proj_w, out_proj_wscale, conv_state, ssm_state, out,
     // B): states float32 [B, CONV_DIM, CONV_K - 1] and [B, H, P, N], updated in place.
@@ -182,10 +202,5 @@ PYBIND11_MODULE(binding, m) {
                             uintptr_t, int, int, uintptr_t) { not_built("attn_decode"); });
     m.def("mlp_forward", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, int) {
         not_built("mlp_forward");
-    });
-    m.def("mamba_forward_fp8", [](uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
-                                  uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
-                                  uintptr_t, int, int, uintptr_t, uintptr_t) {
-        not_built("mamba_forward_fp8");
     });
 }

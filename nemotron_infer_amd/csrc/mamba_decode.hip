@@ -183,6 +183,7 @@ __global__ __launch_bounds__(kGnThreads) void mamba_gated_norm_kernel(const Mamb
         }
     }
     // conv state of the group's B and C channels: [s0, s1, s2] -> [s1, s2, xBC]
+    if (!a.bc_state) return;
     const uint16_t* xbc = a.proj + (size_t)b * a.proj_ld + a.inter;
     for (int i = tid; i < 2 * kN; i += kGnThreads) {
         const int c = i < kN ? a.inter + grp * kN + i : a.inter + a.G * kN + grp * kN + (i - kN);
@@ -207,6 +208,11 @@ hipError_t launch_mamba_decode_mixer(const MambaDecodeArgs& a, int batch, hipStr
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(mamba_gated_norm_kernel, dim3(a.G, batch), dim3(kGnThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_mamba_gated_norm(const MambaDecodeArgs& a, int rows, hipStream_t stream) {
+    hipLaunchKernelGGL(mamba_gated_norm_kernel, dim3(a.G, rows), dim3(kGnThreads), 0, stream, a);
     return hipGetLastError();
 }
 

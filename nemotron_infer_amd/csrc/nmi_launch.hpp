@@ -211,9 +211,33 @@ struct MambaDecodeArgs {
     uint16_t* g;            // [batch, inter] bf16: gated-norm output (out_proj's input)
     int H, P, G, inter, conv_dim;
     float eps;
+    int bc_state;           // 1: the gated-norm kernel also shifts the B and C conv states (decode)
 };
 bool mamba_decode_supported(int H, int P, int G, int d_state, int conv_k);
 hipError_t launch_mamba_decode_mixer(const MambaDecodeArgs& a, int batch, hipStream_t stream);
+// The gated RMSNorm alone over `rows` rows of y and z (a.proj, row stride a.proj_ld).
+hipError_t launch_mamba_gated_norm(const MambaDecodeArgs& a, int rows, hipStream_t stream);
+
+// Mamba-2 mixer over prompts (mamba_prefill.hip): the causal conv1d + SiLU over each sequence
+// of S tokens, then the SSM scan from a zero state; the final states when the pointers are set.
+struct MambaPrefillArgs {
+    const uint16_t* proj;   // [batch * S, proj_ld] bf16: z | xBC | dt
+    int64_t proj_ld;
+    uint16_t* xc;           // [batch * S, xc_ld] bf16: conv outputs x | B | C
+    int64_t xc_ld;
+    const float* conv_w;    // [conv_dim, 4]
+    const float* conv_b;
+    const float* A_log;
+    const float* D;
+    const float* dt_bias;
+    float* conv_state;      // [batch, conv_dim, 3] or nullptr
+    float* ssm_state;       // [batch, H, P, 128] or nullptr
+    uint16_t* y;            // [batch * S, y_ld] bf16
+    int64_t y_ld;
+    int S, H, P, G, inter, conv_dim;
+    int x_vec, y_vec;       // 16-byte x reads / y stores possible (row strides and P multiples of 8)
+};
+hipError_t launch_mamba_prefill_mixer(const MambaPrefillArgs& a, int batch, hipStream_t stream);
 
 // Causal attention over a prompt (sdpa_prefill.hip), token-major q [S, ldq], k [S, ldk], o
 // [S, ldo] (head h at column 128 h), V through V^T [H_KV, 128, sdpa_prefill_vt_ld(S)] written by

@@ -503,6 +503,61 @@ def mamba_decode_fp8(x: torch.Tensor, norm_w: torch.Tensor, in_w, in_s, conv_w, 
     return out
 
 
+def mamba_forward_fp8(x: torch.Tensor, norm_w: torch.Tensor, in_w, in_s, conv_w, conv_b, A_log, D, dt_bias, gnorm_w,
+                      out_w, out_s, n_heads: int, head_dim: int, n_groups: int, batch: int = 1,
+                      conv_state_out: torch.Tensor | None = None, ssm_state_out: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None, eps: float = 1e-5, use_workspace: bool = True) -> torch.Tensor:
+    """The fp8 Mamba-2 block over prompts (model/mamba_block.cuh:346-425): x, out [batch * S,
+    hidden] bf16 (batch sequences of S tokens), each from a zero state; the final states go to
+    conv_state_out [batch, conv_dim, 3] / ssm_state_out [batch, n_heads, head_dim, 128] when given."""
+    x2 = _as_2d(x)
+    if not x2.is_contiguous() or x2.dtype != torch.bfloat16:
+        raise ValueError("x must be a contiguous bf16 tensor")
+    M, hidden = x2.shape
+    if batch < 1 or M % batch:
+        raise ValueError(f"{M} rows do not split into {batch} sequences")
+    S = M // batch
+    inter = n_heads * head_dim
+    conv_dim = inter + 2 * n_groups * 128
+    _check_f32(conv_w, (conv_dim, 4), "conv_w")
+    _check_f32(conv_b, (conv_dim,), "conv_b")
+    for name, t in (("A_log", A_log), ("D", D), ("dt_bias", dt_bias)):
+        _check_f32(t, (n_heads,), name)
+    _check_f32(gnorm_w, (inter,), "gnorm_w")
+    if conv_state_out is not None:
+        _check_f32(conv_state_out, (batch, conv_dim, 3), "conv_state_out")
+    if ssm_state_out is not None:
+        _check_f32(ssm_state_out, (batch, n_heads, head_dim, 128), "ssm_state_out")
+    in_w = _check_w(in_w, hidden)
+    if in_w.shape[0] != inter + conv_dim + n_heads:
+        raise ValueError(f"in_proj has {in_w.shape[0]} rows, expected {inter + conv_dim + n_heads}")
+    out_w = _check_w(out_w, inter)
+    if out_w.shape[0] != hidden:
+        raise ValueError(f"out_proj has {out_w.shape[0]} rows, hidden size is {hidden}")
+    _check_s(in_s, in_w.shape[0])
+    _check_s(out_s, hidden)
+    if norm_w.dtype != torch.float32 or tuple(norm_w.shape) != (hidden,) or not norm_w.is_contiguous():
+        raise ValueError(f"norm_w must be a contiguous float32 vector of {hidden} values")
+    if out is None:
+        out = torch.empty_like(x)
+    _check_out(out, M, hidden) if x.dim() == 2 else _check_out(out, 1, hidden)
+    _check_device(x2, norm_w, in_w, in_s, conv_w, conv_b, A_log, D, dt_bias, gnorm_w, out_w, out_s, out)
+    L = _lib.lib()
+    ws = None
+    if use_workspace:
+        ws = _block_ws(x.device, L.nmi_mamba_forward_workspace_bytes(batch, S, hidden, n_heads, head_dim, n_groups,
+                                                                     128))
+    rc = L.nmi_mamba_forward_fp8(x2.data_ptr(), norm_w.data_ptr(), in_w.data_ptr(), in_s.data_ptr(), conv_w.data_ptr(),
+                                 conv_b.data_ptr(), A_log.data_ptr(), D.data_ptr(), dt_bias.data_ptr(),
+                                 gnorm_w.data_ptr(), out_w.data_ptr(), out_s.data_ptr(), out.data_ptr(), batch, S,
+                                 None if conv_state_out is None else conv_state_out.data_ptr(),
+                                 None if ssm_state_out is None else ssm_state_out.data_ptr(), hidden, n_heads, head_dim,
+                                 n_groups, 128, 4, eps, None if ws is None else ws.data_ptr(),
+                                 0 if ws is None else ws.numel(), _stream())
+    _lib.check(rc, "nmi_mamba_forward_fp8")
+    return out
+
+
 class GemvChain:
     """The GEMVs of a decode step with as few launches as the dependencies allow
     (nmi_gemv_chain_*; M = 1).

@@ -1,6 +1,6 @@
-"""CPU oracle for nemotron_infer's Mamba-2 block at decode -- TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for nemotron_infer's Mamba-2 block (decode and prefill) -- TEST INFRASTRUCTURE ONLY.
 
-Restates on the CPU what the reference's decode path computes, so that the HIP kernels can be
+Restates on the CPU what the reference's Mamba block computes, so that the HIP kernels can be
 checked against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg use it.  bf16 tensors are uint16 bit patterns, as in ``oracle.linear``;
 every step is computed in float64 and rounded once where the reference rounds (to bf16 for
@@ -19,6 +19,12 @@ activations, float32 for states).
 * ``mamba_decode_block_fp8`` -- model/mamba_block.cuh:436-515: rmsnorm -> in_proj (one linear
   over all rows: [z | xBC | dt]) -> conv_step -> ssm_step on x | B | C -> gated_rmsnorm(y, z) ->
   out_proj -> residual add; returns out and the new states.
+* ``mamba_forward_block_fp8`` -- model/mamba_block.cuh:346-425 for one sequence of S tokens on
+  bf16 activations (the reference quantizes them to e4m3 into its GEMMs; this build does not):
+  rmsnorm -> in_proj -> ``conv_step`` token by token from a zero state (the prefill conv,
+  causal_conv1d.cuh:30-90) -> ``ssm_step`` token by token from a zero state (the recurrence the
+  chunked scan ssd_scan_chunked.cuh implements) -> gated_rmsnorm -> out_proj -> residual add;
+  returns out and the final states.
 * ``ssd_quadratic`` -- the definition the recurrence implements (the semiseparable form of
   tools/ref_full_model.py:66-118's chunked SSD, with zero initial state):
   y_t = sum_{s <= t} (C_t . B_s) exp(A sum_{s < r <= t} dt_r) dt_s x_s + D x_t, in float64.
@@ -27,7 +33,8 @@ Pinned in tests/test_oracle_mamba.py: t decode steps from zero state against ``s
 (a different algorithm: no recurrence) and against torch's ``F.conv1d`` with causal padding
 for the conv; the gated norm against torch's float32 restatement of HF's gated RMSNorm
 (ref_full_model.py:62-66) and closed forms; planted mistakes (a wrong group mapping, the decay
-applied after the input, silu missing from the gate) are caught.
+applied after the input, silu missing from the gate) are caught; the prefill block against
+token-by-token decode (outputs and final states identical).
 """
 from __future__ import annotations
 
@@ -147,3 +154,32 @@ def ssd_quadratic(x, Bm, Cm, dt, A_log, D, G):
             y[t] += (cb * decay * dt[s])[:, None] * x[s]
         y[t] += np.asarray(D, np.float64)[:, None] * x[t]
     return y
+
+
+def mamba_forward_block_fp8(x_bits, norm_w, in_codes, in_s, conv_w, conv_b, A_log, D, dt_bias, gnorm_w, out_codes,
+                            out_s, H, P, G, N, eps=1e-5, return_stages=False):
+    """One sequence x [S, hidden] bf16 bits.  Returns (out, conv_state [1, C, 3], ssm_state
+    [1, H, P, N]) (+ the stages)."""
+    x_bits = np.atleast_2d(np.asarray(x_bits, np.uint16))
+    S = x_bits.shape[0]
+    h = block.rmsnorm_bf16(x_bits, norm_w, eps)
+    proj = linear.linear_fp8_w8a16(h, in_codes, in_s)
+    z, xbc, dt = split_proj(proj, H, P, G, N)
+    inter = H * P
+    conv_dim = xbc.shape[1]
+    cs = np.zeros((1, conv_dim, 3), F32)
+    ss = np.zeros((1, H, P, N), F32)
+    xc = np.zeros_like(xbc)
+    y = np.zeros((S, inter), np.uint16)
+    for t in range(S):
+        o, cs = conv_step(xbc[t:t + 1], conv_w, conv_b, cs)
+        xc[t] = o[0]
+        yt, ss = ssm_step(o[:, :inter], o[:, inter:inter + G * N], o[:, inter + G * N:], dt[t:t + 1], A_log, D,
+                          dt_bias, ss, G)
+        y[t] = yt[0]
+    g = gated_rmsnorm(y, z, gnorm_w, G, eps)
+    mix = linear.linear_fp8_w8a16(g, out_codes, out_s)
+    out = block.add_bf16(x_bits, mix)
+    if return_stages:
+        return out, cs, ss, dict(normed=h, proj=proj, xconv=xc, y=y, g=g, mix=mix)
+    return out, cs, ss

@@ -118,7 +118,7 @@ def test_out_of_scope_entries_fail_loudly():
     with pytest.raises(NotImplementedError):
         B.mlp_forward(*([0] * 6))
     with pytest.raises(NotImplementedError):
-        B.mamba_forward_fp8(*([0] * 17))
+        B.mamba_forward(*([0] * 15))
 
 
 def test_binding_reports_validation_errors():

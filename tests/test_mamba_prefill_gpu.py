@@ -1,0 +1,173 @@
+"""GPU parity of the Mamba-2 block over prompts, nmi_mamba_forward_fp8
+(model/mamba_block.cuh:346-425: conv over the sequence, ops/mamba2/causal_conv1d.cuh:30-90;
+SSD scan, ops/mamba2/ssd_scan_chunked.cuh), at the model's dimensions (hidden 3136, 96 heads of
+80, 8 groups, state 128).
+
+Bars:
+* final conv state: bit-exact (the last three inputs of each channel, zero-padded).
+* y (the scan's output) and the final SSM state vs oracle.mamba run token by token in float64
+  from the GPU's own in_proj output: y to the parity gate; the state to rel_l2 <= 1e-4 and 1e-2
+  relative + 1e-4 absolute per element (conv outputs may differ by an ulp where float32 and
+  float64 SiLU round differently, moving what they feed slightly).
+* the block's output vs the oracle given the GPU's gated-norm output (out_proj + residual,
+  parity gate), and end to end rel_l2 <= 4e-3 over all elements.
+* the block vs the same prompt fed token by token through nmi_mamba_decode_fp8 from zero
+  states, and the next decode step from either's states: rel_l2 <= 4e-3 over all elements and
+  the final states within the state bar (the prefill's in_proj runs the GEMM kernels, the
+  decode's the GEMV, so their sums differ in order and their histories by rounding flips).
+"""
+import numpy as np
+import pytest
+import torch
+
+from nemotron_infer_amd import ops, synth
+from oracle import block, linear, mamba
+from tests.gpu_util import DEV, announce, bits, s_to_dev, w_to_dev, x_to_dev
+from tests.test_mamba_gpu import G, H, HIDDEN, INTER, N, P, PROJ, CONV_DIM, EPS, _bf16_np, _check_state, _params
+
+pytestmark = pytest.mark.gpu
+
+_W = {}
+
+
+def _weights():
+    if not _W:
+        iw, isc = synth.make_weight(PROJ, HIDDEN, 8500, "cpu")
+        ow, osc = synth.make_weight(HIDDEN, INTER, 8501, "cpu")
+        g = torch.Generator().manual_seed(8502)
+        _W.update(norm=(1.0 + 0.1 * torch.randn(HIDDEN, generator=g)).float().numpy(),
+                  inp=(iw.numpy(), isc.numpy()), out=(ow.numpy(), osc.numpy()), prm=_params(8503))
+    return _W
+
+
+def _dev(W):
+    p = {k: torch.from_numpy(v).to(DEV) for k, v in W["prm"].items()}
+    return (torch.from_numpy(W["norm"]).to(DEV), w_to_dev(W["inp"][0]), s_to_dev(W["inp"][1]), p["conv_w"],
+            p["conv_b"], p["A_log"], p["D"], p["dt_bias"], p["gnorm_w"], w_to_dev(W["out"][0]), s_to_dev(W["out"][1]))
+
+
+def _oracle_mixer_sequence(proj, prm):
+    """The scan and conv token by token from zero states on the GPU's proj: (y, conv, ssm)."""
+    S = proj.shape[0]
+    cs = np.zeros((1, CONV_DIM, 3), np.float32)
+    ss = np.zeros((1, H, P, N), np.float32)
+    ys = np.zeros((S, INTER), np.uint16)
+    for t in range(S):
+        y, _, cs, ss, _ = mamba.mixer_step(proj[t:t + 1], prm["conv_w"], prm["conv_b"], prm["A_log"], prm["D"],
+                                           prm["dt_bias"], prm["gnorm_w"], cs, ss, H, P, G, N, EPS)
+        ys[t] = y[0]
+    return ys, cs, ss
+
+
+@pytest.mark.parametrize("S", [1, 2, 3, 64, 65, 200])
+def test_mamba_forward_matches_oracle(S):
+    announce("mamba_forward", S)
+    W = _weights()
+    dw = _dev(W)
+    x = _bf16_np((S, HIDDEN), 8600 + S)
+    xd = x_to_dev(x)
+    cs = torch.full((1, CONV_DIM, 3), 5.0, device=DEV)
+    ss = torch.full((1, H, P, N), 5.0, device=DEV)
+    out = ops.mamba_forward_fp8(xd, *dw, H, P, G, conv_state_out=cs, ssm_state_out=ss, eps=EPS)
+    # stages through the library's separate calls: rmsnorm, in_proj
+    h = ops.rmsnorm_bf16(xd, dw[0], EPS)
+    proj = bits(ops.linear_fp8_w8a16(h, dw[1], dw[2], use_workspace=S >= 512))
+    torch.cuda.synchronize()
+    prm = W["prm"]
+    yr, csr, ssr = _oracle_mixer_sequence(proj, prm)
+    assert np.array_equal(cs.cpu().numpy(), csr), "conv state"
+    _check_state(ss.cpu().numpy(), ssr, f"ssm state S={S}")
+    # the block's own y is not exposed: check the gated norm + out_proj + residual on the oracle's
+    # y end to end, and the output stage-locally through a rerun that returns the stages
+    g_ref = mamba.gated_rmsnorm(yr, proj[:, :INTER], prm["gnorm_w"], G, EPS)
+    out_ref = block.add_bf16(x, linear.linear_fp8_w8a16(g_ref, *W["out"]))
+    r = linear.parity(bits(out), out_ref)
+    assert r["nan_ok"] and r["rel_l2_all"] <= 4e-3, ("from the GPU's proj", r)
+    full_ref, _, _ = mamba.mamba_forward_block_fp8(x, W["norm"], *W["inp"], prm["conv_w"], prm["conv_b"],
+                                                   prm["A_log"], prm["D"], prm["dt_bias"], prm["gnorm_w"], *W["out"],
+                                                   H, P, G, N, EPS)
+    r = linear.parity(bits(out), full_ref)
+    assert r["nan_ok"] and r["rel_l2_all"] <= 4e-3, ("end to end", r)
+
+
+def test_mamba_forward_scan_output_matches_oracle():
+    """The scan's output through the block itself: with out_proj replaced by a 0/1 selection of
+    the first 3136 columns (scale 1), out - input is the gated-norm output g (up to the final bf16
+    rounding of the sum), which is checked against the oracle's g from the oracle's scan on the
+    GPU's own in_proj output."""
+    S = 96
+    announce("mamba_forward_scan_output", S)
+    W = _weights()
+    dw = list(_dev(W))
+    sel = torch.zeros((HIDDEN, INTER), dtype=torch.float32)
+    sel[torch.arange(HIDDEN), torch.arange(HIDDEN)] = 1.0
+    dw[9] = sel.to(torch.float8_e4m3fn).view(torch.uint8).to(DEV)
+    dw[10] = torch.ones(HIDDEN, dtype=torch.float32, device=DEV)
+    x = _bf16_np((S, HIDDEN), 8700)
+    xd = x_to_dev(x)
+    out = ops.mamba_forward_fp8(xd, *dw, H, P, G, eps=EPS)
+    h = ops.rmsnorm_bf16(xd, dw[0], EPS)
+    proj = bits(ops.linear_fp8_w8a16(h, dw[1], dw[2], use_workspace=False))
+    torch.cuda.synchronize()
+    prm = W["prm"]
+    yr, _, _ = _oracle_mixer_sequence(proj, prm)
+    g_ref = mamba.gated_rmsnorm(yr, proj[:, :INTER], prm["gnorm_w"], G, EPS)[:, :HIDDEN]
+    xf = linear.bf16_to_f32(x).astype(np.float64)
+    got_g = linear.bf16_to_f32(bits(out)).astype(np.float64) - xf
+    ref = linear.bf16_to_f32(block.add_bf16(x, g_ref)).astype(np.float64) - xf
+    rel = np.linalg.norm(got_g - ref) / np.linalg.norm(ref)
+    assert rel <= 4e-3, rel
+
+
+def test_mamba_forward_batch_and_decode_continuation():
+    """Two sequences in one call equal two single-sequence calls (outputs and states); then
+    decode steps continue from the prefill's states as they would from a token-by-token
+    decode of the same prompt."""
+    from nemotron_infer_amd.csrc import binding as B
+
+    announce("mamba_forward_batch_decode")
+    W = _weights()
+    dw = _dev(W)
+    S = 40
+    x = _bf16_np((2 * S, HIDDEN), 8800)
+    xd = x_to_dev(x)
+    cs = torch.zeros((2, CONV_DIM, 3), device=DEV)
+    ss = torch.zeros((2, H, P, N), device=DEV)
+    both = ops.mamba_forward_fp8(xd, *dw, H, P, G, batch=2, conv_state_out=cs, ssm_state_out=ss, eps=EPS)
+    for b in range(2):
+        cs1 = torch.zeros((1, CONV_DIM, 3), device=DEV)
+        ss1 = torch.zeros((1, H, P, N), device=DEV)
+        one = ops.mamba_forward_fp8(xd[b * S:(b + 1) * S].contiguous(), *dw, H, P, G, conv_state_out=cs1,
+                                    ssm_state_out=ss1, eps=EPS)
+        torch.cuda.synchronize()
+        assert torch.equal(one.view(torch.int16), both[b * S:(b + 1) * S].view(torch.int16)), b
+        assert torch.equal(cs1[0], cs[b]) and torch.equal(ss1[0], ss[b]), b
+    # binding form of sequence 0 (in place, bump allocator), then decode from its states vs decode
+    # from token-by-token states
+    xi = xd[:S].clone()
+    cs_b = torch.zeros((1, CONV_DIM, 3), device=DEV)
+    ss_b = torch.zeros((1, H, P, N), device=DEV)
+    B.reset_allocator()
+    B.mamba_forward_fp8(xi.data_ptr(), *[t.data_ptr() for t in dw], xi.data_ptr(), 1, S, cs_b.data_ptr(),
+                        ss_b.data_ptr())
+    B.sync()
+    assert torch.equal(xi.view(torch.int16), both[:S].view(torch.int16))
+    cs_t = torch.zeros((1, CONV_DIM, 3), device=DEV)
+    ss_t = torch.zeros((1, H, P, N), device=DEV)
+    outs_t = [ops.mamba_decode_fp8(xd[t:t + 1].contiguous(), *dw, cs_t, ss_t, H, P, G, eps=EPS) for t in range(S)]
+    torch.cuda.synchronize()
+    dec = bits(torch.cat(outs_t))
+    r = linear.parity(dec, bits(both[:S]))
+    assert r["nan_ok"] and r["rel_l2_all"] <= 4e-3, ("prefill vs token-by-token decode", r)
+    # conv states hold in_proj outputs, which the two paths (GEMV at decode, GEMM here) round alike
+    # but for rare one-ulp flips
+    diff = (cs_t != cs_b).sum().item()
+    assert diff <= max(2, 1e-3 * cs_t.numel()), diff
+    assert torch.allclose(cs_t, cs_b, rtol=1e-2, atol=1e-6)
+    _check_state(ss_b.cpu().numpy(), ss_t.cpu().numpy(), "ssm state prefill vs decode")
+    xn = x_to_dev(_bf16_np((1, HIDDEN), 8801))
+    a1 = ops.mamba_decode_fp8(xn, *dw, cs_b, ss_b, H, P, G, eps=EPS)
+    a2 = ops.mamba_decode_fp8(xn, *dw, cs_t, ss_t, H, P, G, eps=EPS)
+    torch.cuda.synchronize()
+    r = linear.parity(bits(a1), bits(a2))
+    assert r["nan_ok"] and r["rel_l2_all"] <= 4e-3, ("next decode step", r)

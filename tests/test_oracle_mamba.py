@@ -194,3 +194,33 @@ def test_block_matches_a_float32_torch_step():
     assert rel < 2e-2, rel
     np.testing.assert_allclose(ss2[0], S.numpy(), rtol=3e-2, atol=3e-3)
     assert np.array_equal(cs2[0, :, :2], cs[0, :, 1:])
+
+
+def test_forward_block_continues_like_decode_steps():
+    """The prefill block over S tokens leaves the states S decode steps from zero would: its
+    final states equal those of the decode oracle run token by token, and its outputs equal the
+    decode outputs of each token (the block is per-token at decode, per-sequence at prefill)."""
+    H, P, G, N, hidden = 4, 8, 2, 16, 64
+    inter, conv_dim = H * P, H * P + 2 * G * N
+    rng = np.random.default_rng(9)
+
+    def wq(rows, cols):
+        wf = rng.standard_normal((rows, cols)).astype(F32) * 0.1
+        s = np.full(rows, np.abs(wf).max() / 448, F32)
+        codes = torch.from_numpy(wf / s[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        return codes, s
+
+    S = 7
+    x = bf16(rng.standard_normal((S, hidden)))
+    nw = (1 + 0.1 * rng.standard_normal(hidden)).astype(F32)
+    inw, outw = wq(inter + conv_dim + H, hidden), wq(hidden, inter)
+    prm = (rng.standard_normal((conv_dim, 4)).astype(F32) * 0.3, rng.standard_normal(conv_dim).astype(F32) * 0.1,
+           rng.uniform(-1, 1, H).astype(F32), rng.standard_normal(H).astype(F32),
+           rng.standard_normal(H).astype(F32) * 0.1, (1 + 0.1 * rng.standard_normal(inter)).astype(F32))
+    out, cs, ss = mamba.mamba_forward_block_fp8(x, nw, *inw, *prm, *outw, H, P, G, N)
+    cs_d = np.zeros((1, conv_dim, 3), F32)
+    ss_d = np.zeros((1, H, P, N), F32)
+    for t in range(S):
+        o, cs_d, ss_d = mamba.mamba_decode_block_fp8(x[t:t + 1], nw, *inw, *prm, *outw, cs_d, ss_d, H, P, G, N)
+        assert np.array_equal(o[0], out[t]), t
+    assert np.array_equal(cs, cs_d) and np.array_equal(ss, ss_d)
