@@ -179,10 +179,10 @@ int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int6
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Device-side e4m3 decode of `n` codes through the kernels' own conversion helpers:
- * out_f32[i] = float(e4m3(codes[i])) (the GEMV's decode), out_scaled[i] = out_f32[i] * scale
- * (f32 RNE product, as in the GEMV epilogue), out_bf16[i] = bf16(e4m3(codes[i])) (the GEMM's
- * weight-tile dequant; exact).  Test entry point for the 256-code bit-exact check; mirrors
+ * Device-side e4m3 decode of `n` codes through the kernels' own conversion helper (e4m3 ->
+ * bf16, exact; every GEMV and MFMA kernel decodes weights this way): out_bf16[i] =
+ * bf16(e4m3(codes[i])), out_f32[i] = that value widened to float (exact), out_scaled[i] =
+ * out_f32[i] * scale (f32 RNE product, as in the reference's GEMV epilogue).  Test entry point for the 256-code bit-exact check; mirrors
  * static_cast<float>(__nv_fp8_e4m3) (ops/gemv.cuh:40-42) and the per-row scale product of
  * the epilogue (ops/gemv.cuh:87-88).  n must be a positive multiple of 4; codes 4-byte,
  * out_f32/out_scaled 16-byte and out_bf16 8-byte aligned.

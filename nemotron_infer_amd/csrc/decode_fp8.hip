@@ -1,10 +1,10 @@
 // decode_fp8.hip -- device-side e4m3 decode through the kernels' own conversion helpers.
 //
-// Test entry for the 256-code bit-exact check: every code goes through e4m3x4_to_f32 (the
-// GEMV's decode, v_cvt_pk_f32_fp8) and e4m3x4_to_bf16 (the GEMM's weight-tile dequant,
-// v_cvt_scalef32_pk_bf16_fp8), with the code at each of the four byte positions of a dword
-// as the kernels see it.  out_scaled = decode * scale is the float32 product the GEMV
-// epilogue forms before rounding (ops/gemv.cuh:87-88 in the reference).
+// Test entry for the 256-code bit-exact check: every code goes through e4m3x4_to_bf16
+// (v_cvt_scalef32_pk_bf16_fp8, the decode of every GEMV and MFMA kernel here), with the code at
+// each of the four byte positions of a dword as the kernels see it; out_f32 is that bf16 value
+// widened (exact).  out_scaled = decode * scale is the float32 product of the reference's GEMV
+// epilogue (ops/gemv.cuh:87-88).
 #include "nmi_device.hpp"
 #include "nmi_launch.hpp"
 
@@ -20,10 +20,10 @@ __global__ __launch_bounds__(256) void decode_e4m3_kernel(const uint32_t* __rest
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nwords) return;
     const uint32_t w = codes[i];
-    const f32x4 f = e4m3x4_to_f32(w);
-    reinterpret_cast<float4*>(out_f32)[i] = float4{f.x, f.y, f.z, f.w};
-    reinterpret_cast<float4*>(out_scaled)[i] = float4{f.x * scale, f.y * scale, f.z * scale, f.w * scale};
     const uint2 b = e4m3x4_to_bf16(w);
+    const float4 f{bf16lo_to_f32(b.x), bf16hi_to_f32(b.x), bf16lo_to_f32(b.y), bf16hi_to_f32(b.y)};
+    reinterpret_cast<float4*>(out_f32)[i] = f;
+    reinterpret_cast<float4*>(out_scaled)[i] = float4{f.x * scale, f.y * scale, f.z * scale, f.w * scale};
     reinterpret_cast<uint2*>(out_bf16)[i] = b;
 }
 

@@ -1,10 +1,10 @@
 // nmi_device.hpp -- gfx950 (CDNA4) device helpers shared by the fp8 W8A16 kernels.
 //
-// * e4m3 -> f32 decode through v_cvt_pk_f32_fp8 (OCP E4M3 on gfx950), four codes per dword,
-//   byte b of the dword -> element b.  This is the value static_cast<float>(__nv_fp8_e4m3)
-//   gives in the reference (nemotron_infer/csrc/include/ops/gemv.cuh:40-42).
-// * e4m3 -> bf16 decode through v_cvt_scalef32_pk_bf16_fp8 with scale 1.0; every e4m3 value is
-//   exactly representable in bf16, so this is exact (used to stage weight tiles for MFMA).
+// * e4m3 -> bf16 decode through v_cvt_scalef32_pk_bf16_fp8 with scale 1.0 (OCP E4M3 on gfx950),
+//   four codes per dword, byte b -> element b.  Every e4m3 value is exactly representable in
+//   bf16, so this is the value static_cast<float>(__nv_fp8_e4m3) gives in the reference
+//   (nemotron_infer/csrc/include/ops/gemv.cuh:40-42) and the only decode the kernels use: the
+//   GEMVs feed the pairs to v_dot2_f32_bf16, the MFMA kernels to their bf16 operands.
 // * bf16 -> f32 by shifting the bit pattern; f32 -> bf16 round-to-nearest-even through
 //   v_cvt_pk_bf16_f32 (the conversion __float2bfloat16_rn performs in gemv.cuh:88).
 // * a 16-lane sum that uses DPP row operations (quad_perm, row_half_mirror, row_mirror), and
@@ -23,13 +23,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-// Four e4m3 codes packed little-endian in `w` -> four floats.
-__device__ __forceinline__ f32x4 e4m3x4_to_f32(uint32_t w) {
-    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);  // bytes 0, 1
-    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);   // bytes 2, 3
-    return f32x4{lo.x, lo.y, hi.x, hi.y};
-}
 
 // Four e4m3 codes -> four bf16 (two packed dwords), exact.
 __device__ __forceinline__ uint2 e4m3x4_to_bf16(uint32_t w) {
