@@ -2,7 +2,7 @@
 """bench.py -- fp8 (e4m3) W8A16 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--no-extras]
-                    [--only stream|decode|prefill|block|skinny]
+                    [--only stream|decode|prefill|prefill_small|block|skinny|attn|mamba|engine|prefill_attn|prefill_mamba]
 
 Headline (``value``): BASELINE config 4, the full decode-step weight stream at M = 1 -- 4
 attention layers (q|k|v grouped: they share one normed input, model/attention_block.cuh:400-402;
@@ -65,7 +65,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extras", action="store_true", help="headline, roofline and CPU baseline only")
-    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn", "mamba", "engine", "prefill_attn", "prefill_mamba"],
+    p.add_argument("--only", choices=["stream", "decode", "prefill", "block", "skinny", "attn", "mamba", "engine", "prefill_attn", "prefill_mamba",
+                                       "prefill_small"],
                    help="run one extra leg alone and print its JSON record (for profiling that leg); "
                         "not the bench contract line")
     p.add_argument("--pmc-calibration", action="store_true",
@@ -279,6 +280,49 @@ def bench_prefill(dev, reps=20):
     return {"workload": "config3_prefill_m2048", "tflops": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_dma_kernel (4 waves, 256x256 tiles, DMA-fed LDS; stream-K when tiles < CUs / 2)",
             "shapes": out}
+
+
+def bench_prefill_small_m(dev, reps=20):
+    """Short prompts: the three config-3 shapes at M = 64, 128, 256 (the GEMM path below the
+    256x256 DMA kernel's M >= 512).  Weights rotated over copies of >= 1 GiB, since at these M
+    the launch also streams W (the arithmetic intensity is about 2M flop/B, below MI355X's
+    ~315 flop/B ridge up to M ~ 150)."""
+    import torch
+
+    from nemotron_infer_amd import ops, synth
+
+    T = Timer()
+    set_bytes = sum(l.N * l.K for l in synth.PREFILL_SET)
+    R = max(2, math.ceil(ROTATION_BYTES / set_bytes))
+    ws = [synth.make_weight(l.N, l.K, 3000 + i, dev) for i, l in enumerate(synth.PREFILL_SET)]
+    copies = [[(w.clone(), s.clone()) for (w, s) in ws] for _ in range(R)]
+    del ws
+    res = {}
+    for M in (64, 128, 256):
+        shapes = {}
+        tot_f = tot_b = tot_ms = 0.0
+        for i, lin in enumerate(synth.PREFILL_SET):
+            x = synth.make_act(M, lin.K, 3200 + M + i, dev, kind=lin.act)
+            y = torch.empty((M, lin.N), dtype=torch.bfloat16, device=dev)
+            calls = [lambda r=r: ops.gemm_fp8_w8a16(x, copies[r][i][0], copies[r][i][1], out=y) for r in range(R)]
+            for c in calls:
+                c()
+            g = T.capture(lambda: [c() for c in calls])
+            steady(T, g, 0.1)
+            n = max(1, reps // R)
+            d = T.time_replays([g] * n) / (n * R)
+            fl = synth.linear_flops(M, lin.N, lin.K)
+            by = synth.linear_bytes(M, lin.N, lin.K)
+            shapes[lin.name] = {"us": round(d * 1e3, 2), "TFLOP/s": round(fl / (d * 1e-3) / 1e12, 1),
+                                "GB/s": round(by / (d * 1e-3) / 1e9, 1)}
+            tot_f += fl
+            tot_b += by
+            tot_ms += d
+            del g, calls, x, y
+        res[f"M={M}"] = {"TFLOP/s": round(tot_f / (tot_ms * 1e-3) / 1e12, 1),
+                         "GB/s": round(tot_b / (tot_ms * 1e-3) / 1e9, 1), "shapes": shapes}
+    del copies
+    return {"workload": "config3 shapes at short-prompt M", "weight_copies_rotated": R, "results": res}
 
 
 def bench_skinny(dev, host, reps=20):
@@ -851,6 +895,8 @@ def main():
             leg = bench_attn_prefill(dev)
         elif args.only == "prefill_mamba":
             leg = bench_mamba_prefill(dev)
+        elif args.only == "prefill_small":
+            leg = bench_prefill_small_m(dev)
         elif args.only == "engine":
             leg = bench_engine_decode(dev)
         else:
@@ -869,6 +915,8 @@ def main():
         log("prefill GEMM (config 3) ...")
         extras["prefill_gemm"] = bench_prefill(dev)
         log(f"prefill: {extras['prefill_gemm']['tflops']} TFLOP/s")
+        extras["prefill_small_m"] = bench_prefill_small_m(dev)
+        log(f"prefill small M: { {k: v['TFLOP/s'] for k, v in extras['prefill_small_m']['results'].items()} }")
         log("skinny M (config 2) ...")
         extras["skinny"] = bench_skinny(dev, host)
         log("mlp block ...")

@@ -160,10 +160,13 @@ int nmi_gemv_chain_destroy(nmi_gemv_chain* chain);
 
 /* Workspace bytes the kernels can use for M rows, total_n output rows (the sum over groups)
  * and K on the current device; 0 when the selected kernel needs none (the GEMV, the default
- * 4x4x4 skinny kernel, which splits K inside the workgroup only, and M < 512).  With the 4x4x4
- * kernel's K split (s4.kg > 1): 64 KiB of arrival counters and the fp32 partials,
- * s4.kg x M x total_n x 4 bytes (fewer K groups when K has fewer windows).  For M >= 512
- * about 64 MiB: a 64 KiB flag region and one 256 x 256 fp32 partial tile per CU. */
+ * 4x4x4 skinny kernel, which splits K inside the workgroup only).  With the 4x4x4 kernel's K
+ * split (s4.kg > 1): 64 KiB of arrival counters and the fp32 partials, s4.kg x M x total_n x 4
+ * bytes (fewer K groups when K has fewer windows).  For 17 <= M < 512 (the short-prompt GEMM) a
+ * 64 KiB region it leaves alone, then the fp32 partials of its K split (0 when the schedule does
+ * not split K).  For M >= 512 about 64 MiB: a 64 KiB flag region and one 256 x 256 fp32 partial
+ * tile per CU.  Every kernel leaves the first 64 KiB as it found it (zero at rest), so one
+ * zero-filled workspace serves every M in turn. */
 size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K);
 
 /*
@@ -216,8 +219,9 @@ int nmi_rmsnorm_bf16(const void* x_bf16, const float* w, void* y_bf16, int M, in
  * RMSNorm applied while the up projection stages its activations, relu^2 and the residual add
  * in the projections' stores), larger M three (a separate RMSNorm).
  * workspace: nmi_mlp_workspace_bytes(M, hidden, inter) bytes, 16-byte aligned, no
- * initialisation needed (from M = 512 it includes the GEMMs' stream-K region, whose flags each
- * call zeroes with one small kernel); calls that may overlap in time need distinct workspaces.  NULL
+ * initialisation needed (for 17 <= M < 512 it includes the short-prompt GEMMs' K-split partials;
+ * from M = 512 the GEMMs' stream-K region, whose flags each call zeroes with one small kernel);
+ * calls that may overlap in time need distinct workspaces.  NULL
  * takes it from the bump allocator (nmi_alloc, so a slab may be hipMalloc'd), valid until
  * nmi_alloc_rewind(), as the reference's blocks do (binding.cu:7-9).
  * Requires M >= 1, hidden and inter positive multiples of 16, input, norm_w and both weights
@@ -229,13 +233,16 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
                         int inter, float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * nmi_mlp_forward_fp8 without any allocation: the same block and result (bit for bit), with
- * the transient buffers in a file-scope device array of nmi_mlp_noalloc_scratch_bytes() bytes
- * (4 MiB) that each GPU the library runs on holds until the process ends.  No counterpart in
- * the reference: for callers that cannot allocate (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc).  Calls no hipMalloc / hipFree.  Needs
- * nmi_mlp_workspace_bytes(M, hidden, inter) <= the array's size (hidden 3136, inter 12544:
- * M <= 133), else NMI_ERR_WORKSPACE.  Every call on a GPU shares that GPU's array: calls that
+ * nmi_mlp_forward_fp8 without any allocation: the same block, with the transient buffers in a
+ * file-scope device array of nmi_mlp_noalloc_scratch_bytes() bytes (4 MiB) that each GPU the
+ * library runs on holds until the process ends.  No counterpart in the reference: for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Calls no hipMalloc / hipFree.  The result equals nmi_mlp_forward_fp8's bit for
+ * bit for M <= 16; for 17 <= M the short-prompt GEMMs run without their K split (whose partials
+ * would not fit), so the two agree up to float32 summation order (bit for bit with tuning knob
+ * gemm.splits = 1).  Needs the block's buffers without the split partials (M * inter * 2 bytes,
+ * plus M * hidden * 2 for M > 2, each rounded up to 256) within the array (hidden 3136, inter
+ * 12544: M <= 133), else NMI_ERR_WORKSPACE.  Every call on a GPU shares that GPU's array: calls that
  * may overlap in time on one GPU (other streams, other threads) race.  Same argument
  * requirements as nmi_mlp_forward_fp8.
  */
@@ -394,7 +401,9 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
  * GEMV kernel (M = 2, or M = 1 with "gemv.multirow" = 1), "gemv.t" = 4 also 4 rows per step for
  * the M = 1 stream kernel, "gemv.wgs": its workgroups per CU (1, 2), "gemv.grid": its exact
  * workgroup count, "gemv.balance": 2 keeps the plain grid instead of one whose waves get equal row
- * counts, "sdpa.chunk": cache positions per workgroup of the attention decode, "gemm.tile", "gemm.sk",
+ * counts, "sdpa.chunk": cache positions per workgroup of the attention decode, "gemm.tile" (1, 2:
+ * short-prompt kernel, 20, 21, 24), "gemm.sk", "gemm.splits": workgroups splitting K in the
+ * short-prompt GEMM (1: none), "gemm.short": 1 selects its forms with 128 weight rows per workgroup,
  * "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
  * "s4.dma": 2 selects the windowed form of the 4x4x4 skinny kernel instead of the pipelined one,
  * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace

@@ -9,6 +9,7 @@
 // split, and the o GEMV with the residual add in its stores -- three or four launches.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "nmi_fp8_linear.h"
@@ -75,13 +76,19 @@ struct FwdLayout {
     size_t gemm, normed, q, k, v, o, vt, total;
 };
 
-size_t gemm_region(int M) { return choose_path(M) == Path::Gemm ? round256(gemm_workspace_bytes(M)) : 0; }
+// The GEMMs' region (stream-K flags and partials from M = 512, the short-prompt kernel's K-split
+// partials below): the largest of the q, k, v (launched one by one on the GEMM path) and o needs.
+size_t gemm_region(int M, int hidden, int QD, int KD) {
+    if (choose_path(M) != Path::Gemm) return 0;
+    return round256(std::max(std::max(linear_workspace_bytes(M, QD, hidden), linear_workspace_bytes(M, KD, hidden)),
+                             linear_workspace_bytes(M, hidden, QD)));
+}
 
 FwdLayout fwd_layout(int S, int hidden, int n_heads, int n_kv) {
     FwdLayout L{};
     const size_t QD = (size_t)n_heads * kSdpaHead, KD = (size_t)n_kv * kSdpaHead;
     L.gemm = 0;
-    L.normed = L.gemm + gemm_region(S);
+    L.normed = L.gemm + gemm_region(S, hidden, (int)QD, (int)KD);
     L.q = L.normed + round256((size_t)S * hidden * 2);
     L.k = L.q + round256((size_t)S * QD * 2);
     L.v = L.k + round256((size_t)S * KD * 2);
@@ -201,7 +208,7 @@ int nmi_attn_forward_fp8(const void* input_bf16, const float* norm_w, const void
     uint16_t* o = reinterpret_cast<uint16_t*>(base + lay.o);
     uint16_t* vt = reinterpret_cast<uint16_t*>(base + lay.vt);
     hipError_t e = hipSuccess;
-    if (gws) e = launch_sk_flags_clear(gemm_ws, st);   // the workspace may hold anything
+    if (gws && gemm_workspace_has_flags(S)) e = launch_sk_flags_clear(gemm_ws, st);   // the workspace may hold anything
     if (e != hipSuccess) return hip_status(e, fn);
     // q, k, v of the normed input
     GemvGroup qkv[3] = {

@@ -7,11 +7,13 @@
 // ride on the linears: relu^2 and the residual add are output epilogues of the up and down
 // projections, and where the up projection runs on the GEMV kernel (M <= 2) the RMSNorm is
 // applied while that kernel stages its activations -- two launches and one [M, inter] buffer.
-// For larger M the RMSNorm is its own launch (rmsnorm.hip) into a second buffer, and from
-// M = 512 (the GEMM path) the workspace also holds the GEMMs' stream-K region, whose flags one
-// small kernel zeroes at the start of every call.
+// For larger M the RMSNorm is its own launch (rmsnorm.hip) into a second buffer.  On the GEMM
+// path (M > 16) the workspace also holds the GEMMs' region: from M = 512 the stream-K flags and
+// partial tiles, whose flags one small kernel zeroes at the start of every call; below, the
+// short-prompt kernel's K-split partials (which need no initialisation).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "nmi_fp8_linear.h"
@@ -32,6 +34,11 @@ int hip_status(hipError_t e, const char* what) {
     return (int)e;
 }
 
+int fail2(int code, const char* fn, const char* msg) {
+    set_last_error("%s: %s", fn, msg);
+    return code;
+}
+
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -41,10 +48,15 @@ size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 // projection.
 bool norm_fused(int M, int hidden) { return choose_path(M) == Path::Gemv && gemv_norm_supported(M, hidden); }
 
-size_t gemm_region(int M) { return choose_path(M) == Path::Gemm ? round256(gemm_workspace_bytes(M)) : 0; }
+// split = false leaves the short-prompt GEMMs unsplit (no partial region): the allocation-free
+// form, whose buffers must fit a fixed array
+size_t gemm_region(int M, int hidden, int inter, bool split) {
+    if (choose_path(M) != Path::Gemm || (!split && !gemm_workspace_has_flags(M))) return 0;
+    return round256(std::max(linear_workspace_bytes(M, inter, hidden), linear_workspace_bytes(M, hidden, inter)));
+}
 
-size_t mlp_bytes(int M, int hidden, int inter) {
-    size_t b = gemm_region(M) + round256((size_t)M * inter * 2);
+size_t mlp_bytes(int M, int hidden, int inter, bool split) {
+    size_t b = gemm_region(M, hidden, inter, split) + round256((size_t)M * inter * 2);
     if (!norm_fused(M, hidden)) b += round256((size_t)M * hidden * 2);
     return b;
 }
@@ -69,28 +81,43 @@ int nmi_rmsnorm_bf16(const void* x_bf16, const float* w, void* y_bf16, int M, in
 
 size_t nmi_mlp_workspace_bytes(int M, int hidden, int inter) {
     if (M < 1 || hidden < 16 || inter < 16) return 0;
-    return mlp_bytes(M, hidden, inter);
+    return mlp_bytes(M, hidden, inter, true);
 }
 
 int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void* up_w_e4m3, const float* up_scale,
                         const void* down_w_e4m3, const float* down_scale, void* out_bf16, int M, int hidden,
                         int inter, float eps, void* workspace, size_t workspace_bytes, void* stream) {
-    const char* fn = "nmi_mlp_forward_fp8";
+    return mlp_forward_fp8(input_bf16, norm_w, up_w_e4m3, up_scale, down_w_e4m3, down_scale, out_bf16, M, hidden,
+                           inter, eps, workspace, workspace_bytes, stream, true, "nmi_mlp_forward_fp8");
+}
+
+}  // extern "C"
+
+namespace nmi {
+
+size_t mlp_workspace_bytes(int M, int hidden, int inter, bool split) {
+    if (M < 1 || hidden < 16 || inter < 16) return 0;
+    return mlp_bytes(M, hidden, inter, split);
+}
+
+int mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void* up_w_e4m3, const float* up_scale,
+                    const void* down_w_e4m3, const float* down_scale, void* out_bf16, int M, int hidden, int inter,
+                    float eps, void* workspace, size_t workspace_bytes, void* stream, bool split, const char* fn) {
     if (!input_bf16 || !norm_w || !up_w_e4m3 || !up_scale || !down_w_e4m3 || !down_scale || !out_bf16)
-        return fail(NMI_ERR_INVALID_ARG, "nmi_mlp_forward_fp8: NULL pointer argument");
+        return fail2(NMI_ERR_INVALID_ARG, fn, "NULL pointer argument");
     if (M < 1 || hidden < 16 || hidden % 16 != 0 || inter < 16 || inter % 16 != 0) {
         set_last_error("%s: M=%d hidden=%d inter=%d (need M >= 1, hidden and inter positive multiples of 16)",
                        fn, M, hidden, inter);
         return NMI_ERR_INVALID_ARG;
     }
     if (!aligned(input_bf16, 16) || !aligned(norm_w, 16) || !aligned(up_w_e4m3, 16) || !aligned(down_w_e4m3, 16))
-        return fail(NMI_ERR_ALIGNMENT, "nmi_mlp_forward_fp8: input, norm_w and the weights must be 16-byte aligned");
+        return fail2(NMI_ERR_ALIGNMENT, fn, "input, norm_w and the weights must be 16-byte aligned");
     if (!aligned(up_scale, 4) || !aligned(down_scale, 4) || !aligned(out_bf16, 2))
-        return fail(NMI_ERR_ALIGNMENT, "nmi_mlp_forward_fp8: misaligned scale or output");
-    const size_t need = mlp_bytes(M, hidden, inter);
+        return fail2(NMI_ERR_ALIGNMENT, fn, "misaligned scale or output");
+    const size_t need = mlp_bytes(M, hidden, inter, split);
     if (workspace) {
         if (!aligned(workspace, 16))
-            return fail(NMI_ERR_ALIGNMENT, "nmi_mlp_forward_fp8: workspace must be 16-byte aligned");
+            return fail2(NMI_ERR_ALIGNMENT, fn, "workspace must be 16-byte aligned");
         if (workspace_bytes < need) {
             set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
             return NMI_ERR_WORKSPACE;
@@ -103,11 +130,11 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
     const uint16_t* in = static_cast<const uint16_t*>(input_bf16);
     uint16_t* out = static_cast<uint16_t*>(out_bf16);
     char* base = static_cast<char*>(workspace);
-    const size_t gws = gemm_region(M);
-    void* gemm_ws = gws ? base : nullptr;        // the GEMMs' stream-K flags and partial tiles
+    const size_t gws = gemm_region(M, hidden, inter, split);
+    void* gemm_ws = gws ? base : nullptr;        // the GEMMs' stream-K region or K-split partials
     uint16_t* act = reinterpret_cast<uint16_t*>(base + gws);
     const Norm norm{norm_w, eps};
-    if (gws) {
+    if (gws && gemm_workspace_has_flags(M)) {
         // the workspace may hold anything (bump-allocated or reused): zero the flag region
         const hipError_t ez = launch_sk_flags_clear(gemm_ws, st);
         if (ez != hipSuccess) return hip_status(ez, fn);
@@ -131,4 +158,4 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
     return hip_status(dispatch_linear(act, inter, M, inter, &down, 1, gemm_ws, gws, st), fn);
 }
 
-}  // extern "C"
+}  // namespace nmi

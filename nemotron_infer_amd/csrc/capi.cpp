@@ -6,6 +6,7 @@
 // fp8 blocks do (model/mlp_block.cuh:142: M == 1 -> GEMV, otherwise GEMM).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -96,6 +97,22 @@ Tuning& tuning() {
 }  // namespace nmi
 
 namespace nmi {
+
+size_t linear_workspace_bytes(int M, int64_t total_n, int K) {
+    if (M < 1 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
+    const int t = tuning().gemm_tile;
+    if (M > 16 && M < 512)                            // the short-prompt kernel's K-split partials
+        return (t == 0 || t == 2) ? gemm_short_workspace_bytes(M, (int)std::min<int64_t>(total_n, 1 << 30), K) : 0;
+    if (M > 16) return gemm_workspace_bytes(M);       // stream-K flags and partials of the GEMM
+    // the split-K 16x16x32 kernel ("skinny.path" = 1, or "m1.path" = 2 for M = 1) and the K
+    // split of the 4x4x4 kernel's pipelined form use a workspace
+    const Path path = choose_path(M);
+    if (path == Path::Skinny) return skinny_workspace_bytes(M, K, total_n, device_info().num_cu);
+    if (path == Path::Skinny4) return skinny4_workspace_bytes(M, K, total_n, device_info().num_cu);
+    return 0;
+}
+
+bool gemm_workspace_has_flags(int M) { return M >= 512 && choose_path(M) == Path::Gemm; }
 
 // M == 1 -> GEMV kernel, M == 2 -> GEMV kernel (measured faster than the MFMA kernels there),
 // M <= 16 -> 4x4x4 MFMA skinny kernel, M > 16 -> MFMA GEMM.
@@ -316,16 +333,7 @@ int nmi_gemv_chain_destroy(nmi_gemv_chain* chain) {
     return hip_status(e, "nmi_gemv_chain_destroy");
 }
 
-size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) {
-    if (M < 1 || K < 16 || K % 16 != 0 || total_n < 1) return 0;
-    if (M > 16) return gemm_workspace_bytes(M);       // stream-K partials of the GEMM
-    // the split-K 16x16x32 kernel ("skinny.path" = 1, or "m1.path" = 2 for M = 1) and the K
-    // split of the 4x4x4 kernel's pipelined form use a workspace
-    const Path path = choose_path(M);
-    if (path == Path::Skinny) return skinny_workspace_bytes(M, K, total_n, device_info().num_cu);
-    if (path == Path::Skinny4) return skinny4_workspace_bytes(M, K, total_n, device_info().num_cu);
-    return 0;
-}
+size_t nmi_linear_workspace_bytes(int M, int64_t total_n, int K) { return linear_workspace_bytes(M, total_n, K); }
 
 int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
                        const float* w_scale, void* y_bf16, int64_t ldy, int M, int N, int K,
@@ -383,6 +391,8 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "sdpa.chunk")) t.sdpa_chunk = value;
     else if (!std::strcmp(knob, "gemv.grid")) t.gemv_grid = value;
     else if (!std::strcmp(knob, "gemv.balance")) t.gemv_balance = value;
+    else if (!std::strcmp(knob, "gemm.splits")) t.gemm_splits = value;
+    else if (!std::strcmp(knob, "gemm.short")) t.gemm_short = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

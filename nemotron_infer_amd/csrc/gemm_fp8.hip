@@ -1011,20 +1011,23 @@ hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
                        hipStream_t stream, const Epi& epi, void* ws, size_t ws_bytes) {
     int tile = tuning().gemm_tile;
-    if (tile != 1 && tile != 20 && tile != 21 && tile != 24) {
-        // M < 512: the 128 x 128 16 x 16 x 32 kernel; otherwise the DMA-fed 256 x 256 kernel
-        // where it can take the operands, else the 8-wave 32 x 32 kernel with 256 x 256 tiles
-        // where they fill at least 3/4 of the CUs, 256 x 128 below that.  (Measured on MI355X,
-        // config 3; the other tile shapes and schedules tried -- 16 x 16 x 32 MFMA at 256-wide
-        // tiles, 64-bit LDS reads, 4-wave forms, raised issue priority -- were slower.)
+    if (tile != 1 && tile != 2 && tile != 20 && tile != 21 && tile != 24) {
+        // M < 512: the short-prompt kernel (gemm_short.hip) where it can take the operands, else
+        // the 128 x 128 16 x 16 x 32 kernel; otherwise the DMA-fed 256 x 256 kernel where it can
+        // take the operands, else the 8-wave 32 x 32 kernel with 256 x 256 tiles where they fill
+        // at least 3/4 of the CUs, 256 x 128 below that.  (Measured on MI355X, config 3; the other
+        // tile shapes and schedules tried -- 16 x 16 x 32 MFMA at 256-wide tiles, 64-bit LDS reads,
+        // 4-wave forms, raised issue priority -- were slower.)
         const DeviceInfo& dev = device_info();
         const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-        if (M < 512) tile = 1;
+        if (M < 512) tile = gemm_short_supported(x, ldx, W, ldw, M, N, K) ? 2 : 1;
         else if (dma_supported(x, ldx, W, ldw, M, N, K)) tile = 24;
         else tile = (4 * big >= 3 * (int64_t)dev.num_cu) ? 20 : 21;
     }
     if (tile == 24 && !dma_supported(x, ldx, W, ldw, M, N, K)) tile = 20;
+    if (tile == 2 && !gemm_short_supported(x, ldx, W, ldw, M, N, K)) tile = 1;
     switch (tile) {
+        case 2: return launch_gemm_short(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         case 24: return launch_dma(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi, ws, ws_bytes);
         case 20: return launch_m32<256, 256>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);
         case 21: return launch_m32<256, 128>(x, ldx, W, ldw, s, y, ldy, M, N, K, stream, epi);

@@ -11,6 +11,7 @@
 // out_proj with the residual add in its stores.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "nmi_fp8_linear.h"
@@ -69,13 +70,18 @@ struct FwdLayout {
     int64_t xc_ld;
 };
 
-size_t gemm_region(int M) { return choose_path(M) == Path::Gemm ? round256(gemm_workspace_bytes(M)) : 0; }
+// The GEMMs' region (stream-K flags and partials from M = 512, the short-prompt kernel's K-split
+// partials below): the larger of the in_proj and out_proj needs.
+size_t gemm_region(int M, int hidden, const MambaDims& d) {
+    if (choose_path(M) != Path::Gemm) return 0;
+    return round256(std::max(linear_workspace_bytes(M, d.proj, hidden), linear_workspace_bytes(M, hidden, d.inter)));
+}
 
 FwdLayout fwd_layout(int M, int hidden, const MambaDims& d) {
     FwdLayout L{};
     L.xc_ld = (d.conv_dim + 7) & ~7;
     L.gemm = 0;
-    L.normed = L.gemm + gemm_region(M);
+    L.normed = L.gemm + gemm_region(M, hidden, d);
     L.proj = L.normed + round256((size_t)M * hidden * 2);
     L.xc = L.proj + round256((size_t)M * d.proj_ld * 2);
     L.y = L.xc + round256((size_t)M * L.xc_ld * 2);
@@ -151,7 +157,7 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
     uint16_t* proj = reinterpret_cast<uint16_t*>(base + lay.proj);
     const uint16_t* in = static_cast<const uint16_t*>(input_bf16);
     hipError_t e = hipSuccess;
-    if (gws) e = launch_sk_flags_clear(gemm_ws, st);   // the workspace may hold anything
+    if (gws && gemm_workspace_has_flags(M)) e = launch_sk_flags_clear(gemm_ws, st);   // the workspace may hold anything
     if (e != hipSuccess) return hip_status(e, fn);
     // in_proj over all rows: proj = [z | xBC | dt]
     GemvGroup ip{static_cast<const uint8_t*>(in_proj_w_e4m3), hidden, in_proj_scale, proj, d.proj_ld, d.proj, 0, 0,

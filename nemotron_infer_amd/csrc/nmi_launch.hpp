@@ -50,6 +50,8 @@ struct Tuning {
     int sdpa_chunk = 0;    // attention decode: positions per split (0: kSdpaMinChunk, capped by the grid size)
     int gemv_grid = 0;     // M = 1 stream GEMV (single launches): explicit workgroup count
     int gemv_balance = 0;  // M = 1 stream GEMV (single launches): 2 turns off the grid sizing that makes row groups divide evenly
+    int gemm_splits = 0;   // short-prompt GEMM (17 <= M < 512): workgroups splitting K (0: automatic)
+    int gemm_short = 0;    // short-prompt GEMM: 1 selects the forms with 128 weight rows per workgroup
 };
 Tuning& tuning();
 
@@ -178,6 +180,27 @@ hipError_t launch_gemv_stream_chain(const StreamPhase* tab, const int* wave_step
 // one tile per workgroup.  launch_sk_flags_clear zeroes the flag region (one small kernel, safe
 // under graph capture).
 size_t gemm_workspace_bytes(int M);
+// Short prompts (17 <= M < 512; gemm_short.hip): the pipelined 128-row-tile kernel, with K split
+// between workgroups when a workspace of gemm_short_workspace_bytes(M, N, K) bytes is given
+// (float32 partials, no initialisation needed; 0: the schedule does not split).
+bool gemm_short_supported(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, int M, int N, int K);
+int gemm_short_splits(int M, int N, int K);
+size_t gemm_short_workspace_bytes(int M, int N, int K);
+// Workspace bytes a linear of M rows over matrices of total_n rows and K columns can use
+// (nmi_linear_workspace_bytes); whether that region holds stream-K flags that must start at zero
+// (launch_sk_flags_clear) -- the short-prompt kernel's partials need no initialisation.
+size_t linear_workspace_bytes(int M, int64_t total_n, int K);
+bool gemm_workspace_has_flags(int M);
+// The fp8 MLP block (block.cpp) behind nmi_mlp_forward_fp8 (split = true) and its allocation-free
+// form (split = false: the short-prompt GEMMs run unsplit, so the workspace has no partial
+// region); fn names the entry point in error messages.
+size_t mlp_workspace_bytes(int M, int hidden, int inter, bool split);
+int mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void* up_w_e4m3, const float* up_scale,
+                    const void* down_w_e4m3, const float* down_scale, void* out_bf16, int M, int hidden, int inter,
+                    float eps, void* workspace, size_t workspace_bytes, void* stream, bool split, const char* fn);
+hipError_t launch_gemm_short(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s,
+                             uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi,
+                             void* ws, size_t ws_bytes);
 // Attention decode (sdpa_decode.hip): q [H, 128] against the caches [H_KV, cap, 128] over
 // positions [0, S), then K_new / V_new appended at position S; H / H_KV in 1..kSdpaMaxGroup.
 // The workspace (sdpa_decode_workspace_bytes) holds the fp32 partials of split launches.

@@ -5,7 +5,10 @@
 // one, from the bump allocator, which may hipMalloc a slab.  Callers that cannot allocate (code
 // under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc) use this entry
 // point instead: the transient buffers live in `scratch`, a file-scope device array of
-// kNoAllocScratchBytes that every GPU the library runs on holds until the process ends.
+// kNoAllocScratchBytes that every GPU the library runs on holds until the process ends.  For
+// 17 <= M < 512 the block's GEMMs run without their K split here (its partials would not fit),
+// so results equal nmi_mlp_forward_fp8's up to float32 summation order there, and bit for bit
+// at every other M (and with tuning knob gemm.splits = 1).
 //
 // Host code never passes `scratch` itself (its name is a host-side stand-in, not a device
 // address): the first call on a device, with that device current, resolves the array's address
@@ -58,7 +61,7 @@ int nmi_mlp_forward_fp8_noalloc(const void* input_bf16, const float* norm_w, con
                                 const float* up_scale, const void* down_w_e4m3, const float* down_scale,
                                 void* out_bf16, int M, int hidden, int inter, float eps, void* stream) {
     const char* fn = "nmi_mlp_forward_fp8_noalloc";
-    const size_t need = nmi_mlp_workspace_bytes(M, hidden, inter);
+    const size_t need = nmi::mlp_workspace_bytes(M, hidden, inter, false);
     if (need == 0) {
         nmi::set_last_error("%s: M=%d hidden=%d inter=%d (need M >= 1, hidden and inter >= 16)", fn, M, hidden,
                             inter);
@@ -77,8 +80,8 @@ int nmi_mlp_forward_fp8_noalloc(const void* input_bf16, const float* norm_w, con
                             hipGetErrorString(e), (int)e);
         return (int)e;
     }
-    return nmi_mlp_forward_fp8(input_bf16, norm_w, up_w_e4m3, up_scale, down_w_e4m3, down_scale, out_bf16, M,
-                               hidden, inter, eps, ptr, kNoAllocScratchBytes, stream);
+    return nmi::mlp_forward_fp8(input_bf16, norm_w, up_w_e4m3, up_scale, down_w_e4m3, down_scale, out_bf16, M, hidden,
+                                inter, eps, ptr, kNoAllocScratchBytes, stream, false, fn);
 }
 
 }  // extern "C"

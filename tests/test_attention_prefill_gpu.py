@@ -84,7 +84,7 @@ def _dev_weights(W):
 
 def _composed(xd, dw, S):
     nw, qw, qs, kw, ks, vw, vs, ow, os_ = dw
-    ws = S >= 512
+    ws = S > 16        # as the block: its GEMMs (S > 16) get their split / stream-K workspace
     h = ops.rmsnorm_bf16(xd, nw, EPS)
     q = ops.linear_fp8_w8a16(h, qw, qs, use_workspace=ws)
     k = ops.linear_fp8_w8a16(h, kw, ks, use_workspace=ws)

@@ -95,9 +95,81 @@ def _gemm_tile_reset():
     _lib.tuning_set("gemm.tile", 0)
 
 
-@pytest.mark.parametrize("tile", [1, 20, 21, 24])
+@pytest.fixture
+def _splits_reset():
+    yield
+    _lib.tuning_set("gemm.splits", 0)
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 37, 64), (32, 128, 3136), (33, 300, 3136), (64, 12544, 3136),
+                                   (100, 3136, 12544), (128, 7168, 3136), (129, 520, 1024), (255, 777, 3136),
+                                   (300, 3136, 12544), (511, 256, 128)])
+def test_short_prompt_kernel(M, N, K, _splits_reset):
+    """17 <= M < 512 with K % 64 == 0: the short-prompt kernel (gemm_short.hip), one 32/64/128-row
+    x tile, ragged M and N, with K unsplit, split three ways and split as the schedule picks
+    (float32 partials in the workspace added in split order by the second kernel); per-tensor
+    scales, so the rel_l2-over-all-elements gate applies.  Every split count is deterministic."""
+    x, w, s = _case(M, N, K, M * 7 + N + K)
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    ref = oracle_bits(x, w, s)
+    L = _lib.lib()
+    for sp in (1, 3, 0):
+        _lib.tuning_set("gemm.splits", sp)
+        announce("gemm_short", M, N, K, sp, L.nmi_linear_workspace_bytes(M, N, K))
+        y1 = ops.gemm_fp8_w8a16(xd, wd, sd)
+        y2 = ops.linear_fp8_w8a16(xd, wd, sd)
+        torch.cuda.synchronize()
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), f"splits={sp}: not deterministic"
+        assert_parity(bits(y1), ref, f"short M={M} N={N} K={K} splits={sp}")
+
+
+def test_short_prompt_kernel_strided_and_graph(_splits_reset):
+    """Strided x / W / y views (the grouped q|k|v layout) and HIP graph replays of the split form
+    with eager work in between: every replay equals the eager result."""
+    M, N, K = 80, 1000, 3136
+    announce("gemm_short_strided_graph", M, N, K)
+    x, w, s = _case(M, N, K, 9191)
+    xbig = torch.zeros((M, K + 64), dtype=torch.bfloat16, device=DEV)
+    xbig[:, 64:] = x_to_dev(x)
+    wbig = torch.zeros((N, K + 32), dtype=torch.uint8, device=DEV)
+    wbig[:, 32:] = w_to_dev(w)
+    sd = s_to_dev(s)
+    ybig = torch.full((M, N + 24), 3.0, dtype=torch.bfloat16, device=DEV)
+    xv, wv, yv = xbig[:, 64:], wbig[:, 32:], ybig[:, 8:8 + N]
+    ref = oracle_bits(x, w, s)
+    _lib.tuning_set("gemm.splits", 4)
+    L = _lib.lib()
+    need = L.nmi_linear_workspace_bytes(M, N, K)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+
+    def call():
+        _lib.check(L.nmi_gemm_fp8_w8a16(xv.data_ptr(), xbig.stride(0), wv.data_ptr(), wbig.stride(0), sd.data_ptr(),
+                                        yv.data_ptr(), ybig.stride(0), M, N, K, ws.data_ptr(), need,
+                                        torch.cuda.current_stream().cuda_stream), "short strided")
+    call()
+    torch.cuda.synchronize()
+    eager = bits(yv).copy()
+    assert_parity(eager, ref, "short strided")
+    assert torch.all(ybig[:, :8] == 3.0) and torch.all(ybig[:, 8 + N:] == 3.0)
+    s_ = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s_):
+        with torch.cuda.graph(g, stream=s_):
+            call()
+    for _ in range(3):
+        yv.fill_(0)
+        ws.fill_(7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(yv), eager)
+
+
+@pytest.mark.parametrize("tile", [1, 2, 20, 21, 24])
 def test_every_tile_variant(tile, _gemm_tile_reset):
-    """Each GEMM kernel (1: 128 x 128 on 16 x 16 x 32 MFMA; 20, 21: the 8-wave 32 x 32 x 16 kernel
+    """Each GEMM kernel (1: 128 x 128 on 16 x 16 x 32 MFMA; 2: the short-prompt kernel, which hands
+    K not a multiple of 64 to kernel 1; 20, 21: the 8-wave 32 x 32 x 16 kernel
     with 256 x 256 and 256 x 128 tiles; 24: the DMA-fed kernel, which hands K not a multiple of
     64 to the 8-wave kernel) on ragged M and N, K not a multiple of the 64-wide K step, and
     strided / misaligned y."""

@@ -74,10 +74,11 @@ def _dev(nw, upw, ups, dnw, dns):
 
 
 def _composed(x, nw, upw, ups, dnw, dns):
-    # The block hands its GEMMs (M >= 512) a workspace -- stream-K for the few tiles of the down
-    # projection -- and its smaller-M linears none; the composition does the same, so that both
-    # run the same kernels in the same form (same float32 summation order).
-    ws = x.shape[0] >= 512
+    # The block hands its GEMMs (M > 16) a workspace -- the short-prompt kernel's K split for
+    # 17 <= M < 512, stream-K for the few tiles of the down projection from M = 512 -- and its
+    # smaller-M linears none; the composition does the same, so that both run the same kernels in
+    # the same form (same float32 summation order).
+    ws = x.shape[0] > 16
     h = ops.rmsnorm_bf16(x, nw, EPS)
     up = ops.linear_fp8_w8a16(h, upw, ups, use_workspace=ws)
     r = torch.relu(up)
@@ -144,7 +145,7 @@ def check_block(x, got, nw, upw, ups, dnw, dns, eps, label):
     dev = _dev(nw, upw, ups, dnw, dns)
     xd = x_to_dev(x)
     h = ops.rmsnorm_bf16(xd, dev[0], eps)
-    up = ops.linear_fp8_w8a16(h, dev[1], dev[2], use_workspace=False)
+    up = ops.linear_fp8_w8a16(h, dev[1], dev[2], use_workspace=x.shape[0] > 16)   # as the block
     r_ = torch.relu(up)
     act = bits(r_ * r_)
     h, up = bits(h), bits(up)
