@@ -83,13 +83,16 @@ __device__ __forceinline__ void wait_later(int later) {
 __device__ __forceinline__ int xswz(int row, int c) { return c ^ ((row >> 1) & 7); }
 __device__ __forceinline__ int wswz(int row, int q) { return q ^ ((row >> 2) & 3); }
 
-// TN: 32-row blocks of W per wave (BN = 128 TN); TM: 32-row blocks of x (BM = 32 TM); NS: LDS
-// stages.
-template <int TN, int TM, int NS>
-__global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
-    constexpr int BN = 32 * TN * kWaves, BM = 32 * TM;
+// The 4 waves form a WN x (4 / WN) grid; each wave computes TN 32-row blocks of W times TM
+// 32-row blocks of x, so a workgroup covers BN = 32 TN WN weight rows and BM = 32 TM (4 / WN) x
+// rows.  NS: LDS stages.
+template <int TN, int TM, int WN, int NS, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_short_kernel(const ShortArgs a) {
+    constexpr int WM = kWaves / WN;
+    constexpr int BN = 32 * TN * WN, BM = 32 * TM * WM;
     constexpr int WI = BN / 16 / kWaves;            // W DMA instructions per wave per k tile
     constexpr int XI = BM / 8 / kWaves;             // x DMA instructions per wave per k tile
+    static_assert(WI >= 1, "at least one W DMA per wave");
     constexpr int D = WI + XI;                      // DMA instructions per wave per k tile
     constexpr int WSTAGE = BN * kBK;
     constexpr int STAGE = WSTAGE + BM * kBK * 2;
@@ -101,6 +104,7 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, l32 = lane & 31;
+    const int wn = wave % WN, wm = wave / WN;
     const int tn = (int)blockIdx.x / a.splits, sp = (int)blockIdx.x % a.splits;
     const int n0 = tn * BN, m0 = (int)blockIdx.y * BM;
     const int KT = a.K / kBK;
@@ -157,7 +161,7 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
             uint4 codes[TN];
 #pragma unroll
             for (int u = 0; u < TN; ++u) {
-                const int wr = (wave * TN + u) * 32 + l32;          // this lane's W row of block u
+                const int wr = (wn * TN + u) * 32 + l32;            // this lane's W row of block u
                 codes[u] = *reinterpret_cast<const uint4*>(sw + wr * 64 + 16 * wswz(wr, 2 * jp + h));
             }
 #pragma unroll
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
                 const int c = 4 * jp + 2 * h + half;
 #pragma unroll
                 for (int t = 0; t < TM; ++t) {
-                    const int xr = 32 * t + l32;
+                    const int xr = (wm * TM + t) * 32 + l32;
                     const bf16x8 bf = *reinterpret_cast<const bf16x8*>(sx + xr * 128 + 16 * xswz(xr, c));
 #pragma unroll
                     for (int u = 0; u < TN; ++u)
@@ -182,21 +186,21 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
         }
     }
 
-    // Register r of lane l in block (u, t): n = n0 + 32 (TN wave + u) + 8 (r / 4) + 4 h + r % 4,
-    // m = m0 + 32 t + l32.
+    // Register r of lane l in block (u, t): n = n0 + 32 (TN wn + u) + 8 (r / 4) + 4 h + r % 4,
+    // m = m0 + 32 (TM wm + t) + l32.
     if (a.splits > 1) {
         // partial tile of this split, raw sums (the reduce kernel scales)
         float* part = a.part + (size_t)sp * a.M * a.N;
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-            const int m = m0 + 32 * t + l32;
+            const int m = m0 + 32 * (TM * wm + t) + l32;
             if (m >= a.M) continue;
             float* row = part + (size_t)m * a.N;
 #pragma unroll
             for (int u = 0; u < TN; ++u)
 #pragma unroll
                 for (int gq = 0; gq < 4; ++gq) {
-                    const int n = n0 + 32 * (TN * wave + u) + 4 * h + 8 * gq;
+                    const int n = n0 + 32 * (TN * wn + u) + 4 * h + 8 * gq;
                     if (a.part_vec && n + 3 < a.N) {
                         *reinterpret_cast<float4*>(row + n) = float4{acc[u][t][4 * gq], acc[u][t][4 * gq + 1],
                                                                      acc[u][t][4 * gq + 2], acc[u][t][4 * gq + 3]};
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < TN; ++u) {
-        const int nb = n0 + 32 * (TN * wave + u) + 4 * h;
+        const int nb = n0 + 32 * (TN * wn + u) + 4 * h;
         float sc[4][4];
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq)
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
         if (a.epi.kind == kEpiResidual) {
 #pragma unroll
             for (int t = 0; t < TM; ++t) {
-                const int m = min(m0 + 32 * t + l32, a.M - 1);
+                const int m = min(m0 + 32 * (TM * wm + t) + l32, a.M - 1);
 #pragma unroll
                 for (int gq = 0; gq < 4; ++gq)
 #pragma unroll
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
         }
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-            const int m = m0 + 32 * t + l32;
+            const int m = m0 + 32 * (TM * wm + t) + l32;
             if (m >= a.M) continue;
             uint16_t* yr = a.y + (int64_t)m * a.ldy;
 #pragma unroll
@@ -249,38 +253,42 @@ __global__ __launch_bounds__(256, 1) void gemm_short_kernel(const ShortArgs a) {
 }
 
 // Sum of the splits' partials in split order, the scale, one rounding, the epilogue.  One
-// thread per output element pair (n, n + 1) of a row.
+// thread per 4 consecutive outputs of a row (16-byte partial loads when N % 4 == 0).
 __global__ __launch_bounds__(256) void gemm_short_reduce_kernel(const ShortArgs a) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int half_n = (a.N + 1) / 2;
-    if (i >= (int64_t)a.M * half_n) return;
-    const int m = (int)(i / half_n), n = 2 * (int)(i % half_n);
+    const int q_n = (a.N + 3) / 4;
+    if (i >= (int64_t)a.M * q_n) return;
+    const int m = (int)(i / q_n), n = 4 * (int)(i % q_n);
     const size_t stride = (size_t)a.M * a.N;
     const float* p = a.part + (size_t)m * a.N + n;
-    const bool two = n + 1 < a.N;
-    float v0 = 0.f, v1 = 0.f;
-    for (int sp = 0; sp < a.splits; ++sp) {
-        v0 += p[sp * stride];
-        if (two) v1 += p[sp * stride + 1];
+    const int cnt = min(4, a.N - n);
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.part_vec) {
+        for (int sp = 0; sp < a.splits; ++sp) {
+            const float4 f = *reinterpret_cast<const float4*>(p + sp * stride);
+            v[0] += f.x; v[1] += f.y; v[2] += f.z; v[3] += f.w;
+        }
+    } else {
+        for (int sp = 0; sp < a.splits; ++sp)
+            for (int e = 0; e < cnt; ++e) v[e] += p[sp * stride + e];
     }
-    uint16_t r0 = 0, r1 = 0;
-    if (a.epi.kind == kEpiResidual) {
-        r0 = a.epi.res[(int64_t)m * a.epi.ldres + n];
-        if (two) r1 = a.epi.res[(int64_t)m * a.epi.ldres + n + 1];
-    }
-    uint16_t* yr = a.y + (int64_t)m * a.ldy;
-    yr[n] = epilogue(v0, a.s[n], a.epi.kind, r0);
-    if (two) yr[n + 1] = epilogue(v1, a.s[n + 1], a.epi.kind, r1);
+    uint16_t r[4] = {0, 0, 0, 0};
+    if (a.epi.kind == kEpiResidual)
+        for (int e = 0; e < cnt; ++e) r[e] = a.epi.res[(int64_t)m * a.epi.ldres + n + e];
+    uint16_t* yr = a.y + (int64_t)m * a.ldy + n;
+    for (int e = 0; e < cnt; ++e) yr[e] = epilogue(v[e], a.s[n + e], a.epi.kind, r[e]);
 }
 
-template <int TN, int TM, int NS>
+template <int TN, int TM, int WN, int NS, int OCC>
 hipError_t launch_short_t(ShortArgs a, int tiles_m, hipStream_t stream) {
-    constexpr int lds = NS * (32 * TN * kWaves * kBK + 32 * TM * kBK * 2);
+    constexpr int lds = NS * (32 * TN * WN * kBK + 32 * TM * (kWaves / WN) * kBK * 2);
+    static_assert(lds * OCC <= 160 * 1024, "LDS of OCC workgroups per CU");
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_short_kernel<TN, TM, NS>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        reinterpret_cast<const void*>(&gemm_short_kernel<TN, TM, WN, NS, OCC>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemm_short_kernel<TN, TM, NS>), dim3(a.tiles_n * a.splits, tiles_m), dim3(256), lds, stream,
-                       a);
+    hipLaunchKernelGGL((gemm_short_kernel<TN, TM, WN, NS, OCC>), dim3(a.tiles_n * a.splits, tiles_m), dim3(256), lds,
+                       stream, a);
     return hipGetLastError();
 }
 
@@ -294,35 +302,59 @@ bool gemm_short_supported(const uint16_t* x, int64_t ldx, const uint8_t* W, int6
 
 namespace {
 
-// The schedule for M: W blocks per wave (TN), x blocks (TM), LDS stages, workgroups per CU.
-// TN = 2 (256 weight rows per workgroup) halves the x bytes each weight byte brings along and the
-// LDS reads per MFMA against TN = 1; its stages fill most of the LDS, so one workgroup per CU.
-// (Tuning knob gemm.short = 1 selects the TN = 1 forms, two workgroups per CU.)
+// The kernel forms: W blocks per wave, x blocks per wave, waves along N (the rest along M), LDS
+// stages, workgroups per CU.  Larger BN brings fewer x bytes along per weight byte (every
+// workgroup reads its BM rows of x from L2) and fewer LDS reads per MFMA; smaller BN gives more
+// workgroups without splitting K (whose partials cost 8 M bytes per weight row and split).
 struct ShortCfg {
-    int tn, tm, ns, per_cu;
+    int tn, tm, wn, ns, per_cu;
+    int bn() const { return 32 * tn * wn; }
+    int bm() const { return 32 * tm * (kWaves / wn); }
 };
-ShortCfg short_cfg(int M) {
-    if (tuning().gemm_short == 1) {
-        if (M <= 32) return {1, 1, 6, 2};
-        if (M <= 64) return {1, 2, 4, 2};
-        return {1, 4, 3, 2};
+constexpr ShortCfg kForms[] = {
+    {2, 1, 4, 7, 1},   // 0: 256 x 32
+    {1, 1, 4, 6, 2},   // 1: 128 x 32
+    {2, 2, 4, 6, 1},   // 2: 256 x 64
+    {1, 2, 4, 4, 2},   // 3: 128 x 64
+    {1, 1, 2, 6, 2},   // 4: 64 x 64
+    {2, 4, 4, 4, 1},   // 5: 256 x 128
+    {2, 2, 2, 4, 1},   // 6: 128 x 128
+    {1, 2, 2, 3, 2},   // 7: 64 x 128
+};
+constexpr int kNumForms = sizeof(kForms) / sizeof(kForms[0]);
+
+// The form for (M, N): among those whose x tile fits M best, the widest one whose tiles fill
+// three quarters of the workgroup slots without a K split; else the narrowest (then K is split).
+// Above M = 64 the 128 x 128 form with a 64 x 64 block per wave (fewest LDS reads per MFMA).
+// Measured on the config-3 shapes at M = 64 / 128 / 256: every form within ~15% of the others;
+// 128 x 128 ahead by 10% at M = 128 and 256.  Tuning knob gemm.short = f + 1 forces form f.
+int short_form(int M, int N) {
+    const int forced = tuning().gemm_short;
+    if (forced >= 1 && forced <= kNumForms) return forced - 1;
+    int lo, hi;                                     // candidate forms, widest first
+    if (M <= 32) { lo = 0; hi = 1; }
+    else if (M <= 64) { lo = 2; hi = 4; }
+    else { lo = 6; hi = 6; }                        // 128 x 128: measured ahead of 256 x 128 and 64 x 128
+    const int cu = device_info().num_cu;
+    for (int f = lo; f <= hi; ++f) {
+        const ShortCfg& c = kForms[f];
+        const int64_t tiles = (int64_t)((N + c.bn() - 1) / c.bn()) * ((M + c.bm() - 1) / c.bm());
+        if (4 * tiles >= 3 * (int64_t)c.per_cu * cu) return f;
     }
-    if (M <= 32) return {2, 1, 7, 1};
-    if (M <= 64) return {2, 2, 6, 1};
-    return {2, 4, 4, 1};
+    return hi;
 }
 
 }  // namespace
 
 int gemm_short_splits(int M, int N, int K) {
-    const ShortCfg c = short_cfg(M);
-    const int bn = 128 * c.tn, bm = 32 * c.tm;
+    const ShortCfg& c = kForms[short_form(M, N)];
+    const int bn = c.bn(), bm = c.bm();
     const int tiles = ((N + bn - 1) / bn) * ((M + bm - 1) / bm);
     const int KT = K / kBK;
     if (tuning().gemm_splits > 0) return std::min(tuning().gemm_splits, KT);
     // as many workgroups as run at once (one round), at least 4 k tiles each, and the partials
     // (4 M bytes per weight row and split, written and read back) at most the weight bytes
-    const int want = c.per_cu * device_info().num_cu / tiles;
+    const int want = std::max(1, c.per_cu * device_info().num_cu / tiles);
     const int by_k = std::max(1, KT / 4);
     const int by_bytes = std::max(1, (int)((int64_t)K / (4 * (int64_t)M)));
     return std::max(1, std::min(want, std::min(by_k, by_bytes)));
@@ -333,7 +365,6 @@ int gemm_short_splits(int M, int N, int K) {
 // workgroups covers.
 size_t gemm_short_workspace_bytes(int M, int N, int K) {
     if (M < 1 || N < 1 || K < kBK) return 0;
-    const ShortCfg c = short_cfg(M);
     const int KT = K / kBK;
     int64_t rows;
     if (tuning().gemm_splits > 0) {
@@ -343,7 +374,10 @@ size_t gemm_short_workspace_bytes(int M, int N, int K) {
     } else {
         const int64_t cap = std::max(1, std::min(KT / 4, (int)((int64_t)K / (4 * (int64_t)M))));
         if (cap <= 1) return 0;
-        rows = std::min<int64_t>(cap * N, (int64_t)c.per_cu * device_info().num_cu * 128 * c.tn);
+        // over the forms M can take: at most the rows one round of workgroups covers
+        int64_t round_rows = 0;
+        for (const ShortCfg& c : kForms) round_rows = std::max<int64_t>(round_rows, (int64_t)c.per_cu * c.bn());
+        rows = std::min<int64_t>(cap * N, round_rows * device_info().num_cu);
     }
     return kFlagRegion + (size_t)rows * M * sizeof(float);
 }
@@ -351,11 +385,12 @@ size_t gemm_short_workspace_bytes(int M, int N, int K) {
 hipError_t launch_gemm_short(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s,
                              uint16_t* y, int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi,
                              void* ws, size_t ws_bytes) {
-    const ShortCfg c = short_cfg(M);
+    const int form = short_form(M, N);
+    const ShortCfg& c = kForms[form];
     ShortArgs a{};
     a.x = x; a.ldx = ldx; a.W = W; a.ldw = ldw; a.s = s; a.y = y; a.ldy = ldy;
     a.M = M; a.N = N; a.K = K; a.epi = epi;
-    a.tiles_n = (N + 128 * c.tn - 1) / (128 * c.tn);
+    a.tiles_n = (N + c.bn() - 1) / c.bn();
     const int KT = K / kBK;
     int splits = gemm_short_splits(M, N, K);
     if (splits > 1 && (!ws || ws_bytes < kFlagRegion + (size_t)splits * M * N * sizeof(float))) splits = 1;
@@ -363,20 +398,21 @@ hipError_t launch_gemm_short(const uint16_t* x, int64_t ldx, const uint8_t* W, i
     a.splits = (KT + a.kt_per - 1) / a.kt_per;      // no empty split
     a.part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kFlagRegion) : nullptr;
     a.part_vec = N % 4 == 0 ? 1 : 0;
-    const int tiles_m = (M + 32 * c.tm - 1) / (32 * c.tm);
+    const int tiles_m = (M + c.bm() - 1) / c.bm();
     hipError_t e;
-    if (c.tn == 1) {
-        if (c.tm == 1) e = launch_short_t<1, 1, 6>(a, tiles_m, stream);
-        else if (c.tm == 2) e = launch_short_t<1, 2, 4>(a, tiles_m, stream);
-        else e = launch_short_t<1, 4, 3>(a, tiles_m, stream);
-    } else {
-        if (c.tm == 1) e = launch_short_t<2, 1, 7>(a, tiles_m, stream);
-        else if (c.tm == 2) e = launch_short_t<2, 2, 6>(a, tiles_m, stream);
-        else e = launch_short_t<2, 4, 4>(a, tiles_m, stream);
+    switch (form) {
+        case 0: e = launch_short_t<2, 1, 4, 7, 1>(a, tiles_m, stream); break;
+        case 1: e = launch_short_t<1, 1, 4, 6, 2>(a, tiles_m, stream); break;
+        case 2: e = launch_short_t<2, 2, 4, 6, 1>(a, tiles_m, stream); break;
+        case 3: e = launch_short_t<1, 2, 4, 4, 2>(a, tiles_m, stream); break;
+        case 4: e = launch_short_t<1, 1, 2, 6, 2>(a, tiles_m, stream); break;
+        case 5: e = launch_short_t<2, 4, 4, 4, 1>(a, tiles_m, stream); break;
+        case 6: e = launch_short_t<2, 2, 2, 4, 1>(a, tiles_m, stream); break;
+        default: e = launch_short_t<1, 2, 2, 3, 2>(a, tiles_m, stream); break;
     }
     if (e != hipSuccess || a.splits == 1) return e;
-    const int64_t n2 = (int64_t)M * ((N + 1) / 2);
-    hipLaunchKernelGGL(gemm_short_reduce_kernel, dim3((unsigned)((n2 + 255) / 256)), dim3(256), 0, stream, a);
+    const int64_t n4 = (int64_t)M * ((N + 3) / 4);
+    hipLaunchKernelGGL(gemm_short_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -51,7 +51,7 @@ struct Tuning {
     int gemv_grid = 0;     // M = 1 stream GEMV (single launches): explicit workgroup count
     int gemv_balance = 0;  // M = 1 stream GEMV (single launches): 2 turns off the grid sizing that makes row groups divide evenly
     int gemm_splits = 0;   // short-prompt GEMM (17 <= M < 512): workgroups splitting K (0: automatic)
-    int gemm_short = 0;    // short-prompt GEMM: 1 selects the forms with 128 weight rows per workgroup
+    int gemm_short = 0;    // short-prompt GEMM: f + 1 forces kernel form f (0..7, gemm_short.hip)
 };
 Tuning& tuning();
 

@@ -123,6 +123,28 @@ def test_short_prompt_kernel(M, N, K, _splits_reset):
         assert_parity(bits(y1), ref, f"short M={M} N={N} K={K} splits={sp}")
 
 
+@pytest.fixture
+def _short_reset():
+    yield
+    _lib.tuning_set("gemm.short", 0)
+    _lib.tuning_set("gemm.splits", 0)
+
+
+@pytest.mark.parametrize("form", range(8))
+def test_short_prompt_kernel_every_form(form, _short_reset):
+    """Each tile form of the short-prompt kernel (forced with gemm.short), unsplit and split, on
+    ragged M and N: BM of 32, 64 or 128 rows against M from 17 to 300."""
+    _lib.tuning_set("gemm.short", form + 1)
+    for M, N, K in [(17, 200, 640), (70, 1000, 3136), (300, 333, 1280)]:
+        x, w, s = _case(M, N, K, 31 * form + M + N)
+        xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+        ref = oracle_bits(x, w, s)
+        for sp in (1, 4):
+            _lib.tuning_set("gemm.splits", sp)
+            announce("gemm_short_form", form, M, N, K, sp)
+            assert_parity(bits(ops.gemm_fp8_w8a16(xd, wd, sd)), ref, f"form={form} M={M} N={N} K={K} splits={sp}")
+
+
 def test_short_prompt_kernel_strided_and_graph(_splits_reset):
     """Strided x / W / y views (the grouped q|k|v layout) and HIP graph replays of the split form
     with eager work in between: every replay equals the eager result."""
