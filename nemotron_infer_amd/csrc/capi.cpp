@@ -266,7 +266,7 @@ int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_ch
             int rc = check_linear(P.x_bf16, P.K, G.w_e4m3, G.ldw, G.w_scale, G.y_bf16, G.ldy, 1, G.N, P.K, fn);
             if (rc) return rc;
             ph.g[i] = StreamGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
-                                  static_cast<uint16_t*>(G.y_bf16), nullptr, G.N, 0, kEpiNone, 0};
+                                  static_cast<uint16_t*>(G.y_bf16), nullptr, G.N, 0, kEpiNone, 0, 0, 0};
             rgs += (G.N + kStreamChainT - 1) / kStreamChainT;
         }
         if (p == 0 || P.wait_prev) seg.push_back(ChainSegment{p, 0, 0, 0, 0});

@@ -392,16 +392,17 @@ int pow2_pieces(int need) { return need <= 2 ? 2 : (need <= 4 ? 4 : 8); }
 }  // namespace
 
 bool gemv_norm_supported(int M, int K) {
-    if (M == 1 && tuning().gemv_multirow == 0) return gemv_stream_supported(K);
+    if (M <= 2 && tuning().gemv_multirow == 0 && gemv_stream_supported(M, K, true)) return true;
     const int C = K >> 4;
     return (M == 1 || M == 2) && 2 * C <= 256 * (8 / M);
 }
 
 hipError_t launch_gemv_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
                                int ngroups, hipStream_t stream, const Norm& norm) {
-    // M = 1: the stream kernel (gemv_stream.hip), unless tuning knob gemv.multirow selects this one
-    if (M == 1 && tuning().gemv_multirow == 0 && gemv_stream_supported(K))
-        return launch_gemv_stream(x, K, groups, ngroups, stream, norm);
+    // M <= 2: the stream kernel (gemv_stream.hip) where it takes the shape, unless tuning knob
+    // gemv.multirow selects this one
+    if (M <= 2 && tuning().gemv_multirow == 0 && gemv_stream_supported(M, K, norm.w != nullptr))
+        return launch_gemv_stream(x, ldx, M, K, groups, ngroups, stream, norm);
     const DeviceInfo& dev = device_info();
     if (norm.w && !gemv_norm_supported(M, K)) return hipErrorInvalidValue;
     GemvArgs a{};

@@ -50,10 +50,17 @@ constexpr int kLoads = 4;              // 16-byte loads per row and lane in one 
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// 16 e4m3 codes times 16 bf16 activations (low and high 8 of the chunk), two accumulators.
-__device__ __forceinline__ void dot16s(const uint4 w, const uint4 xl, const uint4 xh, float& a0, float& a1) {
-    const uint2 p0 = e4m3x4_to_bf16(w.x), p1 = e4m3x4_to_bf16(w.y);
-    const uint2 p2 = e4m3x4_to_bf16(w.z), p3 = e4m3x4_to_bf16(w.w);
+// 16 e4m3 codes -> 16 bf16 in four packed pairs of pairs.
+struct Codes16 {
+    uint2 p0, p1, p2, p3;
+};
+__device__ __forceinline__ Codes16 conv16(const uint4 w) {
+    return Codes16{e4m3x4_to_bf16(w.x), e4m3x4_to_bf16(w.y), e4m3x4_to_bf16(w.z), e4m3x4_to_bf16(w.w)};
+}
+
+// 16 converted codes times 16 bf16 activations (low and high 8 of the chunk), two accumulators.
+__device__ __forceinline__ void dot16s(const Codes16& c, const uint4 xl, const uint4 xh, float& a0, float& a1) {
+    const uint2 p0 = c.p0, p1 = c.p1, p2 = c.p2, p3 = c.p3;
     a0 = dot2_bf16(p0.x, xl.x, a0);
     a1 = dot2_bf16(p0.y, xl.y, a1);
     a0 = dot2_bf16(p1.x, xl.z, a0);
@@ -74,6 +81,8 @@ struct Cursor {
     int S, sw, C;           // the phase's slices, chunks per slice, chunks
     int rows;               // rows of the row group that exist (1..T)
     int epi;
+    int ldy, ldres;         // output / residual row strides (activation rows)
+    int M;                  // activation rows (single launches)
     const uint8_t* w0;      // first weight row of the row group
     int64_t ldw;
     const float* s0;        // its scale
@@ -119,6 +128,9 @@ __device__ __forceinline__ void locate(const StreamArgs& a, const NMI_CONST Stre
     c.C = ph.C;
     c.rows = min(T, gr.N - row0);
     c.epi = gr.epi;
+    c.ldy = gr.ldy;
+    c.ldres = gr.ldres;
+    c.M = CHAIN ? 1 : a.M;
     c.ldw = gr.ldw;
     c.w0 = gr.W + (int64_t)row0 * gr.ldw;
     c.s0 = gr.s + row0;
@@ -160,7 +172,7 @@ __device__ __forceinline__ Cursor cursor_next(const StreamArgs& a, const NMI_CON
 // residual).  Every address is clamped into the valid range (rows past the group's end read its
 // last row, chunks past the slice its last chunk), so the loads are unconditional; a null step
 // reads chunk 0 of its rows from every lane.
-template <int T, bool RES, bool XG>
+template <int T, bool RES, bool XG, int MR>
 __device__ __forceinline__ void issue_w(const Cursor& c, int lane, Buf<T, XG>& b) {
     const int cb = c.valid ? c.j * c.sw : 0;                       // first chunk of the slice
     const int clast = c.valid ? min(cb + c.sw, c.C) - 1 : 0;       // last chunk of the slice
@@ -171,9 +183,11 @@ __device__ __forceinline__ void issue_w(const Cursor& c, int lane, Buf<T, XG>& b
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) b.w[t][i] = load_stream16(wr + (int64_t)min(cb + l + 64 * i, clast) * 16);
     }
-    const int tr = min(lane < T ? lane : 0, c.rows - 1);
+    // lane t MR + m: output row t of activation row m
+    const int lt = lane < T * MR ? lane : 0;
+    const int tr = min(lt / MR, c.rows - 1);
     b.sc = c.s0[tr];
-    if constexpr (RES) b.res = c.r0[tr];
+    if constexpr (RES) b.res = c.r0[(int64_t)min(lt % MR, c.M - 1) * c.ldres + tr];
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -198,44 +212,64 @@ __device__ __forceinline__ void issue_x(const Cursor& c, int lane, Buf<T, true>&
 // Compute step c from b into the running sums; on the last slice of the row group reduce, apply
 // the scale and the epilogue, and store (lane t < rows stores row t).  A null step computes
 // nothing it keeps and stores nothing.
-template <int T, bool XG, bool RES>
+template <int T, bool XG, bool RES, int MR>
 __device__ __forceinline__ void compute(const Cursor& c, int lane, const Buf<T, XG>& b, const uint4* xs, int xs_half,
-                                        float (&a0)[T], float (&a1)[T]) {
+                                        float (&a0)[T][MR], float (&a1)[T][MR]) {
+    static_assert(!XG || MR == 1, "x from global memory is for one activation row");
     const int cb = c.j * c.sw;
     const int nvalid = min(c.sw, c.C - cb);
     const bool first = c.j == 0, last = c.valid && c.j == c.S - 1;
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        a0[t] = first ? 0.f : a0[t];
-        a1[t] = first ? 0.f : a1[t];
-    }
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            a0[t][m] = first ? 0.f : a0[t][m];
+            a1[t][m] = first ? 0.f : a1[t][m];
+        }
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int c_in = lane + 64 * i;
         const bool ok = c_in < nvalid;
-        uint4 lo, hi;
+        uint4 lo[MR], hi[MR];
         if constexpr (XG) {
-            lo = b.x[i][0];
-            hi = b.x[i][1];
+            lo[0] = b.x[i][0];
+            hi[0] = b.x[i][1];
         } else {
             const int cc = cb + min(c_in, nvalid - 1);
-            lo = xs[cc];
-            hi = xs[xs_half + cc];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                lo[m] = xs[2 * m * xs_half + cc];
+                hi[m] = xs[(2 * m + 1) * xs_half + cc];
+            }
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            float b0 = a0[t], b1 = a1[t];
-            dot16s(b.w[t][i], lo, hi, b0, b1);
-            a0[t] = ok ? b0 : a0[t];
-            a1[t] = ok ? b1 : a1[t];
+            if constexpr (MR == 1) {
+                // converted inside the dot product: the form the one-row kernels were tuned with
+                float b0 = a0[t][0], b1 = a1[t][0];
+                dot16s(conv16(b.w[t][i]), lo[0], hi[0], b0, b1);
+                a0[t][0] = ok ? b0 : a0[t][0];
+                a1[t][0] = ok ? b1 : a1[t][0];
+            } else {
+                const Codes16 cw = conv16(b.w[t][i]);          // converted once for both rows
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float b0 = a0[t][m], b1 = a1[t][m];
+                    dot16s(cw, lo[m], hi[m], b0, b1);
+                    a0[t][m] = ok ? b0 : a0[t][m];
+                    a1[t][m] = ok ? b1 : a1[t][m];
+                }
+            }
         }
     }
     float v = 0.f;
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const float sum = wave_sum(a0[t] + a1[t]);
-        v = lane == t ? sum : v;
-    }
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float sum = wave_sum(a0[t][m] + a1[t][m]);
+            v = lane == t * MR + m ? sum : v;
+        }
     // epilogue() of nmi_device.hpp, on the raw 32-bit residual load: the shift drops its upper
     // half, so no zero-extension of a register of the step in flight is ever needed here
     const uint16_t lin = f32_to_bf16_rne(v * b.sc);
@@ -247,9 +281,13 @@ __device__ __forceinline__ void compute(const Cursor& c, int lane, const Buf<T, 
     } else if (RES) {
         out = f32_to_bf16_rne(__uint_as_float(b.res << 16) + bf16_to_f32(lin));
     }
-    // the descriptor covers the valid rows of the last slice only; other lanes and steps drop
-    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(c.y0, 0, last ? c.rows * 2 : 0, 0x00020000);
-    __builtin_amdgcn_raw_buffer_store_b16(out, yr, lane < T ? lane * 2 : 0x40000000, 0, 0);
+    // the descriptor covers the output rows of the last slice only (other steps drop every
+    // store); lanes past T MR or past the valid rows store out of range
+    const int st_t = lane / MR, st_m = lane % MR;
+    const bool st_ok = lane < T * MR && st_t < c.rows && st_m < c.M;
+    const __amdgpu_buffer_rsrc_t yr =
+        __builtin_amdgcn_make_buffer_rsrc(c.y0, 0, last ? ((MR - 1) * c.ldy + c.rows) * 2 : 0, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b16(out, yr, st_ok ? (st_m * c.ldy + st_t) * 2 : 0x40000000, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -261,12 +299,13 @@ __device__ __forceinline__ int single_steps(const StreamArgs& a, int gw, int nw)
 
 // CHAIN: the phases come from a.tab (device memory, read as constant memory), x per step from
 // global memory.  Otherwise one phase in a.one, x staged in LDS (NORM: RMSNorm-ed on the way).
-template <int T, bool CHAIN, bool XG, bool NORM, bool RES, int XPC>
+template <int T, bool CHAIN, bool XG, bool NORM, bool RES, int XPC, int MR>
 __global__ __launch_bounds__(256, 2) void gemv_stream_kernel(const StreamArgs a) {
     static_assert(!(NORM && (XG || CHAIN)), "the fused RMSNorm stages x in LDS (single launches)");
     static_assert(!CHAIN || XG, "chains read x per step");
-    extern __shared__ uint4 xs[];                  // [half][xs_half] (LDS mode)
-    __shared__ float red[NORM ? kWaves : 1];
+    static_assert(MR == 1 || !(XG || CHAIN), "two activation rows are staged in LDS (single launches)");
+    extern __shared__ uint4 xs[];                  // [row][half][xs_half] (LDS mode)
+    __shared__ float red[NORM ? kWaves * MR : 1];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -279,54 +318,66 @@ __global__ __launch_bounds__(256, 2) void gemv_stream_kernel(const StreamArgs a)
     const int nsteps = CHAIN ? ((const NMI_CONST int*)a.wave_steps)[gw] : single_steps(a, gw, nw);
 
     Buf<T, XG> A, B;
-    float a0[T], a1[T];
+    float a0[T][MR], a1[T][MR];
 #pragma unroll
-    for (int t = 0; t < T; ++t) a0[t] = a1[t] = 0.f;
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) a0[t][m] = a1[t][m] = 0.f;
 
     Cursor c0 = cursor_start<T, CHAIN>(a, tab, gw);
     if constexpr (!XG) {
-        // stage x [K] (single phase): pieces of 8 activations, piece e -> chunk e >> 1, half e & 1;
-        // issued before the first weights, written to LDS after them
+        // stage x [MR][K] (single phase): per activation row, pieces of 8 activations, piece e ->
+        // chunk e >> 1, half e & 1; issued before the first weights, written to LDS after them
         const NMI_CONST StreamPhase& ph = phase_at<false>(a, tab, 0);
         const int npieces = 2 * ph.C;                // XPC * 256 >= npieces
-        uint4 xr[XPC];
+        uint4 xr[MR][XPC];
         float4 gr[NORM ? 2 * XPC : 1];
 #pragma unroll
         for (int q = 0; q < XPC; ++q) {
             const int e = min(tid + 256 * q, npieces - 1);
-            xr[q] = load16(ph.x + (int64_t)e * 8);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) xr[m][q] = load16(ph.x + (int64_t)min(m, a.M - 1) * a.ldx + (int64_t)e * 8);
             if constexpr (NORM) {
                 gr[2 * q] = *reinterpret_cast<const float4*>(a.norm_w + e * 8);
                 gr[2 * q + 1] = *reinterpret_cast<const float4*>(a.norm_w + e * 8 + 4);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        issue_w<T, RES, XG>(c0, lane, A);
-        float r = 1.f;
+        issue_w<T, RES, XG, MR>(c0, lane, A);
+        float r[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) r[m] = 1.f;
         if constexpr (NORM) {
-            // sum of squares: per thread over its pieces in order, the wave sum, then the four waves
-            // (0 + 1) + (2 + 3) -- the order of rmsnorm.hip
-            float ss = 0.f;
+            // sum of squares per row: per thread over its pieces in order, the wave sum, then the
+            // four waves (0 + 1) + (2 + 3) -- the order of rmsnorm.hip
 #pragma unroll
-            for (int q = 0; q < XPC; ++q)
-                if (tid + 256 * q < npieces) ss = sumsq8(xr[q], ss);
-            ss = wave_sum(ss);
-            if (lane == 0) red[wave] = ss;
-            __syncthreads();
-            r = rms_factor((red[0] + red[1]) + (red[2] + red[3]), ph.K, a.eps);
-        }
+            for (int m = 0; m < MR; ++m) {
+                float ss = 0.f;
 #pragma unroll
-        for (int q = 0; q < XPC; ++q) {
-            const int e = tid + 256 * q;
-            if (e < npieces) {
-                uint4 v = xr[q];
-                if constexpr (NORM) v = rms_scale8(v, gr[2 * q], gr[2 * q + 1], r);
-                xs[(e & 1) * xs_half + (e >> 1)] = v;
+                for (int q = 0; q < XPC; ++q)
+                    if (tid + 256 * q < npieces) ss = sumsq8(xr[m][q], ss);
+                ss = wave_sum(ss);
+                if (lane == 0) red[wave * MR + m] = ss;
             }
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                r[m] = rms_factor((red[m] + red[MR + m]) + (red[2 * MR + m] + red[3 * MR + m]), ph.K, a.eps);
         }
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int q = 0; q < XPC; ++q) {
+                const int e = tid + 256 * q;
+                if (e < npieces) {
+                    uint4 v = xr[m][q];
+                    if constexpr (NORM) v = rms_scale8(v, gr[2 * q], gr[2 * q + 1], r[m]);
+                    xs[(2 * m + (e & 1)) * xs_half + (e >> 1)] = v;
+                }
+            }
         __syncthreads();
     } else {
-        issue_w<T, RES, XG>(c0, lane, A);
+        issue_w<T, RES, XG, MR>(c0, lane, A);
         if constexpr (XG) issue_x(c0, lane, A);
     }
 
@@ -338,13 +389,13 @@ __global__ __launch_bounds__(256, 2) void gemv_stream_kernel(const StreamArgs a)
     Cursor c1 = cursor_next<T, CHAIN>(a, tab, c0, nw);
     int k = 0;
     for (; k + 2 <= nsteps; k += 2) {
-        issue_w<T, RES, XG>(c1, lane, B);
+        issue_w<T, RES, XG, MR>(c1, lane, B);
         Cursor c2 = cursor_next<T, CHAIN>(a, tab, c1, nw);
-        compute<T, XG, RES>(c0, lane, A, xs, xs_half, a0, a1);
+        compute<T, XG, RES, MR>(c0, lane, A, xs, xs_half, a0, a1);
         if constexpr (XG) issue_x(c1, lane, B);
-        issue_w<T, RES, XG>(c2, lane, A);
+        issue_w<T, RES, XG, MR>(c2, lane, A);
         c0 = cursor_next<T, CHAIN>(a, tab, c2, nw);       // the step after c2, for the next iteration
-        compute<T, XG, RES>(c1, lane, B, xs, xs_half, a0, a1);
+        compute<T, XG, RES, MR>(c1, lane, B, xs, xs_half, a0, a1);
         if constexpr (XG) issue_x(c2, lane, A);
         // rotate: the current step is c2 (in A), its successor c0
         const Cursor t = c0;
@@ -352,7 +403,7 @@ __global__ __launch_bounds__(256, 2) void gemv_stream_kernel(const StreamArgs a)
         c1 = t;
     }
     if (k < nsteps) {
-        compute<T, XG, RES>(c0, lane, A, xs, xs_half, a0, a1);
+        compute<T, XG, RES, MR>(c0, lane, A, xs, xs_half, a0, a1);
     }
 
 }
@@ -374,41 +425,61 @@ int plan_rows(StreamPhase& ph, int T) {
     return n;
 }
 
-template <int T, bool NORM, bool RES, int XPC>
+template <int T, bool NORM, bool RES, int XPC, int MR>
 hipError_t launch_single(const StreamArgs& a, int grid, size_t lds, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_stream_kernel<T, false, false, NORM, RES, XPC>), dim3(grid), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL((gemv_stream_kernel<T, false, false, NORM, RES, XPC, MR>), dim3(grid), dim3(256), lds, stream,
+                       a);
     return hipGetLastError();
 }
 
-template <int T, bool NORM, bool RES>
+template <int T, bool NORM, bool RES, int MR>
 hipError_t launch_single_x(int xpc, const StreamArgs& a, int grid, size_t lds, hipStream_t stream) {
     switch (xpc) {
-        case 2: return launch_single<T, NORM, RES, 2>(a, grid, lds, stream);
-        case 4: return launch_single<T, NORM, RES, 4>(a, grid, lds, stream);
-        case 8: return launch_single<T, NORM, RES, 8>(a, grid, lds, stream);
+        case 2: return launch_single<T, NORM, RES, 2, MR>(a, grid, lds, stream);
+        case 4: return launch_single<T, NORM, RES, 4, MR>(a, grid, lds, stream);
+        case 8:
+            // two activation rows with the fused RMSNorm over 8 staging pieces each would spill:
+            // never launched
+            if constexpr (MR == 2 && NORM) return hipErrorInvalidValue;
+            else return launch_single<T, NORM, RES, 8, MR>(a, grid, lds, stream);
         default:
-            // 4 rows with the fused RMSNorm over 16 staging pieces would spill: never launched
-            if constexpr (T == 4 && NORM) return hipErrorInvalidValue;
-            else return launch_single<T, NORM, RES, 16>(a, grid, lds, stream);
+            // 4 weight rows, or several activation rows, with 16 staging pieces would spill: never launched
+            if constexpr ((T == 4 && NORM) || MR > 1) return hipErrorInvalidValue;
+            else return launch_single<T, NORM, RES, 16, MR>(a, grid, lds, stream);
     }
 }
 
 // The fused RMSNorm (up projection) and the residual (down projection) never come together.
-template <int T>
+template <int T, int MR>
 hipError_t launch_single_t(bool norm, bool res, int xpc, const StreamArgs& a, int grid, size_t lds,
                            hipStream_t stream) {
-    if (norm) return launch_single_x<T, true, false>(xpc, a, grid, lds, stream);
-    if (res) return launch_single_x<T, false, true>(xpc, a, grid, lds, stream);
-    return launch_single_x<T, false, false>(xpc, a, grid, lds, stream);
+    if (norm) return launch_single_x<T, true, false, MR>(xpc, a, grid, lds, stream);
+    if (res) return launch_single_x<T, false, true, MR>(xpc, a, grid, lds, stream);
+    return launch_single_x<T, false, false, MR>(xpc, a, grid, lds, stream);
+}
+
+// x pieces (8 activations) per thread and row: 2 C pieces over 256 threads, in powers of two
+int stream_xpc(int C) {
+    const int need = (2 * C + 255) / 256;
+    return need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 8 ? 8 : 16));
 }
 
 }  // namespace
 
-bool gemv_stream_supported(int K) { return (K >> 4) <= kStreamMaxLdsChunks; }
+// M = 1: K up to 16 * kStreamMaxLdsChunks; M = 2: the two rows' staging pieces fit the registers
+// (8 per thread and row, 4 with the fused RMSNorm), i.e. K <= 16384 (8192).  (M = 4 as four
+// rows per weight step measured slower than the 4x4x4 MFMA kernel: config 2 at M = 4 72 against
+// 44 us.)
+bool gemv_stream_supported(int M, int K, bool norm) {
+    const int C = K >> 4;
+    if (M == 1) return C <= kStreamMaxLdsChunks;
+    if (M == 2) return stream_xpc(C) <= (norm ? 4 : 8);
+    return false;
+}
 
-hipError_t launch_gemv_stream(const uint16_t* x, int K, const GemvGroup* groups, int ngroups, hipStream_t stream,
-                              const Norm& norm) {
-    if (!gemv_stream_supported(K)) return hipErrorInvalidValue;
+hipError_t launch_gemv_stream(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
+                              hipStream_t stream, const Norm& norm) {
+    if (!gemv_stream_supported(M, K, norm.w != nullptr)) return hipErrorInvalidValue;
     const DeviceInfo& dev = device_info();
     StreamArgs a{};
     StreamPhase& ph = a.one;
@@ -417,13 +488,15 @@ hipError_t launch_gemv_stream(const uint16_t* x, int K, const GemvGroup* groups,
     ph.ngroups = ngroups;
     for (int i = 0; i < ngroups; ++i) {
         const GemvGroup& G = groups[i];
-        ph.g[i] = StreamGroup{G.W, G.ldw, G.s, G.y, G.epi.kind == kEpiResidual ? G.epi.res : nullptr, G.N, 0,
-                              G.epi.kind, 0};
+        ph.g[i] = StreamGroup{G.W,  G.ldw, G.s,        G.y, G.epi.kind == kEpiResidual ? G.epi.res : nullptr,
+                              G.N,  0,     G.epi.kind, (int)G.ldy, (int)G.epi.ldres, 0};
     }
+    a.ldx = ldx;
+    a.M = M;
     // rows per step: 2 (measured on the decode shapes, 3-46 MB: more, shorter-lived waves ramp
-    // a single launch faster), or 4 with tuning knob gemv.t = 4 (the chains' choice)
+    // a single launch faster), or 4 with tuning knob gemv.t = 4 (the chains' choice; M = 1)
     const int need_x = (2 * (K >> 4) + 255) / 256;      // x pieces per thread
-    const int T = tuning().gemv_t == 4 && !(norm.w && need_x > 8) ? 4 : 2;
+    const int T = M == 1 && tuning().gemv_t == 4 && !(norm.w && need_x > 8) ? 4 : 2;
     plan_slices(ph);
     const int nrg = plan_rows(ph, T);
     ph.g_begin = 0;
@@ -432,9 +505,10 @@ hipError_t launch_gemv_stream(const uint16_t* x, int K, const GemvGroup* groups,
     a.total_rg = nrg;
     a.norm_w = norm.w;
     a.eps = norm.eps;
-    // x in LDS: two halves of C chunks (rounded up to 64 so that the halves start 1 KiB apart)
+    // x in LDS: per row two halves of C chunks (rounded up to 64 so that the halves start 1 KiB
+    // apart)
     a.xs_half = (ph.C + 63) & ~63;
-    const size_t lds = (size_t)a.xs_half * 2 * sizeof(uint4);
+    const size_t lds = (size_t)M * a.xs_half * 2 * sizeof(uint4);
     // waves: about 3 steps each, at most one workgroup per CU (measured on 12544 x 3136: one
     // workgroup of 4 waves per CU, each wave double-buffering its rows, ramps faster than two)
     const Tuning& tn = tuning();
@@ -450,14 +524,13 @@ hipError_t launch_gemv_stream(const uint16_t* x, int K, const GemvGroup* groups,
         grid = (int)((waves + kWaves - 1) / kWaves);
     }
     if (tn.gemv_grid > 0) grid = tn.gemv_grid;
-    // x pieces (8 activations) per thread: 2 C pieces over 256 threads
-    const int need = (2 * ph.C + 255) / 256;
-    const int xpc = need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 8 ? 8 : 16));
+    const int xpc = stream_xpc(ph.C);
     bool res = false;
     for (int i = 0; i < ngroups; ++i) res = res || groups[i].epi.kind == kEpiResidual;
     if (norm.w && res) return hipErrorInvalidValue;
-    return T == 4 ? launch_single_t<4>(norm.w != nullptr, res, xpc, a, grid, lds, stream)
-                  : launch_single_t<2>(norm.w != nullptr, res, xpc, a, grid, lds, stream);
+    if (M == 2) return launch_single_t<2, 2>(norm.w != nullptr, res, xpc, a, grid, lds, stream);
+    return T == 4 ? launch_single_t<4, 1>(norm.w != nullptr, res, xpc, a, grid, lds, stream)
+                  : launch_single_t<2, 1>(norm.w != nullptr, res, xpc, a, grid, lds, stream);
 }
 
 int stream_chain_plan(StreamPhase* phases, int nphases) {
@@ -485,7 +558,7 @@ hipError_t stream_chain_grid(int total_rg, int* grid) {
     const DeviceInfo& dev = device_info();
     int per_cu = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, gemv_stream_kernel<kStreamChainT, true, true, false, false, 1>, 256, 0);
+        &per_cu, gemv_stream_kernel<kStreamChainT, true, true, false, false, 1, 1>, 256, 0);
     if (e != hipSuccess) return e;
     const int cap = tuning().chain_wgs >= 1 ? tuning().chain_wgs : 2;
     if (cap < per_cu) per_cu = cap;
@@ -503,7 +576,7 @@ hipError_t launch_gemv_stream_chain(const StreamPhase* tab, const int* wave_step
     a.wave_steps = wave_steps;
     a.nphases = nphases;
     a.total_rg = total_rg;
-    hipLaunchKernelGGL((gemv_stream_kernel<kStreamChainT, true, true, false, false, 1>), dim3(grid), dim3(256), 0,
+    hipLaunchKernelGGL((gemv_stream_kernel<kStreamChainT, true, true, false, false, 1, 1>), dim3(grid), dim3(256), 0,
                        stream, a);
     return hipGetLastError();
 }

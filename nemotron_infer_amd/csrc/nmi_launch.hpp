@@ -136,9 +136,11 @@ struct StreamGroup {
     int N;
     int rg_begin;           // first row group of the group within its phase
     int epi;                // kEpiNone / kEpiRelu2 / kEpiResidual
+    int ldy;                // elements between output rows (two activation rows)
+    int ldres;              // elements between residual rows (two activation rows)
     int pad;
 };
-static_assert(sizeof(StreamGroup) == 56, "56-byte group record");
+static_assert(sizeof(StreamGroup) == 64, "64-byte group record");
 struct StreamPhase {
     const uint16_t* x;
     int K;
@@ -158,11 +160,14 @@ struct StreamArgs {
     int nphases;
     int total_rg;
     int xs_half;                // LDS chunks per x half (single launches)
+    int64_t ldx;                // elements between activation rows (single launches, M > 1)
+    int M;                      // activation rows (single launches)
 };
-// Single launch (one phase) on the stream kernel; norm.w applies the RMSNorm to x while staging.
-bool gemv_stream_supported(int K);
-hipError_t launch_gemv_stream(const uint16_t* x, int K, const GemvGroup* groups, int ngroups, hipStream_t stream,
-                              const Norm& norm = Norm{});
+// Single launch (one phase) on the stream kernel for M = 1 or 2 activation rows (x row stride
+// ldx); norm.w applies the RMSNorm to x while staging.
+bool gemv_stream_supported(int M, int K, bool norm);
+hipError_t launch_gemv_stream(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
+                              hipStream_t stream, const Norm& norm = Norm{});
 // Chains: one launch per run of phases up to the next phase that waits for its predecessor.
 // stream_chain_plan fills the slices and row groups of a run's phases and returns its row
 // groups; stream_chain_grid sizes its grid (at most 2 workgroups per CU, or tuning knob

@@ -238,10 +238,10 @@ def test_m1_mfma_path_vs_gemv_full_size():
 @pytest.mark.parametrize("t", [1, 2, 4])
 @pytest.mark.parametrize("p", [2, 3, 4])
 def test_gemv_kernel_small_m(ks, t, p):
-    """The GEMV kernel computing 2..4 activation rows at once (skinny.path = 3): every
-    (K-split, rows per wave, chunks per lane) instantiation, M = 3 on the 4-row variant, K past
-    one LDS window (K = 10000 at M = 4 -> 625 chunks > 256), ragged N."""
-    for k, v in (("skinny.path", 3), ("gemv.ks", ks), ("gemv.t", t), ("gemv.p", p)):
+    """The multi-row GEMV kernel computing 2..4 activation rows at once (skinny.path = 3 with
+    gemv.multirow = 1): every (K-split, rows per wave, chunks per lane) instantiation, M = 3 on the
+    4-row variant, K past one LDS window (K = 10000 at M = 4 -> 625 chunks > 256), ragged N."""
+    for k, v in (("skinny.path", 3), ("gemv.multirow", 1), ("gemv.ks", ks), ("gemv.t", t), ("gemv.p", p)):
         _lib.tuning_set(k, v)
     try:
         for M, N, K in [(2, 300, 3136), (3, 77, 5120), (4, 130, 10000), (4, 1000, 208)]:
@@ -249,8 +249,50 @@ def test_gemv_kernel_small_m(ks, t, p):
             x, w, s = _case(M, N, K, 1000 * ks + 100 * t + 10 * p + M)
             assert_parity(_run(x, w, s, False), oracle_bits(x, w, s), f"ks={ks} t={t} p={p} M={M} N={N} K={K}")
     finally:
-        for k in ("gemv.ks", "gemv.t", "gemv.p"):
+        for k in ("gemv.ks", "gemv.t", "gemv.p", "gemv.multirow"):
             _lib.tuning_set(k, 0)
+
+
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_stream_kernel_small_m(M):
+    """The GEMV path at M = 2 (the stream kernel with two activation rows per weight step, every
+    staging size: 2, 4, 8 pieces per thread and row) and at M = 3, 4 (skinny.path = 3: the
+    multi-row kernel): ragged N, grouped matrices, strided x and y, against the oracle; nothing
+    stored past the groups' columns."""
+    _lib.tuning_set("skinny.path", 3)
+    try:
+        for N, K in [(300, 3136), (77, 5120), (1000, 208), (130, 8192), (3136, 1040)] + ([(50, 16384)] if M == 2 else []):
+            announce("stream_small_m", M, N, K)
+            x, w, s = _case(M, N, K, 500 * M + N + K)
+            assert_parity(_run(x, w, s, False), oracle_bits(x, w, s), f"M={M} N={N} K={K}", per_row_scales=True)
+        # grouped, strided x (ldx = K + 64) and y (ldy = sum N + 24)
+        K, Ns = 3136, (1000, 37, 517)
+        x, w0, s0 = _case(M, Ns[0], K, 9000 + M)
+        xbig = torch.zeros((M, K + 64), dtype=torch.bfloat16, device=DEV)
+        xbig[:, :K] = x_to_dev(x)
+        mats = [(w0, s0)] + [_case(M, n, K, 9100 + M + n)[1:] for n in Ns[1:]]
+        ldy = sum(Ns) + 24
+        ybig = torch.full((M, ldy), 9.0, dtype=torch.bfloat16, device=DEV)
+        L = _lib.lib()
+        groups = (_lib.LinearGroup * 4)()
+        devw = []
+        off = 0
+        for i, ((w, s), n) in enumerate(zip(mats, Ns)):
+            wd, sd = w_to_dev(w), s_to_dev(s)
+            devw.append((wd, sd))
+            groups[i].w_e4m3, groups[i].ldw, groups[i].w_scale = wd.data_ptr(), K, sd.data_ptr()
+            groups[i].y_bf16, groups[i].ldy, groups[i].N = ybig.data_ptr() + 2 * off, ldy, n
+            off += n
+        _lib.check(L.nmi_linear_fp8_w8a16_grouped(xbig.data_ptr(), K + 64, M, K, groups, len(Ns), None, 0, None),
+                   "grouped")
+        torch.cuda.synchronize()
+        off = 0
+        for (w, s), n in zip(mats, Ns):
+            assert_parity(bits(ybig[:, off:off + n]), oracle_bits(x, w, s), f"grouped M={M} N={n}", per_row_scales=True)
+            off += n
+        assert torch.all(ybig[:, off:] == 9.0)
+    finally:
+        _lib.tuning_set("skinny.path", 0)
 
 
 @pytest.mark.parametrize("M", [1, 3, 5, 8, 13, 16])
