@@ -452,6 +452,10 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
     // row 4 t + li.  Issued as explicit instructions: the compiler's own wait counts would merge
     // the paths into the loop (with and without a next window in flight) and wait for the next
     // window's loads too; completion is waited for by wait_loads_barrier and pinned by pin().
+    // The compiler takes the destination registers as written when the statement issues, so an
+    // instantiation must not spill: a register it moved to scratch or reused before the wait
+    // would still receive the load's data.  Every instantiation built here uses no scratch (a
+    // 16-wave variant that spilled faulted on the GPU and was removed).
     auto load_w = [&](u32x4 (&wv)[T][U], int w) {
         const int cb = c_begin + w * kWin + q * 16 * U + blk;
 #pragma unroll
