@@ -403,7 +403,8 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
  * workgroup count, "gemv.balance": 2 keeps the plain grid instead of one whose waves get equal row
  * counts, "sdpa.chunk": cache positions per workgroup of the attention decode, "gemm.tile" (1, 2:
  * short-prompt kernel, 20, 21, 24), "gemm.sk", "gemm.splits": workgroups splitting K in the
- * short-prompt GEMM (1: none), "gemm.short": f + 1 forces its tile form f (0..7),
+ * short-prompt GEMM (1: none), "gemm.short": f + 1 forces its tile form f (0..7), "gemm.sk_cap":
+ * workgroups per tile of the stream-K form at most (0: 2, -1: one workgroup per CU),
  * "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
  * "s4.dma": 2 selects the windowed form of the 4x4x4 skinny kernel instead of the pipelined one,
  * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace

@@ -141,10 +141,7 @@ hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGro
         case Path::Skinny4: return launch_skinny4_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
         case Path::Gemm: break;
     }
-    hipError_t e = hipSuccess;
-    for (int i = 0; i < ng && e == hipSuccess; ++i)
-        e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, st, g[i].epi, ws, ws_bytes);
-    return e;
+    return launch_gemm_grouped(x, ldx, M, K, g, ng, st, ws, ws_bytes);
 }
 
 }  // namespace nmi
@@ -393,6 +390,7 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "gemv.balance")) t.gemv_balance = value;
     else if (!std::strcmp(knob, "gemm.splits")) t.gemm_splits = value;
     else if (!std::strcmp(knob, "gemm.short")) t.gemm_short = value;
+    else if (!std::strcmp(knob, "gemm.sk_cap")) t.gemm_sk_cap = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

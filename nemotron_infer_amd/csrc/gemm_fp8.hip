@@ -198,6 +198,21 @@ struct GemmArgs {
     // DMA-fed kernel's epilogue: s 16-byte aligned; y and the residual 16-byte aligned with row
     // strides that keep every row so (16-byte row pieces)
     int vec_scale, vec16, vec16_res;
+    // DMA-fed kernel: the matrices sharing x (grouped launches; one for a plain GEMM).  Column
+    // band tn of the launch (tiles_n bands over all groups) belongs to the last group whose
+    // tn_begin <= tn, at columns (tn - tn_begin) * 256 of that group.
+    struct Group {
+        const uint8_t* W;
+        int64_t ldw;
+        const float* s;
+        uint16_t* y;
+        int64_t ldy;
+        const uint16_t* res;
+        int64_t ldres;
+        int N, tn_begin, epi, vec_scale, vec16, vec16_res;
+    };
+    int ngroups;
+    Group grp[kMaxGroups];
 };
 
 // ---------------------------------------------------------------------------------------
@@ -465,7 +480,7 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
                  : "memory", "m0");
 }
 
-template <bool SK>
+template <bool SK, bool GROUPED>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmArgs a) {
     constexpr int NT = 256, BK = kBK, W_STAGE = 256 * 64, TN = 4, TM = 4;
     __shared__ int sk_up;                           // stream-K: the flag the finisher waited for came
@@ -476,9 +491,48 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int h = lane >> 5, l32 = lane & 31;
-    const int M = a.M, N = a.N, K = a.K, KT = K / BK;
+    const int M = a.M, K = a.K, KT = K / BK;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
     int m0 = 0, n0 = 0;
+    // the current tile's matrix: for a grouped launch chosen per tile (wave-uniform), otherwise
+    // read straight from the kernel arguments wherever used (so nothing needs to stay live)
+    const uint8_t* gW_ = a.grp[0].W;
+    int64_t gldw_ = a.grp[0].ldw;
+    const float* gs_ = a.grp[0].s;
+    uint16_t* gy_ = a.grp[0].y;
+    int64_t gldy_ = a.grp[0].ldy, gldres_ = a.grp[0].ldres;
+    const uint16_t* gres_ = a.grp[0].res;
+    int gN_ = a.grp[0].N, gepi_ = a.grp[0].epi, gvs_ = a.grp[0].vec_scale, gv16_ = a.grp[0].vec16,
+        gv16r_ = a.grp[0].vec16_res;
+#define NMI_G(field, var) (GROUPED ? var : a.grp[0].field)
+#define gW NMI_G(W, gW_)
+#define gldw NMI_G(ldw, gldw_)
+#define gs NMI_G(s, gs_)
+#define gy NMI_G(y, gy_)
+#define gldy NMI_G(ldy, gldy_)
+#define gldres NMI_G(ldres, gldres_)
+#define gres NMI_G(res, gres_)
+#define gN NMI_G(N, gN_)
+#define gepi NMI_G(epi, gepi_)
+#define gvs NMI_G(vec_scale, gvs_)
+#define gv16 NMI_G(vec16, gv16_)
+#define gv16r NMI_G(vec16_res, gv16r_)
+    // column band tn of the launch -> its group's matrix and n0
+    auto select = [&](const int tn) __attribute__((always_inline)) {
+        if constexpr (GROUPED) {
+            int gi = 0;
+#pragma unroll
+            for (int i = 1; i < kMaxGroups; ++i)
+                if (i < a.ngroups && tn >= a.grp[i].tn_begin) gi = i;
+            gi = __builtin_amdgcn_readfirstlane(gi);
+            const GemmArgs::Group& G = a.grp[gi];
+            gW_ = G.W; gldw_ = G.ldw; gs_ = G.s; gy_ = G.y; gldy_ = G.ldy; gres_ = G.res; gldres_ = G.ldres;
+            gN_ = G.N; gepi_ = G.epi; gvs_ = G.vec_scale; gv16_ = G.vec16; gv16r_ = G.vec16_res;
+            n0 = (tn - G.tn_begin) * 256;
+        } else {
+            n0 = tn * 256;
+        }
+    };
 
     f32x16 acc[TN][TM];
     auto zero_acc = [&]() __attribute__((always_inline)) {
@@ -501,14 +555,14 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         const int lane = tid_r & 63, h = lane >> 5, l32 = lane & 31;
         // DMA sources, 32-bit byte offsets from the operand bases.  W instruction i of this wave:
         // rows (4 i + wave) * 16 + lane / 4, LDS chunk lane % 4; x instruction i: rows
-        // (4 i + wave) * 8 + lane / 8, LDS chunk lane % 8.  Rows past M or N are clamped (their
+        // (4 i + wave) * 8 + lane / 8, LDS chunk lane % 8.  Rows past M or gN are clamped (their
         // results are not stored).
         uint32_t woff[4], xoff[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = (4 * i + wave) * 16 + (lane >> 2);
             const int q = (lane & 3) ^ ((r >> 2) & 3);
-            woff[i] = (uint32_t)(min(n0 + r, N - 1) * a.ldw + 16 * q);
+            woff[i] = (uint32_t)(min(n0 + r, gN - 1) * gldw + 16 * q);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -521,7 +575,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         // DMA part 0: the W tile; parts 1, 2: the two halves of the x tile
         auto dma_to = [&](uint32_t base, int kt, int part, int k) {
             if (part == 0) {
-                dma16(a.W + (int64_t)kt * BK, woff[k], base + (4 * k + wave) * 16 * 64);
+                dma16(gW + (int64_t)kt * BK, woff[k], base + (4 * k + wave) * 16 * 64);
             } else {
                 const int i = 4 * (part - 1) + k;
                 dma16(reinterpret_cast<const uint8_t*>(a.x) + (int64_t)kt * BK * 2, xoff[i],
@@ -652,19 +706,19 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
     // Register r of lane l is n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32.
     constexpr int PITCH = 520;                      // bytes per staged row
     auto store = [&]() __attribute__((always_inline)) {
-        // tiles wholly inside N take the branch-free path (one uniform test)
-        const bool inner = n0 + 256 <= N;
+        // tiles wholly inside gN take the branch-free path (one uniform test)
+        const bool inner = n0 + 256 <= gN;
         // the lane's 64 scales: one batch of loads (data-parallel form), or one batch per
         // 32-column block i (stream-K form, which has fewer registers to spare)
         constexpr int SB = SK ? 1 : TN;
         auto load_scales = [&](int i0, float (&sc)[SB][4][4]) {
-            if (inner && a.vec_scale) {
+            if (inner && gvs) {
 #pragma unroll
                 for (int i = 0; i < SB; ++i)
 #pragma unroll
                     for (int gq = 0; gq < 4; ++gq) {
                         const float4 s4 =
-                            *reinterpret_cast<const float4*>(a.s + n0 + wn * 128 + (i0 + i) * 32 + 8 * gq + 4 * h);
+                            *reinterpret_cast<const float4*>(gs + n0 + wn * 128 + (i0 + i) * 32 + 8 * gq + 4 * h);
                         sc[i][gq][0] = s4.x; sc[i][gq][1] = s4.y; sc[i][gq][2] = s4.z; sc[i][gq][3] = s4.w;
                     }
             } else {
@@ -674,7 +728,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                     for (int gq = 0; gq < 4; ++gq)
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            sc[i][gq][r] = a.s[min(n0 + wn * 128 + (i0 + i) * 32 + 8 * gq + 4 * h + r, N - 1)];
+                            sc[i][gq][r] = gs[min(n0 + wn * 128 + (i0 + i) * 32 + 8 * gq + 4 * h + r, gN - 1)];
             }
         };
         float sc[SB][4][4];
@@ -700,8 +754,8 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         const int c8 = (tid & 31) * 8;
         const int n = n0 + c8;
         const int rows = min(256, M - m0);
-        const bool full = a.vec16 && (inner || n + 7 < N);
-        const bool res16 = a.epi.kind == kEpiResidual && full && a.vec16_res;
+        const bool full = gv16 && (inner || n + 7 < gN);
+        const bool res16 = gepi == kEpiResidual && full && gv16r;
 #pragma unroll
         for (int batch = 0; batch < 4; ++batch) {
             uint32_t w[8][4];
@@ -712,12 +766,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                 const uint2 v0 = src[0], v1 = src[1];
                 w[p][0] = v0.x; w[p][1] = v0.y; w[p][2] = v1.x; w[p][3] = v1.y;
             }
-            if (a.epi.kind == kEpiResidual) {
+            if (gepi == kEpiResidual) {
 #pragma unroll
                 for (int p = 0; p < 8; ++p) {
                     const int row = (tid >> 5) + 8 * (8 * batch + p);
                     if (row >= rows) continue;
-                    const uint16_t* rp = a.epi.res + (int64_t)(m0 + row) * a.epi.ldres + n;
+                    const uint16_t* rp = gres + (int64_t)(m0 + row) * gldres + n;
                     uint32_t rv[4];
                     if (res16) {
                         const uint4 r4 = *reinterpret_cast<const uint4*>(rp);
@@ -725,13 +779,13 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            rv[e] = (n + 2 * e < N ? (uint32_t)rp[2 * e] : 0u) |
-                                    ((n + 2 * e + 1 < N ? (uint32_t)rp[2 * e + 1] : 0u) << 16);
+                            rv[e] = (n + 2 * e < gN ? (uint32_t)rp[2 * e] : 0u) |
+                                    ((n + 2 * e + 1 < gN ? (uint32_t)rp[2 * e + 1] : 0u) << 16);
                     }
 #pragma unroll
                     for (int e = 0; e < 4; ++e) w[p][e] = add_bf16x2(w[p][e], rv[e]);
                 }
-            } else if (a.epi.kind == kEpiRelu2) {
+            } else if (gepi == kEpiRelu2) {
 #pragma unroll
                 for (int p = 0; p < 8; ++p)
 #pragma unroll
@@ -741,13 +795,13 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
             for (int p = 0; p < 8; ++p) {
                 const int row = (tid >> 5) + 8 * (8 * batch + p);
                 if (row >= rows) continue;
-                uint16_t* yp = a.y + (int64_t)(m0 + row) * a.ldy + n;
+                uint16_t* yp = gy + (int64_t)(m0 + row) * gldy + n;
                 if (full) {
                     *reinterpret_cast<uint4*>(yp) = uint4{w[p][0], w[p][1], w[p][2], w[p][3]};
                 } else {
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
-                        if (n + e < N) yp[e] = (uint16_t)(w[p][e >> 1] >> (16 * (e & 1)));
+                        if (n + e < gN) yp[e] = (uint16_t)(w[p][e >> 1] >> (16 * (e & 1)));
                 }
             }
         }
@@ -766,7 +820,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
         const int tn = tile / a.tiles_m;
         m0 = (tile - tn * a.tiles_m) * 256;
-        n0 = tn * 256;
+        select(tn);
         zero_acc();
         run(0, KT);
         store();
@@ -786,7 +840,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
             const int tile = xb + r * Gx + v;
             const int tm = tile / a.tiles_n;
             m0 = tm * 256;
-            n0 = (tile - tm * a.tiles_n) * 256;
+            select(tile - tm * a.tiles_n);
             zero_acc();
             run(0, KT);
             store();
@@ -802,7 +856,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
             const int kb = max(start, t0) - t0, ke = it - t0;
             const int tm = tile / a.tiles_n;
             m0 = tm * 256;
-            n0 = (tile - tm * a.tiles_n) * 256;
+            select(tile - tm * a.tiles_n);
             zero_acc();
             run(kb, ke);
             if (ke == KT && kb > 0) {
@@ -897,6 +951,19 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         }
     }
 }
+#undef gN
+#undef gW
+#undef gldw
+#undef gs
+#undef gy
+#undef gldy
+#undef gldres
+#undef gres
+#undef N
+#undef gepi
+#undef gvs
+#undef gv16
+#undef gv16r
 
 // Stream-K workspace: the flag slots share the 64 KiB counter region of the skinny kernel's
 // workspace layout (zero at rest in both; the last 4 bytes are the error word, NMI_WS_ERROR_OFFSET),
@@ -942,32 +1009,45 @@ bool dma_supported(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw
 // tiles), but 955 vs 1002 on up_proj (392 tiles) and 879 vs 1050 on qkv (224 tiles): with every
 // CU busy the clock drops (~1.85 vs ~2.3 GHz with 104 busy) and the partial tiles cost traffic,
 // so filling a partly idle last round does not pay.
-hipError_t launch_dma(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s, uint16_t* y,
-                      int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi, void* ws, size_t ws_bytes) {
+// ng > 1: matrices sharing x in one launch (their column bands follow one another in the
+// launch's tile numbering, each tile looks up its matrix).  Measured on MI355X: the attention
+// block's q | k | v at S = 2048 (160 + 32 + 32 tiles) as one launch took the block 496 -> 380 us.
+hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g, int ng, int M, int K,
+                             hipStream_t stream, void* ws, size_t ws_bytes) {
     constexpr int lds = kDmaStages * kDmaStage;
-    constexpr auto dp_kernel = &gemm_fp8_w8a16_dma_kernel<false>;
-    constexpr auto sk_kernel = &gemm_fp8_w8a16_dma_kernel<true>;
     static const hipError_t attr = [] {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(dp_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(sk_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    lds);
+        hipError_t e = hipSuccess;
+        for (const void* k : {reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<false, false>),
+                              reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<true, false>),
+                              reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<false, true>),
+                              reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<true, true>)})
+            if (e == hipSuccess) e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         return e;
     }();
     if (attr != hipSuccess) return attr;
+    if (ng < 1 || ng > kMaxGroups) return hipErrorInvalidValue;
+    const bool grouped = ng > 1;
+    const auto dp_kernel = grouped ? &gemm_fp8_w8a16_dma_kernel<false, true> : &gemm_fp8_w8a16_dma_kernel<false, false>;
+    const auto sk_kernel = grouped ? &gemm_fp8_w8a16_dma_kernel<true, true> : &gemm_fp8_w8a16_dma_kernel<true, false>;
     GemmArgs a{};
-    a.x = x; a.ldx = ldx; a.W = W; a.ldw = ldw; a.s = s; a.y = y; a.ldy = ldy;
-    a.M = M; a.N = N; a.K = K; a.epi = epi;
+    a.x = x; a.ldx = ldx;
+    a.M = M; a.K = K;
     a.tiles_m = (M + 255) / 256;
-    a.tiles_n = (N + 255) / 256;
+    a.ngroups = ng;
+    int tn = 0;
+    for (int i = 0; i < ng; ++i) {
+        const GemvGroup& G = g[i];
+        const Epi& e = G.epi;
+        a.grp[i] = GemmArgs::Group{G.W, G.ldw, G.s, G.y, G.ldy, e.kind == kEpiResidual ? e.res : nullptr, e.ldres, G.N, tn,
+                                   e.kind,
+                                   (reinterpret_cast<uintptr_t>(G.s) & 15) == 0 ? 1 : 0,
+                                   ((reinterpret_cast<uintptr_t>(G.y) & 15) == 0 && (G.ldy & 7) == 0) ? 1 : 0,
+                                   ((reinterpret_cast<uintptr_t>(e.res) & 15) == 0 && (e.ldres & 7) == 0) ? 1 : 0};
+        tn += (G.N + 255) / 256;
+    }
+    a.tiles_n = tn;
     const int T = a.tiles_m * a.tiles_n;
     a.per_xcd = (T + 7) / 8;
-    a.vec_store = ((reinterpret_cast<uintptr_t>(y) & 7) == 0 && (ldy & 3) == 0) ? 1 : 0;
-    a.vec_res = ((reinterpret_cast<uintptr_t>(epi.res) & 7) == 0 && (epi.ldres & 3) == 0) ? 1 : 0;
-    a.vec_scale = (reinterpret_cast<uintptr_t>(s) & 15) == 0 ? 1 : 0;
-    a.vec16 = ((reinterpret_cast<uintptr_t>(y) & 15) == 0 && (ldy & 7) == 0) ? 1 : 0;
-    a.vec16_res = ((reinterpret_cast<uintptr_t>(epi.res) & 15) == 0 && (epi.ldres & 7) == 0) ? 1 : 0;
     const int G = device_info().num_cu;             // one 144 KiB workgroup per CU
     const bool fits = ws && ws_bytes >= kSkFlagBytes + (size_t)G * kDmaPartialBytes && G % 8 == 0 &&
                       G * 4 <= (int)kSkFlagBytes && (int64_t)T * (K / kBK) < ((int64_t)1 << 31);
@@ -979,11 +1059,24 @@ hipError_t launch_dma(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
         a.sk_error = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + NMI_WS_ERROR_OFFSET);
         a.sk_spin = tuning().gemm_sk_spin > 0 ? tuning().gemm_sk_spin : (1 << 26);
         a.sk_lostflag = tuning().gemm_sk_lostflag == 1 ? 1 : 0;
-        hipLaunchKernelGGL(sk_kernel, dim3(G), dim3(256), lds, stream, a);
+        // at most two workgroups per tile of an XCD (tuning knob gemm.sk_cap: another cap; -1: one
+        // workgroup per CU).  Measured on MI355X: down_proj at M = 2048 (104 tiles) 174.7 -> 160.0
+        // us; the attention block's k and v projections (32 tiles each, cut 8 ways on all CUs)
+        // took the block 618 -> 496 us at S = 2048; caps of 3 and 4 in between.
+        int gx = G / 8;
+        const int cap = tuning().gemm_sk_cap == 0 ? 2 : tuning().gemm_sk_cap;
+        if (cap > 0) gx = std::min(gx, (T + 7) / 8 * cap);
+        hipLaunchKernelGGL(sk_kernel, dim3(8 * gx), dim3(256), lds, stream, a);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(dp_kernel, dim3(8 * a.per_xcd), dim3(256), lds, stream, a);
     return hipGetLastError();
+}
+
+hipError_t launch_dma(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw, const float* s, uint16_t* y,
+                      int64_t ldy, int M, int N, int K, hipStream_t stream, const Epi& epi, void* ws, size_t ws_bytes) {
+    const GemvGroup g{W, ldw, s, y, ldy, N, 0, 0, epi};
+    return launch_dma_groups(x, ldx, &g, 1, M, K, stream, ws, ws_bytes);
 }
 
 }  // namespace
@@ -1005,6 +1098,20 @@ hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream) {
 size_t gemm_workspace_bytes(int M) {
     if (M < 512 || tuning().gemm_sk == 2) return 0;
     return kSkFlagBytes + (size_t)device_info().num_cu * kDmaPartialBytes;
+}
+
+// A grouped GEMM (matrices sharing x) as one launch of the DMA-fed kernel where it takes every
+// matrix (M >= 512, automatic tile choice); otherwise one launch per matrix.
+hipError_t launch_gemm_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* g, int ng,
+                               hipStream_t stream, void* ws, size_t ws_bytes) {
+    bool one = ng > 1 && M >= 512 && tuning().gemm_tile == 0;
+    for (int i = 0; one && i < ng; ++i) one = dma_supported(x, ldx, g[i].W, g[i].ldw, M, g[i].N, K);
+    if (one) return launch_dma_groups(x, ldx, g, ng, M, K, stream, ws, ws_bytes);
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < ng && e == hipSuccess; ++i)
+        e = launch_gemm(x, ldx, g[i].W, g[i].ldw, g[i].s, g[i].y, g[i].ldy, M, g[i].N, K, stream, g[i].epi, ws,
+                        ws_bytes);
+    return e;
 }
 
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,

@@ -52,6 +52,7 @@ struct Tuning {
     int gemv_balance = 0;  // M = 1 stream GEMV (single launches): 2 turns off the grid sizing that makes row groups divide evenly
     int gemm_splits = 0;   // short-prompt GEMM (17 <= M < 512): workgroups splitting K (0: automatic)
     int gemm_short = 0;    // short-prompt GEMM: f + 1 forces kernel form f (0..7, gemm_short.hip)
+    int gemm_sk_cap = 0;   // GEMM stream-K: at most this many workgroups per tile (0: 2; -1: one per CU)
 };
 Tuning& tuning();
 
@@ -277,6 +278,10 @@ hipError_t launch_sdpa_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k
                                uint16_t* o, int64_t ldo, int S, int H, int H_KV, hipStream_t stream);
 
 hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream);
+// Several matrices sharing x: one launch of the DMA-fed kernel where it takes them all (M >= 512),
+// else launch_gemm per matrix.
+hipError_t launch_gemm_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* g, int ng,
+                               hipStream_t stream, void* ws, size_t ws_bytes);
 hipError_t launch_gemm(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw,
                        const float* s, uint16_t* y, int64_t ldy, int M, int N, int K,
                        hipStream_t stream, const Epi& epi = Epi{}, void* ws = nullptr, size_t ws_bytes = 0);

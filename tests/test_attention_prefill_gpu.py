@@ -86,9 +86,8 @@ def _composed(xd, dw, S):
     nw, qw, qs, kw, ks, vw, vs, ow, os_ = dw
     ws = S > 16        # as the block: its GEMMs (S > 16) get their split / stream-K workspace
     h = ops.rmsnorm_bf16(xd, nw, EPS)
-    q = ops.linear_fp8_w8a16(h, qw, qs, use_workspace=ws)
-    k = ops.linear_fp8_w8a16(h, kw, ks, use_workspace=ws)
-    v = ops.linear_fp8_w8a16(h, vw, vs, use_workspace=ws)
+    # q | k | v as the block runs them: one grouped dispatch (one launch at S >= 512)
+    q, k, v = ops.linear_fp8_w8a16_grouped(h, [(qw, qs), (kw, ks), (vw, vs)], use_workspace=ws)
     o = ops.sdpa_prefill_bf16(q, k, v, H_Q, H_KV)
     attn = ops.linear_fp8_w8a16(o, ow, os_, use_workspace=ws)
     return xd + attn, (h, q, k, v, o)

@@ -344,6 +344,72 @@ def test_dma_kernel_forms_agree_on_config3(_sk_reset):
     assert_parity(bits(y_sk), bits(y_dp), "stream-K vs data parallel")
 
 
+@pytest.fixture
+def _cap_reset():
+    yield
+    _lib.tuning_set("gemm.sk", 0)
+    _lib.tuning_set("gemm.sk_cap", 0)
+
+
+@pytest.mark.parametrize("cap", [-1, 1, 3])
+def test_stream_k_workgroups_per_tile_cap(cap, _cap_reset):
+    """Stream-K with another cap on the workgroups per tile (-1: one workgroup per CU, the tiles
+    cut thinnest; 1: each XCD's share of the tiles held by as many workgroups as tiles) on
+    down_proj's shape and few ragged tiles: within the parity gate of the oracle, repeated calls
+    bit-identical, the flag region left zero."""
+    _lib.tuning_set("gemm.sk_cap", cap)
+    for M, N, K in [(2048, 3136, 12544), (640, 1000, 1024)]:
+        announce("stream_k_cap", cap, M, N, K)
+        x, w, s = _case(M, N, K, 31 * cap + M + N, scales="log_uniform", act="relu2")
+        xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+        ws = _gemm_ws(M, N, K)
+        y1 = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+        y2 = torch.empty_like(y1)
+        _gemm_call(xd, wd, sd, y1, ws)
+        _gemm_call(xd, wd, sd, y2, ws)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(ws[:64 * 1024]) == 0, "flag region not re-armed"
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+        assert_parity(bits(y1), oracle_bits(x, w, s), f"cap={cap} M={M} N={N} K={K}", per_row_scales=True)
+
+
+@pytest.mark.parametrize("M,Ns,K", [(2048, (5120, 1024, 1024), 3136), (640, (1000, 256, 136), 1024),
+                                    (513, (300, 40), 192)], ids=["qkv_config3", "ragged_sk", "ragged_two"])
+def test_grouped_prefill_is_one_launch_of_the_dma_kernel(M, Ns, K, _sk_reset):
+    """Matrices sharing x at M >= 512 (q|k|v at prefill) run as one launch of the DMA-fed kernel,
+    their column bands one after another in the launch's tile numbering.  The outputs go to
+    column views of one [M, sum N] buffer (the attention block's layout), ragged N in each
+    group.  In the data-parallel form (each tile one workgroup over all of K) every group equals
+    its separate call bit for bit; in the default form (stream-K where the tiles are few) each
+    matches the oracle within the parity gate; the flag region is left zero."""
+    announce("grouped_prefill", M, Ns, K)
+    cases = [_case(M, N, K, 17 * i + M + N, scales="log_uniform") for i, N in enumerate(Ns)]
+    x = cases[0][0]
+    xd = x_to_dev(x)
+    wd = [(w_to_dev(w), s_to_dev(s)) for _, w, s in cases]
+    total = sum(Ns)
+    offs = np.cumsum((0,) + Ns)
+    ybig = torch.full((M, total + 8), 3.0, dtype=torch.bfloat16, device=DEV)
+    outs = [ybig[:, offs[i]:offs[i + 1]] for i in range(len(Ns))]
+    ws = _gemm_ws(M, total, K)
+    L = _lib.lib()
+    arr = (_lib.LinearGroup * len(Ns))()
+    for i, ((w, s), y) in enumerate(zip(wd, outs)):
+        arr[i] = _lib.LinearGroup(w.data_ptr(), w.stride(0), s.data_ptr(), y.data_ptr(), y.stride(0), w.shape[0])
+    for sk in (2, 0):
+        _lib.tuning_set("gemm.sk", sk)
+        _lib.check(L.nmi_linear_fp8_w8a16_grouped(xd.data_ptr(), K, M, K, arr, len(Ns), ws.data_ptr(), ws.numel(),
+                                                  None), "grouped (column views)")
+        separate = [ops.linear_fp8_w8a16(xd, w, s) for w, s in wd]
+        torch.cuda.synchronize()
+        assert torch.all(ybig[:, total:] == 3.0)
+        assert torch.count_nonzero(ws[:64 * 1024]) == 0, "flag region not re-armed"
+        for i, ((_, w, s), yg, ys) in enumerate(zip(cases, outs, separate)):
+            if sk == 2:
+                assert np.array_equal(bits(yg), bits(ys)), f"group {i} sk={sk}"
+            assert_parity(bits(yg), oracle_bits(x, w, s), f"grouped {i} sk={sk} N={Ns[i]}", per_row_scales=True)
+
+
 def test_stream_k_lost_flag_sets_the_error_word(_sk_reset):
     """The stream-K wait is bounded: with the contributors' flags never raised (test knob
     gemm.sk_lostflag) and a short poll limit (gemm.sk_spin), every finisher gives up, the
