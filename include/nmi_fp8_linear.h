@@ -400,18 +400,20 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
  * Tuning knobs for sweeps ("gemv.ks", "gemv.t", "gemv.p", "gemv.xg": schedule of the multi-row
  * GEMV kernel (M = 2, or M = 1 with "gemv.multirow" = 1), "gemv.t" = 4 also 4 rows per step for
  * the M = 1 stream kernel, "gemv.wgs": its workgroups per CU (1, 2), "gemv.grid": its exact
- * workgroup count, "gemv.balance": 2 keeps the plain grid instead of one whose waves get equal row
- * counts, "sdpa.chunk": cache positions per workgroup of the attention decode, "gemm.tile" (1, 2:
- * short-prompt kernel, 20, 21, 24), "gemm.sk", "gemm.splits": workgroups splitting K in the
- * short-prompt GEMM (1: none), "gemm.short": f + 1 forces its tile form f (0..7), "gemm.sk_cap":
- * workgroups per tile of the stream-K form at most (0: 2, -1: one workgroup per CU),
- * "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
+ * workgroup count, "gemv.balance": 2 keeps the plain grid instead of one whose waves get equal
+ * row counts, "sdpa.chunk": cache positions per workgroup of the attention decode, "gemm.tile"
+ * (1, 2: short-prompt kernel, 20, 21, 24), "gemm.sk", "gemm.splits": workgroups splitting K in
+ * the short-prompt GEMM (1: none), "gemm.short": f + 1 forces its tile form f (0..7),
+ * "gemm.sk_cap": workgroups per tile of the stream-K form at most (0: 2, -1: one workgroup per
+ * CU), "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
  * "s4.dma": 2 selects the windowed form of the 4x4x4 skinny kernel instead of the pipelined one,
  * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace
- * nmi_linear_workspace_bytes then reports), "chain.wgs": workgroups per CU of a GEMV chain
- * created afterwards); 0 restores the automatic choice.  Process-wide, not thread-safe against
- * concurrent launches; results do not depend on them beyond float32 summation order.  No
- * counterpart in the reference (its launch shapes are compile-time constants,
+ * nmi_linear_workspace_bytes then reports), "s16": the 16x16x32 skinny kernel (0: automatic, from
+ * M = 5 by K, 1: for 2 <= M <= 16, 2: never), "s16.r": its row tiles of 16 (1) or 32 (2),
+ * "s16.b": 4 load batches of four slabs, "s16.w": 16 waves per workgroup, "chain.wgs": workgroups
+ * per CU of a GEMV chain created afterwards); 0 restores the automatic choice.  Process-wide, not
+ * thread-safe against concurrent launches; results do not depend on them beyond float32 summation
+ * order.  No counterpart in the reference (its launch shapes are compile-time constants,
  * ops/gemv.cuh:100-103).
  */
 int nmi_tuning_set(const char* knob, int value);

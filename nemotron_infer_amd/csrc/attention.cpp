@@ -80,8 +80,9 @@ struct FwdLayout {
 // partials below): the largest of the q, k, v (launched one by one on the GEMM path) and o needs.
 size_t gemm_region(int M, int hidden, int QD, int KD) {
     if (choose_path(M) != Path::Gemm) return 0;
-    return round256(std::max(std::max(linear_workspace_bytes(M, QD, hidden), linear_workspace_bytes(M, KD, hidden)),
-                             linear_workspace_bytes(M, hidden, QD)));
+    const size_t qkv = std::max(linear_workspace_bytes(M, (int64_t)QD + 2 * (int64_t)KD, hidden),
+                                std::max(linear_workspace_bytes(M, QD, hidden), linear_workspace_bytes(M, KD, hidden)));
+    return round256(std::max(qkv, linear_workspace_bytes(M, hidden, QD)));
 }
 
 FwdLayout fwd_layout(int S, int hidden, int n_heads, int n_kv) {

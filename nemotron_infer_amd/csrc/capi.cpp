@@ -138,7 +138,11 @@ hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGro
     switch (path) {
         case Path::Gemv: return launch_gemv_grouped(x, ldx, M, K, g, ng, st, norm);
         case Path::Skinny: return launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
-        case Path::Skinny4: return launch_skinny4_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+        case Path::Skinny4: {
+            hipError_t e = hipSuccess;
+            if (launch_skinny16_grouped(x, ldx, M, K, g, ng, st, &e)) return e;
+            return launch_skinny4_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+        }
         case Path::Gemm: break;
     }
     return launch_gemm_grouped(x, ldx, M, K, g, ng, st, ws, ws_bytes);
@@ -391,6 +395,10 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "gemm.splits")) t.gemm_splits = value;
     else if (!std::strcmp(knob, "gemm.short")) t.gemm_short = value;
     else if (!std::strcmp(knob, "gemm.sk_cap")) t.gemm_sk_cap = value;
+    else if (!std::strcmp(knob, "s16")) t.s16 = value;
+    else if (!std::strcmp(knob, "s16.r")) t.s16_r = value;
+    else if (!std::strcmp(knob, "s16.b")) t.s16_b = value;
+    else if (!std::strcmp(knob, "s16.w")) t.s16_w = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

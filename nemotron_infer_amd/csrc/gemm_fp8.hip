@@ -1082,16 +1082,16 @@ hipError_t launch_dma(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t 
 }  // namespace
 
 namespace {
-__global__ __launch_bounds__(256) void sk_flags_clear_kernel(uint32_t* __restrict__ flags, int n) {
-    for (int i = (int)threadIdx.x; i < n; i += 256) flags[i] = 0u;
+__global__ __launch_bounds__(256) void sk_flags_clear_kernel(uint4* __restrict__ flags) {
+#pragma unroll
+    for (int i = 0; i < (int)(kSkFlagBytes / 16 / 256); ++i) flags[i * 256 + threadIdx.x] = uint4{0u, 0u, 0u, 0u};
 }
 }  // namespace
 
-// Zeroes the flags the stream-K forms use: one per workgroup of their grid (num_cu x the
-// kernel's occupancy, at most 4 for any of them), not the whole 64 KiB region.
+// Zeroes the whole 64 KiB flag region (the stream-K flags and the error word) with one workgroup
+// of 16-byte stores.
 hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream) {
-    const int n = (int)std::min<size_t>((size_t)4 * device_info().num_cu, kSkFlagBytes / 4);
-    hipLaunchKernelGGL(sk_flags_clear_kernel, dim3(1), dim3(256), 0, stream, static_cast<uint32_t*>(ws), n);
+    hipLaunchKernelGGL(sk_flags_clear_kernel, dim3(1), dim3(256), 0, stream, static_cast<uint4*>(ws));
     return hipGetLastError();
 }
 

@@ -53,6 +53,10 @@ struct Tuning {
     int gemm_splits = 0;   // short-prompt GEMM (17 <= M < 512): workgroups splitting K (0: automatic)
     int gemm_short = 0;    // short-prompt GEMM: f + 1 forces kernel form f (0..7, gemm_short.hip)
     int gemm_sk_cap = 0;   // GEMM stream-K: at most this many workgroups per tile (0: 2; -1: one per CU)
+    int s16 = 0;           // 16x16x32 skinny kernel: 0 automatic (M >= 5, by K), 1 for 2 <= M <= 16, 2 never
+    int s16_r = 0;         // 16x16x32 skinny kernel: row tiles of 16 per workgroup (1, 2; 0: by rows)
+    int s16_b = 0;         // 16x16x32 skinny kernel: slabs per load batch (4; 0: 2)
+    int s16_w = 0;         // 16x16x32 skinny kernel: waves per workgroup (16; 0: 8)
 };
 Tuning& tuning();
 
@@ -105,6 +109,14 @@ hipError_t launch_skinny_grouped(const uint16_t* x, int64_t ldx, int M, int K, c
 size_t skinny4_workspace_bytes(int M, int K, int64_t total_rows, int num_cu);
 hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
                                   int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+// M <= 16 on 16x16x32 MFMA, one row tile per workgroup with K split between its waves
+// (skinny16_fp8.hip): taken for the M and K skinny16_wanted() accepts when the operands suit it
+// (K % 64 == 0, 16-byte aligned x rows and weight rows).  launch_skinny16_grouped returns false,
+// launching nothing, when the kernel cannot take the call; otherwise *err is the launch's status.
+bool skinny16_wanted(int M, int K);
+bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
+                             hipStream_t stream, hipError_t* err);
 
 // The GEMV kernel for 1 <= M <= 4 activation rows (x row stride ldx elements).  With norm.w
 // set (only where gemv_norm_supported(M, K)), x is the raw input and every workgroup applies

@@ -1,0 +1,248 @@
+// skinny16_fp8.hip -- fp8 (OCP e4m3) W8A16 linear for small M (up to 16 activation rows) on
+// 16x16x32 bf16 MFMA (gfx950): one row tile per workgroup, K split between its waves.
+//
+//   y[m,n] = bf16_rne( (sum_k float(W[n,k]) * float(x[m,k])) * s[n] )
+//
+// The crossover between the reference's M == 1 GEMV (ops/gemv.cuh:48-104) and its prefill GEMM
+// (ops/gemm.cuh:325-403, reached for every M > 1 at model/mlp_block.cuh:149-171).  Up to M = 16
+// the work is bound by streaming W from HBM (<= 31.5 flop/B), and at the decode shapes a launch
+// moves only 3-40 MB, so what sets its time is how many memory round trips lie on its critical
+// path and how many bytes each CU keeps in flight.
+//
+// * A workgroup owns one row tile (16 R weight rows) over all of K; its NW waves split K into
+//   contiguous runs of 64-k slabs.  Lane (r, p) = (lane % 16, lane / 16) loads, per slab, 16
+//   codes of row 16 j + r (j < R) at k = 16 p (one instruction: 16 rows x 64 contiguous bytes)
+//   and the 32 bytes x[r][16 p .. 16 p + 15] straight from global memory (the activations are a
+//   few hundred KiB, read by every workgroup: L2 hits).  Codes 0-7 and 8-15 feed two
+//   v_mfma_f32_16x16x32_bf16 (A = weights: row r, k 8 p + e; B = activations: column m = r);
+//   D[n][m] lands as rows 4 p + i, column r of lane (r, p).  Columns m >= M read row M - 1 and
+//   are not stored.
+// * Loads go in two batches of B slabs, the next in flight while this one is multiplied; every
+//   batch is issued (slabs past the wave's run read one word every lane shares), so the
+//   compiler's wait counts are exact on every path.  A short K has its whole run in flight at
+//   once: the launch is one weight round trip, the products, and the store.
+// * The waves' sums meet in LDS and are added in wave order (a fixed order: results do not depend
+//   on timing), then the per-row scale, one bf16 rounding and the epilogue.  No workspace, no
+//   inter-workgroup communication.
+#include "nmi_device.hpp"
+#include "nmi_launch.hpp"
+
+#include <algorithm>
+
+namespace nmi {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct S16Group {
+    const uint8_t* W;
+    int64_t ldw;
+    const float* s;
+    uint16_t* y;
+    int64_t ldy;
+    const uint16_t* res;
+    int64_t ldres;
+    int N;
+    int tile_begin;      // first row tile of this matrix in the launch's tile numbering
+    int epi;
+    int vec;             // s 16-byte aligned, y (and res) 8-byte aligned with row strides % 4 == 0
+};
+
+struct S16Args {
+    const uint16_t* x;
+    int64_t ldx;
+    int M, K;
+    int ngroups;
+    S16Group g[kMaxGroups];
+};
+
+// Stores four outputs n0 .. n0 + 3 of activation row m (lane layout of the MFMA result).
+__device__ __forceinline__ void s16_store(const S16Group& G, int m, int n0, const f32x4 v) {
+    if (n0 >= G.N) return;
+    if (G.vec && n0 + 3 < G.N) {
+        const float4 sc = *reinterpret_cast<const float4*>(G.s + n0);
+        uint2 rr{0u, 0u};
+        if (G.epi == kEpiResidual) rr = *reinterpret_cast<const uint2*>(G.res + (int64_t)m * G.ldres + n0);
+        const uint16_t o0 = epilogue(v[0], sc.x, G.epi, (uint16_t)(rr.x & 0xFFFFu));
+        const uint16_t o1 = epilogue(v[1], sc.y, G.epi, (uint16_t)(rr.x >> 16));
+        const uint16_t o2 = epilogue(v[2], sc.z, G.epi, (uint16_t)(rr.y & 0xFFFFu));
+        const uint16_t o3 = epilogue(v[3], sc.w, G.epi, (uint16_t)(rr.y >> 16));
+        *reinterpret_cast<uint2*>(G.y + (int64_t)m * G.ldy + n0) =
+            uint2{(uint32_t)o0 | ((uint32_t)o1 << 16), (uint32_t)o2 | ((uint32_t)o3 << 16)};
+        return;
+    }
+    uint16_t rr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        rr[i] = (G.epi == kEpiResidual && n0 + i < G.N) ? G.res[(int64_t)m * G.ldres + n0 + i] : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (n0 + i < G.N) G.y[(int64_t)m * G.ldy + n0 + i] = epilogue(v[i], G.s[n0 + i], G.epi, rr[i]);
+}
+
+// R: row tiles of 16 per workgroup; B: slabs per batch (two batches in flight per wave); NW: waves.
+template <int R, int B, int NW>
+__global__ __launch_bounds__(64 * NW) void skinny16_kernel(const S16Args a) {
+    __shared__ f32x4 red[NW][R][64];
+
+    const int tile = blockIdx.x;
+    int gi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < a.ngroups && tile >= a.g[i].tile_begin) gi = i;
+    const S16Group& G = a.g[gi];
+    const int row0 = (tile - G.tile_begin) * 16 * R;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int r = lane & 15, p = lane >> 4;
+    const int M = a.M;
+    const int S = a.K >> 6;
+    const int s_beg = wave * S / NW, s_end = (wave + 1) * S / NW;
+    const int n = s_end - s_beg;
+    const int nb = (n + B - 1) / B;
+
+    const uint8_t* wrow[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) wrow[j] = G.W + (int64_t)min(row0 + 16 * j + r, G.N - 1) * G.ldw + 16 * p;
+    const uint16_t* xrow = a.x + (int64_t)min(r, M - 1) * a.ldx + 16 * p;
+    const uint8_t* wdummy = G.W;
+    const uint16_t* xdummy = a.x;
+
+    struct Batch {
+        u32x4 w[B][R];
+        u32x4 x[B][2];
+    };
+    auto load = [&](Batch& bt, int b) {
+#pragma unroll
+        for (int e = 0; e < B; ++e) {
+            const int i = b * B + e;
+            const int s = s_beg + i;
+            const bool ok = i < n;
+            const uint16_t* xp = ok ? xrow + s * 64 : xdummy;
+            bt.x[e][0] = *reinterpret_cast<const u32x4*>(xp);
+            bt.x[e][1] = *reinterpret_cast<const u32x4*>(ok ? xp + 8 : xdummy);
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+                bt.w[e][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ok ? wrow[j] + s * 64 : wdummy));
+        }
+    };
+
+    f32x4 acc[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](const Batch& bt, int b) {
+#pragma unroll
+        for (int e = 0; e < B; ++e) {
+            if (b * B + e >= n) break;
+            const bf16x8 B0 = __builtin_bit_cast(bf16x8, bt.x[e][0]);
+            const bf16x8 B1 = __builtin_bit_cast(bf16x8, bt.x[e][1]);
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const u32x4 w = bt.w[e][j];
+                const uint2 c0 = e4m3x4_to_bf16(w[0]), c1 = e4m3x4_to_bf16(w[1]);
+                const uint2 c2 = e4m3x4_to_bf16(w[2]), c3 = e4m3x4_to_bf16(w[3]);
+                const bf16x8 A0 = __builtin_bit_cast(bf16x8, uint4{c0.x, c0.y, c1.x, c1.y});
+                const bf16x8 A1 = __builtin_bit_cast(bf16x8, uint4{c2.x, c2.y, c3.x, c3.y});
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, acc[j], 0, 0, 0);
+            }
+        }
+    };
+
+    Batch ba, bb;
+    load(ba, 0);
+    load(bb, 1);
+    for (int b = 0; b < nb; b += 2) {
+        consume(ba, b);
+        load(ba, b + 2);
+        consume(bb, b + 1);
+        load(bb, b + 3);
+    }
+
+    // the waves' sums in wave order, then the epilogue (wave j stores row tile j)
+#pragma unroll
+    for (int j = 0; j < R; ++j) red[wave][j][lane] = acc[j];
+    __syncthreads();
+    if (wave < R) {
+        f32x4 v = red[0][wave][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 u = red[w][wave][lane];
+            v = f32x4{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
+        }
+        if (r < M) s16_store(G, r, row0 + 16 * wave + 4 * p, v);
+    }
+}
+
+template <int R, int B, int NW>
+hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
+    int tb = 0;
+    for (int i = 0; i < ng; ++i) {
+        const GemvGroup& G = groups[i];
+        const Epi& e = G.epi;
+        const bool res = e.kind == kEpiResidual;
+        const bool vec = (reinterpret_cast<uintptr_t>(G.s) & 15) == 0 && (reinterpret_cast<uintptr_t>(G.y) & 7) == 0 &&
+                         (G.ldy & 3) == 0 &&
+                         (!res || ((reinterpret_cast<uintptr_t>(e.res) & 7) == 0 && (e.ldres & 3) == 0));
+        a.g[i] = S16Group{G.W, G.ldw, G.s, G.y, G.ldy, res ? e.res : nullptr, e.ldres, G.N, tb, e.kind, vec ? 1 : 0};
+        tb += (G.N + 16 * R - 1) / (16 * R);
+    }
+    if (tb < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((skinny16_kernel<R, B, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Where this kernel is taken by default (tuning knob s16 = 1: every 2 <= M <= 16, 2: never).
+// Measured on MI355X against the 4x4x4 kernel (kernel time, config 2's shapes): at M = 16 faster
+// for q | k | v, k alone (8.1 vs 11.3 us), o (12.1 vs 13.1) and up (17.8 vs 23.4), even on down
+// (K = 12544: 21.5 vs 21.3); at M = 8 faster for q (9.8 vs 10.6), k (7.1 vs 8.0) and up (16.0 vs
+// 16.6) but slower for o (10.2 vs 9.8, K = 5120) and down (17.7 vs 16.6): the activation reads
+// per weight byte grow with M / R, and so does what the kernel saves.
+bool skinny16_wanted(int M, int K) {
+    const int knob = tuning().s16;
+    if (knob == 2 || M > 16 || M < 2) return false;
+    if (knob == 1) return true;
+    return M >= 5 && (K <= 4096 || (M >= 12 && K <= 8192));
+}
+
+bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
+                             hipStream_t stream, hipError_t* err) {
+    if (!skinny16_wanted(M, K) || ngroups < 1 || ngroups > kMaxGroups || K < 64 || K % 64 != 0) return false;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (ldx & 7) != 0) return false;
+    int64_t rows = 0;
+    for (int i = 0; i < ngroups; ++i) {
+        if ((reinterpret_cast<uintptr_t>(groups[i].W) & 15) != 0 || (groups[i].ldw & 15) != 0) return false;
+        rows += groups[i].N;
+    }
+    S16Args a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.M = M;
+    a.K = K;
+    a.ngroups = ngroups;
+    // row tiles of 32 from 4096 rows (half the activation reads per weight byte; measured faster
+    // on q | k | v and up), else 16 (more workgroups); eight waves; batches of two slabs.  Tuning
+    // knobs: s16.r (1, 2) forces the row tile, s16.b = 4 batches of four, s16.w = 16 waves.
+    const Tuning& tn = tuning();
+    const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : (rows >= 4096 ? 2 : 1);
+    const int Bt = tn.s16_b == 4 ? 4 : 2, NW = tn.s16_w == 16 ? 16 : 8;
+    const int form = (R == 2 ? 4 : 0) + (Bt == 2 ? 2 : 0) + (NW == 16 ? 1 : 0);
+    switch (form) {
+        case 0: *err = s16_launch<1, 4, 8>(a, groups, ngroups, stream); break;
+        case 1: *err = s16_launch<1, 4, 16>(a, groups, ngroups, stream); break;
+        case 2: *err = s16_launch<1, 2, 8>(a, groups, ngroups, stream); break;
+        case 3: *err = s16_launch<1, 2, 16>(a, groups, ngroups, stream); break;
+        case 4: *err = s16_launch<2, 4, 8>(a, groups, ngroups, stream); break;
+        case 5: *err = s16_launch<2, 2, 16>(a, groups, ngroups, stream); break;   // <2, 4, 16> would spill
+        case 6: *err = s16_launch<2, 2, 8>(a, groups, ngroups, stream); break;
+        default: *err = s16_launch<2, 2, 16>(a, groups, ngroups, stream); break;
+    }
+    return true;
+}
+
+}  // namespace nmi

@@ -73,12 +73,12 @@ def _dev(nw, upw, ups, dnw, dns):
     return (torch.from_numpy(nw).to(DEV), w_to_dev(upw), s_to_dev(ups), w_to_dev(dnw), s_to_dev(dns))
 
 
-def _composed(x, nw, upw, ups, dnw, dns):
-    # The block hands its GEMMs (M > 16) a workspace -- the short-prompt kernel's K split for
-    # 17 <= M < 512, stream-K for the few tiles of the down projection from M = 512 -- and its
-    # smaller-M linears none; the composition does the same, so that both run the same kernels in
-    # the same form (same float32 summation order).
-    ws = x.shape[0] > 16
+def _composed(x, nw, upw, ups, dnw, dns, ws=True):
+    # The block hands its linears a workspace -- the 16x16x32 skinny kernel's partials for
+    # 5 <= M <= 16, the short-prompt kernel's K split for 17 <= M < 512, stream-K for the few tiles
+    # of the down projection from M = 512 (the other kernels ignore it; the block gives the split-K
+    # 16x16x32 kernel of skinny.path = 1 none); the composition does the same, so that both run
+    # the same kernels in the same form (same float32 summation order).
     h = ops.rmsnorm_bf16(x, nw, EPS)
     up = ops.linear_fp8_w8a16(h, upw, ups, use_workspace=ws)
     r = torch.relu(up)
@@ -145,7 +145,7 @@ def check_block(x, got, nw, upw, ups, dnw, dns, eps, label):
     dev = _dev(nw, upw, ups, dnw, dns)
     xd = x_to_dev(x)
     h = ops.rmsnorm_bf16(xd, dev[0], eps)
-    up = ops.linear_fp8_w8a16(h, dev[1], dev[2], use_workspace=x.shape[0] > 16)   # as the block
+    up = ops.linear_fp8_w8a16(h, dev[1], dev[2], use_workspace=True)   # as the block
     r_ = torch.relu(up)
     act = bits(r_ * r_)
     h, up = bits(h), bits(up)
@@ -189,7 +189,7 @@ def test_block_equals_composition_under_knobs(knobs, Ms):
         announce("mlp_block_knobs", knobs, M)
         x = x_to_dev(_act(M, HIDDEN, 300 + M))
         got = ops.mlp_forward_fp8(x, *dev, eps=EPS)
-        ref = _composed(x, *dev)
+        ref = _composed(x, *dev, ws=knobs.get("skinny.path") != 1 and knobs.get("m1.path") != 2)
         assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (knobs, M)
 
 
@@ -213,7 +213,7 @@ def test_block_norm_fusion_limits(hidden, Ms):
         assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (hidden, M)
 
 
-@pytest.mark.parametrize("M", [1, 3, 64, 520])
+@pytest.mark.parametrize("M", [1, 3, 8, 64, 520])
 def test_block_in_place_and_bump_allocator(M):
     announce("mlp_block_inplace_alloc", M)
     dev = _dev(*_weights(HIDDEN, INTER))

@@ -1,0 +1,176 @@
+"""GPU parity of the 16x16x32 skinny kernel (skinny16_fp8.hip: M <= 16, one row tile per
+workgroup, K split between its eight waves whose sums are added in wave order), against the
+torch fp32 dequant-then-F.linear oracle.
+
+Tolerance: rel_l2 <= 1e-3 and max |diff| <= 2 bf16 ulp at max(|ref|, 2^-8 rms(ref)) (plus
+rel_l2 over all elements where the scales are per tensor).  Size-independent properties:
+repeated calls are bit-identical (fixed summation order), graph replays equal the eager call,
+and nothing outside the output views is written.
+"""
+import numpy as np
+import pytest
+import torch
+
+from nemotron_infer_amd import _lib, ops, synth
+from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_to_dev, w_to_dev,
+                            x_to_dev)
+
+pytestmark = pytest.mark.gpu
+
+KNOBS = ("s16", "s16.r", "s16.b", "s16.w", "skinny.path")
+
+
+@pytest.fixture(autouse=True)
+def _reset_tuning():
+    for k in KNOBS:
+        _lib.tuning_set(k, 0)
+    yield
+    for k in KNOBS:
+        _lib.tuning_set(k, 0)
+
+
+def _case(M, N, K, seed, scales="log_uniform", act="normal"):
+    w, s = synth.make_weight(N, K, seed, "cpu", scales=scales)
+    x = synth.make_act(M, K, seed + 1, "cpu", kind=act)
+    return x.view(torch.int16).numpy().view(np.uint16), w.numpy(), s.numpy()
+
+
+def _check(M, N, K, seed, label, scales="log_uniform", act="normal"):
+    x, w, s = _case(M, N, K, seed, scales=scales, act=act)
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    y1 = ops.linear_fp8_w8a16(xd, wd, sd)
+    y2 = ops.linear_fp8_w8a16(xd, wd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), f"{label}: not deterministic"
+    assert_parity(bits(y1), oracle_bits(x, w, s), label, per_row_scales=scales != "per_tensor")
+    return bits(y1)
+
+
+@pytest.mark.parametrize("M", [5, 8, 12, 16])
+def test_config2_decode_shapes(M):
+    """Config 2's decode shapes (q, k, v, o, up, down) at M from 5 to 16 on this kernel (s16 = 1;
+    by default o and down go to it only from M = 12), per-row log-uniform scales (K from 3136 to
+    12544: 6 to 25 slabs per wave)."""
+    _lib.tuning_set("s16", 1)
+    for lin in synth.DECODE_SET:
+        announce("s16_config2", M, lin.name, lin.N, lin.K)
+        _check(M, lin.N, lin.K, 5000 + M + lin.N % 97, f"M={M} {lin.name}", act=lin.act)
+
+
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_small_m_when_forced(M):
+    """s16 = 1 takes M = 2 .. 4 too (columns m >= M of the MFMA read row M - 1 and are dropped);
+    M = 2 reaches it with skinny.path = 2 (otherwise the GEMV kernel takes M = 2)."""
+    _lib.tuning_set("s16", 1)
+    _lib.tuning_set("skinny.path", 2)
+    for N, K in [(3136, 3136), (1000, 12544), (37, 64)]:
+        announce("s16_small_m", M, N, K)
+        _check(M, N, K, 5100 + M + N, f"M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("R,B,W", [(1, 2, 8), (2, 2, 8), (1, 4, 8), (2, 4, 8), (1, 2, 16), (2, 2, 16), (1, 4, 16)])
+def test_ragged_shapes_each_form(R, B, W):
+    """Every form (row tiles of 16 or 32, batches of two or four slabs, eight or sixteen waves) on
+    ragged N (partial last tiles), K of one slab (waves with nothing to do), K whose slabs do not
+    divide between the waves, runs longer than two batches, and many tiles."""
+    _lib.tuning_set("s16", 1)
+    _lib.tuning_set("s16.r", R)
+    _lib.tuning_set("s16.b", B)
+    _lib.tuning_set("s16.w", W)
+    for M, N, K in [(16, 37, 64), (7, 1000, 3136), (16, 300, 12544), (9, 20000, 192), (16, 16, 128),
+                    (6, 257, 6272), (13, 2048, 1088), (5, 100, 576)]:
+        announce("s16_ragged", R, B, W, M, N, K)
+        _check(M, N, K, 5200 + 7 * R + B + W + M + N + K, f"R={R} B={B} W={W} M={M} N={N} K={K}")
+
+
+def test_row_tiles_and_batches_agree():
+    """Row tiles of 16 or 32 and batches of two or four slabs sum each output over the same waves'
+    runs in the same order: every such form gives the same bytes."""
+    M, N, K = 16, 3136, 12544
+    announce("s16_forms_agree", M, N, K)
+    _lib.tuning_set("s16", 1)
+    ys = []
+    for R, B in [(1, 2), (2, 2), (1, 4), (2, 4)]:
+        _lib.tuning_set("s16.r", R)
+        _lib.tuning_set("s16.b", B)
+        ys.append(_check(M, N, K, 5250, f"R={R} B={B}"))
+    for y in ys[1:]:
+        assert np.array_equal(ys[0], y)
+
+
+def test_per_tensor_scales_and_relu2_activations():
+    """Per-tensor scales (the strict all-element rel_l2 gate applies) on down_proj's shape with
+    relu^2-distributed activations (many exact zeros)."""
+    announce("s16_per_tensor")
+    _check(16, 3136, 12544, 5301, "per-tensor down_proj", scales="per_tensor", act="relu2")
+
+
+def test_grouped_qkv_strided_outputs():
+    """q | k | v in one launch, each output a column view of one [M, sum N] buffer with ragged
+    widths (scalar stores where a view is not 8-byte aligned): every group matches the oracle and
+    equals its separate call bit for bit (the launch takes row tiles of 32 for its 7120 rows, the
+    k and v calls alone 16: the same sums), and nothing past the views is written."""
+    M, K = 11, 3136
+    Ns = (5120, 1000, 1000)
+    announce("s16_grouped", M, Ns, K)
+    cases = [_case(M, N, K, 5400 + i) for i, N in enumerate(Ns)]
+    x = cases[0][0]
+    xd = x_to_dev(x)
+    wd = [(w_to_dev(w), s_to_dev(s)) for _, w, s in cases]
+    total = sum(Ns)
+    offs = np.cumsum((0,) + Ns)
+    ybig = torch.full((M, total + 8), 3.0, dtype=torch.bfloat16, device=DEV)
+    outs = [ybig[:, offs[i]:offs[i + 1]] for i in range(len(Ns))]
+    L = _lib.lib()
+    arr = (_lib.LinearGroup * len(Ns))()
+    for i, ((w, s), y) in enumerate(zip(wd, outs)):
+        arr[i] = _lib.LinearGroup(w.data_ptr(), w.stride(0), s.data_ptr(), y.data_ptr(), y.stride(0), w.shape[0])
+    _lib.check(L.nmi_linear_fp8_w8a16_grouped(xd.data_ptr(), K, M, K, arr, len(Ns), None, 0, None), "grouped")
+    separate = [ops.linear_fp8_w8a16(xd, w, s) for w, s in wd]
+    torch.cuda.synchronize()
+    assert torch.all(ybig[:, total:] == 3.0)
+    for i, (_, w, s) in enumerate(cases):
+        assert np.array_equal(bits(outs[i]), bits(separate[i])), f"group {i}"
+        assert_parity(bits(outs[i]), oracle_bits(x, w, s), f"grouped {i}", per_row_scales=True)
+
+
+def test_k_not_a_multiple_of_64_goes_to_the_4x4x4_kernel():
+    """K not a multiple of 64 runs the 4x4x4 kernel instead: the same bytes as with s16 = 2, within
+    the parity gate of the oracle."""
+    for M, N, K in [(8, 300, 3152), (12, 1000, 80)]:
+        announce("s16_fallback", M, N, K)
+        x, w, s = _case(M, N, K, 5500 + K)
+        xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+        y = ops.linear_fp8_w8a16(xd, wd, sd)
+        _lib.tuning_set("s16", 2)
+        y4 = ops.linear_fp8_w8a16(xd, wd, sd)
+        _lib.tuning_set("s16", 0)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y4.view(torch.int16))
+        assert_parity(bits(y), oracle_bits(x, w, s), f"fallback K={K}", per_row_scales=True)
+
+
+def test_graph_replays_equal_eager():
+    """A captured launch replayed with eager work in between: every replay equals the eager
+    result."""
+    M, N, K = 16, 12544, 3136
+    announce("s16_graph", M, N, K)
+    x, w, s = _case(M, N, K, 5600)
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    y = ops.linear_fp8_w8a16(xd, wd, sd)
+    torch.cuda.synchronize()
+    eager = bits(y).copy()
+    assert_parity(eager, oracle_bits(x, w, s), "eager", per_row_scales=True)
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            ops.linear_fp8_w8a16(xd, wd, sd, out=y)
+    for rep in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(y), eager), rep
+        ops.linear_fp8_w8a16(xd, wd, sd)                      # eager work between replays
+        torch.cuda.synchronize()
