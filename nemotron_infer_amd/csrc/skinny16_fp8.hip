@@ -17,6 +17,11 @@
 //   v_mfma_f32_16x16x32_bf16 (A = weights: row r, k 8 p + e; B = activations: column m = r);
 //   D[n][m] lands as rows 4 p + i, column r of lane (r, p).  Columns m >= M read row M - 1 and
 //   are not stored.
+// * Row-run form (the default, skinny16_rows_kernel): the weights are loaded 4 rows x 256
+//   contiguous bytes per instruction and turned into the MFMA layout through a wave-private LDS
+//   region; each wave takes a contiguous run of 256-k groups.  The direct form (skinny16_kernel,
+//   tuning knob s16.t = 2) loads the MFMA layout itself, 16 rows x 64 bytes per instruction: the
+//   longer runs per row are worth 10-20% of the kernel time on these shapes (DRAM efficiency).
 // * Loads go in two batches of B slabs, the next in flight while this one is multiplied; every
 //   batch is issued (slabs past the wave's run read one word every lane shares), so the
 //   compiler's wait counts are exact on every path.  A short K has its whole run in flight at
@@ -177,7 +182,132 @@ __global__ __launch_bounds__(64 * NW) void skinny16_kernel(const S16Args a) {
     }
 }
 
-template <int R, int B, int NW>
+// Row-run form: the same products and sums, with the weights loaded as 4 rows x 256 contiguous
+// bytes per instruction (lane 16 i + b: row 4 q + i of the load, 16-byte chunk b of a 256-k
+// group of four slabs) and turned into the MFMA layout through a wave-private LDS region (rows
+// 272 bytes apart: reads of 16 rows at one column hit distinct banks).  Longer contiguous runs
+// per row than the 16 x 64 bytes of the direct form.  Each wave takes a contiguous run of
+// groups; slabs past K are skipped.
+template <int R, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(R == 1 ? 4 : 1))) void skinny16_rows_kernel(
+    const S16Args a) {
+    constexpr int kPitch = 272;                        // bytes per staged row
+    __shared__ f32x4 red[NW][R][64];
+    __shared__ __attribute__((aligned(16))) uint8_t stage[NW][16 * R * kPitch];
+
+    const int tile = blockIdx.x;
+    int gi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < a.ngroups && tile >= a.g[i].tile_begin) gi = i;
+    const S16Group& G = a.g[gi];
+    const int row0 = (tile - G.tile_begin) * 16 * R;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int r = lane & 15, p = lane >> 4;           // MFMA layout
+    const int li = lane >> 4, lb = lane & 15;         // load layout: row 4 q + li, chunk lb
+    const int M = a.M;
+    const int S = a.K >> 6;
+    const int G4 = (S + 3) >> 2;
+    const int g_beg = wave * G4 / NW, g_end = (wave + 1) * G4 / NW;
+    const int n = g_end - g_beg;
+    const int nb = n;
+    const int C = a.K >> 4;                            // 16-byte chunks per row
+
+    const uint8_t* wrow[R][4];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wrow[j][q] = G.W + (int64_t)min(row0 + 16 * j + 4 * q + li, G.N - 1) * G.ldw;
+    const uint16_t* xrow = a.x + (int64_t)min(r, M - 1) * a.ldx + 16 * p;
+    const uint8_t* wdummy = G.W;
+    const uint16_t* xdummy = a.x;
+    uint8_t* st = stage[wave];
+
+    struct Batch {
+        u32x4 w[R][4];
+        u32x4 x[4][2];
+    };
+    auto load = [&](Batch& bt, int b) {
+        const bool ok = b < n;
+        const int g4 = g_beg + b;
+        const int chunk = min(g4 * 16 + lb, C - 1);
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                bt.w[j][q] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(ok ? wrow[j][q] + (int64_t)chunk * 16 : wdummy));
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            const int s = g4 * 4 + sl;
+            const bool sok = ok && s < S;
+            const uint16_t* xp = sok ? xrow + s * 64 : xdummy;
+            bt.x[sl][0] = *reinterpret_cast<const u32x4*>(xp);
+            bt.x[sl][1] = *reinterpret_cast<const u32x4*>(sok ? xp + 8 : xdummy);
+        }
+    };
+
+    f32x4 acc[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](const Batch& bt, int b) {
+        if (b >= n) return;
+        const int g4 = g_beg + b;
+        // the group's rows into the wave's region, then read back in the MFMA layout (one wave
+        // writes and reads it: LDS keeps a wave's operations in order)
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<u32x4*>(st + (16 * j + 4 * q + li) * kPitch + 16 * lb) = bt.w[j][q];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            if (g4 * 4 + sl >= S) break;
+            const bf16x8 B0 = __builtin_bit_cast(bf16x8, bt.x[sl][0]);
+            const bf16x8 B1 = __builtin_bit_cast(bf16x8, bt.x[sl][1]);
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(st + (16 * j + r) * kPitch + sl * 64 + 16 * p);
+                const uint2 c0 = e4m3x4_to_bf16(w[0]), c1 = e4m3x4_to_bf16(w[1]);
+                const uint2 c2 = e4m3x4_to_bf16(w[2]), c3 = e4m3x4_to_bf16(w[3]);
+                const bf16x8 A0 = __builtin_bit_cast(bf16x8, uint4{c0.x, c0.y, c1.x, c1.y});
+                const bf16x8 A1 = __builtin_bit_cast(bf16x8, uint4{c2.x, c2.y, c3.x, c3.y});
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, acc[j], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    Batch ba, bb;
+    load(ba, 0);
+    load(bb, 1);
+    for (int b = 0; b < nb; b += 2) {
+        consume(ba, b);
+        load(ba, b + 2);
+        consume(bb, b + 1);
+        load(bb, b + 3);
+    }
+
+#pragma unroll
+    for (int j = 0; j < R; ++j) red[wave][j][lane] = acc[j];
+    __syncthreads();
+    if (wave < R) {
+        f32x4 v = red[0][wave][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 u = red[w][wave][lane];
+            v = f32x4{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
+        }
+        if (r < M) s16_store(G, r, row0 + 16 * wave + 4 * p, v);
+    }
+}
+
+template <int R, int B, int NW, bool ROWS = false>
 hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
     int tb = 0;
     for (int i = 0; i < ng; ++i) {
@@ -191,23 +321,25 @@ hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t s
         tb += (G.N + 16 * R - 1) / (16 * R);
     }
     if (tb < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((skinny16_kernel<R, B, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
+    if constexpr (ROWS) hipLaunchKernelGGL((skinny16_rows_kernel<R, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
+    else hipLaunchKernelGGL((skinny16_kernel<R, B, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
-// Where this kernel is taken by default (tuning knob s16 = 1: every 2 <= M <= 16, 2: never).
-// Measured on MI355X against the 4x4x4 kernel (kernel time, config 2's shapes): at M = 16 faster
-// for q | k | v, k alone (8.1 vs 11.3 us), o (12.1 vs 13.1) and up (17.8 vs 23.4), even on down
-// (K = 12544: 21.5 vs 21.3); at M = 8 faster for q (9.8 vs 10.6), k (7.1 vs 8.0) and up (16.0 vs
-// 16.6) but slower for o (10.2 vs 9.8, K = 5120) and down (17.7 vs 16.6): the activation reads
-// per weight byte grow with M / R, and so does what the kernel saves.
+// Where this kernel is taken by default (tuning knob s16 = 1: every 2 <= M <= 16, 2: never):
+// from M = 5.  Measured on MI355X (rocprof kernel time, config 2's shapes, row-run form against
+// the 4x4x4 kernel): at M = 16 q 10.1 vs 15.0 us, k 8.2 vs 11.2, o 10.9 vs 13.2, up 18.4 vs
+// 23.6, down 18.5 vs 21.5; at M = 8 q 9.1 vs 10.5, k 7.3 vs 8.0, o 9.4 vs 9.8, up 16.1 vs 16.5,
+// down 14.5 vs 16.4; at M = 4 the 4x4x4 kernel is as fast or faster (q 8.8 vs 8.9, k 6.4 vs
+// 7.0, up 13.2 vs 15.6).
 bool skinny16_wanted(int M, int K) {
     const int knob = tuning().s16;
     if (knob == 2 || M > 16 || M < 2) return false;
     if (knob == 1) return true;
-    return M >= 5 && (K <= 4096 || (M >= 12 && K <= 8192));
+    (void)K;
+    return M >= 5;
 }
 
 bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
@@ -225,12 +357,18 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
     a.M = M;
     a.K = K;
     a.ngroups = ngroups;
-    // row tiles of 32 from 4096 rows (half the activation reads per weight byte; measured faster
-    // on q | k | v and up), else 16 (more workgroups); eight waves; batches of two slabs.  Tuning
-    // knobs: s16.r (1, 2) forces the row tile, s16.b = 4 batches of four, s16.w = 16 waves.
+    // the row-run form with row tiles of 32 from 4096 rows (half the activation reads per weight
+    // byte), else 16 (more workgroups).  Tuning knobs: s16.r (1, 2) forces the row tile; s16.t = 2
+    // selects the direct form (16 rows x 64 bytes per load), with s16.b = 4 batches of four
+    // slabs and s16.w = 16 waves.
     const Tuning& tn = tuning();
     const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : (rows >= 4096 ? 2 : 1);
     const int Bt = tn.s16_b == 4 ? 4 : 2, NW = tn.s16_w == 16 ? 16 : 8;
+    if (tn.s16_t != 2) {
+        *err = R == 2 ? s16_launch<2, 1, 8, true>(a, groups, ngroups, stream)
+                      : s16_launch<1, 1, 8, true>(a, groups, ngroups, stream);
+        return true;
+    }
     const int form = (R == 2 ? 4 : 0) + (Bt == 2 ? 2 : 0) + (NW == 16 ? 1 : 0);
     switch (form) {
         case 0: *err = s16_launch<1, 4, 8>(a, groups, ngroups, stream); break;

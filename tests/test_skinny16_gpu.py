@@ -1,6 +1,7 @@
 """GPU parity of the 16x16x32 skinny kernel (skinny16_fp8.hip: M <= 16, one row tile per
-workgroup, K split between its eight waves whose sums are added in wave order), against the
-torch fp32 dequant-then-F.linear oracle.
+workgroup, K split between its eight waves whose sums are added in wave order; the row-run form,
+which loads 4 rows x 256 bytes per instruction and turns them into the MFMA layout through LDS,
+and the direct form), against the torch fp32 dequant-then-F.linear oracle.
 
 Tolerance: rel_l2 <= 1e-3 and max |diff| <= 2 bf16 ulp at max(|ref|, 2^-8 rms(ref)) (plus
 rel_l2 over all elements where the scales are per tensor).  Size-independent properties:
@@ -17,7 +18,7 @@ from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_t
 
 pytestmark = pytest.mark.gpu
 
-KNOBS = ("s16", "s16.r", "s16.b", "s16.w", "skinny.path")
+KNOBS = ("s16", "s16.r", "s16.t", "s16.b", "s16.w", "skinny.path")
 
 
 @pytest.fixture(autouse=True)
@@ -48,10 +49,8 @@ def _check(M, N, K, seed, label, scales="log_uniform", act="normal"):
 
 @pytest.mark.parametrize("M", [5, 8, 12, 16])
 def test_config2_decode_shapes(M):
-    """Config 2's decode shapes (q, k, v, o, up, down) at M from 5 to 16 on this kernel (s16 = 1;
-    by default o and down go to it only from M = 12), per-row log-uniform scales (K from 3136 to
-    12544: 6 to 25 slabs per wave)."""
-    _lib.tuning_set("s16", 1)
+    """Config 2's decode shapes (q, k, v, o, up, down) at M from 5 to 16 (the default form),
+    per-row log-uniform scales (K from 3136 to 12544)."""
     for lin in synth.DECODE_SET:
         announce("s16_config2", M, lin.name, lin.N, lin.K)
         _check(M, lin.N, lin.K, 5000 + M + lin.N % 97, f"M={M} {lin.name}", act=lin.act)
@@ -68,32 +67,37 @@ def test_small_m_when_forced(M):
         _check(M, N, K, 5100 + M + N, f"M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("R,B,W", [(1, 2, 8), (2, 2, 8), (1, 4, 8), (2, 4, 8), (1, 2, 16), (2, 2, 16), (1, 4, 16)])
-def test_ragged_shapes_each_form(R, B, W):
-    """Every form (row tiles of 16 or 32, batches of two or four slabs, eight or sixteen waves) on
-    ragged N (partial last tiles), K of one slab (waves with nothing to do), K whose slabs do not
-    divide between the waves, runs longer than two batches, and many tiles."""
+@pytest.mark.parametrize("T,R,B,W", [(0, 1, 2, 8), (0, 2, 2, 8), (2, 1, 2, 8), (2, 2, 2, 8), (2, 1, 4, 8), (2, 2, 4, 8),
+                                     (2, 1, 2, 16), (2, 2, 2, 16), (2, 1, 4, 16)])
+def test_ragged_shapes_each_form(T, R, B, W):
+    """Every form (row runs through LDS or direct loads; row tiles of 16 or 32; for the direct form
+    batches of two or four slabs and eight or sixteen waves) on ragged N (partial last tiles), K
+    of one slab (waves with nothing to do), K whose slabs do not divide between the waves or into
+    256-k groups, runs longer than two batches, and many tiles."""
     _lib.tuning_set("s16", 1)
+    _lib.tuning_set("s16.t", T)
     _lib.tuning_set("s16.r", R)
     _lib.tuning_set("s16.b", B)
     _lib.tuning_set("s16.w", W)
     for M, N, K in [(16, 37, 64), (7, 1000, 3136), (16, 300, 12544), (9, 20000, 192), (16, 16, 128),
-                    (6, 257, 6272), (13, 2048, 1088), (5, 100, 576)]:
-        announce("s16_ragged", R, B, W, M, N, K)
-        _check(M, N, K, 5200 + 7 * R + B + W + M + N + K, f"R={R} B={B} W={W} M={M} N={N} K={K}")
+                    (6, 257, 6272), (13, 2048, 1088), (5, 100, 576), (11, 64, 2112)]:
+        announce("s16_ragged", T, R, B, W, M, N, K)
+        _check(M, N, K, 5200 + 7 * R + B + W + M + N + K, f"T={T} R={R} B={B} W={W} M={M} N={N} K={K}")
 
 
-def test_row_tiles_and_batches_agree():
-    """Row tiles of 16 or 32 and batches of two or four slabs sum each output over the same waves'
-    runs in the same order: every such form gives the same bytes."""
+@pytest.mark.parametrize("T", [0, 2])
+def test_row_tiles_and_batches_agree(T):
+    """Within a form, row tiles of 16 or 32 (and, for the direct form, batches of two or four
+    slabs) sum each output over the same waves' runs in the same order: the same bytes."""
     M, N, K = 16, 3136, 12544
-    announce("s16_forms_agree", M, N, K)
+    announce("s16_forms_agree", T, M, N, K)
     _lib.tuning_set("s16", 1)
+    _lib.tuning_set("s16.t", T)
     ys = []
-    for R, B in [(1, 2), (2, 2), (1, 4), (2, 4)]:
+    for R, B in ([(1, 2), (2, 2), (1, 4), (2, 4)] if T == 2 else [(1, 2), (2, 2)]):
         _lib.tuning_set("s16.r", R)
         _lib.tuning_set("s16.b", B)
-        ys.append(_check(M, N, K, 5250, f"R={R} B={B}"))
+        ys.append(_check(M, N, K, 5250, f"T={T} R={R} B={B}"))
     for y in ys[1:]:
         assert np.array_equal(ys[0], y)
 
