@@ -212,3 +212,40 @@ def test_block_binding_in_place_and_bump_allocator():
     B.sync()
     assert torch.equal(xi.view(torch.int16), want.view(torch.int16))
     assert torch.equal(c1, c2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("h,p,g", [(8, 24, 1), (24, 16, 3), (8, 32, 4), (16, 40, 8)])
+def test_block_one_token_other_groups(h, p, g):
+    """The block at one token equals the composition of the library's calls (same bytes and
+    states) for one, an odd number and up to eight groups (groups of 32 to 192 values) at small
+    dimensions (head counts a multiple of 8: in_proj rows a multiple of 8)."""
+    hidden, n = 256, 128
+    inter, conv_dim = h * p, h * p + 2 * g * n
+    proj_n = inter + conv_dim + h
+    announce("mamba_block_groups", h, p, g)
+    rng = np.random.default_rng(9000 + h + p + g)
+    f = np.float32
+    iw, isc = synth.make_weight(proj_n, hidden, 9100 + g, "cpu")
+    ow, osc = synth.make_weight(hidden, inter, 9200 + g, "cpu")
+    prm = dict(conv_w=(rng.standard_normal((conv_dim, 4)) * 0.3).astype(f),
+               conv_b=(rng.standard_normal(conv_dim) * 0.1).astype(f),
+               A_log=rng.uniform(-1.0, 1.5, h).astype(f), D=rng.standard_normal(h).astype(f),
+               dt_bias=(rng.standard_normal(h) * 0.5).astype(f),
+               gnorm_w=(1 + 0.1 * rng.standard_normal(inter)).astype(f))
+    d = _dev_params(prm)
+    nw = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(hidden)).astype(f)).to(DEV)
+    dw = (nw, w_to_dev(iw.numpy()), s_to_dev(isc.numpy())) + _order(d) + (w_to_dev(ow.numpy()), s_to_dev(osc.numpy()))
+    cs = rng.standard_normal((1, conv_dim, 3)).astype(f)
+    ss = (rng.standard_normal((1, h, p, n)) * 0.1).astype(f)
+    xd = x_to_dev(_bf16_np((1, hidden), 9300 + g))
+    c1, s1 = torch.from_numpy(cs).to(DEV), torch.from_numpy(ss).to(DEV)
+    c2, s2 = c1.clone(), s1.clone()
+    got = ops.mamba_decode_fp8(xd, *dw, c1, s1, h, p, g, eps=EPS)
+    _, iw_d, isc_d, cw, cb, al, dd, db, gw, ow_d, osc_d = dw
+    hn = ops.rmsnorm_bf16(xd, nw, EPS)
+    proj = ops.linear_fp8_w8a16(hn, iw_d, isc_d, use_workspace=False)
+    y, gg = ops.mamba_mixer_decode(proj, cw, cb, al, dd, db, gw, c2, s2, h, p, g, EPS)
+    ref = xd + ops.linear_fp8_w8a16(gg, ow_d, osc_d, use_workspace=False)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), "block != composition"
+    assert torch.equal(c1, c2) and torch.equal(s1, s2), "states"
