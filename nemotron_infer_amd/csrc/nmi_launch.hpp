@@ -57,7 +57,7 @@ struct Tuning {
     int s16_r = 0;         // 16x16x32 skinny kernel: row tiles of 16 per workgroup (1, 2; 0: by rows)
     int s16_t = 0;         // 16x16x32 skinny kernel: 2 direct form (0: row runs through LDS)
     int s16_b = 0;         // 16x16x32 skinny kernel, direct form: slabs per load batch (4; 0: 2)
-    int s16_w = 0;         // 16x16x32 skinny kernel, direct form: waves per workgroup (16; 0: 8)
+    int s16_w = 0;         // 16x16x32 skinny kernel: waves per workgroup (row runs: 2, 4, 8; direct: 16)
 };
 Tuning& tuning();
 

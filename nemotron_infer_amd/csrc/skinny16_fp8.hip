@@ -357,18 +357,34 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
     a.M = M;
     a.K = K;
     a.ngroups = ngroups;
-    // the row-run form with row tiles of 32 from 4096 rows (half the activation reads per weight
-    // byte), else 16 (more workgroups).  Tuning knobs: s16.r (1, 2) forces the row tile; s16.t = 2
-    // selects the direct form (16 rows x 64 bytes per load), with s16.b = 4 batches of four
-    // slabs and s16.w = 16 waves.
+    // The row-run form with row tiles of 32 from 4096 rows (half the activation reads per weight
+    // byte), else 16 (more workgroups); four waves per workgroup, two where the row tiles outnumber
+    // the CUs (more, shorter-lived workgroups resident per CU: all of a launch's tiles in one
+    // round).  Measured on MI355X, kernel time at M = 8 / 16: four waves against eight q 8.7 /
+    // 9.6 vs 9.2 / 10.2 us, k 6.8 / 7.9 vs 7.3 / 8.2, o 8.6 / 10.4 vs 9.5 / 11.0, down 13.7 / 17.6
+    // vs 14.4 / 18.5; up (392 tiles) with two waves 13.6 / 15.2 against 14.3 / 16.1 (four) and
+    // 16.2 / 18.4 (eight).  Tuning knobs: s16.r (1, 2) forces the row tile, s16.w (2, 4, 8) the
+    // waves; s16.t = 2 selects the direct form (16 rows x 64 bytes per load) with s16.b = 4
+    // batches of four slabs and s16.w = 16 waves.
     const Tuning& tn = tuning();
     const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : (rows >= 4096 ? 2 : 1);
-    const int Bt = tn.s16_b == 4 ? 4 : 2, NW = tn.s16_w == 16 ? 16 : 8;
     if (tn.s16_t != 2) {
-        *err = R == 2 ? s16_launch<2, 1, 8, true>(a, groups, ngroups, stream)
-                      : s16_launch<1, 1, 8, true>(a, groups, ngroups, stream);
+        int tiles = 0;
+        for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
+        const int nw = tn.s16_w == 2 || tn.s16_w == 4 || tn.s16_w == 8 ? tn.s16_w
+                                                                        : (tiles > device_info().num_cu ? 2 : 4);
+        if (nw == 2)
+            *err = R == 2 ? s16_launch<2, 1, 2, true>(a, groups, ngroups, stream)
+                          : s16_launch<1, 1, 2, true>(a, groups, ngroups, stream);
+        else if (nw == 4)
+            *err = R == 2 ? s16_launch<2, 1, 4, true>(a, groups, ngroups, stream)
+                          : s16_launch<1, 1, 4, true>(a, groups, ngroups, stream);
+        else
+            *err = R == 2 ? s16_launch<2, 1, 8, true>(a, groups, ngroups, stream)
+                          : s16_launch<1, 1, 8, true>(a, groups, ngroups, stream);
         return true;
     }
+    const int Bt = tn.s16_b == 4 ? 4 : 2, NW = tn.s16_w == 16 ? 16 : 8;
     const int form = (R == 2 ? 4 : 0) + (Bt == 2 ? 2 : 0) + (NW == 16 ? 1 : 0);
     switch (form) {
         case 0: *err = s16_launch<1, 4, 8>(a, groups, ngroups, stream); break;

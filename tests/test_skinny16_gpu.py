@@ -67,11 +67,13 @@ def test_small_m_when_forced(M):
         _check(M, N, K, 5100 + M + N, f"M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("T,R,B,W", [(0, 1, 2, 8), (0, 2, 2, 8), (2, 1, 2, 8), (2, 2, 2, 8), (2, 1, 4, 8), (2, 2, 4, 8),
+@pytest.mark.parametrize("T,R,B,W", [(0, 1, 2, 0), (0, 2, 2, 0), (0, 1, 2, 2), (0, 2, 2, 2), (0, 1, 2, 4), (0, 2, 2, 4),
+                                     (0, 1, 2, 8), (0, 2, 2, 8), (2, 1, 2, 8), (2, 2, 2, 8), (2, 1, 4, 8), (2, 2, 4, 8),
                                      (2, 1, 2, 16), (2, 2, 2, 16), (2, 1, 4, 16)])
 def test_ragged_shapes_each_form(T, R, B, W):
-    """Every form (row runs through LDS or direct loads; row tiles of 16 or 32; for the direct form
-    batches of two or four slabs and eight or sixteen waves) on ragged N (partial last tiles), K
+    """Every form (row runs through LDS with two, four or eight waves or as chosen (W = 0), or
+    direct loads with batches of two or four slabs and eight or sixteen waves; row tiles of 16 or
+    32) on ragged N (partial last tiles), K
     of one slab (waves with nothing to do), K whose slabs do not divide between the waves or into
     256-k groups, runs longer than two batches, and many tiles."""
     _lib.tuning_set("s16", 1)
