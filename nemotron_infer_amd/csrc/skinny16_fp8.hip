@@ -188,9 +188,9 @@ __global__ __launch_bounds__(64 * NW) void skinny16_kernel(const S16Args a) {
 // 272 bytes apart: reads of 16 rows at one column hit distinct banks).  Longer contiguous runs
 // per row than the 16 x 64 bytes of the direct form.  Each wave takes a contiguous run of
 // groups; slabs past K are skipped.
-template <int R, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(R == 1 ? 4 : 1))) void skinny16_rows_kernel(
-    const S16Args a) {
+template <int R, int NW, int D>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(R == 1 && D == 2 ? 4 : 1))) void
+skinny16_rows_kernel(const S16Args a) {
     constexpr int kPitch = 272;                        // bytes per staged row
     __shared__ f32x4 red[NW][R][64];
     __shared__ __attribute__((aligned(16))) uint8_t stage[NW][16 * R * kPitch];
@@ -283,14 +283,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(R == 1 
         __builtin_amdgcn_wave_barrier();
     };
 
-    Batch ba, bb;
-    load(ba, 0);
-    load(bb, 1);
-    for (int b = 0; b < nb; b += 2) {
-        consume(ba, b);
-        load(ba, b + 2);
-        consume(bb, b + 1);
-        load(bb, b + 3);
+    // D groups in flight: buffer d holds groups d, d + D, d + 2 D, ...
+    Batch bt[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(bt[d], d);
+    for (int b = 0; b < nb; b += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            consume(bt[d], b + d);
+            load(bt[d], b + d + D);
+        }
     }
 
 #pragma unroll
@@ -321,7 +323,7 @@ hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t s
         tb += (G.N + 16 * R - 1) / (16 * R);
     }
     if (tb < 1) return hipErrorInvalidValue;
-    if constexpr (ROWS) hipLaunchKernelGGL((skinny16_rows_kernel<R, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
+    if constexpr (ROWS) hipLaunchKernelGGL((skinny16_rows_kernel<R, NW, B>), dim3(tb), dim3(64 * NW), 0, stream, a);
     else hipLaunchKernelGGL((skinny16_kernel<R, B, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
     return hipGetLastError();
 }
@@ -329,17 +331,15 @@ hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t s
 }  // namespace
 
 // Where this kernel is taken by default (tuning knob s16 = 1: every 2 <= M <= 16, 2: never):
-// from M = 5.  Measured on MI355X (rocprof kernel time, config 2's shapes, row-run form against
-// the 4x4x4 kernel): at M = 16 q 10.1 vs 15.0 us, k 8.2 vs 11.2, o 10.9 vs 13.2, up 18.4 vs
-// 23.6, down 18.5 vs 21.5; at M = 8 q 9.1 vs 10.5, k 7.3 vs 8.0, o 9.4 vs 9.8, up 16.1 vs 16.5,
-// down 14.5 vs 16.4; at M = 4 the 4x4x4 kernel is as fast or faster (q 8.8 vs 8.9, k 6.4 vs
-// 7.0, up 13.2 vs 15.6).
+// from M = 3 (M = 2 is the stream GEMV's).  Measured on MI355X (bench, config 2, four launches per
+// step): M = 4 41.3 against 43.3 us on the 4x4x4 kernel, M = 8 43.8 against 53, M = 16 54.2
+// against 74; M = 2 39.7 against 38.6 on the stream GEMV.
 bool skinny16_wanted(int M, int K) {
     const int knob = tuning().s16;
     if (knob == 2 || M > 16 || M < 2) return false;
     if (knob == 1) return true;
     (void)K;
-    return M >= 5;
+    return M >= 3;
 }
 
 bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
@@ -373,15 +373,17 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
         for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
         const int nw = tn.s16_w == 2 || tn.s16_w == 4 || tn.s16_w == 8 ? tn.s16_w
                                                                         : (tiles > device_info().num_cu ? 2 : 4);
+        // two groups in flight per wave (three or four measured slower: the registers cost
+        // resident waves)
         if (nw == 2)
-            *err = R == 2 ? s16_launch<2, 1, 2, true>(a, groups, ngroups, stream)
-                          : s16_launch<1, 1, 2, true>(a, groups, ngroups, stream);
+            *err = R == 2 ? s16_launch<2, 2, 2, true>(a, groups, ngroups, stream)
+                          : s16_launch<1, 2, 2, true>(a, groups, ngroups, stream);
         else if (nw == 4)
-            *err = R == 2 ? s16_launch<2, 1, 4, true>(a, groups, ngroups, stream)
-                          : s16_launch<1, 1, 4, true>(a, groups, ngroups, stream);
+            *err = R == 2 ? s16_launch<2, 2, 4, true>(a, groups, ngroups, stream)
+                          : s16_launch<1, 2, 4, true>(a, groups, ngroups, stream);
         else
-            *err = R == 2 ? s16_launch<2, 1, 8, true>(a, groups, ngroups, stream)
-                          : s16_launch<1, 1, 8, true>(a, groups, ngroups, stream);
+            *err = R == 2 ? s16_launch<2, 2, 8, true>(a, groups, ngroups, stream)
+                          : s16_launch<1, 2, 8, true>(a, groups, ngroups, stream);
         return true;
     }
     const int Bt = tn.s16_b == 4 ? 4 : 2, NW = tn.s16_w == 16 ? 16 : 8;

@@ -1,5 +1,5 @@
 """GPU parity of the 16x16x32 skinny kernel (skinny16_fp8.hip: M <= 16, one row tile per
-workgroup, K split between its eight waves whose sums are added in wave order; the row-run form,
+workgroup, K split between its waves whose sums are added in wave order; the row-run form,
 which loads 4 rows x 256 bytes per instruction and turns them into the MFMA layout through LDS,
 and the direct form), against the torch fp32 dequant-then-F.linear oracle.
 
