@@ -410,8 +410,9 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
  * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace
  * nmi_linear_workspace_bytes then reports), "s16": the 16x16x32 skinny kernel (0: automatic, from
  * M = 3, 1: for 2 <= M <= 16, 2: never), "s16.r": its row tiles of 16 (1) or 32 (2), "s16.w": its
- * waves per workgroup (2, 4, 8), "s16.t": 2 its direct-load form, with "s16.b": 4 load batches of
- * four slabs and "s16.w": 16 waves, "chain.wgs": workgroups per CU of a GEMV chain created
+ * waves per workgroup (2, 4, 8), "s16.t": its load form (1 row runs through registers, 2 direct
+ * loads, with "s16.b": 4 load batches of four slabs and "s16.w": 16 waves, 3 DMA into LDS, the
+ * automatic one, with "s16.b": 3 groups in flight per wave), "chain.wgs": workgroups per CU of a GEMV chain created
  * afterwards); 0 restores the automatic choice.  Process-wide, not thread-safe against concurrent
  * launches; results do not depend on them beyond float32 summation order.  No counterpart in the
  * reference (its launch shapes are compile-time constants, ops/gemv.cuh:100-103).

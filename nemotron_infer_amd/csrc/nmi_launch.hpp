@@ -55,7 +55,7 @@ struct Tuning {
     int gemm_sk_cap = 0;   // GEMM stream-K: at most this many workgroups per tile (0: 2; -1: one per CU)
     int s16 = 0;           // 16x16x32 skinny kernel: 0 automatic (M >= 3), 1 for 2 <= M <= 16, 2 never
     int s16_r = 0;         // 16x16x32 skinny kernel: row tiles of 16 per workgroup (1, 2; 0: by rows)
-    int s16_t = 0;         // 16x16x32 skinny kernel: 2 direct form (0: row runs through LDS)
+    int s16_t = 0;         // 16x16x32 skinny kernel: 1 row runs, 2 direct form, 3 DMA (0: DMA where it fits)
     int s16_b = 0;         // 16x16x32 skinny kernel, direct form: slabs per load batch (4; 0: 2)
     int s16_w = 0;         // 16x16x32 skinny kernel: waves per workgroup (row runs: 2, 4, 8; direct: 16)
 };

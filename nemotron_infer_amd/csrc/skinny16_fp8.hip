@@ -17,15 +17,18 @@
 //   v_mfma_f32_16x16x32_bf16 (A = weights: row r, k 8 p + e; B = activations: column m = r);
 //   D[n][m] lands as rows 4 p + i, column r of lane (r, p).  Columns m >= M read row M - 1 and
 //   are not stored.
-// * Row-run form (the default, skinny16_rows_kernel): the weights are loaded 4 rows x 256
-//   contiguous bytes per instruction and turned into the MFMA layout through a wave-private LDS
-//   region; each wave takes a contiguous run of 256-k groups.  The direct form (skinny16_kernel,
-//   tuning knob s16.t = 2) loads the MFMA layout itself, 16 rows x 64 bytes per instruction: the
-//   longer runs per row are worth 10-20% of the kernel time on these shapes (DRAM efficiency).
-// * Loads go in two batches of B slabs, the next in flight while this one is multiplied; every
-//   batch is issued (slabs past the wave's run read one word every lane shares), so the
-//   compiler's wait counts are exact on every path.  A short K has its whole run in flight at
-//   once: the launch is one weight round trip, the products, and the store.
+// * DMA form (the default, skinny16_dma_kernel): both operands go global -> LDS by
+//   global_load_lds_dwordx4, the weights 4 rows x 256 contiguous bytes and the activations
+//   2 rows x 512 bytes per instruction, into a few wave-private slots; each wave takes a
+//   contiguous run of 256-k groups and reads the operands back in the MFMA layout.  Against the
+//   row-run form (skinny16_rows_kernel, tuning knob s16.t = 1: weights staged through registers
+//   into LDS, activations loaded in the MFMA layout, which touches 16 rows per instruction) it
+//   measured 4-16% faster per launch on the config-2 shapes, the most at M = 16.  The direct form
+//   (skinny16_kernel, s16.t = 2) loads the MFMA layout itself, 16 rows x 64 bytes per weight
+//   instruction: 10-20% slower than the row runs (DRAM efficiency).
+// * In the register forms, loads go in batches, the next in flight while this one is
+//   multiplied; every batch is issued (slabs past the wave's run read one word every lane
+//   shares), so the compiler's wait counts are exact on every path.
 // * The waves' sums meet in LDS and are added in wave order (a fixed order: results do not depend
 //   on timing), then the per-row scale, one bf16 rounding and the epilogue.  No workspace, no
 //   inter-workgroup communication.
@@ -309,8 +312,147 @@ skinny16_rows_kernel(const S16Args a) {
     }
 }
 
-template <int R, int B, int NW, bool ROWS = false>
-hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
+// DMA form: the same products and sums, with both operands brought global -> LDS by
+// global_load_lds_dwordx4 (no register staging, no LDS store instructions) into D slots per
+// wave.  A slot holds one 256-k group: the weights, 16 R rows x 256 bytes (4 rows per
+// instruction), and the activations, 16 rows x 512 bytes (2 rows per instruction: 1 KiB of
+// consecutive bytes, where the MFMA layout touches 16 rows per instruction).  A DMA instruction
+// writes 1 KiB of consecutive LDS (lane l at 16 l), so the layout is set by which global chunk
+// each lane fetches: chunk c of local row r (r < 16) sits at chunk position c ^ r of its row,
+// and a fragment read (16 rows, one logical chunk) hits 16 distinct bank groups.  Waits are
+// explicit vmcnt counts (every group issues the same instructions, and only groups of the wave's
+// run are issued: a wait counts the groups issued after the one it waits for).
+constexpr int kS16DmaW = 4096, kS16DmaX = 8192;     // bytes per slot and row tile / activations
+
+template <int R, int NW, int D>
+constexpr int s16_dma_lds() {
+    return NW * D * (R * kS16DmaW + kS16DmaX) + NW * R * 64 * 16;
+}
+
+template <int R, int NW, int D>
+__global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) {
+    constexpr int kW = R * kS16DmaW, kSlot = kW + kS16DmaX;
+    constexpr int kPer = 4 * R + 8;                    // DMA instructions per group
+    static_assert(D >= 1 && D <= 3 && (D - 1) * kPer <= 63, "vmcnt range");
+    typedef __attribute__((address_space(3))) void lds_void;
+    extern __shared__ __attribute__((aligned(16))) uint8_t s16_lds[];
+
+    const int tile = blockIdx.x;
+    int gi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < a.ngroups && tile >= a.g[i].tile_begin) gi = i;
+    const S16Group& G = a.g[gi];
+    const int row0 = (tile - G.tile_begin) * 16 * R;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int r = lane & 15, p = lane >> 4;           // MFMA layout
+    const int M = a.M;
+    const int S = a.K >> 6;
+    const int G4 = (S + 3) >> 2;
+    const int g_beg = wave * G4 / NW, g_end = (wave + 1) * G4 / NW;
+    const int n = g_end - g_beg;
+    const int CW = a.K >> 4;                           // 16-byte chunks per weight row
+    const int CX = a.K >> 3;                           // 16-byte chunks per activation row
+
+    uint8_t* const slots = s16_lds + wave * D * kSlot;
+    const uint32_t lds_slots = (uint32_t)(uintptr_t)(lds_void*)slots;
+    f32x4* const red = reinterpret_cast<f32x4*>(s16_lds + NW * D * kSlot);
+
+    // per-lane row offsets and chunk swizzles: weights, instruction (j, q) -> local row 4 q + lane / 16,
+    // position lane % 16; activations, instruction i -> row 2 i + lane / 32, position lane % 32
+    uint32_t wbase[R][4];
+    int wsw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int rl = 4 * q + (lane >> 4);
+        wsw[q] = (lane & 15) ^ rl;
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+            wbase[j][q] = (uint32_t)((int64_t)min(row0 + 16 * j + rl, G.N - 1) * G.ldw);
+    }
+    const int xl = lane & 31, xh = lane >> 5;
+
+    auto issue = [&](int b, int d) {
+        if (b >= n) return;
+        const int g4 = g_beg + b;
+        const uint32_t sw = lds_slots + (uint32_t)(d * kSlot);
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                dma16_lds(G.W, wbase[j][q] + 16u * (uint32_t)min(g4 * 16 + wsw[q], CW - 1),
+                        sw + (uint32_t)((4 * j + q) * 1024));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int rho = 2 * i + xh;
+            const uint32_t xoff = (uint32_t)((int64_t)min(rho, M - 1) * a.ldx * 2);
+            dma16_lds(a.x, xoff + 16u * (uint32_t)min(g4 * 32 + (xl ^ rho), CX - 1), sw + (uint32_t)(kW + i * 1024));
+        }
+    };
+
+    f32x4 acc[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int b, int d) {
+        if (b >= n) return;
+        const int g4 = g_beg + b;
+        const uint8_t* sw = slots + d * kSlot;
+        const uint8_t* sx = sw + kW;
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            if (g4 * 4 + sl >= S) break;
+            const bf16x8 B0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + r * 512 + 16 * ((8 * sl + 2 * p) ^ r)));
+            const bf16x8 B1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + r * 512 + 16 * ((8 * sl + 2 * p + 1) ^ r)));
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(sw + j * 4096 + r * 256 + 16 * ((4 * sl + p) ^ r));
+                const uint2 c0 = e4m3x4_to_bf16(w[0]), c1 = e4m3x4_to_bf16(w[1]);
+                const uint2 c2 = e4m3x4_to_bf16(w[2]), c3 = e4m3x4_to_bf16(w[3]);
+                const bf16x8 A0 = __builtin_bit_cast(bf16x8, uint4{c0.x, c0.y, c1.x, c1.y});
+                const bf16x8 A1 = __builtin_bit_cast(bf16x8, uint4{c2.x, c2.y, c3.x, c3.y});
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, acc[j], 0, 0, 0);
+            }
+        }
+    };
+
+    // slot d holds groups d, d + D, ...; when group b is consumed, groups b + 1 .. min(n, b + D) - 1
+    // have been issued after it; before a slot is refilled its LDS reads have completed
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, d);
+    for (int b = 0; b < n; b += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int after = min(n - 1 - (b + d), D - 1);
+            if (after >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPer) : "memory");
+            else if (after == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPer) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            consume(b + d, d);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(b + d + D, d);
+        }
+    }
+
+#pragma unroll
+    for (int j = 0; j < R; ++j) red[(wave * R + j) * 64 + lane] = acc[j];
+    __syncthreads();
+    if (wave < R) {
+        f32x4 v = red[wave * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 u = red[(w * R + wave) * 64 + lane];
+            v = f32x4{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
+        }
+        if (r < M) s16_store(G, r, row0 + 16 * wave + 4 * p, v);
+    }
+}
+
+// Fills the launch's group table (the row tiles of each matrix in order); returns the tile count.
+template <int R>
+int s16_tables(S16Args& a, const GemvGroup* groups, int ng) {
     int tb = 0;
     for (int i = 0; i < ng; ++i) {
         const GemvGroup& G = groups[i];
@@ -322,6 +464,25 @@ hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t s
         a.g[i] = S16Group{G.W, G.ldw, G.s, G.y, G.ldy, res ? e.res : nullptr, e.ldres, G.N, tb, e.kind, vec ? 1 : 0};
         tb += (G.N + 16 * R - 1) / (16 * R);
     }
+    return tb;
+}
+
+template <int R, int NW, int D>
+hipError_t s16_dma_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
+    constexpr int lds = s16_dma_lds<R, NW, D>();
+    static_assert(lds <= 152 * 1024, "LDS");
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny16_dma_kernel<R, NW, D>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return attr;
+    const int tb = s16_tables<R>(a, groups, ng);
+    if (tb < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((skinny16_dma_kernel<R, NW, D>), dim3(tb), dim3(64 * NW), lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int R, int B, int NW, bool ROWS = false>
+hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
+    const int tb = s16_tables<R>(a, groups, ng);
     if (tb < 1) return hipErrorInvalidValue;
     if constexpr (ROWS) hipLaunchKernelGGL((skinny16_rows_kernel<R, NW, B>), dim3(tb), dim3(64 * NW), 0, stream, a);
     else hipLaunchKernelGGL((skinny16_kernel<R, B, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
@@ -357,17 +518,42 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
     a.M = M;
     a.K = K;
     a.ngroups = ngroups;
-    // The row-run form with row tiles of 32 from 4096 rows (half the activation reads per weight
-    // byte), else 16 (more workgroups); four waves per workgroup, two where the row tiles outnumber
-    // the CUs (more, shorter-lived workgroups resident per CU: all of a launch's tiles in one
-    // round).  Measured on MI355X, kernel time at M = 8 / 16: four waves against eight q 8.7 /
+    // Row tiles of 32 from 4096 rows (half the activation reads per weight byte), else 16 (more
+    // workgroups); four waves per workgroup, two where the row tiles outnumber the CUs (more,
+    // shorter-lived workgroups resident per CU: all of a launch's tiles in one round).  Measured
+    // on MI355X for the row-run form, kernel time at M = 8 / 16: four waves against eight q 8.7 /
     // 9.6 vs 9.2 / 10.2 us, k 6.8 / 7.9 vs 7.3 / 8.2, o 8.6 / 10.4 vs 9.5 / 11.0, down 13.7 / 17.6
     // vs 14.4 / 18.5; up (392 tiles) with two waves 13.6 / 15.2 against 14.3 / 16.1 (four) and
-    // 16.2 / 18.4 (eight).  Tuning knobs: s16.r (1, 2) forces the row tile, s16.w (2, 4, 8) the
-    // waves; s16.t = 2 selects the direct form (16 rows x 64 bytes per load) with s16.b = 4
-    // batches of four slabs and s16.w = 16 waves.
+    // 16.2 / 18.4 (eight).  The DMA form (default; it needs 32-bit offsets within x and each W)
+    // keeps the same choices, two groups in flight per wave: eager per-launch time at M = 8 / 16
+    // against the row runs q 9.7 / 9.9 vs 10.5 / 10.9 us, o 9.5 / 9.8 vs 9.7 / 10.9, up 12.9 /
+    // 14.0 vs 13.5 / 15.3, down 12.9 / 14.6 vs 13.6 / 17.3; three groups in flight measured 1-2 us
+    // slower per launch (LDS for fewer resident waves).  Tuning knobs: s16.r (1, 2) forces the row
+    // tile, s16.w (2, 4, 8) the waves; s16.t = 1 the row-run form, 2 the direct form (16 rows x 64
+    // bytes per load) with s16.b = 4 batches of four slabs and s16.w = 16 waves, 3 the DMA form
+    // with s16.b = 3 groups in flight.
     const Tuning& tn = tuning();
     const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : (rows >= 4096 ? 2 : 1);
+    bool dma_ok = (ldx * 2) * (int64_t)(M - 1) + 2 * (int64_t)K < ((int64_t)1 << 31);
+    for (int i = 0; i < ngroups; ++i)
+        dma_ok = dma_ok && groups[i].ldw * (int64_t)(groups[i].N - 1) + K < ((int64_t)1 << 31);
+    if ((tn.s16_t == 0 || tn.s16_t == 3) && dma_ok) {
+        int tiles = 0;
+        for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
+        const int nw = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w : (tiles > device_info().num_cu ? 2 : 4);
+        const int D = tn.s16_b == 3 && !(R == 2 && nw == 4) ? 3 : 2;
+        const int form = (R - 1) * 4 + (nw == 4 ? 2 : 0) + (D - 2);
+        switch (form) {
+            case 0: *err = s16_dma_launch<1, 2, 2>(a, groups, ngroups, stream); break;
+            case 1: *err = s16_dma_launch<1, 2, 3>(a, groups, ngroups, stream); break;
+            case 2: *err = s16_dma_launch<1, 4, 2>(a, groups, ngroups, stream); break;
+            case 3: *err = s16_dma_launch<1, 4, 3>(a, groups, ngroups, stream); break;
+            case 4: *err = s16_dma_launch<2, 2, 2>(a, groups, ngroups, stream); break;
+            case 5: *err = s16_dma_launch<2, 2, 3>(a, groups, ngroups, stream); break;
+            default: *err = s16_dma_launch<2, 4, 2>(a, groups, ngroups, stream); break;
+        }
+        return true;
+    }
     if (tn.s16_t != 2) {
         int tiles = 0;
         for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
