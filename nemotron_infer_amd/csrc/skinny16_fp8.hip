@@ -322,17 +322,19 @@ skinny16_rows_kernel(const S16Args a) {
 // and a fragment read (16 rows, one logical chunk) hits 16 distinct bank groups.  Waits are
 // explicit vmcnt counts (every group issues the same instructions, and only groups of the wave's
 // run are issued: a wait counts the groups issued after the one it waits for).
-constexpr int kS16DmaW = 4096, kS16DmaX = 8192;     // bytes per slot and row tile / activations
+// XR activation rows are staged: 16, or 8 where M <= 8 (lanes of MFMA columns 8 .. 15 then read
+// row 7, and their products are dropped).
+constexpr int kS16DmaW = 4096;                         // bytes per slot and row tile
 
-template <int R, int NW, int D>
+template <int R, int NW, int D, int XR>
 constexpr int s16_dma_lds() {
-    return NW * D * (R * kS16DmaW + kS16DmaX) + NW * R * 64 * 16;
+    return NW * D * (R * kS16DmaW + XR * 512) + NW * R * 64 * 16;
 }
 
-template <int R, int NW, int D>
+template <int R, int NW, int D, int XR>
 __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) {
-    constexpr int kW = R * kS16DmaW, kSlot = kW + kS16DmaX;
-    constexpr int kPer = 4 * R + 8;                    // DMA instructions per group
+    constexpr int kW = R * kS16DmaW, kSlot = kW + XR * 512;
+    constexpr int kPer = 4 * R + XR / 2;               // DMA instructions per group
     static_assert(D >= 1 && D <= 3 && (D - 1) * kPer <= 63, "vmcnt range");
     typedef __attribute__((address_space(3))) void lds_void;
     extern __shared__ __attribute__((aligned(16))) uint8_t s16_lds[];
@@ -386,7 +388,7 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
                 dma16_lds(G.W, wbase[j][q] + 16u * (uint32_t)min(g4 * 16 + wsw[q], CW - 1),
                         sw + (uint32_t)((4 * j + q) * 1024));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < XR / 2; ++i) {
             const int rho = 2 * i + xh;
             const uint32_t xoff = (uint32_t)((int64_t)min(rho, M - 1) * a.ldx * 2);
             dma16_lds(a.x, xoff + 16u * (uint32_t)min(g4 * 32 + (xl ^ rho), CX - 1), sw + (uint32_t)(kW + i * 1024));
@@ -400,12 +402,13 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
         if (b >= n) return;
         const int g4 = g_beg + b;
         const uint8_t* sw = slots + d * kSlot;
-        const uint8_t* sx = sw + kW;
+        const int xr = min(r, XR - 1);
+        const uint8_t* sx = sw + kW + xr * 512;
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) {
             if (g4 * 4 + sl >= S) break;
-            const bf16x8 B0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + r * 512 + 16 * ((8 * sl + 2 * p) ^ r)));
-            const bf16x8 B1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + r * 512 + 16 * ((8 * sl + 2 * p + 1) ^ r)));
+            const bf16x8 B0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + 16 * ((8 * sl + 2 * p) ^ xr)));
+            const bf16x8 B1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + 16 * ((8 * sl + 2 * p + 1) ^ xr)));
 #pragma unroll
             for (int j = 0; j < R; ++j) {
                 const u32x4 w = *reinterpret_cast<const u32x4*>(sw + j * 4096 + r * 256 + 16 * ((4 * sl + p) ^ r));
@@ -467,16 +470,16 @@ int s16_tables(S16Args& a, const GemvGroup* groups, int ng) {
     return tb;
 }
 
-template <int R, int NW, int D>
+template <int R, int NW, int D, int XR>
 hipError_t s16_dma_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
-    constexpr int lds = s16_dma_lds<R, NW, D>();
+    constexpr int lds = s16_dma_lds<R, NW, D, XR>();
     static_assert(lds <= 152 * 1024, "LDS");
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny16_dma_kernel<R, NW, D>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&skinny16_dma_kernel<R, NW, D, XR>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
     const int tb = s16_tables<R>(a, groups, ng);
     if (tb < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((skinny16_dma_kernel<R, NW, D>), dim3(tb), dim3(64 * NW), lds, stream, a);
+    hipLaunchKernelGGL((skinny16_dma_kernel<R, NW, D, XR>), dim3(tb), dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
 
@@ -540,17 +543,29 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
     if ((tn.s16_t == 0 || tn.s16_t == 3) && dma_ok) {
         int tiles = 0;
         for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
-        const int nw = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w : (tiles > device_info().num_cu ? 2 : 4);
-        const int D = tn.s16_b == 3 && !(R == 2 && nw == 4) ? 3 : 2;
+        const bool x8 = M <= 8;
+        int nw = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w : (tiles > device_info().num_cu ? 2 : 4);
+        if (tn.s16_w == 8 && x8 && R == 1) nw = 8;
+        const int D = tn.s16_b == 3 && nw != 8 && !(R == 2 && nw == 4 && !x8) ? 3 : 2;
+        if (x8) {
+            if (R == 1) *err = nw == 2   ? s16_dma_launch<1, 2, 2, 8>(a, groups, ngroups, stream)
+                               : nw == 8 ? s16_dma_launch<1, 8, 2, 8>(a, groups, ngroups, stream)
+                               : D == 3  ? s16_dma_launch<1, 4, 3, 8>(a, groups, ngroups, stream)
+                                         : s16_dma_launch<1, 4, 2, 8>(a, groups, ngroups, stream);
+            else *err = nw == 4 ? s16_dma_launch<2, 4, 2, 8>(a, groups, ngroups, stream)
+                        : D == 3 ? s16_dma_launch<2, 2, 3, 8>(a, groups, ngroups, stream)
+                                 : s16_dma_launch<2, 2, 2, 8>(a, groups, ngroups, stream);
+            return true;
+        }
         const int form = (R - 1) * 4 + (nw == 4 ? 2 : 0) + (D - 2);
         switch (form) {
-            case 0: *err = s16_dma_launch<1, 2, 2>(a, groups, ngroups, stream); break;
-            case 1: *err = s16_dma_launch<1, 2, 3>(a, groups, ngroups, stream); break;
-            case 2: *err = s16_dma_launch<1, 4, 2>(a, groups, ngroups, stream); break;
-            case 3: *err = s16_dma_launch<1, 4, 3>(a, groups, ngroups, stream); break;
-            case 4: *err = s16_dma_launch<2, 2, 2>(a, groups, ngroups, stream); break;
-            case 5: *err = s16_dma_launch<2, 2, 3>(a, groups, ngroups, stream); break;
-            default: *err = s16_dma_launch<2, 4, 2>(a, groups, ngroups, stream); break;
+            case 0: *err = s16_dma_launch<1, 2, 2, 16>(a, groups, ngroups, stream); break;
+            case 1: *err = s16_dma_launch<1, 2, 3, 16>(a, groups, ngroups, stream); break;
+            case 2: *err = s16_dma_launch<1, 4, 2, 16>(a, groups, ngroups, stream); break;
+            case 3: *err = s16_dma_launch<1, 4, 3, 16>(a, groups, ngroups, stream); break;
+            case 4: *err = s16_dma_launch<2, 2, 2, 16>(a, groups, ngroups, stream); break;
+            case 5: *err = s16_dma_launch<2, 2, 3, 16>(a, groups, ngroups, stream); break;
+            default: *err = s16_dma_launch<2, 4, 2, 16>(a, groups, ngroups, stream); break;
         }
         return true;
     }

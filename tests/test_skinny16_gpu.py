@@ -73,7 +73,7 @@ def test_small_m_when_forced(M):
                                      (1, 1, 2, 8), (1, 2, 2, 8), (2, 1, 2, 8), (2, 2, 2, 8), (2, 1, 4, 8), (2, 2, 4, 8),
                                      (2, 1, 2, 16), (2, 2, 2, 16), (2, 1, 4, 16),
                                      (3, 1, 2, 0), (3, 2, 2, 0), (3, 1, 2, 2), (3, 1, 3, 2), (3, 1, 2, 4), (3, 1, 3, 4),
-                                     (3, 2, 2, 2), (3, 2, 3, 2), (3, 2, 2, 4)])
+                                     (3, 2, 2, 2), (3, 2, 3, 2), (3, 2, 2, 4), (3, 2, 3, 4), (3, 1, 2, 8)])
 def test_ragged_shapes_each_form(T, R, B, W):
     """Every form (row runs through LDS with two, four or eight waves or as chosen (W = 0); direct
     loads with batches of two or four slabs and eight or sixteen waves; both operands by DMA into
@@ -92,11 +92,16 @@ def test_ragged_shapes_each_form(T, R, B, W):
         _check(M, N, K, 5200 + 7 * R + B + W + M + N + K, f"T={T} R={R} B={B} W={W} M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("R,W", [(1, 2), (1, 4), (2, 2), (2, 4)])
+@pytest.mark.parametrize("R,W", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4)])
 def test_dma_form_equals_row_runs(R, W):
     """The DMA form splits K between the waves as the row-run form does and feeds the MFMAs the
-    same operands in the same order: the same bytes, at M from 9 to 16 and ragged N and K."""
-    for M, N, K in [(16, 3136, 12544), (9, 1000, 3136), (13, 300, 1088), (16, 37, 64)]:
+    same operands in the same order: the same bytes, with 16 activation rows staged (M from 9 to
+    16) or 8 (M <= 8), on ragged N and K.  (The DMA form has eight waves only with 8 staged rows
+    and row tiles of 16.)"""
+    for M, N, K in [(16, 3136, 12544), (9, 1000, 3136), (13, 300, 1088), (16, 37, 64), (8, 3136, 12544),
+                    (5, 1000, 3136), (3, 300, 1088), (8, 37, 64)]:
+        if W == 8 and M > 8:
+            continue
         announce("s16_dma_eq_rows", R, W, M, N, K)
         _lib.tuning_set("s16", 1)
         _lib.tuning_set("s16.r", R)
