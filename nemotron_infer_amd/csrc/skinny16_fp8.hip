@@ -404,20 +404,43 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
         const uint8_t* sw = slots + d * kSlot;
         const int xr = min(r, XR - 1);
         const uint8_t* sx = sw + kW + xr * 512;
+        struct Slab {
+            u32x4 x0, x1, w[R];
+        };
+        auto read = [&](Slab& o, int sl) {
+            o.x0 = *reinterpret_cast<const u32x4*>(sx + 16 * ((8 * sl + 2 * p) ^ xr));
+            o.x1 = *reinterpret_cast<const u32x4*>(sx + 16 * ((8 * sl + 2 * p + 1) ^ xr));
 #pragma unroll
-        for (int sl = 0; sl < 4; ++sl) {
-            if (g4 * 4 + sl >= S) break;
-            const bf16x8 B0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + 16 * ((8 * sl + 2 * p) ^ xr)));
-            const bf16x8 B1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sx + 16 * ((8 * sl + 2 * p + 1) ^ xr)));
+            for (int j = 0; j < R; ++j)
+                o.w[j] = *reinterpret_cast<const u32x4*>(sw + j * 4096 + r * 256 + 16 * ((4 * sl + p) ^ r));
+        };
+        auto mma = [&](const Slab& o) {
+            const bf16x8 B0 = __builtin_bit_cast(bf16x8, o.x0);
+            const bf16x8 B1 = __builtin_bit_cast(bf16x8, o.x1);
 #pragma unroll
             for (int j = 0; j < R; ++j) {
-                const u32x4 w = *reinterpret_cast<const u32x4*>(sw + j * 4096 + r * 256 + 16 * ((4 * sl + p) ^ r));
+                const u32x4 w = o.w[j];
                 const uint2 c0 = e4m3x4_to_bf16(w[0]), c1 = e4m3x4_to_bf16(w[1]);
                 const uint2 c2 = e4m3x4_to_bf16(w[2]), c3 = e4m3x4_to_bf16(w[3]);
                 const bf16x8 A0 = __builtin_bit_cast(bf16x8, uint4{c0.x, c0.y, c1.x, c1.y});
                 const bf16x8 A1 = __builtin_bit_cast(bf16x8, uint4{c2.x, c2.y, c3.x, c3.y});
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, acc[j], 0, 0, 0);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, acc[j], 0, 0, 0);
+            }
+        };
+        if (g4 * 4 + 4 <= S) {                         // a whole group: every LDS read first
+            Slab o[4];
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) read(o[sl], sl);
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) mma(o[sl]);
+        } else {
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                if (g4 * 4 + sl >= S) break;
+                Slab o;
+                read(o, sl);
+                mma(o);
             }
         }
     };
