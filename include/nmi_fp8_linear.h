@@ -405,16 +405,16 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
  * (1, 2: short-prompt kernel, 20, 21, 24), "gemm.sk", "gemm.splits": workgroups splitting K in
  * the short-prompt GEMM (1: none), "gemm.short": f + 1 forces its tile form f (0..7),
  * "gemm.sk_cap": workgroups per tile of the stream-K form at most (0: 2, -1: one workgroup per
- * CU), "skinny.path", "skinny.ks", "skinny.kg", "skinny.u", "s4.ks", "s4.t", "s4.u", "m1.path",
+ * CU), "skinny.path" (2: the skinny kernels take M = 2 too, 3: the GEMV kernel takes M <= 4),
+ * "m1.path" (3: M = 1 on the 4x4x4 skinny kernel), "s4.ks", "s4.t", "s4.u",
  * "s4.dma": 2 selects the windowed form of the 4x4x4 skinny kernel instead of the pipelined one,
  * "s4.kg": K groups split between workgroups by the pipelined form (> 1; needs the workspace
  * nmi_linear_workspace_bytes then reports), "s16": the 16x16x32 skinny kernel (0: automatic, from
  * M = 3, 1: for 2 <= M <= 16, 2: never), "s16.r": its row tiles of 16 (1) or 32 (2), "s16.w": its
- * waves per workgroup (2, 4, 8), "s16.t": its load form (1 row runs through registers, 2 direct
- * loads, with "s16.b": 4 load batches of four slabs and "s16.w": 16 waves, 3 DMA into LDS, the
- * automatic one, with "s16.b": 3 groups in flight per wave), "chain.wgs": workgroups per CU of a GEMV chain created
- * afterwards); 0 restores the automatic choice.  Process-wide, not thread-safe against concurrent
- * launches; results do not depend on them beyond float32 summation order.  No counterpart in the
+ * waves per workgroup (2, 4), "s16.t": 1 its row-run form instead of the DMA form, "chain.wgs":
+ * workgroups per CU of a GEMV chain created afterwards); 0 restores the automatic choice.
+ * Process-wide, not thread-safe against concurrent launches; results do not depend on them
+ * beyond float32 summation order.  No counterpart in the
  * reference (its launch shapes are compile-time constants, ops/gemv.cuh:100-103).
  */
 int nmi_tuning_set(const char* knob, int value);

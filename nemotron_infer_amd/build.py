@@ -31,7 +31,7 @@ INCLUDE = os.path.join(ROOT, "include")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-HIP_SOURCES = ["gemv_stream.hip", "gemv_fp8.hip", "skinny_fp8.hip", "skinny4_fp8.hip", "skinny16_fp8.hip", "gemm_fp8.hip", "gemm_short.hip", "decode_fp8.hip", "rmsnorm.hip", "noalloc.hip", "sdpa_decode.hip",
+HIP_SOURCES = ["gemv_stream.hip", "gemv_fp8.hip", "skinny4_fp8.hip", "skinny16_fp8.hip", "gemm_fp8.hip", "gemm_short.hip", "decode_fp8.hip", "rmsnorm.hip", "noalloc.hip", "sdpa_decode.hip",
                "mamba_decode.hip", "sdpa_prefill.hip", "mamba_prefill.hip"]
 HOST_SOURCES = ["capi.cpp", "allocator.cpp", "block.cpp", "attention.cpp", "mamba.cpp"]
 HIP_FLAGS = [

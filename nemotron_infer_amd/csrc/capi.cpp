@@ -104,10 +104,8 @@ size_t linear_workspace_bytes(int M, int64_t total_n, int K) {
     if (M > 16 && M < 512)                            // the short-prompt kernel's K-split partials
         return (t == 0 || t == 2) ? gemm_short_workspace_bytes(M, (int)std::min<int64_t>(total_n, 1 << 30), K) : 0;
     if (M > 16) return gemm_workspace_bytes(M);       // stream-K flags and partials of the GEMM
-    // the split-K 16x16x32 kernel ("skinny.path" = 1, or "m1.path" = 2 for M = 1) and the K
-    // split of the 4x4x4 kernel's pipelined form use a workspace
+    // the K split of the 4x4x4 kernel's pipelined form ("s4.kg" > 1) uses a workspace
     const Path path = choose_path(M);
-    if (path == Path::Skinny) return skinny_workspace_bytes(M, K, total_n, device_info().num_cu);
     if (path == Path::Skinny4) return skinny4_workspace_bytes(M, K, total_n, device_info().num_cu);
     return 0;
 }
@@ -115,16 +113,14 @@ size_t linear_workspace_bytes(int M, int64_t total_n, int K) {
 bool gemm_workspace_has_flags(int M) { return M >= 512 && choose_path(M) == Path::Gemm; }
 
 // M == 1 -> GEMV kernel, M == 2 -> GEMV kernel (measured faster than the MFMA kernels there),
-// M <= 16 -> 4x4x4 MFMA skinny kernel, M > 16 -> MFMA GEMM.
+// M <= 16 -> the skinny kernels (16x16x32, or 4x4x4 where that one declines), M > 16 -> MFMA GEMM.
 Path choose_path(int M) {
     const Tuning& t = tuning();
     if (M == 1) {
         if (t.m1_path == 3) return Path::Skinny4;
-        if (t.m1_path == 2) return Path::Skinny;
         return Path::Gemv;
     }
     if (M <= 16) {
-        if (t.skinny_path == 1) return Path::Skinny;
         if ((t.skinny_path == 3 && M <= 4) || (t.skinny_path == 0 && M == 2)) return Path::Gemv;
         return Path::Skinny4;
     }
@@ -137,7 +133,6 @@ hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGro
     if (norm.w && path != Path::Gemv) return hipErrorInvalidValue;
     switch (path) {
         case Path::Gemv: return launch_gemv_grouped(x, ldx, M, K, g, ng, st, norm);
-        case Path::Skinny: return launch_skinny_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
         case Path::Skinny4: {
             hipError_t e = hipSuccess;
             if (launch_skinny16_grouped(x, ldx, M, K, g, ng, st, &e)) return e;
@@ -373,9 +368,6 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "gemv.p")) t.gemv_p = value;
     else if (!std::strcmp(knob, "gemv.xg")) t.gemv_xg = value;
     else if (!std::strcmp(knob, "gemm.tile")) t.gemm_tile = value;
-    else if (!std::strcmp(knob, "skinny.ks")) t.skinny_ks = value;
-    else if (!std::strcmp(knob, "skinny.kg")) t.skinny_kg = value;
-    else if (!std::strcmp(knob, "skinny.u")) t.skinny_u = value;
     else if (!std::strcmp(knob, "m1.path")) t.m1_path = value;
     else if (!std::strcmp(knob, "skinny.path")) t.skinny_path = value;
     else if (!std::strcmp(knob, "s4.ks")) t.s4_ks = value;
@@ -397,7 +389,6 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "gemm.sk_cap")) t.gemm_sk_cap = value;
     else if (!std::strcmp(knob, "s16")) t.s16 = value;
     else if (!std::strcmp(knob, "s16.r")) t.s16_r = value;
-    else if (!std::strcmp(knob, "s16.b")) t.s16_b = value;
     else if (!std::strcmp(knob, "s16.w")) t.s16_w = value;
     else if (!std::strcmp(knob, "s16.t")) t.s16_t = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);

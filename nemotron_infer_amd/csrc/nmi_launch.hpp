@@ -30,12 +30,9 @@ struct Tuning {
     int gemv_p = 0;        // M = 1 GEMV: 16-byte chunks per lane per row per batch (2, 3, 4)
     int gemv_xg = 0;       // M = 1 GEMV: 1 reads x from global memory instead of LDS
     int gemm_tile = 0;     // GEMM tile variant id (see gemm_fp8.hip)
-    int skinny_ks = 0;     // skinny kernel: waves of a workgroup that split K (1, 2, 4)
-    int skinny_kg = 0;     // skinny kernel: workgroups that split K (needs a workspace)
-    int skinny_u = 0;      // skinny kernel: 16-byte weight loads per lane per batch (8, 16)
-    int m1_path = 0;       // M = 1: 0 automatic, 1 GEMV kernel, 2 split-K skinny kernel, 3 4x4x4 kernel
-    int skinny_path = 0;   // 2 <= M <= 16: 0 automatic, 1 split-K 16x16x32 kernel, 2 4x4x4 kernel,
-                           // 3 GEMV kernel (M <= 4)
+    int m1_path = 0;       // M = 1: 0 automatic, 1 GEMV kernel, 3 4x4x4 kernel
+    int skinny_path = 0;   // 2 <= M <= 16: 0 automatic, 2 the skinny kernels also at M = 2, 3 GEMV
+                           // kernel (M <= 4)
     int s4_ks = 0;         // 4x4x4 skinny kernel: waves splitting K (1, 2, 4)
     int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
@@ -55,9 +52,8 @@ struct Tuning {
     int gemm_sk_cap = 0;   // GEMM stream-K: at most this many workgroups per tile (0: 2; -1: one per CU)
     int s16 = 0;           // 16x16x32 skinny kernel: 0 automatic (M >= 3), 1 for 2 <= M <= 16, 2 never
     int s16_r = 0;         // 16x16x32 skinny kernel: row tiles of 16 per workgroup (1, 2; 0: by rows)
-    int s16_t = 0;         // 16x16x32 skinny kernel: 1 row runs, 2 direct form, 3 DMA (0: DMA where it fits)
-    int s16_b = 0;         // 16x16x32 skinny kernel, direct form: slabs per load batch (4; 0: 2)
-    int s16_w = 0;         // 16x16x32 skinny kernel: waves per workgroup (row runs: 2, 4, 8; direct: 16)
+    int s16_t = 0;         // 16x16x32 skinny kernel: 1 row runs (0: DMA where it fits)
+    int s16_w = 0;         // 16x16x32 skinny kernel: waves per workgroup (2, 4; 0: by row tiles)
 };
 Tuning& tuning();
 
@@ -96,13 +92,6 @@ struct Norm {
 // M = 1 GEMV over up to kMaxGroups matrices that share x [K] (one launch).
 hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,
                                   hipStream_t stream);
-
-// 1 <= M <= 16 on bf16 MFMA over up to kMaxGroups matrices sharing x [M, K].  With a
-// workspace of at least skinny_workspace_bytes() bytes (zero-filled before its first use; every
-// launch leaves it re-armed) K is also split between workgroups.
-size_t skinny_workspace_bytes(int M, int K, int64_t total_rows, int num_cu);
-hipError_t launch_skinny_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
-                                 int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // 2 <= M <= 16 on 4x4x4 MFMA with coalesced weight reads.  With a workspace of at least
 // skinny4_workspace_bytes() bytes (zero-filled before its first use; every launch leaves it
@@ -303,7 +292,7 @@ hipError_t launch_decode(const uint8_t* codes, float* out_f32, float* out_scaled
                          uint16_t* out_bf16, float scale, int n, hipStream_t stream);
 
 // Kernel chosen for a linear with M activation rows (tuning knobs may override).
-enum class Path { Gemv, Skinny, Skinny4, Gemm };
+enum class Path { Gemv, Skinny4, Gemm };
 Path choose_path(int M);
 
 // One or more linears sharing x [M, K] on the kernel choose_path(M) names (GEMM: one launch per

@@ -10,23 +10,23 @@
 // path and how many bytes each CU keeps in flight.
 //
 // * A workgroup owns one row tile (16 R weight rows) over all of K; its NW waves split K into
-//   contiguous runs of 64-k slabs.  Lane (r, p) = (lane % 16, lane / 16) loads, per slab, 16
-//   codes of row 16 j + r (j < R) at k = 16 p (one instruction: 16 rows x 64 contiguous bytes)
-//   and the 32 bytes x[r][16 p .. 16 p + 15] straight from global memory (the activations are a
-//   few hundred KiB, read by every workgroup: L2 hits).  Codes 0-7 and 8-15 feed two
-//   v_mfma_f32_16x16x32_bf16 (A = weights: row r, k 8 p + e; B = activations: column m = r);
-//   D[n][m] lands as rows 4 p + i, column r of lane (r, p).  Columns m >= M read row M - 1 and
-//   are not stored.
+//   contiguous runs of 256-k groups (four 64-k slabs).  Per slab, lane (r, p) = (lane % 16,
+//   lane / 16) holds 16 codes of row 16 j + r (j < R) at k = 16 p and the 32 bytes
+//   x[r][16 p .. 16 p + 15] (the activations are a few hundred KiB, read by every workgroup: L2
+//   hits).  Codes 0-7 and 8-15 feed two v_mfma_f32_16x16x32_bf16 (A = weights: row r, k 8 p + e;
+//   B = activations: column m = r); D[n][m] lands as rows 4 p + i, column r of lane (r, p).
+//   Columns m >= M read row M - 1 and are not stored.
 // * DMA form (the default, skinny16_dma_kernel): both operands go global -> LDS by
 //   global_load_lds_dwordx4, the weights 4 rows x 256 contiguous bytes and the activations
 //   2 rows x 512 bytes per instruction, into a few wave-private slots; each wave takes a
 //   contiguous run of 256-k groups and reads the operands back in the MFMA layout.  Against the
 //   row-run form (skinny16_rows_kernel, tuning knob s16.t = 1: weights staged through registers
 //   into LDS, activations loaded in the MFMA layout, which touches 16 rows per instruction) it
-//   measured 4-16% faster per launch on the config-2 shapes, the most at M = 16.  The direct form
-//   (skinny16_kernel, s16.t = 2) loads the MFMA layout itself, 16 rows x 64 bytes per weight
-//   instruction: 10-20% slower than the row runs (DRAM efficiency).
-// * In the register forms, loads go in batches, the next in flight while this one is
+//   measured 4-16% faster per launch on the config-2 shapes, the most at M = 16.  The row runs
+//   remain for operands beyond the DMA form's 32-bit offsets.  (A direct form that loaded the
+//   MFMA layout itself, 16 rows x 64 bytes per weight instruction, was 10-20% slower than the
+//   row runs: DRAM efficiency.)
+// * In the row-run form, loads go in batches, the next in flight while this one is
 //   multiplied; every batch is issued (slabs past the wave's run read one word every lane
 //   shares), so the compiler's wait counts are exact on every path.
 // * The waves' sums meet in LDS and are added in wave order (a fixed order: results do not depend
@@ -87,102 +87,6 @@ __device__ __forceinline__ void s16_store(const S16Group& G, int m, int n0, cons
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         if (n0 + i < G.N) G.y[(int64_t)m * G.ldy + n0 + i] = epilogue(v[i], G.s[n0 + i], G.epi, rr[i]);
-}
-
-// R: row tiles of 16 per workgroup; B: slabs per batch (two batches in flight per wave); NW: waves.
-template <int R, int B, int NW>
-__global__ __launch_bounds__(64 * NW) void skinny16_kernel(const S16Args a) {
-    __shared__ f32x4 red[NW][R][64];
-
-    const int tile = blockIdx.x;
-    int gi = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxGroups; ++i)
-        if (i < a.ngroups && tile >= a.g[i].tile_begin) gi = i;
-    const S16Group& G = a.g[gi];
-    const int row0 = (tile - G.tile_begin) * 16 * R;
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-    const int r = lane & 15, p = lane >> 4;
-    const int M = a.M;
-    const int S = a.K >> 6;
-    const int s_beg = wave * S / NW, s_end = (wave + 1) * S / NW;
-    const int n = s_end - s_beg;
-    const int nb = (n + B - 1) / B;
-
-    const uint8_t* wrow[R];
-#pragma unroll
-    for (int j = 0; j < R; ++j) wrow[j] = G.W + (int64_t)min(row0 + 16 * j + r, G.N - 1) * G.ldw + 16 * p;
-    const uint16_t* xrow = a.x + (int64_t)min(r, M - 1) * a.ldx + 16 * p;
-    const uint8_t* wdummy = G.W;
-    const uint16_t* xdummy = a.x;
-
-    struct Batch {
-        u32x4 w[B][R];
-        u32x4 x[B][2];
-    };
-    auto load = [&](Batch& bt, int b) {
-#pragma unroll
-        for (int e = 0; e < B; ++e) {
-            const int i = b * B + e;
-            const int s = s_beg + i;
-            const bool ok = i < n;
-            const uint16_t* xp = ok ? xrow + s * 64 : xdummy;
-            bt.x[e][0] = *reinterpret_cast<const u32x4*>(xp);
-            bt.x[e][1] = *reinterpret_cast<const u32x4*>(ok ? xp + 8 : xdummy);
-#pragma unroll
-            for (int j = 0; j < R; ++j)
-                bt.w[e][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ok ? wrow[j] + s * 64 : wdummy));
-        }
-    };
-
-    f32x4 acc[R];
-#pragma unroll
-    for (int j = 0; j < R; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto consume = [&](const Batch& bt, int b) {
-#pragma unroll
-        for (int e = 0; e < B; ++e) {
-            if (b * B + e >= n) break;
-            const bf16x8 B0 = __builtin_bit_cast(bf16x8, bt.x[e][0]);
-            const bf16x8 B1 = __builtin_bit_cast(bf16x8, bt.x[e][1]);
-#pragma unroll
-            for (int j = 0; j < R; ++j) {
-                const u32x4 w = bt.w[e][j];
-                const uint2 c0 = e4m3x4_to_bf16(w[0]), c1 = e4m3x4_to_bf16(w[1]);
-                const uint2 c2 = e4m3x4_to_bf16(w[2]), c3 = e4m3x4_to_bf16(w[3]);
-                const bf16x8 A0 = __builtin_bit_cast(bf16x8, uint4{c0.x, c0.y, c1.x, c1.y});
-                const bf16x8 A1 = __builtin_bit_cast(bf16x8, uint4{c2.x, c2.y, c3.x, c3.y});
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, acc[j], 0, 0, 0);
-            }
-        }
-    };
-
-    Batch ba, bb;
-    load(ba, 0);
-    load(bb, 1);
-    for (int b = 0; b < nb; b += 2) {
-        consume(ba, b);
-        load(ba, b + 2);
-        consume(bb, b + 1);
-        load(bb, b + 3);
-    }
-
-    // the waves' sums in wave order, then the epilogue (wave j stores row tile j)
-#pragma unroll
-    for (int j = 0; j < R; ++j) red[wave][j][lane] = acc[j];
-    __syncthreads();
-    if (wave < R) {
-        f32x4 v = red[0][wave][lane];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            const f32x4 u = red[w][wave][lane];
-            v = f32x4{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
-        }
-        if (r < M) s16_store(G, r, row0 + 16 * wave + 4 * p, v);
-    }
 }
 
 // Row-run form: the same products and sums, with the weights loaded as 4 rows x 256 contiguous
@@ -506,12 +410,11 @@ hipError_t s16_dma_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream
     return hipGetLastError();
 }
 
-template <int R, int B, int NW, bool ROWS = false>
-hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
+template <int R, int NW>
+hipError_t s16_rows_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
     const int tb = s16_tables<R>(a, groups, ng);
     if (tb < 1) return hipErrorInvalidValue;
-    if constexpr (ROWS) hipLaunchKernelGGL((skinny16_rows_kernel<R, NW, B>), dim3(tb), dim3(64 * NW), 0, stream, a);
-    else hipLaunchKernelGGL((skinny16_kernel<R, B, NW>), dim3(tb), dim3(64 * NW), 0, stream, a);
+    hipLaunchKernelGGL((skinny16_rows_kernel<R, NW, 2>), dim3(tb), dim3(64 * NW), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -519,8 +422,8 @@ hipError_t s16_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t s
 
 // Where this kernel is taken by default (tuning knob s16 = 1: every 2 <= M <= 16, 2: never):
 // from M = 3 (M = 2 is the stream GEMV's).  Measured on MI355X (bench, config 2, four launches per
-// step): M = 4 41.3 against 43.3 us on the 4x4x4 kernel, M = 8 43.8 against 53, M = 16 54.2
-// against 74; M = 2 39.7 against 38.6 on the stream GEMV.
+// step, DMA form): M = 4 38.9 against 43.3 us on the 4x4x4 kernel, M = 8 40.5 against 53, M = 16
+// 46.3 against 74; M = 2 equal to the stream GEMV within the timing noise.
 bool skinny16_wanted(int M, int K) {
     const int knob = tuning().s16;
     if (knob == 2 || M > 16 || M < 2) return false;
@@ -546,81 +449,45 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
     a.ngroups = ngroups;
     // Row tiles of 32 from 4096 rows (half the activation reads per weight byte), else 16 (more
     // workgroups); four waves per workgroup, two where the row tiles outnumber the CUs (more,
-    // shorter-lived workgroups resident per CU: all of a launch's tiles in one round).  Measured
-    // on MI355X for the row-run form, kernel time at M = 8 / 16: four waves against eight q 8.7 /
-    // 9.6 vs 9.2 / 10.2 us, k 6.8 / 7.9 vs 7.3 / 8.2, o 8.6 / 10.4 vs 9.5 / 11.0, down 13.7 / 17.6
-    // vs 14.4 / 18.5; up (392 tiles) with two waves 13.6 / 15.2 against 14.3 / 16.1 (four) and
-    // 16.2 / 18.4 (eight).  The DMA form (default; it needs 32-bit offsets within x and each W)
-    // keeps the same choices, two groups in flight per wave: eager per-launch time at M = 8 / 16
+    // shorter-lived workgroups resident per CU: all of a launch's tiles in one round); two groups
+    // in flight per wave.  Measured on MI355X for the row-run form, kernel time at M = 8 / 16: four
+    // waves against eight q 8.7 / 9.6 vs 9.2 / 10.2 us, k 6.8 / 7.9 vs 7.3 / 8.2, o 8.6 / 10.4 vs
+    // 9.5 / 11.0, down 13.7 / 17.6 vs 14.4 / 18.5; up (392 tiles) with two waves 13.6 / 15.2
+    // against 14.3 / 16.1 (four) and 16.2 / 18.4 (eight).  The DMA form (default; it needs 32-bit
+    // offsets within x and each W) keeps the same choices: eager per-launch time at M = 8 / 16
     // against the row runs q 9.7 / 9.9 vs 10.5 / 10.9 us, o 9.5 / 9.8 vs 9.7 / 10.9, up 12.9 /
     // 14.0 vs 13.5 / 15.3, down 12.9 / 14.6 vs 13.6 / 17.3; three groups in flight measured 1-2 us
-    // slower per launch (LDS for fewer resident waves).  Tuning knobs: s16.r (1, 2) forces the row
-    // tile, s16.w (2, 4, 8) the waves; s16.t = 1 the row-run form, 2 the direct form (16 rows x 64
-    // bytes per load) with s16.b = 4 batches of four slabs and s16.w = 16 waves, 3 the DMA form
-    // with s16.b = 3 groups in flight.
+    // slower per launch (the LDS holds fewer waves), eight waves with 8 staged rows equal within
+    // the noise.  Tuning knobs: s16.r (1, 2) forces the row tile, s16.w (2, 4) the waves, s16.t = 1
+    // the row-run form.
     const Tuning& tn = tuning();
     const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : (rows >= 4096 ? 2 : 1);
+    int tiles = 0;
+    for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
+    const bool four = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w == 4 : tiles <= device_info().num_cu;
     bool dma_ok = (ldx * 2) * (int64_t)(M - 1) + 2 * (int64_t)K < ((int64_t)1 << 31);
     for (int i = 0; i < ngroups; ++i)
         dma_ok = dma_ok && groups[i].ldw * (int64_t)(groups[i].N - 1) + K < ((int64_t)1 << 31);
-    if ((tn.s16_t == 0 || tn.s16_t == 3) && dma_ok) {
-        int tiles = 0;
-        for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
-        const bool x8 = M <= 8;
-        int nw = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w : (tiles > device_info().num_cu ? 2 : 4);
-        if (tn.s16_w == 8 && x8 && R == 1) nw = 8;
-        const int D = tn.s16_b == 3 && nw != 8 && !(R == 2 && nw == 4 && !x8) ? 3 : 2;
-        if (x8) {
-            if (R == 1) *err = nw == 2   ? s16_dma_launch<1, 2, 2, 8>(a, groups, ngroups, stream)
-                               : nw == 8 ? s16_dma_launch<1, 8, 2, 8>(a, groups, ngroups, stream)
-                               : D == 3  ? s16_dma_launch<1, 4, 3, 8>(a, groups, ngroups, stream)
-                                         : s16_dma_launch<1, 4, 2, 8>(a, groups, ngroups, stream);
-            else *err = nw == 4 ? s16_dma_launch<2, 4, 2, 8>(a, groups, ngroups, stream)
-                        : D == 3 ? s16_dma_launch<2, 2, 3, 8>(a, groups, ngroups, stream)
-                                 : s16_dma_launch<2, 2, 2, 8>(a, groups, ngroups, stream);
-            return true;
-        }
-        const int form = (R - 1) * 4 + (nw == 4 ? 2 : 0) + (D - 2);
+    if (tn.s16_t != 1 && dma_ok) {
+        const int form = (M <= 8 ? 4 : 0) + (R == 2 ? 2 : 0) + (four ? 1 : 0);
         switch (form) {
             case 0: *err = s16_dma_launch<1, 2, 2, 16>(a, groups, ngroups, stream); break;
-            case 1: *err = s16_dma_launch<1, 2, 3, 16>(a, groups, ngroups, stream); break;
-            case 2: *err = s16_dma_launch<1, 4, 2, 16>(a, groups, ngroups, stream); break;
-            case 3: *err = s16_dma_launch<1, 4, 3, 16>(a, groups, ngroups, stream); break;
-            case 4: *err = s16_dma_launch<2, 2, 2, 16>(a, groups, ngroups, stream); break;
-            case 5: *err = s16_dma_launch<2, 2, 3, 16>(a, groups, ngroups, stream); break;
-            default: *err = s16_dma_launch<2, 4, 2, 16>(a, groups, ngroups, stream); break;
+            case 1: *err = s16_dma_launch<1, 4, 2, 16>(a, groups, ngroups, stream); break;
+            case 2: *err = s16_dma_launch<2, 2, 2, 16>(a, groups, ngroups, stream); break;
+            case 3: *err = s16_dma_launch<2, 4, 2, 16>(a, groups, ngroups, stream); break;
+            case 4: *err = s16_dma_launch<1, 2, 2, 8>(a, groups, ngroups, stream); break;
+            case 5: *err = s16_dma_launch<1, 4, 2, 8>(a, groups, ngroups, stream); break;
+            case 6: *err = s16_dma_launch<2, 2, 2, 8>(a, groups, ngroups, stream); break;
+            default: *err = s16_dma_launch<2, 4, 2, 8>(a, groups, ngroups, stream); break;
         }
         return true;
     }
-    if (tn.s16_t != 2) {
-        int tiles = 0;
-        for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
-        const int nw = tn.s16_w == 2 || tn.s16_w == 4 || tn.s16_w == 8 ? tn.s16_w
-                                                                        : (tiles > device_info().num_cu ? 2 : 4);
-        // two groups in flight per wave (three or four measured slower: the registers cost
-        // resident waves)
-        if (nw == 2)
-            *err = R == 2 ? s16_launch<2, 2, 2, true>(a, groups, ngroups, stream)
-                          : s16_launch<1, 2, 2, true>(a, groups, ngroups, stream);
-        else if (nw == 4)
-            *err = R == 2 ? s16_launch<2, 2, 4, true>(a, groups, ngroups, stream)
-                          : s16_launch<1, 2, 4, true>(a, groups, ngroups, stream);
-        else
-            *err = R == 2 ? s16_launch<2, 2, 8, true>(a, groups, ngroups, stream)
-                          : s16_launch<1, 2, 8, true>(a, groups, ngroups, stream);
-        return true;
-    }
-    const int Bt = tn.s16_b == 4 ? 4 : 2, NW = tn.s16_w == 16 ? 16 : 8;
-    const int form = (R == 2 ? 4 : 0) + (Bt == 2 ? 2 : 0) + (NW == 16 ? 1 : 0);
+    const int form = (R == 2 ? 2 : 0) + (four ? 1 : 0);
     switch (form) {
-        case 0: *err = s16_launch<1, 4, 8>(a, groups, ngroups, stream); break;
-        case 1: *err = s16_launch<1, 4, 16>(a, groups, ngroups, stream); break;
-        case 2: *err = s16_launch<1, 2, 8>(a, groups, ngroups, stream); break;
-        case 3: *err = s16_launch<1, 2, 16>(a, groups, ngroups, stream); break;
-        case 4: *err = s16_launch<2, 4, 8>(a, groups, ngroups, stream); break;
-        case 5: *err = s16_launch<2, 2, 16>(a, groups, ngroups, stream); break;   // <2, 4, 16> would spill
-        case 6: *err = s16_launch<2, 2, 8>(a, groups, ngroups, stream); break;
-        default: *err = s16_launch<2, 2, 16>(a, groups, ngroups, stream); break;
+        case 0: *err = s16_rows_launch<1, 2>(a, groups, ngroups, stream); break;
+        case 1: *err = s16_rows_launch<1, 4>(a, groups, ngroups, stream); break;
+        case 2: *err = s16_rows_launch<2, 2>(a, groups, ngroups, stream); break;
+        default: *err = s16_rows_launch<2, 4>(a, groups, ngroups, stream); break;
     }
     return true;
 }

@@ -37,7 +37,7 @@ from tests.gpu_util import DEV, announce, bits, s_to_dev, w_to_dev, x_to_dev
 
 pytestmark = pytest.mark.gpu
 
-KNOBS = ("m1.path", "skinny.path", "gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "s4.ks")
+KNOBS = ("m1.path", "skinny.path", "s16", "gemv.ks", "gemv.t", "gemv.p", "gemv.xg", "gemm.tile", "s4.ks")
 HIDDEN, INTER, EPS = synth.HIDDEN, synth.INTER, 1e-5
 
 
@@ -74,11 +74,10 @@ def _dev(nw, upw, ups, dnw, dns):
 
 
 def _composed(x, nw, upw, ups, dnw, dns, ws=True):
-    # The block hands its linears a workspace -- the 16x16x32 skinny kernel's partials for
-    # 5 <= M <= 16, the short-prompt kernel's K split for 17 <= M < 512, stream-K for the few tiles
-    # of the down projection from M = 512 (the other kernels ignore it; the block gives the split-K
-    # 16x16x32 kernel of skinny.path = 1 none); the composition does the same, so that both run
-    # the same kernels in the same form (same float32 summation order).
+    # The block hands its linears a workspace -- the short-prompt kernel's K split for
+    # 17 <= M < 512, stream-K for the few tiles of the down projection from M = 512 (the other
+    # kernels ignore it); the composition does the same, so that both run the same kernels in the
+    # same form (same float32 summation order).
     h = ops.rmsnorm_bf16(x, nw, EPS)
     up = ops.linear_fp8_w8a16(h, upw, ups, use_workspace=ws)
     r = torch.relu(up)
@@ -174,7 +173,7 @@ def test_block_matches_oracle(M):
 @pytest.mark.parametrize("knobs,Ms", [
     ({"m1.path": 3}, [1]),                           # M = 1 on the 4x4x4 kernel: separate RMSNorm
     ({"skinny.path": 3}, [2, 3, 4]),                 # GEMV kernel for M <= 4 (fused only M <= 2)
-    ({"skinny.path": 1, "m1.path": 2}, [1, 5]),      # split-K 16x16x32 kernel without workspace
+    ({"s16": 2}, [5, 16]),                           # the 4x4x4 kernel instead of the 16x16x32 one
     ({"gemv.ks": 2, "gemv.t": 2, "gemv.p": 3}, [1, 2]),
     ({"gemv.ks": 4, "gemv.t": 1}, [1]),
     ({"gemv.xg": 1}, [1]),                           # the fused form always stages x in LDS
@@ -189,7 +188,7 @@ def test_block_equals_composition_under_knobs(knobs, Ms):
         announce("mlp_block_knobs", knobs, M)
         x = x_to_dev(_act(M, HIDDEN, 300 + M))
         got = ops.mlp_forward_fp8(x, *dev, eps=EPS)
-        ref = _composed(x, *dev, ws=knobs.get("skinny.path") != 1 and knobs.get("m1.path") != 2)
+        ref = _composed(x, *dev)
         assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (knobs, M)
 
 

@@ -1,5 +1,7 @@
-"""GPU parity of the skinny kernel (1 <= M <= 16, bf16 MFMA over e4m3 weights converted in
-registers) and of the grouped entry point, against the torch fp32 dequant-then-F.linear oracle.
+"""GPU parity of the 4x4x4 skinny kernel (1 <= M <= 16, bf16 MFMA over e4m3 weights converted in
+registers; the 16x16x32 kernel, which takes M >= 3 by default, has its own tests and is switched
+off here unless a test names it), of the small-M GEMV forms and of the grouped entry point,
+against the torch fp32 dequant-then-F.linear oracle.
 
 Tolerance: rel_l2 <= 1e-3 and max |diff| <= 2 bf16 ulp at max(|ref|, 2^-8 rms(ref)).
 Size-independent properties: the workspace's arrival counters are re-armed after every
@@ -21,8 +23,7 @@ from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_t
 
 pytestmark = pytest.mark.gpu
 
-KNOBS = ("skinny.ks", "skinny.kg", "skinny.u", "m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u",
-         "s4.dma", "s4.kg")
+KNOBS = ("m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u", "s4.dma", "s4.kg")
 
 
 @pytest.fixture(autouse=True)
@@ -50,16 +51,19 @@ def _run(x, w, s, use_ws):
 @pytest.mark.parametrize("name", ["kat_gemv_n64_k3136", "tiny_m4_n8_k16", "ragged_m3_n37_k208",
                                   "skinny_m16_n48_k3136", "special_nan_zero"])
 @pytest.mark.parametrize("use_ws", [False, True])
-@pytest.mark.parametrize("path", [0, 1])
-def test_fixtures_all_m(name, use_ws, path):
+@pytest.mark.parametrize("kernel", ["4x4x4", "16x16x32"])
+def test_fixtures_all_m(name, use_ws, kernel):
     """Every fixture, every leading-row count 1..M of it, through both skinny kernels (the 4x4x4
-    kernel, path 0, and the split-K 16x16x32 kernel, path 1; M = 1 is forced onto the latter
-    with m1.path = 2)."""
+    kernel, M = 1 forced onto it with m1.path = 3; the 16x16x32 kernel for 2 <= M <= 16 with
+    s16 = 1, M = 1 on the GEMV kernel; fixtures whose K is not a multiple of 64 fall back to the
+    4x4x4 kernel there)."""
     g = load_golden(name)
     x, w, s = g["x_bf16"], g["w_codes"], g["w_scale"]
     ref64 = linear.bf16_rne(g["y_f64"].astype(np.float32))
-    _lib.tuning_set("m1.path", 2)
-    _lib.tuning_set("skinny.path", path)
+    if kernel == "4x4x4":
+        _lib.tuning_set("m1.path", 3)
+    else:
+        _lib.tuning_set("s16", 1)
     for M in range(1, x.shape[0] + 1):
         announce("skinny_fixture", name, M, use_ws)
         y = _run(x[:M], w, s, use_ws)
@@ -69,33 +73,19 @@ def test_fixtures_all_m(name, use_ws, path):
 @pytest.mark.parametrize("M", list(range(1, 17)))
 def test_every_m_ragged(M):
     """Ragged N (not a multiple of 4, 16 or 64) and K (not a multiple of 64), both kernels (the
-    4x4x4 one in both forms) and both workspace modes."""
-    _lib.tuning_set("m1.path", 2)
+    4x4x4 one in both forms, M = 1 included; the 16x16x32 one with s16 = 1, path 1) and both
+    workspace modes."""
+    _lib.tuning_set("m1.path", 3)
+    _lib.tuning_set("skinny.path", 2)
     for N, K in [(37, 208), (1000, 3136), (130, 12544 + 16)]:
         x, w, s = _case(M, N, K, 17 * M + N + K)
         ref = oracle_bits(x, w, s)
         for path, dma in ((0, 0), (0, 2), (1, 0)):
-            _lib.tuning_set("skinny.path", path)
+            _lib.tuning_set("s16", 1 if path == 1 else 2)
             _lib.tuning_set("s4.dma", dma)
             for use_ws in (False, True):
                 announce("skinny_ragged", M, N, K, path, dma, use_ws)
                 assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} path={path} dma={dma} ws={use_ws}")
-
-
-@pytest.mark.parametrize("ksw", [1, 2, 4])
-@pytest.mark.parametrize("u", [8, 16])
-@pytest.mark.parametrize("kg", [1, 3, 7])
-def test_every_schedule(ksw, u, kg):
-    """Each (waves splitting K, loads per batch, workgroups splitting K) instantiation, incl.
-    LDS windows (M = 16 stages 64 chunks per window) and K groups with a partial last group."""
-    _lib.tuning_set("skinny.path", 1)
-    _lib.tuning_set("skinny.ks", ksw)
-    _lib.tuning_set("skinny.u", u)
-    _lib.tuning_set("skinny.kg", kg)
-    for M, N, K in [(16, 300, 3136), (5, 77, 5120), (2, 1024, 1040)]:
-        announce("skinny_schedule", ksw, u, kg, M, N, K)
-        x, w, s = _case(M, N, K, 1000 * ksw + 100 * u + 10 * kg + M)
-        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"ksw={ksw} u={u} kg={kg} M={M}")
 
 
 @pytest.mark.parametrize("ks", [1, 2, 4])
@@ -119,22 +109,23 @@ def test_s4_every_schedule(ks, t, u, dma):
 
 
 @pytest.mark.parametrize("M", [2, 4, 8, 16])
-@pytest.mark.parametrize("path,dma", [(0, 0), (0, 2), (1, 0)])
-def test_config2_shapes(M, path, dma):
+@pytest.mark.parametrize("dma", [0, 2])
+def test_config2_shapes(M, dma):
     """Config 2 (M in {2,4,8,16}, the six decode shapes, per-row log-uniform scales) on the
-    4x4x4 kernel in both forms and on the split-K kernel (with its workspace)."""
-    _lib.tuning_set("skinny.path", path)
+    4x4x4 kernel in both forms (M = 2 too, with skinny.path = 2)."""
+    _lib.tuning_set("skinny.path", 2)
     _lib.tuning_set("s4.dma", dma)
     for lin in synth.DECODE_SET:
-        announce("skinny_config2", M, path, dma, lin.name)
+        announce("skinny_config2", M, dma, lin.name)
         x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, act=lin.act)
-        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} path={path} dma={dma} {lin.name}")
+        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} dma={dma} {lin.name}")
 
 
 def test_workspace_rearmed_and_deterministic():
-    """After a split-K launch the counters read back zero; repeated calls are bit-identical."""
+    """After a K-split launch of the 4x4x4 kernel (s4.kg = 3) the counters read back zero;
+    repeated calls are bit-identical."""
     M, N, K = 8, 3136, 12544
-    _lib.tuning_set("skinny.path", 1)
+    _lib.tuning_set("s4.kg", 3)
     announce("skinny_rearm", M, N, K)
     x, w, s = _case(M, N, K, 4)
     xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
@@ -156,9 +147,11 @@ def test_workspace_rearmed_and_deterministic():
 
 
 def test_workspace_shared_between_shapes():
-    """One workspace used by calls of different shapes in turn (small N, then large N, then
-    small again): a counter slot is never overwritten by another call's partials."""
-    _lib.tuning_set("skinny.path", 1)
+    """One workspace used by K-split calls of the 4x4x4 kernel of different shapes in turn
+    (small N, then large N, then small again): a counter slot is never overwritten by another
+    call's partials."""
+    _lib.tuning_set("s4.kg", 3)
+    _lib.tuning_set("skinny.path", 2)
     L = _lib.lib()
     cases = [(16, 48, 3136), (2, 5120, 3136), (16, 48, 3136), (4, 1024, 12544), (2, 5120, 3136)]
     nbytes = max(L.nmi_linear_workspace_bytes(M, N, K) for M, N, K in cases)
@@ -175,9 +168,10 @@ def test_workspace_shared_between_shapes():
 
 
 def test_workspace_never_returns_stale_partials():
-    """The same shape (same workspace slots) with new inputs each call: every result must match
-    its own oracle, so no partial written by an earlier call can be read back."""
-    _lib.tuning_set("skinny.path", 1)
+    """The same shape (same workspace slots) with new inputs each call (the 4x4x4 kernel's K
+    split): every result must match its own oracle, so no partial written by an earlier call
+    can be read back."""
+    _lib.tuning_set("s4.kg", 3)
     M, N, K = 4, 5120, 3136
     w, s = synth.make_weight(N, K, 5, "cpu", scales="log_uniform")
     wd, sd = w.to(DEV), s.to(DEV)
@@ -191,16 +185,14 @@ def test_workspace_never_returns_stale_partials():
 
 def test_grouped_qkv_matches_separate():
     """q|k|v in one launch (attention_block.cuh:400-402 runs them as three GEMVs) equals the
-    three separate calls under the same (pinned) schedule, bit for bit, for M = 1 on both
-    kernels and M = 4."""
+    three separate calls under the same (pinned) schedule, bit for bit, for M = 1 on the GEMV
+    and 4x4x4 kernels and M = 4."""
     lins = synth.DECODE_SET[:3]
     for M in (1, 4):
-        for path in (1, 2):
+        for path in (1, 3):
             if M > 1 and path == 1:
                 continue
             _lib.tuning_set("m1.path", path)
-            _lib.tuning_set("skinny.kg", 2)
-            _lib.tuning_set("skinny.ks", 2)
             _lib.tuning_set("gemv.ks", 2)
             _lib.tuning_set("s4.t", 1)
             _lib.tuning_set("s4.ks", 1)
@@ -226,12 +218,13 @@ def test_grouped_rejects_bad_groups():
 
 
 def test_m1_mfma_path_vs_gemv_full_size():
-    """M = 1 at config 0's full size through both kernels: both within tolerance of the oracle."""
+    """M = 1 at config 0's full size through the GEMV and 4x4x4 kernels: both within tolerance
+    of the oracle."""
     N, K = 12544, 3136
     announce("m1_paths", N, K)
     x, w, s = _case(1, N, K, 5, scales="per_tensor")
     ref = oracle_bits(x[0], w, s)
-    for path in (1, 2):
+    for path in (1, 3):
         _lib.tuning_set("m1.path", path)
         y = bits(ops.linear_fp8_w8a16(x_to_dev(x[0]), w_to_dev(w), s_to_dev(s)))
         assert_parity(y, ref, f"m1.path={path}")
