@@ -144,7 +144,10 @@ __device__ __forceinline__ void skinny4_finish(f32x4 (&acc)[T][G], f32x4 (&parti
 // tile (agent-scope stores, visible to every XCD), the row block's arrival count, and in the
 // last workgroup to arrive the sum of the K groups' partials in order 0..kgroups-1, the scale, one
 // bf16 rounding and the epilogue.  Every word that crosses workgroups is written and read with
-// agent-scope operations only; the counter is re-armed by the last arrival.
+// agent-scope atomics; the arrival is an agent-scope acquire-release read-modify-write (after the
+// workgroup barrier that orders the partial stores of all its threads before it), so the last
+// arrival's reads of the others' partials happen after their stores.  The counter is re-armed
+// by the last arrival.
 template <int KS, int T, int G>
 __device__ __forceinline__ void skinny4_finish_split(f32x4 (&acc)[T][G],
                                                      f32x4 (&partial)[KS > 1 ? KS : 1][kWaves / KS][T][G][4],
@@ -208,7 +211,7 @@ __device__ __forceinline__ void skinny4_finish_split(f32x4 (&acc)[T][G],
     __syncthreads();
     if (tid == 0) {
         const uint32_t prev =
-            __hip_atomic_fetch_add(a.counters + rb_all, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(a.counters + rb_all, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         last_flag = (prev == (uint32_t)(a.kgroups - 1)) ? 1u : 0u;
     }
     __syncthreads();
