@@ -223,7 +223,11 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
 }
 
 // GEMV chain: the planned phase table and per-wave step counts live in device memory for the
-// handle's lifetime; one launch per segment (a run of phases up to the next one that waits).
+// handle's lifetime; one launch per segment (a run of phases up to the next one that waits).  A
+// segment of one phase (every phase of a fully dependent chain) is launched as the single GEMV
+// launch of that phase instead: x staged once per workgroup in LDS rather than read per step,
+// the same arithmetic and so the same bytes (measured on MI355X: config 1 as a dependent chain
+// 33.0 -> 30.4 us, the rate of four separate launches).
 struct ChainSegment {
     int p0, nphases;                        // phases of the segment
     int total_rg;                           // its row groups
@@ -234,6 +238,7 @@ struct nmi_gemv_chain {
     StreamPhase* dev = nullptr;             // the phase table
     int* wave_steps = nullptr;              // steps of each wave, segment by segment
     std::vector<ChainSegment> seg;
+    std::vector<StreamPhase> host;          // the phase table on the host (single-phase segments)
     int nphases = 0;
     int device = -1;
 };
@@ -282,6 +287,7 @@ int nmi_gemv_chain_create(const nmi_gemv_phase* phases, int nphases, nmi_gemv_ch
     auto* c = new nmi_gemv_chain;
     c->nphases = nphases;
     c->seg = seg;
+    c->host = host;
     if (e == hipSuccess) e = hipGetDevice(&c->device);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->dev), host.size() * sizeof(StreamPhase));
     if (e == hipSuccess)
@@ -313,8 +319,19 @@ int nmi_gemv_chain_launch(const nmi_gemv_chain* chain, void* workspace, size_t w
     if (hipGetDevice(&dev) == hipSuccess && dev != chain->device)
         return fail(NMI_ERR_INVALID_ARG, "%s: chain was created on device %d, current is %d", fn, chain->device, dev);
     for (const ChainSegment& sg : chain->seg) {
-        const hipError_t e = launch_gemv_stream_chain(chain->dev + sg.p0, chain->wave_steps + sg.steps_off, sg.nphases,
-                                                      sg.total_rg, sg.grid, static_cast<hipStream_t>(stream));
+        hipError_t e;
+        if (sg.nphases == 1) {
+            const StreamPhase& ph = chain->host[(size_t)sg.p0];
+            GemvGroup g[kMaxGroups];
+            for (int i = 0; i < ph.ngroups; ++i) {
+                const StreamGroup& G = ph.g[i];
+                g[i] = GemvGroup{G.W, G.ldw, G.s, G.y, G.N, G.N, 0, 0, Epi{}};
+            }
+            e = launch_gemv_grouped(ph.x, ph.K, 1, ph.K, g, ph.ngroups, static_cast<hipStream_t>(stream), Norm{});
+        } else {
+            e = launch_gemv_stream_chain(chain->dev + sg.p0, chain->wave_steps + sg.steps_off, sg.nphases,
+                                         sg.total_rg, sg.grid, static_cast<hipStream_t>(stream));
+        }
         if (e != hipSuccess) return hip_status(e, fn);
     }
     return NMI_OK;
