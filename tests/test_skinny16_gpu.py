@@ -155,6 +155,34 @@ def test_grouped_qkv_strided_outputs():
         assert_parity(bits(outs[i]), oracle_bits(x, w, s), f"grouped {i}", per_row_scales=True)
 
 
+@pytest.mark.parametrize("T", [1, 0])
+@pytest.mark.parametrize("M", [3, 8, 16])
+def test_strided_operands(T, M):
+    """ldx > K, ldw > K, ldy > N (slices of wider buffers, 16-byte aligned) through both load
+    forms: the DMA and register loads follow the strides, the results equal the contiguous
+    call's bit for bit, and nothing outside the output slice is written."""
+    N, K = 1000, 3136
+    _lib.tuning_set("s16", 1)
+    _lib.tuning_set("s16.t", T)
+    announce("s16_strided", T, M, N, K)
+    x, w, s = _case(M, N, K, 5700 + M)
+    xbig = torch.zeros((M, K + 64), dtype=torch.bfloat16, device=DEV)
+    xbig[:, 32:32 + K] = x_to_dev(x)
+    wbig = torch.zeros((N, K + 48), dtype=torch.uint8, device=DEV)
+    wbig[:, 16:16 + K] = w_to_dev(w)
+    ybig = torch.full((M, N + 40), 7.0, dtype=torch.bfloat16, device=DEV)
+    sd = s_to_dev(s)
+    L = _lib.lib()
+    xv, wv, yv = xbig[:, 32:], wbig[:, 16:], ybig[:, 8:]
+    _lib.check(L.nmi_linear_fp8_w8a16(xv.data_ptr(), xbig.stride(0), wv.data_ptr(), wbig.stride(0), sd.data_ptr(),
+                                      yv.data_ptr(), ybig.stride(0), M, N, K, None), "strided")
+    y = ops.linear_fp8_w8a16(x_to_dev(x), w_to_dev(w), sd)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(ybig[:, 8:8 + N]), bits(y))
+    assert_parity(bits(y), oracle_bits(x, w, s), f"strided T={T} M={M}")
+    assert torch.all(ybig[:, :8] == 7.0) and torch.all(ybig[:, 8 + N:] == 7.0)
+
+
 def test_k_not_a_multiple_of_64_goes_to_the_4x4x4_kernel():
     """K not a multiple of 64 runs the 4x4x4 kernel instead: the same bytes as with s16 = 2, within
     the parity gate of the oracle."""
