@@ -65,8 +65,9 @@ int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, v
 /*
  * General W8A16 linear with explicit strides and an M dispatch that refines the
  * reference's M == 1 switch: M <= 2 -> the GEMV kernel (one pass over W for both activation
- * rows), 3 <= M <= 16 -> the skinny kernel (weight-streaming, 4x4x4 bf16 MFMA), M > 16 -> the
- * MFMA GEMM.  Replaces the fp8 branch of mlp_block_forward_fp8
+ * rows), 3 <= M <= 16 -> the skinny kernels (weight-streaming on bf16 MFMA: 16x16x32 with both
+ * operands brought into LDS by DMA; 4x4x4 where K is not a multiple of 64 or x / W are not
+ * 16-byte aligned), M > 16 -> the MFMA GEMM.  Replaces the fp8 branch of mlp_block_forward_fp8
  * (nemotron_infer/csrc/include/model/mlp_block.cuh:142-171) and the per-projection calls
  * in attention_block.cuh:330-350,400-409 and mamba_block.cuh:383-391,419-423,476-481,508-509.
  * Unlike the reference's M > 1 branch, activations are NOT quantized to e4m3
@@ -77,9 +78,9 @@ int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, in
                          void* stream);
 
 /*
- * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the skinny kernels
- * (2 <= M <= 16: the split-K 16x16x32 variant, or the 4x4x4 kernel's K split when the tuning
- * knob s4.kg > 1 selects it) split K between workgroups, and the prefill GEMM (M >= 512)
+ * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the 4x4x4 skinny
+ * kernel (2 <= M <= 16, when the tuning knob s4.kg > 1 selects its K split) and the
+ * short-prompt GEMM (17 <= M < 512) split K between workgroups, and the prefill GEMM (M >= 512)
  * split the k tiles of a few large tiles between all CUs (stream-K: fp32 partial tiles and
  * per-workgroup flags in the workspace; used when the 256 x 256 tiles cover at most half of
  * the CUs, e.g. N = 3136 at M = 2048).
@@ -159,8 +160,8 @@ int nmi_gemv_chain_launch(const nmi_gemv_chain* chain, void* workspace, size_t w
 int nmi_gemv_chain_destroy(nmi_gemv_chain* chain);
 
 /* Workspace bytes the kernels can use for M rows, total_n output rows (the sum over groups)
- * and K on the current device; 0 when the selected kernel needs none (the GEMV, the default
- * 4x4x4 skinny kernel, which splits K inside the workgroup only).  With the 4x4x4 kernel's K
+ * and K on the current device; 0 when the selected kernel needs none (the GEMV, the skinny
+ * kernels by default, which split K inside the workgroup only).  With the 4x4x4 kernel's K
  * split (s4.kg > 1): 64 KiB of arrival counters and the fp32 partials, s4.kg x M x total_n x 4
  * bytes (fewer K groups when K has fewer windows).  For 17 <= M < 512 (the short-prompt GEMM) a
  * 64 KiB region it leaves alone, then the fp32 partials of its K split (0 when the schedule does
