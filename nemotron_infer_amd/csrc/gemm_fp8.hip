@@ -797,7 +797,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                 if (row >= rows) continue;
                 uint16_t* yp = gy + (int64_t)(m0 + row) * gldy + n;
                 if (full) {
-                    *reinterpret_cast<uint4*>(yp) = uint4{w[p][0], w[p][1], w[p][2], w[p][3]};
+                    // streaming store: the tile's output is not read again by this launch
+                    // (measured on MI355X: q|k|v at M = 2048 74.7 -> 73.3 us, down_proj 161 -> 159)
+                    __builtin_nontemporal_store(u32x4{w[p][0], w[p][1], w[p][2], w[p][3]}, reinterpret_cast<u32x4*>(yp));
                 } else {
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
