@@ -64,10 +64,10 @@ int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, v
 
 /*
  * General W8A16 linear with explicit strides and an M dispatch that refines the
- * reference's M == 1 switch: M <= 2 -> the GEMV kernel (one pass over W for both activation
- * rows), 3 <= M <= 16 -> the skinny kernels (weight-streaming on bf16 MFMA: 16x16x32 with both
- * operands brought into LDS by DMA; 4x4x4 where K is not a multiple of 64 or x / W are not
- * 16-byte aligned), M > 16 -> the MFMA GEMM.  Replaces the fp8 branch of mlp_block_forward_fp8
+ * reference's M == 1 switch: M == 1 -> the GEMV kernel, 2 <= M <= 16 -> the skinny kernels
+ * (weight-streaming on bf16 MFMA: 16x16x32 with both operands brought into LDS by DMA; where K
+ * is not a multiple of 64 or x / W are not 16-byte aligned, the GEMV kernel at M = 2 (one pass
+ * over W for both activation rows) and the 4x4x4 kernel above), M > 16 -> the MFMA GEMM.  Replaces the fp8 branch of mlp_block_forward_fp8
  * (nemotron_infer/csrc/include/model/mlp_block.cuh:142-171) and the per-projection calls
  * in attention_block.cuh:330-350,400-409 and mamba_block.cuh:383-391,419-423,476-481,508-509.
  * Unlike the reference's M > 1 branch, activations are NOT quantized to e4m3

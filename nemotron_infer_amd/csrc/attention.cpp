@@ -218,7 +218,7 @@ int nmi_attn_forward_fp8(const void* input_bf16, const float* norm_w, const void
         {static_cast<const uint8_t*>(v_w_e4m3), hidden, v_scale, v, KD, KD, 0, 0, Epi{}},
     };
     const Norm norm{norm_w, eps};
-    if (choose_path(S) == Path::Gemv && gemv_norm_supported(S, hidden)) {
+    if (gemv_fuses_norm(S, hidden)) {
         e = dispatch_linear(in, hidden, S, hidden, qkv, 3, nullptr, 0, st, norm);
     } else {
         uint16_t* normed = reinterpret_cast<uint16_t*>(base + lay.normed);
@@ -332,7 +332,7 @@ int nmi_attn_decode_fp8(const void* input_bf16, const float* norm_w, const void*
     };
     const Norm norm{norm_w, eps};
     hipError_t e;
-    if (choose_path(1) == Path::Gemv && gemv_norm_supported(1, hidden)) {
+    if (gemv_fuses_norm(1, hidden)) {
         e = dispatch_linear(in, hidden, 1, hidden, qkv, 3, nullptr, 0, st, norm);
     } else {
         uint16_t* normed = reinterpret_cast<uint16_t*>(base + lay.normed);

@@ -5,9 +5,10 @@
 // M = 1 five launches over four bump-allocated buffers: rmsnorm_bf16 -> normed, gemv_fp8 ->
 // up, relu^2 -> act, gemv_fp8 -> down, residual add -> out.  Here the element-wise steps
 // ride on the linears: relu^2 and the residual add are output epilogues of the up and down
-// projections, and where the up projection runs on the GEMV kernel (M <= 2) the RMSNorm is
-// applied while that kernel stages its activations -- two launches and one [M, inter] buffer.
-// For larger M the RMSNorm is its own launch (rmsnorm.hip) into a second buffer.  On the GEMM
+// projections, and where the up projection runs on the GEMV kernel (M = 1, and M = 2 where the
+// 16x16x32 skinny kernel does not take it) the RMSNorm is applied while that kernel stages its
+// activations -- two launches and one [M, inter] buffer.  Otherwise the RMSNorm is its own
+// launch (rmsnorm.hip) into a second buffer.  On the GEMM
 // path (M > 16) the workspace also holds the GEMMs' region: from M = 512 the stream-K flags and
 // partial tiles, whose flags one small kernel zeroes at the start of every call; below, the
 // short-prompt kernel's K-split partials (which need no initialisation).
@@ -46,7 +47,7 @@ size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 // Workspace layout: the prefill GEMM's stream-K region (M >= 512: flags, then partial tiles),
 // act [M, inter] bf16, then normed [M, hidden] bf16 when the RMSNorm is not fused into the up
 // projection.
-bool norm_fused(int M, int hidden) { return choose_path(M) == Path::Gemv && gemv_norm_supported(M, hidden); }
+bool norm_fused(int M, int hidden) { return gemv_fuses_norm(M, hidden); }
 
 // split = false leaves the short-prompt GEMMs unsplit (no partial region): the allocation-free
 // form, whose buffers must fit a fixed array

@@ -112,8 +112,9 @@ size_t linear_workspace_bytes(int M, int64_t total_n, int K) {
 
 bool gemm_workspace_has_flags(int M) { return M >= 512 && choose_path(M) == Path::Gemm; }
 
-// M == 1 -> GEMV kernel, M == 2 -> GEMV kernel (measured faster than the MFMA kernels there),
-// M <= 16 -> the skinny kernels (16x16x32, or 4x4x4 where that one declines), M > 16 -> MFMA GEMM.
+// M == 1 -> GEMV kernel, M == 2 -> GEMV kernel when it fuses the RMSNorm, else the 16x16x32
+// skinny kernel where it takes the shape (dispatch_linear), M <= 16 -> the skinny kernels
+// (16x16x32, or 4x4x4 where that one declines), M > 16 -> MFMA GEMM.
 Path choose_path(int M) {
     const Tuning& t = tuning();
     if (M == 1) {
@@ -127,12 +128,23 @@ Path choose_path(int M) {
     return Path::Gemm;
 }
 
+bool gemv_fuses_norm(int M, int K) {
+    if (choose_path(M) != Path::Gemv || !gemv_norm_supported(M, K)) return false;
+    return !(M == 2 && tuning().skinny_path == 0 && K % 64 == 0 && skinny16_wanted(M, K));
+}
+
 hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGroup* g, int ng, void* ws,
                            size_t ws_bytes, hipStream_t st, const Norm& norm) {
     const Path path = choose_path(M);
     if (norm.w && path != Path::Gemv) return hipErrorInvalidValue;
     switch (path) {
-        case Path::Gemv: return launch_gemv_grouped(x, ldx, M, K, g, ng, st, norm);
+        case Path::Gemv: {
+            // M = 2 without a fused RMSNorm: the 16x16x32 skinny kernel where it takes the shape
+            hipError_t e = hipSuccess;
+            if (M == 2 && !norm.w && tuning().skinny_path == 0 && launch_skinny16_grouped(x, ldx, M, K, g, ng, st, &e))
+                return e;
+            return launch_gemv_grouped(x, ldx, M, K, g, ng, st, norm);
+        }
         case Path::Skinny4: {
             hipError_t e = hipSuccess;
             if (launch_skinny16_grouped(x, ldx, M, K, g, ng, st, &e)) return e;

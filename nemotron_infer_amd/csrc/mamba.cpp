@@ -163,7 +163,7 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
     GemvGroup ip{static_cast<const uint8_t*>(in_proj_w_e4m3), hidden, in_proj_scale, proj, d.proj_ld, d.proj, 0, 0,
                  Epi{}};
     const Norm norm{norm_w, eps};
-    if (choose_path(M) == Path::Gemv && gemv_norm_supported(M, hidden)) {
+    if (gemv_fuses_norm(M, hidden)) {
         e = dispatch_linear(in, hidden, M, hidden, &ip, 1, nullptr, 0, st, norm);
     } else {
         uint16_t* normed = reinterpret_cast<uint16_t*>(base + lay.normed);
@@ -330,7 +330,7 @@ int nmi_mamba_decode_fp8(const void* input_bf16, const float* norm_w, const void
     GemvGroup ip{static_cast<const uint8_t*>(in_proj_w_e4m3), hidden, in_proj_scale, proj, d.proj_ld, d.proj, 0, 0,
                  Epi{}};
     hipError_t e;
-    if (choose_path(batch) == Path::Gemv && gemv_norm_supported(batch, hidden)) {
+    if (gemv_fuses_norm(batch, hidden)) {
         e = dispatch_linear(in, hidden, batch, hidden, &ip, 1, nullptr, 0, st, norm);
     } else {
         uint16_t* normed = reinterpret_cast<uint16_t*>(base + lay.normed);

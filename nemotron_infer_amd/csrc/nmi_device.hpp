@@ -169,6 +169,11 @@ __device__ __forceinline__ void dma16_lds(const void* base, uint32_t off, uint32
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
                  : "memory", "m0");
 }
+// The same with the non-temporal hint (streamed weights: read once per launch).
+__device__ __forceinline__ void dma16_lds_nt(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "s"(lds_addr)
+                 : "memory", "m0");
+}
 __device__ __forceinline__ void dma16_lds_device(const void* base, uint32_t off, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc1" ::"v"(off), "s"(base), "s"(lds_addr)
                  : "memory", "m0");

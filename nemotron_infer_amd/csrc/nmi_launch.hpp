@@ -294,6 +294,11 @@ hipError_t launch_decode(const uint8_t* codes, float* out_f32, float* out_scaled
 // Kernel chosen for a linear with M activation rows (tuning knobs may override).
 enum class Path { Gemv, Skinny4, Gemm };
 Path choose_path(int M);
+// Whether a block runs the RMSNorm inside its first projection (the GEMV kernel staging x, M <= 2)
+// rather than as its own launch: where the GEMV kernel takes that projection and supports the
+// fused form; at M = 2 only where the 16x16x32 skinny kernel would not take the projection, so
+// that a block's projections always run on the kernels the separate linear calls use.
+bool gemv_fuses_norm(int M, int K);
 
 // One or more linears sharing x [M, K] on the kernel choose_path(M) names (GEMM: one launch per
 // matrix).  norm (GEMV path only, where gemv_norm_supported) applies the RMSNorm to x first.

@@ -289,7 +289,7 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
         for (int j = 0; j < R; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                dma16_lds(G.W, wbase[j][q] + 16u * (uint32_t)min(g4 * 16 + wsw[q], CW - 1),
+                dma16_lds_nt(G.W, wbase[j][q] + 16u * (uint32_t)min(g4 * 16 + wsw[q], CW - 1),
                         sw + (uint32_t)((4 * j + q) * 1024));
 #pragma unroll
         for (int i = 0; i < XR / 2; ++i) {
@@ -420,16 +420,15 @@ hipError_t s16_rows_launch(S16Args& a, const GemvGroup* groups, int ng, hipStrea
 
 }  // namespace
 
-// Where this kernel is taken by default (tuning knob s16 = 1: every 2 <= M <= 16, 2: never):
-// from M = 3 (M = 2 is the stream GEMV's).  Measured on MI355X (bench, config 2, four launches per
-// step, DMA form): M = 4 38.9 against 43.3 us on the 4x4x4 kernel, M = 8 40.5 against 53, M = 16
-// 46.3 against 74; M = 2 equal to the stream GEMV within the timing noise.
+// Where this kernel is taken (tuning knob s16 = 2: never): 2 <= M <= 16; M = 2 only when the
+// GEMV kernel would not fuse an RMSNorm (the caller decides).  Measured on MI355X (bench, config
+// 2, four launches per step, DMA form with non-temporal weight loads): M = 2 34.4 against 38.5 us
+// on the stream GEMV, M = 4 35.6 against 43.3 on the 4x4x4 kernel, M = 8 38.3 against 53, M = 16
+// 44.2 against 74.
 bool skinny16_wanted(int M, int K) {
     const int knob = tuning().s16;
-    if (knob == 2 || M > 16 || M < 2) return false;
-    if (knob == 1) return true;
     (void)K;
-    return M >= 3;
+    return knob != 2 && M >= 2 && M <= 16;
 }
 
 bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
