@@ -140,9 +140,12 @@ def test_rmsnorm_rejects_bad_arguments():
 
 def test_mlp_workspace_bytes():
     L = _lib.lib()
-    # M <= 2 (GEMV path): only act [M, inter] bf16; otherwise also normed [M, hidden]
+    # RMSNorm fused into the up projection (M = 1; M = 2 where the 16x16x32 skinny kernel does
+    # not take the up projection, e.g. hidden not a multiple of 64): only act [M, inter] bf16;
+    # otherwise also normed [M, hidden]
     assert L.nmi_mlp_workspace_bytes(1, 3136, 12544) == 12544 * 2
-    assert L.nmi_mlp_workspace_bytes(2, 3136, 12544) == 2 * 12544 * 2
+    assert L.nmi_mlp_workspace_bytes(2, 3136, 12544) == 2 * 12544 * 2 + ((2 * 3136 * 2 + 255) // 256) * 256
+    assert L.nmi_mlp_workspace_bytes(2, 3136 + 16, 12544) == 2 * 12544 * 2
     assert L.nmi_mlp_workspace_bytes(3, 3136, 12544) == 3 * 12544 * 2 + ((3 * 3136 * 2 + 255) // 256) * 256
     assert L.nmi_mlp_workspace_bytes(64, 64, 256) == 64 * 256 * 2 + 64 * 64 * 2
     assert L.nmi_mlp_workspace_bytes(0, 3136, 12544) == 0
