@@ -226,8 +226,10 @@ skinny16_rows_kernel(const S16Args a) {
 // and a fragment read (16 rows, one logical chunk) hits 16 distinct bank groups.  Waits are
 // explicit vmcnt counts (every group issues the same instructions, and only groups of the wave's
 // run are issued: a wait counts the groups issued after the one it waits for).
-// XR activation rows are staged: 16, or 8 where M <= 8 (lanes of MFMA columns 8 .. 15 then read
-// row 7, and their products are dropped).
+// XR activation rows are staged: 16, 8 where M <= 8, 4 where M <= 4 (lanes of MFMA columns
+// XR .. 15 then read row XR - 1, and their products are dropped).  Fewer staged rows measured
+// faster: M = 8 on 8 rows 40.4 against 42.7 us per config-2 step on 16, M = 2 on 4 rows 33.4-34.1
+// against 34.3 on 8.
 constexpr int kS16DmaW = 4096;                         // bytes per slot and row tile
 
 template <int R, int NW, int D, int XR>
@@ -468,6 +470,16 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
     for (int i = 0; i < ngroups; ++i)
         dma_ok = dma_ok && groups[i].ldw * (int64_t)(groups[i].N - 1) + K < ((int64_t)1 << 31);
     if (tn.s16_t != 1 && dma_ok) {
+        if (M <= 4) {                                  // 4 staged activation rows
+            const int f4 = (R == 2 ? 2 : 0) + (four ? 1 : 0);
+            switch (f4) {
+                case 0: *err = s16_dma_launch<1, 2, 2, 4>(a, groups, ngroups, stream); break;
+                case 1: *err = s16_dma_launch<1, 4, 2, 4>(a, groups, ngroups, stream); break;
+                case 2: *err = s16_dma_launch<2, 2, 2, 4>(a, groups, ngroups, stream); break;
+                default: *err = s16_dma_launch<2, 4, 2, 4>(a, groups, ngroups, stream); break;
+            }
+            return true;
+        }
         const int form = (M <= 8 ? 4 : 0) + (R == 2 ? 2 : 0) + (four ? 1 : 0);
         switch (form) {
             case 0: *err = s16_dma_launch<1, 2, 2, 16>(a, groups, ngroups, stream); break;
