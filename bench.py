@@ -325,18 +325,22 @@ def bench_prefill_small_m(dev, reps=20):
     return {"workload": "config3 shapes at short-prompt M", "weight_copies_rotated": R, "results": res}
 
 
-def bench_skinny(dev, host, reps=20):
+def bench_skinny(dev, reps=20):
+    """Config 2: the config-1 shapes at M in {2, 4, 8, 16}, weights with per-row log-uniform
+    scales, every activation row its own N(0, 1) draw (down_proj included)."""
     import torch
 
     from nemotron_infer_amd import ops, synth
 
-    set_bytes = sum(l.weight_bytes for l in synth.DECODE_SET)
+    L = synth.SKINNY_SET
+    set_bytes = sum(l.weight_bytes for l in L)
     R = max(2, math.ceil(ROTATION_BYTES / set_bytes))
-    copies = rotated(dev, [(w, s) for _, _, w, s in host], R)
+    base = [synth.make_weight(l.N, l.K, 2100 + i, dev, scales="log_uniform") for i, l in enumerate(L)]
+    copies = [[(w.clone(), s.clone()) for w, s in base] for _ in range(R)]
+    del base
     res = {}
     T = Timer()
-    L = synth.DECODE_SET
-    for M in (2, 4, 8, 16):
+    for M in synth.SKINNY_M:
         xs = tuple(synth.make_act(M, L[i].K, 2200 + M + i, dev, kind=L[i].act) for i in (0, 3, 4, 5))
         ys = step_buffers(dev, M)
         steps = [make_step(ops, xs, copies[r], ys) for r in range(R)]
@@ -881,7 +885,7 @@ def main():
         del a, b
     if args.only:
         if args.only == "skinny":
-            leg = bench_skinny(dev, decode_inputs())
+            leg = bench_skinny(dev)
         elif args.only == "stream":
             leg = bench_decode_stream(args, dev)
             leg = {k: v for k, v in leg.items()}
@@ -918,7 +922,7 @@ def main():
         extras["prefill_small_m"] = bench_prefill_small_m(dev)
         log(f"prefill small M: { {k: v['TFLOP/s'] for k, v in extras['prefill_small_m']['results'].items()} }")
         log("skinny M (config 2) ...")
-        extras["skinny"] = bench_skinny(dev, host)
+        extras["skinny"] = bench_skinny(dev)
         log("mlp block ...")
         extras["mlp_block"] = bench_mlp_block(dev)
         log(f"mlp block: {extras['mlp_block']['decode_m1']}")

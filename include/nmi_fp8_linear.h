@@ -15,6 +15,11 @@
  * Return value: NMI_OK (0) on success; a negative NMI_ERR_* for argument errors detected on
  * the host before anything is launched; a positive hipError_t value when a HIP call fails.
  * nmi_last_error() describes the last failure of the calling thread.
+ * NMI_ERR_ASYNC reports a failure of an earlier launch on the device that the host learnt of
+ * since (a stream-K GEMM that gave up waiting for a partial tile, see nmi_linear_fp8_w8a16_ws):
+ * every entry point that launches a linear, a GEMM or a block returns it, launching nothing, at
+ * its first call after that launch has finished; nmi_sync after synchronising, nmi_async_status
+ * without synchronising.  Each such failure is reported once.
  *
  * Layouts: x row m starts at x + m*ldx elements; W row n at W + n*ldw bytes; y row m at
  * y + m*ldy elements.  Row-sliced calls pass offset pointers (W + r0*ldw, s + r0, y + r0)
@@ -45,6 +50,7 @@ enum {
     NMI_ERR_UNSUPPORTED = -3,
     NMI_ERR_WORKSPACE = -4,
     NMI_ERR_ALLOC = -5,
+    NMI_ERR_ASYNC = -6,
 };
 
 /* Version of this ABI (major*10000 + minor*100 + patch). */
@@ -91,10 +97,13 @@ int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, in
  * likewise hand a workspace to their prefill GEMMs (model/mlp_block.cuh:133,156,160-161).
  * Stream-K ordering: a contributor stores its partial tile, then releases its flag at device
  * scope; the finisher polls the flag and acquires at device scope before reading the partial.
- * The wait is bounded: if a flag never comes (a workgroup that never ran), the finisher gives
- * up, leaves that partial out and sets the 32-bit error word at byte NMI_WS_ERROR_OFFSET of
- * the workspace to 1.  After that the results of the launch are wrong and the workspace must be
- * zero-filled again before its next use; the word stays set until then.
+ * The wait is bounded: if a flag does not come in time (a workgroup that is stalled or never
+ * ran), the finisher gives up, leaves that partial out, marks the slot abandoned and sets the
+ * 32-bit error word at byte NMI_WS_ERROR_OFFSET of the workspace to 1 and the device's
+ * asynchronous error (NMI_ERR_ASYNC, returned by the next call).  The results of that launch are
+ * wrong; the flags still end it at zero (a contributor that finds its slot abandoned lowers its
+ * flag again), so the workspace needs no reset and the next launch on it is correct.  The error
+ * word stays set until the workspace is zero-filled.
  */
 #define NMI_WS_ERROR_OFFSET 65532
 int nmi_linear_fp8_w8a16_ws(const void* x_bf16, int64_t ldx, const void* w_e4m3, int64_t ldw,
@@ -437,8 +446,16 @@ int nmi_alloc_rewind(void);
 int nmi_alloc_reset(void);
 int nmi_alloc_stats(size_t* total_allocated, size_t* num_slabs);
 
-/* hipDeviceSynchronize(); replaces the binding's sync() (csrc/include/binding.cu:62). */
+/* hipDeviceSynchronize(); replaces the binding's sync() (csrc/include/binding.cu:62).  Returns
+ * NMI_ERR_ASYNC if a launch that finished had an asynchronous error not yet reported. */
 int nmi_sync(void);
+
+/*
+ * The current device's asynchronous error, read and cleared without synchronising the GPU:
+ * NMI_ERR_ASYNC (with nmi_last_error()) if a launch that has finished had one not yet reported,
+ * else NMI_OK.  No counterpart in the reference, which checks no kernel for errors.
+ */
+int nmi_async_status(void);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,7 @@ NMI_ERR_ALIGNMENT = -2
 NMI_ERR_UNSUPPORTED = -3
 NMI_ERR_WORKSPACE = -4
 NMI_ERR_ALLOC = -5
+NMI_ERR_ASYNC = -6            # an earlier launch's asynchronous error (stream-K wait gave up)
 NMI_WS_ERROR_OFFSET = 65532   # byte offset of the stream-K error word in a linear workspace
 
 # Every symbol the header declares, with its ctypes signature.
@@ -55,6 +56,7 @@ SIGNATURES = {
     "nmi_alloc_reset": ([], _i),
     "nmi_alloc_stats": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
     "nmi_sync": ([], _i),
+    "nmi_async_status": ([], _i),
     "nmi_gemv_chain_create": ([_vp, _i, ctypes.POINTER(_vp)], _i),
     "nmi_gemv_chain_workspace_bytes": ([_i], _sz),
     "nmi_gemv_chain_launch": ([_vp, _vp, _sz, _vp], _i),

@@ -162,6 +162,7 @@ int nmi_attn_forward_fp8(const void* input_bf16, const float* norm_w, const void
                          void* v_cache_bf16, int cache_cap, int hidden, int n_heads, int n_kv_heads, float eps,
                          void* workspace, size_t workspace_bytes, void* stream) {
     const char* fn = "nmi_attn_forward_fp8";
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     if (!input_bf16 || !norm_w || !q_w_e4m3 || !q_scale || !k_w_e4m3 || !k_scale || !v_w_e4m3 || !v_scale ||
         !o_w_e4m3 || !o_scale || !out_bf16)
         return fail(NMI_ERR_INVALID_ARG, "nmi_attn_forward_fp8: NULL pointer argument");
@@ -287,6 +288,7 @@ int nmi_attn_decode_fp8(const void* input_bf16, const float* norm_w, const void*
                         int S_cache, int cache_cap, void* out_bf16, int hidden, int n_heads, int n_kv_heads,
                         float eps, void* workspace, size_t workspace_bytes, void* stream) {
     const char* fn = "nmi_attn_decode_fp8";
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     if (!input_bf16 || !norm_w || !q_w_e4m3 || !q_scale || !k_w_e4m3 || !k_scale || !v_w_e4m3 || !v_scale ||
         !o_w_e4m3 || !o_scale || !k_cache_bf16 || !v_cache_bf16 || !out_bf16)
         return fail(NMI_ERR_INVALID_ARG, "nmi_attn_decode_fp8: NULL pointer argument");

@@ -104,6 +104,7 @@ size_t mlp_workspace_bytes(int M, int hidden, int inter, bool split) {
 int mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void* up_w_e4m3, const float* up_scale,
                     const void* down_w_e4m3, const float* down_scale, void* out_bf16, int M, int hidden, int inter,
                     float eps, void* workspace, size_t workspace_bytes, void* stream, bool split, const char* fn) {
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     if (!input_bf16 || !norm_w || !up_w_e4m3 || !up_scale || !down_w_e4m3 || !down_scale || !out_bf16)
         return fail2(NMI_ERR_INVALID_ARG, fn, "NULL pointer argument");
     if (M < 1 || hidden < 16 || hidden % 16 != 0 || inter < 16 || inter % 16 != 0) {

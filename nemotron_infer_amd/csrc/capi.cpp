@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -92,6 +93,45 @@ const DeviceInfo& device_info() {
 Tuning& tuning() {
     static Tuning t;
     return t;
+}
+
+namespace {
+constexpr int kAsyncMaxDevices = 64;
+std::atomic<uint32_t*> g_async_words{nullptr};
+std::once_flag g_async_once;
+}  // namespace
+
+uint32_t* async_error_word() {
+    std::call_once(g_async_once, [] {
+        // pinned, coherent host memory: the kernel's system-scope store is visible to the host
+        // without a GPU synchronisation; one word per device
+        void* p = nullptr;
+        if (hipHostMalloc(&p, kAsyncMaxDevices * sizeof(uint32_t), hipHostMallocCoherent | hipHostMallocPortable) ==
+                hipSuccess &&
+            p) {
+            std::memset(p, 0, kAsyncMaxDevices * sizeof(uint32_t));
+            g_async_words.store(static_cast<uint32_t*>(p), std::memory_order_release);
+        } else {
+            (void)hipGetLastError();
+        }
+    });
+    uint32_t* w = g_async_words.load(std::memory_order_acquire);
+    const int dev = device_info().device;
+    return (w && dev >= 0 && dev < kAsyncMaxDevices) ? w + dev : nullptr;
+}
+
+bool take_async_error(const char* fn) {
+    uint32_t* w = g_async_words.load(std::memory_order_acquire);
+    if (!w) return false;                           // no stream-K launch yet in this process
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kAsyncMaxDevices) return false;
+    if (__atomic_load_n(w + dev, __ATOMIC_ACQUIRE) == 0u) return false;
+    __atomic_store_n(w + dev, 0u, __ATOMIC_RELAXED);
+    set_last_error("%s: a stream-K GEMM launched earlier on device %d gave up waiting for a partial tile, so that "
+                   "launch's output is wrong (the error word of its workspace, byte %d, is set; its flags were left "
+                   "re-armed); nothing was launched by this call",
+                   fn, dev, NMI_WS_ERROR_OFFSET);
+    return true;
 }
 
 }  // namespace nmi
@@ -184,6 +224,7 @@ int nmi_gemv_fp8(const void* x_bf16, const void* w_e4m3, const float* w_scale, v
                  int N, int K, void* stream) {
     int rc = check_linear(x_bf16, K, w_e4m3, K, w_scale, y_bf16, N, 1, N, K, "nmi_gemv_fp8");
     if (rc) return rc;
+    if (take_async_error("nmi_gemv_fp8")) return NMI_ERR_ASYNC;
     return hip_status(launch_gemv_m1(static_cast<const uint16_t*>(x_bf16),
                                      static_cast<const uint8_t*>(w_e4m3), K, w_scale,
                                      static_cast<uint16_t*>(y_bf16), N, K,
@@ -205,6 +246,7 @@ int nmi_linear_fp8_w8a16_ws(const void* x_bf16, int64_t ldx, const void* w_e4m3,
     const char* fn = workspace ? "nmi_linear_fp8_w8a16_ws" : "nmi_linear_fp8_w8a16";
     int rc = check_linear(x_bf16, ldx, w_e4m3, ldw, w_scale, y_bf16, ldy, M, N, K, fn);
     if (rc) return rc;
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     if (workspace && !aligned(workspace, 256))
         return fail(NMI_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", fn);
     GemvGroup g{static_cast<const uint8_t*>(w_e4m3), ldw, w_scale, static_cast<uint16_t*>(y_bf16), ldy, N, 0, 0, Epi{}};
@@ -218,6 +260,7 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
     const char* fn = "nmi_linear_fp8_w8a16_grouped";
     if (!groups || ngroups < 1 || ngroups > NMI_MAX_GROUPS)
         return fail(NMI_ERR_INVALID_ARG, "%s: ngroups=%d must be in [1, %d]", fn, ngroups, NMI_MAX_GROUPS);
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     if (workspace && !aligned(workspace, 256))
         return fail(NMI_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", fn);
     if (total_rows(groups, ngroups) > (int64_t)1 << 30)
@@ -327,6 +370,7 @@ int nmi_gemv_chain_launch(const nmi_gemv_chain* chain, void* workspace, size_t w
     (void)workspace;
     (void)workspace_bytes;
     if (!chain || !chain->dev) return fail(NMI_ERR_INVALID_ARG, "%s: invalid chain", fn);
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     int dev = -1;
     if (hipGetDevice(&dev) == hipSuccess && dev != chain->device)
         return fail(NMI_ERR_INVALID_ARG, "%s: chain was created on device %d, current is %d", fn, chain->device, dev);
@@ -368,6 +412,7 @@ int nmi_gemm_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, int6
     if (rc) return rc;
     if (workspace && !aligned(workspace, 256))
         return fail(NMI_ERR_ALIGNMENT, "nmi_gemm_fp8_w8a16: workspace must be 256-byte aligned");
+    if (take_async_error("nmi_gemm_fp8_w8a16")) return NMI_ERR_ASYNC;
     return hip_status(launch_gemm(static_cast<const uint16_t*>(x_bf16), ldx,
                                   static_cast<const uint8_t*>(w_e4m3), ldw, w_scale,
                                   static_cast<uint16_t*>(y_bf16), ldy, M, N, K,
@@ -424,6 +469,12 @@ int nmi_tuning_set(const char* knob, int value) {
     return NMI_OK;
 }
 
-int nmi_sync(void) { return hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+int nmi_sync(void) {
+    const int rc = hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (rc) return rc;
+    return take_async_error("nmi_sync") ? NMI_ERR_ASYNC : NMI_OK;
+}
+
+int nmi_async_status(void) { return take_async_error("nmi_async_status") ? NMI_ERR_ASYNC : NMI_OK; }
 
 }  // extern "C"

@@ -187,12 +187,15 @@ struct GemmArgs {
     Epi epi;
     // Stream-K (DMA-fed kernel): sk_total = tiles * K steps (0: one tile per workgroup); the
     // workspace's flag slots (zero at rest), its error word (set when a wait for a flag gave up)
-    // and fp32 partial tiles, one per workgroup; the wait's poll limit; sk_lostflag (tests only):
-    // contributors do not raise their flags, so that every wait runs into its limit.
+    // and fp32 partial tiles, one per workgroup; this device's error word in pinned host memory
+    // (set with it); the wait's poll limit; sk_lostflag (tests only): contributors raise their
+    // flags only after their finisher has given up waiting (a late flag), so that every wait
+    // runs into its limit.
     int64_t sk_total;
     uint32_t* sk_flags;
     float* sk_part;
     uint32_t* sk_error;
+    uint32_t* sk_host_error;
     int sk_spin;
     int sk_lostflag;
     // DMA-fed kernel's epilogue: s 16-byte aligned; y and the residual 16-byte aligned with row
@@ -872,11 +875,13 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                     if ((int64_t)cv * total / Gx == (int64_t)(cv + 1) * total / Gx) continue;   // empty range
                     const int c = 8 * cv + xcd;
                     // Bounded wait for the contributor's flag: relaxed polls, then an agent-scope
-                    // acquire fence (paired with the contributor's release store of the flag, it
-                    // makes the partial visible to this thread and, through the barrier, to the
-                    // workgroup).  At the limit the wait gives up: the error word is set, the
-                    // partial is left out and the flag is not re-armed -- the tile is wrong and the
-                    // workspace must be zeroed before its next use, but the kernel exits.
+                    // acquire fence (paired with the contributor's release exchange of the flag,
+                    // it makes the partial visible to this thread and, through the barrier, to the
+                    // workgroup).  At the limit the wait gives up unless the flag comes up in the
+                    // same instant: it marks the slot abandoned (2) with a compare-exchange from 0,
+                    // leaves the partial out and sets the workspace's and the device's error words
+                    // -- the tile is wrong, the kernel exits, and the contributor, finding the mark
+                    // when it raises its flag, lowers it again, so every flag ends the launch at 0.
                     if (tid == 0) {
                         bool up = false;
                         for (int spin = 0;; ++spin) {
@@ -887,10 +892,16 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                             if (spin >= a.sk_spin) break;
                             __builtin_amdgcn_s_sleep(1);
                         }
+                        if (!up) {
+                            uint32_t expect = 0u;
+                            up = !__hip_atomic_compare_exchange_strong(a.sk_flags + c, &expect, 2u, __ATOMIC_RELAXED,
+                                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
                         if (up) {
                             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
                         } else {
                             __hip_atomic_store(a.sk_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            __hip_atomic_store(a.sk_host_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                         }
                         sk_up = up ? 1 : 0;
                     }
@@ -946,10 +957,20 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                     }
                 __builtin_amdgcn_s_waitcnt(0);          // the partial's stores have completed
                 __syncthreads();
-                // release at agent scope: the workgroup's partial (ordered before this store by the
-                // barrier) is visible to whoever acquires the flag
-                if (tid == 0 && !a.sk_lostflag)
-                    __hip_atomic_store(a.sk_flags + g, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                // release at agent scope: the workgroup's partial (ordered before this exchange by
+                // the barrier) is visible to whoever acquires the flag.  A finisher that gave up
+                // left the mark 2: lower the flag again (the finisher no longer looks at it).
+                if (tid == 0) {
+                    if (a.sk_lostflag) {
+                        // tests: raise the flag only once the finisher has given up (bounded)
+                        for (int spin = 0; spin < (1 << 22); ++spin) {
+                            if (__hip_atomic_load(a.sk_flags + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 2u) break;
+                            __builtin_amdgcn_s_sleep(1);
+                        }
+                    }
+                    if (__hip_atomic_exchange(a.sk_flags + g, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == 2u)
+                        __hip_atomic_store(a.sk_flags + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             } else {
                 store();
             }
@@ -1058,7 +1079,9 @@ hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g,
     const bool fits = ws && ws_bytes >= kSkFlagBytes + (size_t)G * kDmaPartialBytes && G % 8 == 0 &&
                       G * 4 <= (int)kSkFlagBytes && (int64_t)T * (K / kBK) < ((int64_t)1 << 31);
     const int knob = tuning().gemm_sk;
-    if (fits && knob != 2 && (knob == 1 || 2 * (int64_t)T <= G)) {
+    uint32_t* host_error = nullptr;
+    if (fits && knob != 2 && (knob == 1 || 2 * (int64_t)T <= G) && (host_error = async_error_word()) != nullptr) {
+        a.sk_host_error = host_error;
         a.sk_total = (int64_t)T * (K / kBK);
         a.sk_flags = static_cast<uint32_t*>(ws);
         a.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);

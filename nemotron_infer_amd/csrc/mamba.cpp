@@ -107,6 +107,7 @@ int nmi_mamba_forward_fp8(const void* input_bf16, const float* norm_w, const voi
                           float* ssm_state_out, int hidden, int n_heads, int head_dim, int n_groups, int d_state,
                           int conv_k, float eps, void* workspace, size_t workspace_bytes, void* stream) {
     const char* fn = "nmi_mamba_forward_fp8";
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     if (!input_bf16 || !norm_w || !in_proj_w_e4m3 || !in_proj_scale || !conv_w || !conv_b || !A_log || !D ||
         !dt_bias || !gnorm_w || !out_proj_w_e4m3 || !out_proj_scale || !out_bf16)
         return fail(NMI_ERR_INVALID_ARG, "nmi_mamba_forward_fp8: NULL pointer argument");
@@ -280,6 +281,7 @@ int nmi_mamba_decode_fp8(const void* input_bf16, const float* norm_w, const void
                          int hidden, int n_heads, int head_dim, int n_groups, int d_state, int conv_k, float eps,
                          void* workspace, size_t workspace_bytes, void* stream) {
     const char* fn = "nmi_mamba_decode_fp8";
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
     if (!input_bf16 || !norm_w || !in_proj_w_e4m3 || !in_proj_scale || !conv_w || !conv_b || !A_log || !D ||
         !dt_bias || !gnorm_w || !out_proj_w_e4m3 || !out_proj_scale || !conv_state || !ssm_state || !out_bf16)
         return fail(NMI_ERR_INVALID_ARG, "nmi_mamba_decode_fp8: NULL pointer argument");

@@ -22,6 +22,15 @@ void set_last_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 // Per-device properties, queried once per device (thread-safe).
 const DeviceInfo& device_info();
 
+// Asynchronous errors of the stream-K GEMM: a finisher that gave up waiting for a partial tile
+// (that launch's output is wrong) sets the current device's word in pinned host memory as well as
+// the workspace's.  async_error_word() returns the device's word (allocated on first use, one
+// array for the process; nullptr if that fails, and then the GEMM does not use stream-K).
+// take_async_error(fn) reads and clears it without synchronising the GPU; when it was set it
+// records a message naming fn and returns true (the caller returns NMI_ERR_ASYNC).
+uint32_t* async_error_word();
+bool take_async_error(const char* fn);
+
 // Tuning knobs (0 = automatic).  Set through nmi_tuning_set() for sweeps; never needed for
 // correctness.
 struct Tuning {
@@ -40,7 +49,7 @@ struct Tuning {
     int s4_kg = 0;         // 4x4x4 skinny kernel: workgroups splitting K (> 1, with a workspace; 0, 1: none)
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
     int gemm_sk_spin = 0;  // GEMM stream-K: polls of a flag before the wait gives up (0: 2^26)
-    int gemm_sk_lostflag = 0;  // GEMM stream-K (tests): 1 = contributors do not raise their flags
+    int gemm_sk_lostflag = 0;  // GEMM stream-K (tests): 1 = contributors raise their flags only after the finisher gave up
     int chain_wgs = 0;     // GEMV chain: workgroups per CU (0: 2, or fewer if fewer are resident)
     int gemv_wgs = 0;      // M = 1 stream GEMV: workgroups per CU at most (1, 2; 0: 1)
     int gemv_multirow = 0; // M = 1: 1 runs the multi-row GEMV kernel (gemv_fp8.hip) instead of the stream kernel

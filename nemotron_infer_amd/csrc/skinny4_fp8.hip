@@ -452,30 +452,17 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
         }
     };
     // this wave's batch of window w: lane 4 blk + li loads chunk (window slice q) + blk + 16 u of
-    // row 4 t + li.  Issued as explicit instructions: the compiler's own wait counts would merge
-    // the paths into the loop (with and without a next window in flight) and wait for the next
-    // window's loads too; completion is waited for by wait_loads_barrier and pinned by pin().
-    // The compiler takes the destination registers as written when the statement issues, so an
-    // instantiation must not spill: a register it moved to scratch or reused before the wait
-    // would still receive the load's data.  Every instantiation built here uses no scratch (a
-    // 16-wave variant that spilled faulted on the GPU and was removed).
+    // row 4 t + li (chunks past the slice clamped to its last one), as ordinary non-temporal loads
+    // that the compiler tracks: it waits for a destination register itself before the register's
+    // first use, so nothing depends on how it allocates, copies or spills them.
     auto load_w = [&](u32x4 (&wv)[T][U], int w) {
         const int cb = c_begin + w * kWin + q * 16 * U + blk;
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                asm volatile("global_load_dwordx4 %0, %1, off nt"
-                             : "=v"(wv[t][u])
-                             : "v"(wrow[t] + (int64_t)min(cb + 16 * u, c_end - 1) * 16)
-                             : "memory");
-    };
-    // after a wait: the registers are read only from here on
-    auto pin = [&](u32x4 (&wv)[T][U]) {
-#pragma unroll
-        for (int t = 0; t < T; ++t)
-#pragma unroll
-            for (int u = 0; u < U; ++u) asm volatile("" : "+v"(wv[t][u]));
+                wv[t][u] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(wrow[t] + (int64_t)min(cb + 16 * u, c_end - 1) * 16));
     };
     auto consume = [&](const u32x4 (&wv)[T][U], int b) {
 #pragma unroll
@@ -506,35 +493,48 @@ __global__ __launch_bounds__(256) void skinny4_dma_kernel(const Skinny4Args a) {
 
     // Two windows in flight: (wa, buffer 0) holds the even windows, (wb, buffer 1) the odd ones.
     // Each window's x DMA is issued before its weights, so waiting until only the next window's
-    // weight loads are outstanding covers this window's weights and both windows' x.
+    // weight loads are outstanding covers this window's weights and x and the next window's x.
+    // The control flow keeps the compiler's own waits (it tracks the weight loads, not the x DMA)
+    // from covering the next window's weights: one window alone is its own path; otherwise every
+    // path into the loop over window pairs (windows w + 2 and w + 3 exist: both loads are issued
+    // unconditionally) and into the tail (two or three windows left) has the same loads in flight,
+    // and the tail's two cases are written out separately.
     u32x4 wa[T][U], wb[T][U];
     stage(0, 0);
     load_w(wa, 0);
-    if (nw > 1) {
+    if (nw == 1) {
+        wait_loads_barrier<0>();
+        consume(wa, 0);
+    } else {
         stage(1, 1);
         load_w(wb, 1);
-    }
-    for (int w = 0;; w += 2) {
-        if (w + 1 < nw) wait_loads_barrier<T * U>();
-        else wait_loads_barrier<0>();
-        pin(wa);
-        consume(wa, 0);
-        if (w + 1 >= nw) break;
-        asm volatile("s_barrier" ::: "memory");        // every wave is done reading buffer 0
-        if (w + 2 < nw) {
+        int w = 0;
+        for (; w + 4 <= nw; w += 2) {
+            wait_loads_barrier<T * U>();
+            consume(wa, 0);
+            asm volatile("s_barrier" ::: "memory");    // every wave is done reading buffer 0
             stage(w + 2, 0);
             load_w(wa, w + 2);
             wait_loads_barrier<T * U>();
-        } else {
-            wait_loads_barrier<0>();
-        }
-        pin(wb);
-        consume(wb, 1);
-        if (w + 2 >= nw) break;
-        asm volatile("s_barrier" ::: "memory");        // every wave is done reading buffer 1
-        if (w + 3 < nw) {
+            consume(wb, 1);
+            asm volatile("s_barrier" ::: "memory");    // every wave is done reading buffer 1
             stage(w + 3, 1);
             load_w(wb, w + 3);
+        }
+        // windows w, w + 1 (in flight) and perhaps w + 2
+        wait_loads_barrier<T * U>();
+        consume(wa, 0);
+        if (w + 3 == nw) {
+            asm volatile("s_barrier" ::: "memory");
+            stage(w + 2, 0);
+            load_w(wa, w + 2);
+            wait_loads_barrier<T * U>();
+            consume(wb, 1);
+            wait_loads_barrier<0>();
+            consume(wa, 0);
+        } else {
+            wait_loads_barrier<0>();
+            consume(wb, 1);
         }
     }
 

@@ -3,8 +3,10 @@
 Weights: float32 N(0, 0.02) from a seeded generator, per-tensor scale s = amax / 448,
 codes = RNE(clamp(W / s, +-448)) as float8_e4m3fn, the scale broadcast to a per-row vector
 (nemotron_infer/engine.py:117-121).  Config 2 replaces the scales by per-row draws,
-log-uniform in [1e-4, 1e-2].  Activations: bf16 N(0, 1); the MLP down_proj input is
-relu(z)^2 (sparse, non-negative); config 3 multiplies 0.1% of the activations by 50.
+log-uniform in [1e-4, 1e-2].  Activations: bf16 N(0, 1); in config 1 (and the config-4
+stream) the MLP down_proj input is relu(z)^2 (sparse, non-negative); config 2 gives every M
+row its own N(0, 1) draw on all six shapes; config 3 draws N(0, 1) on all three shapes and
+multiplies 0.1% of the activations by 50.
 
 Generation runs on the device the caller names (torch's own generator for that device), so
 the same seed gives the same bytes on the same kind of device.  Tests that compare with the
@@ -47,10 +49,15 @@ DECODE_SET = (
     Linear("down_proj", HIDDEN, INTER, act="relu2"),
 )
 
-# Config 3: prefill GEMMs at M = 2048.
+# Config 2: the config-1 shapes at M in {2, 4, 8, 16}; every row of every input is N(0, 1)
+# (down_proj included) and the scales are per-row log-uniform.
+SKINNY_SET = tuple(Linear(l.name, l.N, l.K) for l in DECODE_SET)
+SKINNY_M = (2, 4, 8, 16)
+
+# Config 3: prefill GEMMs at M = 2048, every input N(0, 1) with 0.1% x50 outliers.
 PREFILL_SET = (
     Linear("up_proj", INTER, HIDDEN),
-    Linear("down_proj", HIDDEN, INTER, act="relu2"),
+    Linear("down_proj", HIDDEN, INTER),
     Linear("qkv_proj", Q_OUT + 2 * KV_OUT, HIDDEN),
 )
 PREFILL_M = 2048

@@ -356,3 +356,16 @@ def test_workspace_error_offset_matches_the_header():
     L = _lib.lib()
     for knob in ("gemm.sk_spin", "gemm.sk_lostflag", "gemv.grid", "gemv.balance", "sdpa.chunk"):
         assert L.nmi_tuning_set(knob.encode(), 0) == 0, knob
+
+
+def test_async_error_is_a_host_side_word():
+    """nmi_async_status reads the device's asynchronous error word in host memory without a GPU
+    call: before any stream-K launch in the process there is none to report.  NMI_ERR_ASYNC has
+    one value in the header and the binding, and reaches Python as an NmiError with its code."""
+    L = _lib.lib()
+    assert L.nmi_async_status() == _lib.NMI_OK
+    header = open(os.path.join(ROOT, "include", "nmi_fp8_linear.h")).read()
+    assert re.search(r"NMI_ERR_ASYNC\s*=\s*-6\b", header) and _lib.NMI_ERR_ASYNC == -6
+    with pytest.raises(_lib.NmiError) as e:
+        _lib.check(_lib.NMI_ERR_ASYNC, "an entry point")
+    assert e.value.code == _lib.NMI_ERR_ASYNC

@@ -45,14 +45,19 @@ def test_prefill_config3(lin):
     assert_parity(y, oracle_bits(x, w, s), f"prefill {lin.name}")
 
 
-@pytest.mark.parametrize("M", [2, 4, 8, 16])
+@pytest.mark.parametrize("M", synth.SKINNY_M)
 def test_skinny_config2(M):
-    """Config 2: M in {2,4,8,16} on the decode shapes with per-row log-uniform scales."""
-    for lin in synth.DECODE_SET:
+    """Config 2: M in {2,4,8,16} on the decode shapes with per-row log-uniform scales, every
+    activation row its own N(0, 1) draw.  Gated on the flip-exempt rel_l2 and on rel_l2 over
+    all elements (<= 1e-3) alike."""
+    for lin in synth.SKINNY_SET:
         announce("skinny", M, lin.name, lin.N, lin.K)
         x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, scales="log_uniform", act=lin.act)
         y = bits(ops.linear_fp8_w8a16(x_to_dev(x), w_to_dev(w), s_to_dev(s)))
-        assert_parity(y, oracle_bits(x, w, s), f"M={M} {lin.name}", per_row_scales=True)
+        r = assert_parity(y, oracle_bits(x, w, s), f"M={M} {lin.name}", per_row_scales=True,
+                          rel_l2_all_tol=1e-3)
+        print(f"[config2] M={M} {lin.name} rel_l2={r['rel_l2']:.2e} rel_l2_all={r['rel_l2_all']:.2e} "
+              f"max_ulp={r['max_ulp']:.2f} flips={r['n_flip']}/{r['n']}", flush=True)
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 37, 16), (100, 130, 80), (130, 257, 208), (1, 300, 3136),
@@ -332,7 +337,7 @@ def test_dma_kernel_forms_agree_on_config3(_sk_reset):
     match the oracle."""
     M, N, K = 2048, 3136, 12544
     announce("dma_forms_config3", M, N, K)
-    x, w, s = _case(M, N, K, 4321, act="relu2")
+    x, w, s = _case(M, N, K, 4321, outlier_frac=0.001)
     xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
     ref = oracle_bits(x, w, s)
     _lib.tuning_set("gemm.sk", 2)
@@ -410,18 +415,10 @@ def test_grouped_prefill_is_one_launch_of_the_dma_kernel(M, Ns, K, _sk_reset):
             assert_parity(bits(yg), oracle_bits(x, w, s), f"grouped {i} sk={sk} N={Ns[i]}", per_row_scales=True)
 
 
-def test_stream_k_lost_flag_sets_the_error_word(_sk_reset):
-    """The stream-K wait is bounded: with the contributors' flags never raised (test knob
-    gemm.sk_lostflag) and a short poll limit (gemm.sk_spin), every finisher gives up, the
-    kernel exits, and the workspace's error word is set (no flag is left raised).  Zeroing the
-    workspace and running normally then gives the correct result with the word clear."""
-    M, N, K = 2048, 3136, 12544
-    announce("stream_k_lost_flag", M, N, K)
-    x, w, s = _case(M, N, K, 2718, act="relu2")
-    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
-    ws = _gemm_ws(M, N, K)
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
-    err = _lib.NMI_WS_ERROR_OFFSET
+def _late_flag_call(xd, wd, sd, y, ws):
+    """One stream-K launch whose contributors raise their flags only after their finishers gave
+    up (test knob gemm.sk_lostflag) with a short poll limit (gemm.sk_spin): every wait runs into
+    its bound and every kernel exits.  The call itself returns NMI_OK: the error is asynchronous."""
     _lib.tuning_set("gemm.sk_spin", 64)
     _lib.tuning_set("gemm.sk_lostflag", 1)
     try:
@@ -430,11 +427,69 @@ def test_stream_k_lost_flag_sets_the_error_word(_sk_reset):
     finally:
         _lib.tuning_set("gemm.sk_lostflag", 0)
         _lib.tuning_set("gemm.sk_spin", 0)
-    word = ws[err:err + 4].clone().view(torch.int32).item()
-    assert word == 1, word
-    assert torch.count_nonzero(ws[:err]) == 0, "a flag was raised"
-    ws.zero_()
+
+
+def test_stream_k_late_flag_is_reported_and_the_workspace_recovers(_sk_reset):
+    """After a launch whose finishers gave up: the workspace's error word is set and every flag
+    is back at zero (each late contributor found its slot abandoned and lowered its flag); the
+    next call on the device raises NMI_ERR_ASYNC and launches nothing; the error is reported
+    once; and the call after it, on the same workspace (not cleared), matches the oracle."""
+    M, N, K = 2048, 3136, 12544
+    announce("stream_k_late_flag", M, N, K)
+    x, w, s = _case(M, N, K, 2718, outlier_frac=0.001)
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    ws = _gemm_ws(M, N, K)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    err = _lib.NMI_WS_ERROR_OFFSET
+    L = _lib.lib()
+    assert L.nmi_async_status() == _lib.NMI_OK
+    _late_flag_call(xd, wd, sd, y, ws)
+    assert ws[err:err + 4].clone().view(torch.int32).item() == 1
+    assert torch.count_nonzero(ws[:err]) == 0, "a flag was left raised"
+    y.fill_(5.0)
+    with pytest.raises(_lib.NmiError) as e:
+        _gemm_call(xd, wd, sd, y, ws)
+    assert e.value.code == _lib.NMI_ERR_ASYNC and "gave up waiting" in str(e.value), str(e.value)
+    torch.cuda.synchronize()
+    assert torch.all(y == 5.0), "the call that reported the error launched something"
+    assert L.nmi_async_status() == _lib.NMI_OK, "reported twice"
     _gemm_call(xd, wd, sd, y, ws)
     torch.cuda.synchronize()
-    assert ws[err:err + 4].view(torch.int32).item() == 0
-    assert_parity(bits(y), oracle_bits(x, w, s), "after the workspace was cleared")
+    assert L.nmi_async_status() == _lib.NMI_OK
+    assert torch.count_nonzero(ws[:err]) == 0
+    assert_parity(bits(y), oracle_bits(x, w, s), "after the reported error, same workspace")
+
+
+def test_stream_k_late_flag_reaches_sync_ops_and_the_binding(_sk_reset):
+    """The asynchronous error reaches every front end: nmi_sync (and so the pybind module's
+    sync()), ops.gemm_fp8_w8a16 and the pybind block entries raise it once, and the next call of
+    each computes normally."""
+    from nemotron_infer_amd.csrc import binding
+
+    M, N, K = 2048, 3136, 12544
+    announce("stream_k_late_flag_front_ends", M, N, K)
+    x, w, s = _case(M, N, K, 2719)
+    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    ws = _gemm_ws(M, N, K)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    L = _lib.lib()
+    _late_flag_call(xd, wd, sd, y, ws)
+    assert L.nmi_sync() == _lib.NMI_ERR_ASYNC
+    assert L.nmi_sync() == _lib.NMI_OK
+    _late_flag_call(xd, wd, sd, y, ws)
+    with pytest.raises(RuntimeError, match="gave up waiting"):
+        binding.sync()
+    binding.sync()
+    _late_flag_call(xd, wd, sd, y, ws)
+    with pytest.raises(_lib.NmiError, match="gave up waiting"):
+        ops.gemm_fp8_w8a16(xd, wd, sd)
+    ref = oracle_bits(x, w, s)
+    assert_parity(bits(ops.gemm_fp8_w8a16(xd, wd, sd)), ref, "ops after the reported error")
+    _late_flag_call(xd, wd, sd, y, ws)
+    out = torch.empty(64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="gave up waiting"):
+        binding.gemv_fp8(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), out.data_ptr(), 64, K)
+    binding.gemv_fp8(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), out.data_ptr(), 64, K)
+    binding.sync()
+    assert_parity(bits(out), oracle_bits(x[:1], w[:64], s[:64])[0], "binding gemv after the reported error")
+    assert L.nmi_async_status() == _lib.NMI_OK

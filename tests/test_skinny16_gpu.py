@@ -53,7 +53,7 @@ def _check(M, N, K, seed, label, scales="log_uniform", act="normal"):
 def test_config2_decode_shapes(M):
     """Config 2's decode shapes (q, k, v, o, up, down) at M from 5 to 16 (the default form),
     per-row log-uniform scales (K from 3136 to 12544)."""
-    for lin in synth.DECODE_SET:
+    for lin in synth.SKINNY_SET:
         announce("s16_config2", M, lin.name, lin.N, lin.K)
         _check(M, lin.N, lin.K, 5000 + M + lin.N % 97, f"M={M} {lin.name}", act=lin.act)
 

@@ -115,7 +115,7 @@ def test_config2_shapes(M, dma):
     4x4x4 kernel in both forms (M = 2 too, with skinny.path = 2)."""
     _lib.tuning_set("skinny.path", 2)
     _lib.tuning_set("s4.dma", dma)
-    for lin in synth.DECODE_SET:
+    for lin in synth.SKINNY_SET:
         announce("skinny_config2", M, dma, lin.name)
         x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, act=lin.act)
         assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} dma={dma} {lin.name}")
