@@ -251,7 +251,9 @@ int nmi_mlp_forward_fp8(const void* input_bf16, const float* norm_w, const void*
  * bit for M <= 16; for 17 <= M the short-prompt GEMMs run without their K split (whose partials
  * would not fit), so the two agree up to float32 summation order (bit for bit with tuning knob
  * gemm.splits = 1).  Needs the block's buffers without the split partials (M * inter * 2 bytes,
- * plus M * hidden * 2 for M > 2, each rounded up to 256) within the array (hidden 3136, inter
+ * plus M * hidden * 2 for the normed input unless the RMSNorm is fused into the up projection's
+ * GEMV -- M = 1, or M = 2 where hidden is not a multiple of 64 -- each rounded up to 256; this is
+ * nmi_mlp_workspace_bytes under tuning knob gemm.splits = 1) within the array (hidden 3136, inter
  * 12544: M <= 133), else NMI_ERR_WORKSPACE.  Every call on a GPU shares that GPU's array: calls that
  * may overlap in time on one GPU (other streams, other threads) race.  Same argument
  * requirements as nmi_mlp_forward_fp8.

@@ -144,10 +144,7 @@ size_t linear_workspace_bytes(int M, int64_t total_n, int K) {
     if (M > 16 && M < 512)                            // the short-prompt kernel's K-split partials
         return (t == 0 || t == 2) ? gemm_short_workspace_bytes(M, (int)std::min<int64_t>(total_n, 1 << 30), K) : 0;
     if (M > 16) return gemm_workspace_bytes(M);       // stream-K flags and partials of the GEMM
-    // the K split of the 4x4x4 kernel's pipelined form ("s4.kg" > 1) uses a workspace
-    const Path path = choose_path(M);
-    if (path == Path::Skinny4) return skinny4_workspace_bytes(M, K, total_n, device_info().num_cu);
-    return 0;
+    return 0;                                         // the GEMV and skinny kernels use none
 }
 
 bool gemm_workspace_has_flags(int M) { return M >= 512 && choose_path(M) == Path::Gemm; }
@@ -188,7 +185,7 @@ hipError_t dispatch_linear(const uint16_t* x, int64_t ldx, int M, int K, GemvGro
         case Path::Skinny4: {
             hipError_t e = hipSuccess;
             if (launch_skinny16_grouped(x, ldx, M, K, g, ng, st, &e)) return e;
-            return launch_skinny4_grouped(x, ldx, M, K, g, ng, ws, ws_bytes, st);
+            return launch_skinny4_grouped(x, ldx, M, K, g, ng, st);
         }
         case Path::Gemm: break;
     }
@@ -447,11 +444,10 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s4.ks")) t.s4_ks = value;
     else if (!std::strcmp(knob, "s4.t")) t.s4_t = value;
     else if (!std::strcmp(knob, "s4.u")) t.s4_u = value;
-    else if (!std::strcmp(knob, "s4.dma")) t.s4_dma = value;
-    else if (!std::strcmp(knob, "s4.kg")) t.s4_kg = value;
     else if (!std::strcmp(knob, "gemm.sk")) t.gemm_sk = value;
     else if (!std::strcmp(knob, "gemm.sk_spin")) t.gemm_sk_spin = value;
     else if (!std::strcmp(knob, "gemm.sk_lostflag")) t.gemm_sk_lostflag = value;
+    else if (!std::strcmp(knob, "gemm.gh")) t.gemm_gh = value;
     else if (!std::strcmp(knob, "chain.wgs")) t.chain_wgs = value;
     else if (!std::strcmp(knob, "gemv.wgs")) t.gemv_wgs = value;
     else if (!std::strcmp(knob, "gemv.multirow")) t.gemv_multirow = value;

@@ -182,6 +182,7 @@ struct GemmArgs {
     int64_t ldy;
     int M, N, K;
     int tiles_m, tiles_n, per_xcd;
+    int gh;                 // DMA-fed kernel: tile order, row bands per group (tile_coords)
     int vec_store;          // y 8-byte aligned and ldy % 4 == 0
     int vec_res;            // residual 8-byte aligned and ldres % 4 == 0
     Epi epi;
@@ -481,6 +482,21 @@ constexpr size_t kDmaPartialBytes = (size_t)256 * 256 * sizeof(float);   // one 
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr)
                  : "memory", "m0");
+}
+
+// Tile seq of the DMA-fed kernel's tile order -> (row band tm, column band tn): groups of gh row
+// bands, column bands in order within a group, row bands fastest (the last group may be shorter).
+// An XCD takes a contiguous run of seq, so gh sets its footprint: gh = tiles_m gives whole column
+// bands (few W column bands, every x row band), gh = 1 whole row bands.  Every seq below
+// tiles_m * tiles_n maps to one tile inside the grid.
+__device__ __forceinline__ void tile_coords(int seq, int tiles_m, int tiles_n, int gh, int& tm, int& tn) {
+    const int per = gh * tiles_n;
+    const int rg = seq / per;
+    const int r0 = rg * gh;
+    const int h = min(gh, tiles_m - r0);
+    const int loc = seq - rg * per;
+    tn = loc / h;
+    tm = r0 + (loc - tn * h);
 }
 
 template <bool SK, bool GROUPED>
@@ -823,8 +839,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         const int local = g >> 3;
         const int tile = (g & 7) * a.per_xcd + local;
         if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
-        const int tn = tile / a.tiles_m;
-        m0 = (tile - tn * a.tiles_m) * 256;
+        int tm, tn;
+        tile_coords(tile, a.tiles_m, a.tiles_n, a.gh, tm, tn);
+        m0 = tm * 256;
         select(tn);
         zero_acc();
         run(0, KT);
@@ -843,9 +860,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         const int rounds = (te - xb) / Gx;
         for (int r = 0; r < rounds; ++r) {
             const int tile = xb + r * Gx + v;
-            const int tm = tile / a.tiles_n;
+            int tm, tn;
+            tile_coords(tile, a.tiles_m, a.tiles_n, a.gh, tm, tn);
             m0 = tm * 256;
-            select(tile - tm * a.tiles_n);
+            select(tn);
             zero_acc();
             run(0, KT);
             store();
@@ -859,9 +877,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
             const int tile = tb + tl;
             const int t0 = tl * KT;
             const int kb = max(start, t0) - t0, ke = it - t0;
-            const int tm = tile / a.tiles_n;
+            int tm, tn;
+            tile_coords(tile, a.tiles_m, a.tiles_n, a.gh, tm, tn);
             m0 = tm * 256;
-            select(tile - tm * a.tiles_n);
+            select(tn);
             zero_acc();
             run(kb, ke);
             if (ke == KT && kb > 0) {
@@ -1076,12 +1095,14 @@ hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g,
     const int T = a.tiles_m * a.tiles_n;
     a.per_xcd = (T + 7) / 8;
     const int G = device_info().num_cu;             // one 144 KiB workgroup per CU
+    const int gh_knob = tuning().gemm_gh;
     const bool fits = ws && ws_bytes >= kSkFlagBytes + (size_t)G * kDmaPartialBytes && G % 8 == 0 &&
                       G * 4 <= (int)kSkFlagBytes && (int64_t)T * (K / kBK) < ((int64_t)1 << 31);
     const int knob = tuning().gemm_sk;
     uint32_t* host_error = nullptr;
     if (fits && knob != 2 && (knob == 1 || 2 * (int64_t)T <= G) && (host_error = async_error_word()) != nullptr) {
         a.sk_host_error = host_error;
+        a.gh = gh_knob > 0 ? std::min(gh_knob, a.tiles_m) : 1;
         a.sk_total = (int64_t)T * (K / kBK);
         a.sk_flags = static_cast<uint32_t*>(ws);
         a.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);
@@ -1098,6 +1119,7 @@ hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g,
         hipLaunchKernelGGL(sk_kernel, dim3(8 * gx), dim3(256), lds, stream, a);
         return hipGetLastError();
     }
+    a.gh = gh_knob > 0 ? std::min(gh_knob, a.tiles_m) : a.tiles_m;
     hipLaunchKernelGGL(dp_kernel, dim3(8 * a.per_xcd), dim3(256), lds, stream, a);
     return hipGetLastError();
 }

@@ -45,8 +45,6 @@ struct Tuning {
     int s4_ks = 0;         // 4x4x4 skinny kernel: waves splitting K (1, 2, 4)
     int s4_t = 0;          // 4x4x4 skinny kernel: row groups of 4 per wave (1, 2)
     int s4_u = 0;          // 4x4x4 skinny kernel: chunks per lane per batch (2, 4, 8)
-    int s4_dma = 0;        // 4x4x4 skinny kernel: 0 pipelined form where it applies, 2 windowed form
-    int s4_kg = 0;         // 4x4x4 skinny kernel: workgroups splitting K (> 1, with a workspace; 0, 1: none)
     int gemm_sk = 0;       // GEMM stream-K: 1 whenever a workspace allows; otherwise one tile per workgroup
     int gemm_sk_spin = 0;  // GEMM stream-K: polls of a flag before the wait gives up (0: 2^26)
     int gemm_sk_lostflag = 0;  // GEMM stream-K (tests): 1 = contributors raise their flags only after the finisher gave up
@@ -59,6 +57,7 @@ struct Tuning {
     int gemm_splits = 0;   // short-prompt GEMM (17 <= M < 512): workgroups splitting K (0: automatic)
     int gemm_short = 0;    // short-prompt GEMM: f + 1 forces kernel form f (0..7, gemm_short.hip)
     int gemm_sk_cap = 0;   // GEMM stream-K: at most this many workgroups per tile (0: 2; -1: one per CU)
+    int gemm_gh = 0;       // DMA-fed GEMM: row bands per group of the tile order (0: all of them, stream-K: 1)
     int s16 = 0;           // 16x16x32 skinny kernel: 0 automatic (M >= 3), 1 for 2 <= M <= 16, 2 never
     int s16_r = 0;         // 16x16x32 skinny kernel: row tiles of 16 per workgroup (1, 2; 0: by rows)
     int s16_t = 0;         // 16x16x32 skinny kernel: 1 row runs (0: DMA where it fits)
@@ -102,12 +101,10 @@ struct Norm {
 hipError_t launch_gemv_m1_grouped(const uint16_t* x, int K, const GemvGroup* groups, int ngroups,
                                   hipStream_t stream);
 
-// 2 <= M <= 16 on 4x4x4 MFMA with coalesced weight reads.  With a workspace of at least
-// skinny4_workspace_bytes() bytes (zero-filled before its first use; every launch leaves it
-// re-armed; 0 = the schedule has no K split) K is also split between workgroups.
-size_t skinny4_workspace_bytes(int M, int K, int64_t total_rows, int num_cu);
+// 2 <= M <= 16 on 4x4x4 MFMA with coalesced weight reads and x staged by LDS DMA; the GEMM takes
+// the call where x rows are not 16-byte aligned or x spans 4 GiB or more.
 hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups,
-                                  int ngroups, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                                  int ngroups, hipStream_t stream);
 
 // M <= 16 on 16x16x32 MFMA, one row tile per workgroup with K split between its waves
 // (skinny16_fp8.hip): taken for the M and K skinny16_wanted() accepts when the operands suit it

@@ -26,6 +26,31 @@ both weights per row as test_mlp_block.cu:57-70 does and feeds the input as bf16
 holds ``chain_f64``: the block computed in float64 with a bf16 rounding after every step, as
 the fp8 block's M == 1 path stores its intermediates (mlp_block.cuh:140-148, 173-175), the
 rounding done here on the float64 bit pattern.
+
+The attention block fixture ``attn_block_h256_q4_kv2_s40`` follows
+tools/dump_attention_block.py:20-58 exactly: torch seed 777, HIDDEN 256, 4 query heads, 2 KV
+heads, head 128, S 40 (more than one KV tile), EPS 1e-5, the same draws in the same order, and
+the HF-formula forward (plain RMSNorm, no RoPE, GQA by repeating the KV heads, causal SDPA with
+scale 1/sqrt(128), o projection, residual), here in float64, stored as float32 ``expected_f32``
+with the intermediates; and ``decode_last_f32``, the last token decoded after a prefill of the
+others under the reference's decode contract, whose query attends the cached positions only (its
+own k and v are appended after the attention, ops/attention/sdpa_decode.cuh:57-180), unlike the
+HF row, which also attends the token itself.  test_attention_block.cu:161-194 quantizes the weights per row
+(test_attention_block.cu's up_fp8_perrow) and feeds the input as bf16; the codes and scales of
+that quantization are stored too.
+
+The Mamba block fixture ``mamba_block_h64_h4p16_g2_n128_s24`` follows
+tools/dump_mamba_block.py:1-40 and its forward: torch seed 1234, HIDDEN 64, 4 heads of 16, 2
+groups, conv width 4, chunk 8, S 24 (three chunks), EPS 1e-5, dt limited to (0, inf), the same
+draws in the same order and the HF forward -- plain RMSNorm, in_proj split into z | xBC | dt,
+depthwise causal conv1d + SiLU, dt = softplus(dt + dt_bias), the chunked SSD (intra-chunk
+products with the decay exp(cumA[l] - cumA[s]), chunk states, the state passed from chunk to
+chunk, then C against it; head h reads group h // (H / G)), y + D x, the gated RMSNorm with
+the gate applied before the norm per group of INTER / G channels, out_proj, residual.  One
+change: the SSM state size is 128 (the reference's dump uses 16) because this build's kernels
+serve the model's state size only; every draw keeps its recipe (shapes grow with N).  The SSD
+is written here from its definition in float64; the final conv and SSM states of the sequence
+are stored for the prefill-to-decode continuation.
 """
 from __future__ import annotations
 
@@ -91,6 +116,124 @@ def save(name: str, **arrays):
     path = os.path.join(HERE, name + ".npz")
     np.savez_compressed(path, **arrays)
     return path
+
+
+def _rmsnorm64(x, w, eps):
+    x = x.double()
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w.double()
+
+
+def attention_fixture():
+    """tools/dump_attention_block.py:20-58 (seed 777), forward in float64."""
+    HID, HQ, HKV, HEAD, S, EPS = 256, 4, 2, 128, 40, 1e-5
+    g = torch.Generator().manual_seed(777)
+    norm_w = torch.randn(HID, generator=g, dtype=torch.float32)
+    q_w = torch.randn(HQ * HEAD, HID, generator=g, dtype=torch.float32) * 0.1
+    k_w = torch.randn(HKV * HEAD, HID, generator=g, dtype=torch.float32) * 0.1
+    v_w = torch.randn(HKV * HEAD, HID, generator=g, dtype=torch.float32) * 0.1
+    o_w = torch.randn(HID, HQ * HEAD, generator=g, dtype=torch.float32) * 0.1
+    x = torch.randn(1, S, HID, generator=g, dtype=torch.float32).reshape(S, HID)
+    with torch.no_grad():
+        h = _rmsnorm64(x, norm_w, EPS)
+        q = (h @ q_w.double().T).reshape(S, HQ, HEAD).transpose(0, 1)
+        k = (h @ k_w.double().T).reshape(S, HKV, HEAD).transpose(0, 1)
+        v = (h @ v_w.double().T).reshape(S, HKV, HEAD).transpose(0, 1)
+        rep = HQ // HKV
+        k = k.repeat_interleave(rep, dim=0)
+        v = v.repeat_interleave(rep, dim=0)
+        att = torch.nn.functional.scaled_dot_product_attention(q[None], k[None], v[None], is_causal=True)[0]
+        att = att.transpose(0, 1).reshape(S, HQ * HEAD)
+        o = att @ o_w.double().T
+        out = x.double() + o
+        # the reference's decode of the last token after a prefill of the others: its query
+        # attends the cached positions [0, S - 1) only, its own k and v are appended afterwards
+        # (ops/attention/sdpa_decode.cuh:57-120 loops over [0, S_cache), :122-180 appends)
+        ql, kp, vp = q[:, S - 1:], k[:, :S - 1], v[:, :S - 1]
+        p = torch.softmax((ql @ kp.transpose(1, 2)) / np.sqrt(HEAD), dim=-1)
+        dec = (p @ vp).transpose(0, 1).reshape(1, HQ * HEAD) @ o_w.double().T + x[S - 1:].double()
+    codes = {n: perrow_quant(w.numpy()) for n, w in (("q", q_w), ("k", k_w), ("v", v_w), ("o", o_w))}
+    return save("attn_block_h256_q4_kv2_s40", x_f32=x.numpy(), x_bf16=bf16_bits(x.numpy()), norm_w=norm_w.numpy(),
+                q_w_f32=q_w.numpy(), k_w_f32=k_w.numpy(), v_w_f32=v_w.numpy(), o_w_f32=o_w.numpy(),
+                **{f"{n}_codes": c for n, (c, _) in codes.items()}, **{f"{n}_scale": sc for n, (_, sc) in codes.items()},
+                expected_f32=out.float().numpy(), normed_f32=h.float().numpy(), attn_f32=att.float().numpy(),
+                o_f32=o.float().numpy(), decode_last_f32=dec.float().numpy(), eps=np.float32(EPS))
+
+
+def ssd_chunked(xdt, adt, Bh, Ch, chunk):
+    """The chunked SSD of Mamba-2 in float64: xdt [S, H, P] (x * dt), adt [S, H] (A * dt), Bh, Ch
+    [S, H, N] (per head).  Within a chunk, y[l] = sum_{s <= l} (C[l] . B[s]) exp(cumA[l] - cumA[s])
+    xdt[s]; each chunk's state is sum_s B[s] exp(cumA[last] - cumA[s]) xdt[s]; the state entering a
+    chunk is the previous one decayed over that chunk plus its state; the chunk's outputs add
+    C[l] . state_in exp(cumA[l]).  Returns y [S, H, P] and the final state [H, P, N]."""
+    S, H, P = xdt.shape
+    N = Bh.shape[-1]
+    y = torch.zeros(S, H, P, dtype=torch.float64)
+    state = torch.zeros(H, P, N, dtype=torch.float64)
+    for c0 in range(0, S, chunk):
+        sl = slice(c0, min(S, c0 + chunk))
+        cum = torch.cumsum(adt[sl], dim=0)                         # [L, H]
+        L = cum.shape[0]
+        decay = torch.exp(cum[:, None, :] - cum[None, :, :])       # [l, s, H]
+        decay = decay * torch.tril(torch.ones(L, L, dtype=torch.float64))[:, :, None]
+        cb = torch.einsum("lhn,shn->lsh", Ch[sl], Bh[sl])          # [l, s, H]
+        y[sl] = torch.einsum("lsh,shp->lhp", cb * decay, xdt[sl])
+        y[sl] += torch.einsum("lhn,hpn->lhp", Ch[sl], state) * torch.exp(cum)[:, :, None]
+        to_end = torch.exp(cum[-1][None, :] - cum)                # [s, H]
+        chunk_state = torch.einsum("shn,sh,shp->hpn", Bh[sl], to_end, xdt[sl])
+        state = state * torch.exp(cum[-1])[:, None, None] + chunk_state
+    return y, state
+
+
+def mamba_fixture():
+    """tools/dump_mamba_block.py:1-40 and its forward (seed 1234) with state size 128."""
+    HID, H, P, N, G, CK, CHUNK, S, EPS = 64, 4, 16, 128, 2, 4, 8, 24, 1e-5
+    INTER = H * P
+    CONV = INTER + 2 * G * N
+    PROJ = INTER + CONV + H
+    GS = INTER // G
+    g = torch.Generator().manual_seed(1234)
+    norm_w = torch.randn(HID, generator=g, dtype=torch.float32)
+    in_w = torch.randn(PROJ, HID, generator=g, dtype=torch.float32) * 0.1
+    conv_w = torch.randn(CONV, 1, CK, generator=g, dtype=torch.float32) * 0.2
+    conv_b = torch.randn(CONV, generator=g, dtype=torch.float32) * 0.1
+    A_log = torch.randn(H, generator=g, dtype=torch.float32) * 0.5 - 1.0
+    D = torch.rand(H, generator=g, dtype=torch.float32) * 0.1
+    dt_bias = torch.rand(H, generator=g, dtype=torch.float32) * 0.2
+    gnorm_w = torch.randn(INTER, generator=g, dtype=torch.float32)
+    out_w = torch.randn(HID, INTER, generator=g, dtype=torch.float32) * 0.1
+    x = torch.randn(1, S, HID, generator=g, dtype=torch.float32).reshape(S, HID)
+    with torch.no_grad():
+        h = _rmsnorm64(x, norm_w, EPS)
+        proj = h @ in_w.double().T
+        z, xbc, dt = proj[:, :INTER], proj[:, INTER:INTER + CONV], proj[:, INTER + CONV:]
+        conv = torch.nn.functional.conv1d(xbc.T[None], conv_w.double(), conv_b.double(), padding=CK - 1,
+                                          groups=CONV)[0, :, :S].T
+        xc = torch.nn.functional.silu(conv)                        # [S, CONV]
+        xs, Bs, Cs = xc[:, :INTER], xc[:, INTER:INTER + G * N], xc[:, INTER + G * N:]
+        dts = torch.nn.functional.softplus(dt + dt_bias.double()).clamp(0.0, float("inf"))   # [S, H]
+        A = -torch.exp(A_log.double())
+        xh = xs.reshape(S, H, P)
+        Bh = Bs.reshape(S, G, N).repeat_interleave(H // G, dim=1)
+        Ch = Cs.reshape(S, G, N).repeat_interleave(H // G, dim=1)
+        y, ssm_state = ssd_chunked(xh * dts[:, :, None], A[None, :] * dts, Bh, Ch, CHUNK)
+        y = (y + D.double()[None, :, None] * xh).reshape(S, INTER)
+        gated = y * torch.nn.functional.silu(z)
+        gg = gated.reshape(S, G, GS)
+        gn = (gg * torch.rsqrt(gg.pow(2).mean(-1, keepdim=True) + EPS)).reshape(S, INTER) * gnorm_w.double()
+        mix = gn @ out_w.double().T
+        out = x.double() + mix
+        conv_state = xbc[S - (CK - 1):].T                          # [CONV, 3]: the last three xBC inputs
+    in_codes, in_s = perrow_quant(in_w.numpy())
+    out_codes, out_s = perrow_quant(out_w.numpy())
+    return save("mamba_block_h64_h4p16_g2_n128_s24", x_f32=x.numpy(), x_bf16=bf16_bits(x.numpy()),
+                norm_w=norm_w.numpy(), in_w_f32=in_w.numpy(), conv_w=conv_w.reshape(CONV, CK).numpy(),
+                conv_b=conv_b.numpy(), A_log=A_log.numpy(), D=D.numpy(), dt_bias=dt_bias.numpy(),
+                gnorm_w=gnorm_w.numpy(), out_w_f32=out_w.numpy(), in_codes=in_codes, in_scale=in_s,
+                out_codes=out_codes, out_scale=out_s, expected_f32=out.float().numpy(),
+                normed_f32=h.float().numpy(), xbc_conv_f32=xc.float().numpy(), scan_y_f32=y.float().numpy(),
+                gnormed_f32=gn.float().numpy(), mixer_f32=mix.float().numpy(), dt_f32=dts.float().numpy(),
+                conv_state_f32=conv_state.float().numpy(), ssm_state_f32=ssm_state.float().numpy(),
+                shape=np.array([HID, H, P, N, G, CK, CHUNK, S], np.int32), eps=np.float32(EPS))
 
 
 def main():
@@ -187,6 +330,9 @@ def main():
                         normed_f32=hs.numpy(), up_f32=up.numpy(), act_f32=act.numpy(), down_f32=down.numpy(),
                         chain_normed=hb, chain_up=upb, chain_act=actb, chain_down=downb, chain_f64=outb,
                         eps=np.float32(EPS)))
+
+    written.append(attention_fixture())
+    written.append(mamba_fixture())
 
     with open(os.path.join(HERE, "SHA256SUMS"), "w") as f:
         for p in sorted(written):

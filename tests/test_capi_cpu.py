@@ -339,7 +339,7 @@ def test_tuning_knobs_from_environment():
     import sys
 
     code = "from nemotron_infer_amd import _lib; _lib.lib(); print('loaded')"
-    env = dict(os.environ, NMI_TUNING="s4.dma=2, s4.u=4")
+    env = dict(os.environ, NMI_TUNING="s4.ks=2, s4.u=4")
     r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and "loaded" in r.stdout, r.stderr
     env["NMI_TUNING"] = "no.such.knob=1"

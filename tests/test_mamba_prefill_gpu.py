@@ -59,7 +59,7 @@ def _oracle_mixer_sequence(proj, prm):
     return ys, cs, ss
 
 
-@pytest.mark.parametrize("S", [1, 2, 3, 64, 65, 200])
+@pytest.mark.parametrize("S", [1, 2, 3, 64, 65, 200, 600])
 def test_mamba_forward_matches_oracle(S):
     announce("mamba_forward", S)
     W = _weights()
@@ -117,6 +117,36 @@ def test_mamba_forward_scan_output_matches_oracle():
     ref = linear.bf16_to_f32(block.add_bf16(x, g_ref)).astype(np.float64) - xf
     rel = np.linalg.norm(got_g - ref) / np.linalg.norm(ref)
     assert rel <= 4e-3, rel
+
+
+def test_mamba_forward_two_sequences_past_512_rows():
+    """batch = 2 sequences of 300 tokens: 600 rows, so the projections run the M >= 512 GEMM (the
+    out_proj's 39 tiles on stream-K, its flags cleared by the block, the workspace sized for the
+    Mamba shapes) while each sequence alone (300 rows) would not.  Per sequence against the oracle
+    on the GPU's own in_proj output: conv state bit-exact, SSM state within the state bar, output
+    end to end rel_l2 <= 4e-3."""
+    announce("mamba_forward_two_sequences_600_rows")
+    W = _weights()
+    dw = _dev(W)
+    prm = W["prm"]
+    S = 300
+    x = _bf16_np((2 * S, HIDDEN), 8900)
+    xd = x_to_dev(x)
+    cs = torch.zeros((2, CONV_DIM, 3), device=DEV)
+    ss = torch.zeros((2, H, P, N), device=DEV)
+    out = bits(ops.mamba_forward_fp8(xd, *dw, H, P, G, batch=2, conv_state_out=cs, ssm_state_out=ss, eps=EPS))
+    h = ops.rmsnorm_bf16(xd, dw[0], EPS)
+    proj = bits(ops.linear_fp8_w8a16(h, dw[1], dw[2], use_workspace=True))    # 600 rows, as the block's in_proj
+    torch.cuda.synchronize()
+    for b in range(2):
+        rows = slice(b * S, (b + 1) * S)
+        yr, csr, ssr = _oracle_mixer_sequence(proj[rows], prm)
+        assert np.array_equal(cs.cpu().numpy()[b:b + 1], csr), f"conv state {b}"
+        _check_state(ss.cpu().numpy()[b:b + 1], ssr, f"ssm state {b}")
+        g_ref = mamba.gated_rmsnorm(yr, proj[rows, :INTER], prm["gnorm_w"], G, EPS)
+        out_ref = block.add_bf16(x[rows], linear.linear_fp8_w8a16(g_ref, *W["out"]))
+        r = linear.parity(out[rows], out_ref)
+        assert r["nan_ok"] and r["rel_l2_all"] <= 4e-3, (f"sequence {b}", r)
 
 
 def test_mamba_forward_batch_and_decode_continuation():

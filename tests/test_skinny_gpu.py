@@ -4,10 +4,9 @@ off here unless a test names it), of the small-M GEMV forms and of the grouped e
 against the torch fp32 dequant-then-F.linear oracle.
 
 Tolerance: rel_l2 <= 1e-3 and max |diff| <= 2 bf16 ulp at max(|ref|, 2^-8 rms(ref)).
-Size-independent properties: the workspace's arrival counters are re-armed after every
-launch (the workspace reads back zero there), repeated calls are bit-identical, a grouped call
-equals the separate calls under the same schedule, and M = 1 through this kernel agrees with
-the GEMV kernel within the tolerance.
+Size-independent properties: repeated calls are bit-identical, a grouped call equals the
+separate calls under the same schedule, and M = 1 through this kernel agrees with the GEMV kernel
+within the tolerance.
 """
 import ctypes
 
@@ -23,7 +22,7 @@ from tests.gpu_util import (DEV, announce, assert_parity, bits, oracle_bits, s_t
 
 pytestmark = pytest.mark.gpu
 
-KNOBS = ("m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u", "s4.dma", "s4.kg")
+KNOBS = ("m1.path", "gemv.ks", "skinny.path", "s4.ks", "s4.t", "s4.u")
 
 
 @pytest.fixture(autouse=True)
@@ -73,105 +72,52 @@ def test_fixtures_all_m(name, use_ws, kernel):
 @pytest.mark.parametrize("M", list(range(1, 17)))
 def test_every_m_ragged(M):
     """Ragged N (not a multiple of 4, 16 or 64) and K (not a multiple of 64), both kernels (the
-    4x4x4 one in both forms, M = 1 included; the 16x16x32 one with s16 = 1, path 1) and both
-    workspace modes."""
+    4x4x4 one, M = 1 included; the 16x16x32 one with s16 = 1, path 1) and both workspace modes."""
     _lib.tuning_set("m1.path", 3)
     _lib.tuning_set("skinny.path", 2)
     for N, K in [(37, 208), (1000, 3136), (130, 12544 + 16)]:
         x, w, s = _case(M, N, K, 17 * M + N + K)
         ref = oracle_bits(x, w, s)
-        for path, dma in ((0, 0), (0, 2), (1, 0)):
+        for path in (0, 1):
             _lib.tuning_set("s16", 1 if path == 1 else 2)
-            _lib.tuning_set("s4.dma", dma)
             for use_ws in (False, True):
-                announce("skinny_ragged", M, N, K, path, dma, use_ws)
-                assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} path={path} dma={dma} ws={use_ws}")
+                announce("skinny_ragged", M, N, K, path, use_ws)
+                assert_parity(_run(x, w, s, use_ws), ref, f"M={M} N={N} K={K} path={path} ws={use_ws}")
 
 
 @pytest.mark.parametrize("ks", [1, 2, 4])
-@pytest.mark.parametrize("t", [1, 2])
+@pytest.mark.parametrize("t", [1, 2, 4])
 @pytest.mark.parametrize("u", [2, 4, 8])
-@pytest.mark.parametrize("dma", [0, 2])
-def test_s4_every_schedule(ks, t, u, dma):
+def test_s4_every_schedule(ks, t, u):
     """Each (waves splitting K, row groups per wave, chunks per lane) instantiation of the 4x4x4
-    kernel, in both forms (dma 0: pipelined, two LDS-DMA windows in flight, where its LDS fits;
-    dma 2: the windowed form), for M in {2, 5, 8, 16} (1, 2 and 4 groups of activation rows),
-    with several LDS windows (odd and even window counts, partial last windows) and N not a
+    kernel (two LDS-DMA windows in flight; knob choices whose windows would not fit the LDS are
+    narrowed), for M in {2, 5, 8, 16} (1, 2 and 4 groups of activation rows), with one, two, three
+    and many windows (the loop over window pairs and both tails, partial last windows) and N not a
     multiple of the rows per workgroup."""
     _lib.tuning_set("s4.ks", ks)
     _lib.tuning_set("s4.t", t)
     _lib.tuning_set("s4.u", u)
-    _lib.tuning_set("s4.dma", dma)
-    for M, N, K in [(2, 300, 3136), (5, 77, 5120), (8, 130, 1040), (16, 264, 3136), (13, 72, 208)]:
-        announce("s4_schedule", ks, t, u, dma, M, N, K)
+    for M, N, K in [(2, 300, 3136), (5, 77, 5120), (8, 130, 1040), (16, 264, 3136), (13, 72, 208),
+                    (3, 90, 12544 + 16), (9, 40, 16 * 16 * 3)]:
+        announce("s4_schedule", ks, t, u, M, N, K)
         x, w, s = _case(M, N, K, 100 * ks + 10 * t + u + M)
         assert_parity(_run(x, w, s, False), oracle_bits(x, w, s), f"ks={ks} t={t} u={u} M={M}")
 
 
 @pytest.mark.parametrize("M", [2, 4, 8, 16])
-@pytest.mark.parametrize("dma", [0, 2])
-def test_config2_shapes(M, dma):
+def test_config2_shapes(M):
     """Config 2 (M in {2,4,8,16}, the six decode shapes, per-row log-uniform scales) on the
-    4x4x4 kernel in both forms (M = 2 too, with skinny.path = 2)."""
+    4x4x4 kernel (M = 2 too, with skinny.path = 2)."""
     _lib.tuning_set("skinny.path", 2)
-    _lib.tuning_set("s4.dma", dma)
     for lin in synth.SKINNY_SET:
-        announce("skinny_config2", M, dma, lin.name)
+        announce("skinny_config2", M, lin.name)
         x, w, s = _case(M, lin.N, lin.K, 2000 + M + lin.N % 53, act=lin.act)
-        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} dma={dma} {lin.name}")
+        assert_parity(_run(x, w, s, True), oracle_bits(x, w, s), f"M={M} {lin.name}")
 
 
-def test_workspace_rearmed_and_deterministic():
-    """After a K-split launch of the 4x4x4 kernel (s4.kg = 3) the counters read back zero;
-    repeated calls are bit-identical."""
-    M, N, K = 8, 3136, 12544
-    _lib.tuning_set("s4.kg", 3)
-    announce("skinny_rearm", M, N, K)
-    x, w, s = _case(M, N, K, 4)
-    xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
-    nbytes = _lib.lib().nmi_linear_workspace_bytes(M, N, K)
-    assert nbytes > 0
-    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
-    outs = []
-    L = _lib.lib()
-    for _ in range(3):
-        y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
-        _lib.check(L.nmi_linear_fp8_w8a16_ws(xd.data_ptr(), K, wd.data_ptr(), K, sd.data_ptr(), y.data_ptr(),
-                                             N, M, N, K, ws.data_ptr(), nbytes, None), "ws")
-        torch.cuda.synchronize()
-        outs.append(bits(y))
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
-    counters = ws[: 4 * 16384].cpu().numpy()
-    assert not counters.any(), "arrival counters not re-armed"
-    assert_parity(outs[0], oracle_bits(x, w, s), "rearm")
-
-
-def test_workspace_shared_between_shapes():
-    """One workspace used by K-split calls of the 4x4x4 kernel of different shapes in turn
-    (small N, then large N, then small again): a counter slot is never overwritten by another
-    call's partials."""
-    _lib.tuning_set("s4.kg", 3)
-    _lib.tuning_set("skinny.path", 2)
-    L = _lib.lib()
-    cases = [(16, 48, 3136), (2, 5120, 3136), (16, 48, 3136), (4, 1024, 12544), (2, 5120, 3136)]
-    nbytes = max(L.nmi_linear_workspace_bytes(M, N, K) for M, N, K in cases)
-    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
-    for i, (M, N, K) in enumerate(cases):
-        announce("ws_shared", i, M, N, K)
-        x, w, s = _case(M, N, K, 90 + i)
-        xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
-        y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
-        _lib.check(L.nmi_linear_fp8_w8a16_ws(xd.data_ptr(), K, wd.data_ptr(), K, sd.data_ptr(), y.data_ptr(),
-                                             N, M, N, K, ws.data_ptr(), nbytes, None), "ws")
-        assert_parity(bits(y), oracle_bits(x, w, s), f"shared ws call {i}")
-    assert not ws[: 4 * 16384].cpu().numpy().any()
-
-
-def test_workspace_never_returns_stale_partials():
-    """The same shape (same workspace slots) with new inputs each call (the 4x4x4 kernel's K
-    split): every result must match its own oracle, so no partial written by an earlier call
-    can be read back."""
-    _lib.tuning_set("s4.kg", 3)
+def test_new_inputs_each_call():
+    """The same shape with new inputs each call: every result must match its own oracle (nothing
+    from an earlier call -- LDS windows, registers -- leaks into the next)."""
     M, N, K = 4, 5120, 3136
     w, s = synth.make_weight(N, K, 5, "cpu", scales="log_uniform")
     wd, sd = w.to(DEV), s.to(DEV)
@@ -291,52 +237,12 @@ def test_stream_kernel_small_m(M):
         _lib.tuning_set("skinny.path", 0)
 
 
-@pytest.mark.parametrize("M", [1, 3, 5, 8, 13, 16])
-@pytest.mark.parametrize("kg,t,u", [(0, 0, 0), (2, 0, 0), (5, 2, 2), (3, 1, 4), (7, 4, 2), (4, 2, 4)])
-def test_s4_k_split(M, kg, t, u):
-    """The pipelined form's K split between workgroups (s4.kg > 1; float32 partials in the
-    workspace; the last workgroup of a row block adds them in K-group order): forced K-group
-    counts and the automatic schedule (no split), 1, 2 and 4 row groups per wave, a grouped call with ragged N, K ranges whose last
-    window or last group is partial, and K too short to split. Against the oracle; repeated
-    calls bit-identical; the workspace's counters read back zero."""
-    _lib.tuning_set("m1.path", 3)                    # M = 1 on the 4x4x4 kernel too
-    _lib.tuning_set("s4.kg", kg)
-    _lib.tuning_set("s4.t", t)
-    _lib.tuning_set("s4.u", u)
-    try:
-        K = 3136
-        x = synth.make_act(M, K, 500 + M, "cpu")
-        ws_host = [synth.make_weight(N, K, 510 + i, "cpu", scales="log_uniform") for i, N in enumerate((37, 300, 1000))]
-        xb = x.view(torch.int16).numpy().view(np.uint16)
-        announce("s4_split_grouped", M, kg, t, u)
-        outs = [bits(y) for y in ops.linear_fp8_w8a16_grouped(x.to(DEV), [(w.to(DEV), s.to(DEV)) for w, s in ws_host])]
-        again = [bits(y) for y in ops.linear_fp8_w8a16_grouped(x.to(DEV), [(w.to(DEV), s.to(DEV)) for w, s in ws_host])]
-        for (w, s), y, y2 in zip(ws_host, outs, again):
-            assert np.array_equal(y, y2)
-            assert_parity(y, oracle_bits(xb, w.numpy(), s.numpy()), f"grouped M={M} kg={kg} t={t} u={u}")
-        for N, K2 in [(130, 12544 + 16), (1000, 5120), (48, 208)]:
-            announce("s4_split", M, kg, t, u, N, K2)
-            xs, w, s = _case(M, N, K2, 520 + M + N)
-            assert_parity(_run(xs, w, s, True), oracle_bits(xs, w, s), f"M={M} N={N} K={K2} kg={kg} t={t} u={u}")
-        torch.cuda.synchronize()
-        ws = ops._WORKSPACE.get(0)
-        if ws is not None:
-            assert not ws[: 4 * 16384].cpu().numpy().any(), "arrival counters not re-armed"
-    finally:
-        for k in ("m1.path", "s4.kg"):
-            _lib.tuning_set(k, 0)
-
-
 @pytest.mark.parametrize("M", [3, 5, 16])
-@pytest.mark.parametrize("dma,kg", [(0, 0), (2, 0), (0, 3)])
-def test_s4_strided_operands(M, dma, kg):
-    """ldx > K, ldw > K, ldy > N (slices of wider buffers) through the 4x4x4 kernel in both forms
-    and with the K split: the DMA offsets and the loads follow the strides, and nothing outside
-    the output slice is written."""
+def test_s4_strided_operands(M):
+    """ldx > K, ldw > K, ldy > N (slices of wider buffers) through the 4x4x4 kernel: the DMA
+    offsets and the loads follow the strides, and nothing outside the output slice is written."""
     N, K = 200, 3136
-    _lib.tuning_set("s4.dma", dma)
-    _lib.tuning_set("s4.kg", kg)
-    announce("s4_strided", M, dma, kg)
+    announce("s4_strided", M)
     x, w, s = _case(M, N, K, 900 + M, scales="log_uniform")
     xbig = torch.zeros((M, K + 64), dtype=torch.bfloat16, device=DEV)
     xbig[:, 32:32 + K] = x_to_dev(x)
@@ -351,6 +257,5 @@ def test_s4_strided_operands(M, dma, kg):
     _lib.check(L.nmi_linear_fp8_w8a16_ws(xv.data_ptr(), xbig.stride(0), wv.data_ptr(), wbig.stride(0), sd.data_ptr(),
                                          yv.data_ptr(), ybig.stride(0), M, N, K, ws.data_ptr(), nbytes, None), "ws")
     torch.cuda.synchronize()
-    assert_parity(bits(ybig[:, 8:8 + N]), oracle_bits(x, w, s), f"strided M={M} dma={dma} kg={kg}")
+    assert_parity(bits(ybig[:, 8:8 + N]), oracle_bits(x, w, s), f"strided M={M}")
     assert torch.all(ybig[:, :8] == 7.0) and torch.all(ybig[:, 8 + N:] == 7.0)
-    assert not ws[: 4 * 16384].cpu().numpy().any()

@@ -85,9 +85,12 @@ def test_noalloc_rejects_sizes_beyond_the_array():
     L = _lib.lib()
     up, dn, nw = _weights()
     limit = L.nmi_mlp_noalloc_scratch_bytes()
-    # the block's buffers without the GEMMs' split partials: act [M, inter] and normed [M, hidden]
-    need = lambda m: (m * INTER * 2 + 255) // 256 * 256 + ((m * HID * 2 + 255) // 256 * 256 if m > 2 else 0)  # noqa: E731
-    M = next(m for m in range(1, 4096) if need(m) > limit)
+    # the block's buffers without the GEMMs' split partials: the workspace query with the split off
+    _lib.tuning_set("gemm.splits", 1)
+    try:
+        M = next(m for m in range(1, 4096) if L.nmi_mlp_workspace_bytes(m, HID, INTER) > limit)
+    finally:
+        _lib.tuning_set("gemm.splits", 0)
     assert M == 134                                # M <= 133 fit at the model's sizes
     announce("noalloc_fits", 133)
     x = synth.make_act(133, HID, 8301, DEV)
