@@ -11,19 +11,22 @@
 // (together with the KV cache).
 //
 // Kernel: one workgroup per (query head, tile of 128 query rows), 4 waves of 32 rows; key/value
-// tiles of 64 positions staged in LDS (K as [64][128], V^T as [128][64], both swizzled so that
-// the MFMA operand reads hit distinct banks), the next tile prefetched into registers while the
-// current one is multiplied.  Per wave and key tile (v_mfma_f32_32x32x16_bf16):
+// tiles of 64 positions staged in LDS (K as [64][128], V^T as [128][64] with the positions of each
+// 16-key group in the P operand's order, both swizzled so that the MFMA operand reads hit distinct
+// banks), the next tile prefetched into registers while the current one is multiplied.  Per wave
+// and key tile (v_mfma_f32_32x32x16_bf16):
 // * S^T = K . Q^T (64 keys x 32 queries): the wave's query rows are the B operand, held in
 //   registers for the whole kernel; the scores of one query then sit in one lane (16 registers
 //   per 32-key block, the two lane halves holding alternate 4-key groups), so the row max and
 //   sum are in-lane plus one exchange between the halves.
-// * online softmax in base 2 (scores times log2(e) / sqrt(128)); keys after the query masked.
+// * online softmax in base 2 (weights exp2((s - m) log2(e) / sqrt(128)) with one fma per score),
+//   the running max m raised lazily (only when a score exceeds it by 2^8 in weight, so the
+//   accumulators are rescaled rarely); keys after the query masked on the diagonal tiles only.
 // * O^T += V^T . P^T: P is the B operand straight from the score registers -- a 16-key step's
 //   lane-half h holds keys {4h..4h+3, 8+4h..8+4h+3}, and the V^T operand is read in the same
 //   key order -- in two bf16 parts (hi = bf16(p), lo = bf16(p - hi)), so the weights carry about
 //   16 significant bits and the float32 row sums stay consistent with them.
-// Query tiles are scheduled longest first (the last tiles see the most keys).
+// Query tiles are scheduled longest first over all heads (the last tiles see the most keys).
 #include "nmi_device.hpp"
 #include "nmi_launch.hpp"
 
@@ -39,6 +42,7 @@ constexpr int kBK = 64;           // key positions per tile
 constexpr int kKBytes = kBK * kD * 2;        // K tile, 16 KiB
 constexpr int kVBytes = kD * kBK * 2;        // V^T tile, 16 KiB
 constexpr int kStage = kKBytes + kVBytes;
+constexpr float kLazy = 8.f;       // log2 of the largest unnormalised softmax weight (lazy max)
 
 struct PrefillArgs {
     const uint16_t* q;      // [S, ldq], head h at column 128 h
@@ -62,8 +66,9 @@ __global__ __launch_bounds__(256, 2) void sdpa_prefill_kernel(const PrefillArgs 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, l32 = lane & 31;
-    const int qt = a.qtiles - 1 - (int)blockIdx.x;            // longest tiles first
-    const int head = blockIdx.y;
+    // longest tiles first over all heads: workgroup g takes query tile qtiles - 1 - g / H of head g % H
+    const int qt = a.qtiles - 1 - (int)blockIdx.x / a.H;
+    const int head = (int)blockIdx.x - (int)blockIdx.x / a.H * a.H;
     const int kvh = head / (a.H / a.H_KV);
     const int q0 = qt * kBQ;
     const int qw = q0 + 32 * wave;                              // the wave's first query row
@@ -110,7 +115,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_prefill_kernel(const PrefillArgs 
     for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
-    float m = -FLT_MAX, l = 0.f;
+    float m = -INFINITY, l = 0.f;                               // raw score units
 
     gload(0);
     sstore(0);
@@ -133,56 +138,71 @@ __global__ __launch_bounds__(256, 2) void sdpa_prefill_kernel(const PrefillArgs 
                     sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[b], 0, 0, 0);
                 }
             }
-            // scores (base 2), causal mask; register r of block b is key kv0 + 32 b + 8 (r / 4) + 4 h + r % 4
+            // causal mask, only where the tile reaches past the wave's first query: register r of
+            // block b is key kv0 + 32 b + 8 (r / 4) + 4 h + r % 4, kept where it is <= qrow (then also
+            // < S for every stored query; rows past S are not stored)
+            if (kv0 + kBK - 1 > qw) {
+                // a branch the compiler keeps: the tiles below the diagonal skip the mask entirely
+                asm volatile("" ::: "memory");
+                const int dq = qrow - kv0 - 4 * h;
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (32 * b + 8 * (r >> 2) + (r & 3) > dq) sacc[b][r] = -INFINITY;
+            }
             float tmax = -INFINITY;
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
-                    const float sc = (key <= qrow && key < S) ? sacc[b][r] * a.scale2 : -INFINITY;
-                    sacc[b][r] = sc;
-                    tmax = fmaxf(tmax, sc);
-                }
+                for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[b][r]);
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float mn = fmaxf(m, tmax);
-            const float corr = fexp2(m - mn);
+            // running max m in raw score units, raised lazily: only when a score exceeds it by more
+            // than 8 / scale2 (then the weights exp2((s - m) scale2) stay below 2^8); the rescale of
+            // the accumulators runs when any lane of the wave raises its max.  O / l does not depend
+            // on m.
+            const bool raise = tmax > m + kLazy / a.scale2;
+            if (__builtin_amdgcn_ballot_w64(raise)) {
+                const float mn = raise ? tmax : m;
+                const float corr = raise ? fexp2((m - mn) * a.scale2) : 1.f;
+                l *= corr;
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) oacc[b][r] *= corr;
+                m = mn;
+            }
+            const float mc = m * a.scale2;
             float psum = 0.f;
-            // P^T as B fragments: key step j (16 keys) = block j / 2, registers 8 (j % 2) .. + 7
+            // P^T as B fragments: key step j (16 keys) = block j / 2, registers 8 (j % 2) .. + 7, each
+            // weight in two bf16 parts: hi = bf16(p), lo = bf16(p - hi)
             bf16x8 phi[4], plo[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float hi8[8], lo8[8];
+                uint32_t hw[4], lw[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float p = fexp2(sacc[j >> 1][8 * (j & 1) + e] - mn);
-                    psum += p;
-                    const float ph = bf16_to_f32(f32_to_bf16_rne(p));
-                    hi8[e] = ph;
-                    lo8[e] = p - ph;
+                for (int e = 0; e < 8; e += 2) {
+                    const float p0 = fexp2(__builtin_fmaf(sacc[j >> 1][8 * (j & 1) + e], a.scale2, -mc));
+                    const float p1 = fexp2(__builtin_fmaf(sacc[j >> 1][8 * (j & 1) + e + 1], a.scale2, -mc));
+                    psum += p0;
+                    psum += p1;
+                    const uint32_t w = pack_bf16(p0, p1);
+                    hw[e >> 1] = w;
+                    lw[e >> 1] = pack_bf16(p0 - __uint_as_float(w << 16), p1 - __uint_as_float(w & 0xffff0000u));
                 }
-                phi[j] = __builtin_bit_cast(bf16x8, uint4{pack_bf16(hi8[0], hi8[1]), pack_bf16(hi8[2], hi8[3]),
-                                                          pack_bf16(hi8[4], hi8[5]), pack_bf16(hi8[6], hi8[7])});
-                plo[j] = __builtin_bit_cast(bf16x8, uint4{pack_bf16(lo8[0], lo8[1]), pack_bf16(lo8[2], lo8[3]),
-                                                          pack_bf16(lo8[4], lo8[5]), pack_bf16(lo8[6], lo8[7])});
+                phi[j] = __builtin_bit_cast(bf16x8, uint4{hw[0], hw[1], hw[2], hw[3]});
+                plo[j] = __builtin_bit_cast(bf16x8, uint4{lw[0], lw[1], lw[2], lw[3]});
             }
             psum += __shfl_xor(psum, 32);
-            l = l * corr + psum;
-            m = mn;
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[b][r] *= corr;
+            l += psum;
             // O^T += V^T . P^T: the V^T operand of key step j, lane half h: keys 16 j + 4 h + {0..3}
-            // and 16 j + 8 + 4 h + {0..3}, i.e. the h-th 8 bytes of chunks 2 j and 2 j + 1
+            // and 16 j + 8 + 4 h + {0..3}, which the layout kernel stores as chunk 2 j + h of the row
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
                     const int d = 32 * b + l32;
-                    const uint2 v0 = *reinterpret_cast<const uint2*>(st + kKBytes + v_off(d, 2 * j) + 8 * h);
-                    const uint2 v1 = *reinterpret_cast<const uint2*>(st + kKBytes + v_off(d, 2 * j + 1) + 8 * h);
-                    const bf16x8 vf = __builtin_bit_cast(bf16x8, uint4{v0.x, v0.y, v1.x, v1.y});
+                    const bf16x8 vf = *reinterpret_cast<const bf16x8*>(st + kKBytes + v_off(d, 2 * j + h));
                     oacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, phi[j], oacc[b], 0, 0, 0);
                     oacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, plo[j], oacc[b], 0, 0, 0);
                 }
@@ -245,15 +265,22 @@ __global__ __launch_bounds__(256) void kv_layout_kernel(const uint16_t* __restri
         }
     }
     __syncthreads();
-    // V^T rows: 128 dims x 8 chunks of 8 positions
+    // V^T rows: 128 dims x 8 chunks of 8 slots.  Within each group of 16 positions the slots hold
+    // the positions in the order 0-3, 8-11, 4-7, 12-15 (slot 4 b + c holds position 4 perm(b) + c,
+    // perm = 0, 2, 1, 3), the key order of the attention kernel's P operand: chunk 2 j + h is then
+    // exactly the 8 keys lane half h multiplies in key step j.
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int i = tid + 256 * u;
         const int d = i >> 3, c = i & 7;
         uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            w[e] = (uint32_t)tile[8 * c + 2 * e][d] | ((uint32_t)tile[8 * c + 2 * e + 1][d] << 16);
+        for (int e = 0; e < 4; ++e) {
+            const int slot = 8 * c + 2 * e;                     // even: slots slot, slot + 1 share b
+            const int bq = (slot >> 2) & 3;
+            const int key = (slot & ~15) + 4 * ((bq == 1 || bq == 2) ? 3 - bq : bq) + (slot & 3);
+            w[e] = (uint32_t)tile[key][d] | ((uint32_t)tile[key + 1][d] << 16);
+        }
         *reinterpret_cast<uint4*>(vt + ((int64_t)kvh * kD + d) * ldvt + p0 + 8 * c) = uint4{w[0], w[1], w[2], w[3]};
     }
 }
@@ -289,7 +316,7 @@ hipError_t launch_sdpa_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k
     a.H_KV = H_KV;
     a.qtiles = (S + kBQ - 1) / kBQ;
     a.scale2 = 1.4426950408889634f / sqrtf((float)kD);
-    hipLaunchKernelGGL(sdpa_prefill_kernel, dim3(a.qtiles, H), dim3(256), 2 * kStage, stream, a);
+    hipLaunchKernelGGL(sdpa_prefill_kernel, dim3(a.qtiles * H), dim3(256), 2 * kStage, stream, a);
     return hipGetLastError();
 }
 
