@@ -457,6 +457,7 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "gemm.splits")) t.gemm_splits = value;
     else if (!std::strcmp(knob, "gemm.short")) t.gemm_short = value;
     else if (!std::strcmp(knob, "gemm.sk_cap")) t.gemm_sk_cap = value;
+    else if (!std::strcmp(knob, "gemm.bm")) t.gemm_bm = value;
     else if (!std::strcmp(knob, "s16")) t.s16 = value;
     else if (!std::strcmp(knob, "s16.r")) t.s16_r = value;
     else if (!std::strcmp(knob, "s16.w")) t.s16_w = value;

@@ -499,9 +499,14 @@ __device__ __forceinline__ void tile_coords(int seq, int tiles_m, int tiles_n, i
     tm = r0 + (loc - tn * h);
 }
 
-template <bool SK, bool GROUPED>
+template <bool SK, bool GROUPED, int BM = 256>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmArgs a) {
-    constexpr int NT = 256, BK = kBK, W_STAGE = 256 * 64, TN = 4, TM = 4;
+    // BM = 256: 256 x 256 tiles, each wave 128 x 128 (TM = 4 blocks of 32 x rows); BM = 128:
+    // 128 x 256 tiles, each wave 64 x 128 (TM = 2), data-parallel only
+    static_assert(BM == 256 || (BM == 128 && !SK), "tile rows");
+    constexpr int NT = 256, BK = kBK, W_STAGE = 256 * 64, TN = 4, TM = BM / 64;
+    constexpr int XI = BM / 32;                     // x DMA instructions per wave and k tile
+    constexpr int STAGE = W_STAGE + BM * 128;       // bytes per LDS stage
     __shared__ int sk_up;                           // stream-K: the flag the finisher waited for came
     typedef __attribute__((address_space(3))) void lds_void;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_u16[];      // one name for the dynamic LDS
@@ -576,7 +581,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         // rows (4 i + wave) * 16 + lane / 4, LDS chunk lane % 4; x instruction i: rows
         // (4 i + wave) * 8 + lane / 8, LDS chunk lane % 8.  Rows past M or gN are clamped (their
         // results are not stored).
-        uint32_t woff[4], xoff[8];
+        uint32_t woff[4], xoff[XI];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = (4 * i + wave) * 16 + (lane >> 2);
@@ -584,14 +589,14 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
             woff[i] = (uint32_t)(min(n0 + r, gN - 1) * gldw + 16 * q);
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < XI; ++i) {
             const int r = (4 * i + wave) * 8 + (lane >> 3);
             xoff[i] = (uint32_t)((min(m0 + r, M - 1) * a.ldx + 8 * swz(r, lane & 7)) * 2);
         }
         // LDS byte addresses of the stage being read, the next one and the one being filled
         // (rotated every k tile)
-        uint32_t s_cur = lds0, s_nxt = lds0 + kDmaStage, s_dma = lds0 + 2 * kDmaStage;
-        // DMA part 0: the W tile; parts 1, 2: the two halves of the x tile
+        uint32_t s_cur = lds0, s_nxt = lds0 + STAGE, s_dma = lds0 + 2 * STAGE;
+        // DMA part 0: the W tile; parts 1 (, 2): the x tile (in halves at BM = 256)
         auto dma_to = [&](uint32_t base, int kt, int part, int k) {
             if (part == 0) {
                 dma16(gW + (int64_t)kt * BK, woff[k], base + (4 * k + wave) * 16 * 64);
@@ -604,7 +609,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         auto rd_x = [&](uint32_t sb, int s, int j) -> bf16x8 {
             const uint8_t* base = lds + (sb - lds0) + W_STAGE;
             const int c = 4 * (s >> 1) + 2 * h + (s & 1);
-            const int r = wm * 128 + j * 32 + l32;
+            const int r = wm * (BM / 2) + j * 32 + l32;
             return *reinterpret_cast<const bf16x8*>(base + r * 128 + swz(r, c) * 16);
         };
         auto rd_w = [&](uint32_t sb, int jp, int i) -> uint4 {
@@ -620,32 +625,33 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                                      : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false);
             cf[i][e] = __builtin_bit_cast(uint32_t, v);
         };
-        auto mf = [&](const u32x4 (&cf)[4], const bf16x8 (&xf)[4], int q) {
-            const int i = q >> 2, j = q & 3;
+        auto mf = [&](const u32x4 (&cf)[4], const bf16x8 (&xf)[TM], int q) {
+            const int i = q / TM, j = q % TM;
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, cf[i]), xf[j], acc[i][j], 0, 0, 0);
         };
 
+        constexpr int NP = 1 + BM / 128;            // DMA parts per k tile (4 instructions each)
 #pragma unroll
-        for (int p = 0; p < 3; ++p)
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
             for (int k = 0; k < 4; ++k) dma_to(s_cur, kb, p, k);
         if (kb + 1 < ke) {
 #pragma unroll
-            for (int p = 0; p < 3; ++p)
+            for (int p = 0; p < NP; ++p)
 #pragma unroll
                 for (int k = 0; k < 4; ++k) dma_to(s_nxt, kb + 1, p, k);
-            asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+            if constexpr (BM == 256) asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
         } else {
             asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
         }
         uint4 wr0[4], wr1[4];
-        bf16x8 xa[4], xb[4];
+        bf16x8 xa[TM], xb[TM];
         u32x4 cA[4], cB[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            wr0[i] = rd_w(s_cur, 0, i);
-            xa[i] = rd_x(s_cur, 0, i);
-        }
+        for (int i = 0; i < 4; ++i) wr0[i] = rd_w(s_cur, 0, i);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) xa[j] = rd_x(s_cur, 0, j);
 #pragma unroll
         for (int c = 0; c < 16; ++c) cvt1(wr0, 0, c, cA);
 
@@ -655,6 +661,61 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
             constexpr bool pf = decltype(pf_tag)::value;   // issue the DMA of k tile kt + 2
             const uint32_t st = s_cur, nst = s_nxt;
             const bool more = pf || kt + 1 < ke;
+            if constexpr (BM == 128) {
+                // 128 x 256 tiles: 8 MFMAs per k step (q: W block q / 2, x block q % 2), two
+                // conversions per MFMA, the x and W reads of the next steps in the first slots,
+                // DMA parts 0 (W) and 1 (x) in steps 0 and 1.  The next tile's step-0 operands
+                // are read after the barrier of step 3; cA[0] is converted there and cA[1 .. 3]
+                // in step 0, two slots ahead of their MFMAs.
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    mf(cA, xa, q);
+                    if (q < 2) xb[q] = rd_x(st, 1, q);
+                    else if (q < 6) wr1[q - 2] = rd_w(st, 1, q - 2);
+                    if (pf && (q & 1)) dma_to(s_dma, kt + 2, 0, q >> 1);
+                    cvt1(wr0, 1, 2 * q, cB);
+                    cvt1(wr0, 1, 2 * q + 1, cB);
+                    if (q < 6) {
+                        cvt1(wr0, 0, 4 + 2 * q, cA);
+                        cvt1(wr0, 0, 5 + 2 * q, cA);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    mf(cB, xb, q);
+                    if (q < 2) xa[q] = rd_x(st, 2, q);
+                    if (pf && (q & 1)) dma_to(s_dma, kt + 2, 1, q >> 1);
+                    cvt1(wr1, 0, 2 * q, cA);
+                    cvt1(wr1, 0, 2 * q + 1, cA);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    mf(cA, xa, q);
+                    if (q < 2) xb[q] = rd_x(st, 3, q);
+                    cvt1(wr1, 1, 2 * q, cB);
+                    cvt1(wr1, 1, 2 * q + 1, cB);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    mf(cB, xb, q);
+                    if (more) {
+                        if (q == 1) {
+                            if (pf) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                        }
+                        if (q >= 2 && q < 6) wr0[q - 2] = rd_w(nst, 0, q - 2);
+                        else if (q >= 6) xa[q - 6] = rd_x(nst, 0, q - 6);
+                        if (q >= 6) {
+                            cvt1(wr0, 0, 2 * (q - 6), cA);
+                            cvt1(wr0, 0, 2 * (q - 6) + 1, cA);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
             // k step 0: MFMAs (cA, xa); reads x step 1 -> xb, W pair 1 -> wr1; DMA part 0;
             // cB <- wr0 half 1
 #pragma unroll
@@ -704,6 +765,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
+            }
             }
             const uint32_t t = s_cur;
             s_cur = s_nxt;
@@ -760,7 +822,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
                 const float* sg = sc[i % SB][gq];
 #pragma unroll
                 for (int j = 0; j < TM; ++j) {
-                    const int ml = wm * 128 + j * 32 + l32;
+                    const int ml = wm * (BM / 2) + j * 32 + l32;
                     const uint32_t lo = pack_bf16(acc[i][j][4 * gq + 0] * sg[0], acc[i][j][4 * gq + 1] * sg[1]);
                     const uint32_t hi = pack_bf16(acc[i][j][4 * gq + 2] * sg[2], acc[i][j][4 * gq + 3] * sg[3]);
                     *reinterpret_cast<uint2*>(lds + ml * PITCH + nl * 2) = uint2{lo, hi};
@@ -772,11 +834,11 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         // eight passes per batch: the batch's LDS reads are issued before its stores
         const int c8 = (tid & 31) * 8;
         const int n = n0 + c8;
-        const int rows = min(256, M - m0);
+        const int rows = min(BM, M - m0);
         const bool full = gv16 && (inner || n + 7 < gN);
         const bool res16 = gepi == kEpiResidual && full && gv16r;
 #pragma unroll
-        for (int batch = 0; batch < 4; ++batch) {
+        for (int batch = 0; batch < BM / 64; ++batch) {
             uint32_t w[8][4];
 #pragma unroll
             for (int p = 0; p < 8; ++p) {
@@ -841,7 +903,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_w8a16_dma_kernel(const GemmAr
         if (local >= a.per_xcd || tile >= a.tiles_m * a.tiles_n) return;   // uniform
         int tm, tn;
         tile_coords(tile, a.tiles_m, a.tiles_n, a.gh, tm, tn);
-        m0 = tm * 256;
+        m0 = tm * BM;
         select(tn);
         zero_acc();
         run(0, KT);
@@ -1061,6 +1123,7 @@ bool dma_supported(const uint16_t* x, int64_t ldx, const uint8_t* W, int64_t ldw
 hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g, int ng, int M, int K,
                              hipStream_t stream, void* ws, size_t ws_bytes) {
     constexpr int lds = kDmaStages * kDmaStage;
+    constexpr int lds128 = kDmaStages * (256 * 64 + 128 * 128);
     static const hipError_t attr = [] {
         hipError_t e = hipSuccess;
         for (const void* k : {reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<false, false>),
@@ -1068,6 +1131,9 @@ hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g,
                               reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<false, true>),
                               reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<true, true>)})
             if (e == hipSuccess) e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        for (const void* k : {reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<false, false, 128>),
+                              reinterpret_cast<const void*>(&gemm_fp8_w8a16_dma_kernel<false, true, 128>)})
+            if (e == hipSuccess) e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds128);
         return e;
     }();
     if (attr != hipSuccess) return attr;
@@ -1096,6 +1162,23 @@ hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g,
     a.per_xcd = (T + 7) / 8;
     const int G = device_info().num_cu;             // one 144 KiB workgroup per CU
     const int gh_knob = tuning().gemm_gh;
+    // Where the 256 x 256 tiles cover at most half of the CUs, 128 x 256 tiles (at most twice as
+    // many, one round) give each workgroup a whole tile with the same MFMA work as half a tile
+    // of the stream-K form, without its partial-tile exchange (tuning knob gemm.bm: 128 forces
+    // them, 256 forbids them; gemm.sk = 1 keeps stream-K).  Measured on MI355X (same box):
+    // down_proj at M = 2048 (208 tiles of 128 x 256) 146.3 against 168.8 us in stream-K form;
+    // attention block at S = 2048 250 against 296 us; Mamba block at S = 512 336 against 376 us.
+    const int bm_knob = tuning().gemm_bm;
+    if (bm_knob != 256 && tuning().gemm_sk != 1 && (bm_knob == 128 || 2 * (int64_t)T <= G)) {
+        const auto kernel128 =
+            grouped ? &gemm_fp8_w8a16_dma_kernel<false, true, 128> : &gemm_fp8_w8a16_dma_kernel<false, false, 128>;
+        a.tiles_m = (M + 127) / 128;
+        const int T128 = a.tiles_m * a.tiles_n;
+        a.per_xcd = (T128 + 7) / 8;
+        a.gh = gh_knob > 0 ? std::min(gh_knob, a.tiles_m) : a.tiles_m;
+        hipLaunchKernelGGL(kernel128, dim3(8 * a.per_xcd), dim3(256), lds128, stream, a);
+        return hipGetLastError();
+    }
     const bool fits = ws && ws_bytes >= kSkFlagBytes + (size_t)G * kDmaPartialBytes && G % 8 == 0 &&
                       G * 4 <= (int)kSkFlagBytes && (int64_t)T * (K / kBK) < ((int64_t)1 << 31);
     const int knob = tuning().gemm_sk;

@@ -56,6 +56,7 @@ struct Tuning {
     int gemv_balance = 0;  // M = 1 stream GEMV (single launches): 2 turns off the grid sizing that makes row groups divide evenly
     int gemm_splits = 0;   // short-prompt GEMM (17 <= M < 512): workgroups splitting K (0: automatic)
     int gemm_short = 0;    // short-prompt GEMM: f + 1 forces kernel form f (0..7, gemm_short.hip)
+    int gemm_bm = 0;       // DMA-fed GEMM tile rows: 0 automatic (128 where 256-row tiles cover at most half the CUs), 128, 256
     int gemm_sk_cap = 0;   // GEMM stream-K: at most this many workgroups per tile (0: 2; -1: one per CU)
     int gemm_gh = 0;       // DMA-fed GEMM: row bands per group of the tile order (0: all of them, stream-K: 1)
     int s16 = 0;           // 16x16x32 skinny kernel: 0 automatic (M >= 3), 1 for 2 <= M <= 16, 2 never

@@ -84,7 +84,7 @@ def _dev_weights(W):
 
 def _composed(xd, dw, S):
     nw, qw, qs, kw, ks, vw, vs, ow, os_ = dw
-    ws = True          # as the block: its linears get their partials / split / stream-K workspace
+    ws = True          # as the block: its linears get their split-K / stream-K workspace
     h = ops.rmsnorm_bf16(xd, nw, EPS)
     # q | k | v as the block runs them: one grouped dispatch (one launch at S >= 512)
     q, k, v = ops.linear_fp8_w8a16_grouped(h, [(qw, qs), (kw, ks), (vw, vs)], use_workspace=ws)

@@ -237,6 +237,7 @@ def _sk_reset():
     yield
     _lib.tuning_set("gemm.sk", 0)
     _lib.tuning_set("gemm.tile", 0)
+    _lib.tuning_set("gemm.bm", 0)
 
 
 def _gemm_ws(M, N, K):
@@ -277,9 +278,9 @@ def test_stream_k_forced_on_small_problems(_sk_reset):
 
 def test_stream_k_large_matches_oracle_and_replays_in_a_graph(_sk_reset):
     """M = 1536 on up_proj's shape (294 tiles of 256 x 256 for 256 CUs: two rounds, the second
-    15% full) in stream-K form.  The result matches the oracle and the data-parallel kernel
-    within the parity gate; replays of a captured graph (with eager work between them) equal
-    the eager call."""
+    15% full) in stream-K form (forced), and in 128 x 256 tiles (forced: 588 tiles, three
+    rounds).  The results match the oracle and the data-parallel kernel within the parity gate;
+    replays of a captured graph (with eager work between them) equal the eager call."""
     M, N, K = 1536, 12544, 3136
     announce("stream_k_large", M, N, K)
     x, w, s = _case(M, N, K, 99)
@@ -288,7 +289,10 @@ def test_stream_k_large_matches_oracle_and_replays_in_a_graph(_sk_reset):
     y_dp = ops.gemm_fp8_w8a16(xd, wd, sd)
     ref = oracle_bits(x, w, s)
     assert_parity(bits(y_dp), ref, "data parallel")
-    _lib.tuning_set("gemm.sk", 0)
+    _lib.tuning_set("gemm.bm", 128)
+    assert_parity(bits(ops.gemm_fp8_w8a16(xd, wd, sd)), ref, "128 x 256 tiles")
+    _lib.tuning_set("gemm.bm", 0)
+    _lib.tuning_set("gemm.sk", 1)
     y = ops.gemm_fp8_w8a16(xd, wd, sd)                      # DMA kernel, stream-K form
     assert_parity(bits(y), ref, "stream-K")
     out = torch.empty_like(y)
@@ -307,12 +311,14 @@ def test_stream_k_large_matches_oracle_and_replays_in_a_graph(_sk_reset):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("sk", [0, 2], ids=["stream_k", "data_parallel"])
+@pytest.mark.parametrize("sk", [0, 1, 2], ids=["auto", "stream_k", "data_parallel"])
 def test_dma_kernel_forms(sk, _sk_reset):
-    """The DMA-fed 256 x 256 kernel (tile 24) in both forms on ragged M and N: one, two and three
-    64-wide k tiles (the pipeline's prologue and two-tile tail without the steady loop), few
-    tiles cut between many workgroups (stream-K: some hold no k tile at all), and long K.
-    Repeated calls are bit-identical and leave the flag region zero."""
+    """The DMA-fed kernel (tile 24) in its forms on ragged M and N: automatic (128 x 256 tiles
+    where 256 x 256 tiles cover at most half of the CUs, as in most of these cases), stream-K
+    (forced) and 256 x 256 one tile per workgroup; one, two and three 64-wide k tiles (the
+    pipeline's prologue and two-tile tail without the steady loop), few tiles cut between many
+    workgroups (stream-K: some hold no k tile at all), and long K.  Repeated calls are
+    bit-identical and leave the flag region zero."""
     _lib.tuning_set("gemm.tile", 24)
     _lib.tuning_set("gemm.sk", sk)
     for M, N, K in [(513, 777, 64), (700, 1000, 128), (300, 520, 192), (1030, 2100, 1024),
@@ -332,9 +338,9 @@ def test_dma_kernel_forms(sk, _sk_reset):
 
 
 def test_dma_kernel_forms_agree_on_config3(_sk_reset):
-    """Stream-K and data-parallel forms of the DMA kernel on down_proj's shape (104 tiles, K =
-    12544: tiles cut between two or three workgroups) agree within the parity gate, and both
-    match the oracle."""
+    """The forms of the DMA kernel on down_proj's shape -- 128 x 256 tiles (the default here: 208
+    tiles), stream-K (104 tiles of 256 x 256 cut between two workgroups) and 256 x 256 one tile
+    per workgroup -- agree within the parity gate, and all match the oracle."""
     M, N, K = 2048, 3136, 12544
     announce("dma_forms_config3", M, N, K)
     x, w, s = _case(M, N, K, 4321, outlier_frac=0.001)
@@ -342,11 +348,15 @@ def test_dma_kernel_forms_agree_on_config3(_sk_reset):
     ref = oracle_bits(x, w, s)
     _lib.tuning_set("gemm.sk", 2)
     y_dp = ops.gemm_fp8_w8a16(xd, wd, sd)
-    _lib.tuning_set("gemm.sk", 0)
+    _lib.tuning_set("gemm.sk", 1)
     y_sk = ops.gemm_fp8_w8a16(xd, wd, sd)
+    _lib.tuning_set("gemm.sk", 0)
+    y_128 = ops.gemm_fp8_w8a16(xd, wd, sd)
     assert_parity(bits(y_dp), ref, "dma data parallel")
     assert_parity(bits(y_sk), ref, "dma stream-K")
+    assert_parity(bits(y_128), ref, "dma 128 x 256 tiles")
     assert_parity(bits(y_sk), bits(y_dp), "stream-K vs data parallel")
+    assert np.array_equal(bits(y_128), bits(y_dp)), "128 x 256 and 256 x 256 tiles sum in the same order"
 
 
 @pytest.fixture
@@ -363,6 +373,7 @@ def test_stream_k_workgroups_per_tile_cap(cap, _cap_reset):
     down_proj's shape and few ragged tiles: within the parity gate of the oracle, repeated calls
     bit-identical, the flag region left zero."""
     _lib.tuning_set("gemm.sk_cap", cap)
+    _lib.tuning_set("gemm.sk", 1)
     for M, N, K in [(2048, 3136, 12544), (640, 1000, 1024)]:
         announce("stream_k_cap", cap, M, N, K)
         x, w, s = _case(M, N, K, 31 * cap + M + N, scales="log_uniform", act="relu2")
@@ -384,9 +395,11 @@ def test_grouped_prefill_is_one_launch_of_the_dma_kernel(M, Ns, K, _sk_reset):
     """Matrices sharing x at M >= 512 (q|k|v at prefill) run as one launch of the DMA-fed kernel,
     their column bands one after another in the launch's tile numbering.  The outputs go to
     column views of one [M, sum N] buffer (the attention block's layout), ragged N in each
-    group.  In the data-parallel form (each tile one workgroup over all of K) every group equals
-    its separate call bit for bit; in the default form (stream-K where the tiles are few) each
-    matches the oracle within the parity gate; the flag region is left zero."""
+    group.  In the data-parallel forms (each tile one workgroup over all of K, 256 or 128 rows:
+    both sum each output over the same k order) every group equals its separate call bit for
+    bit, also where the grouped launch and a separate call choose different tile rows; in the
+    stream-K form (forced) each matches the oracle within the parity gate; the flag region is
+    left zero."""
     announce("grouped_prefill", M, Ns, K)
     cases = [_case(M, N, K, 17 * i + M + N, scales="log_uniform") for i, N in enumerate(Ns)]
     x = cases[0][0]
@@ -401,7 +414,7 @@ def test_grouped_prefill_is_one_launch_of_the_dma_kernel(M, Ns, K, _sk_reset):
     arr = (_lib.LinearGroup * len(Ns))()
     for i, ((w, s), y) in enumerate(zip(wd, outs)):
         arr[i] = _lib.LinearGroup(w.data_ptr(), w.stride(0), s.data_ptr(), y.data_ptr(), y.stride(0), w.shape[0])
-    for sk in (2, 0):
+    for sk in (2, 0, 1):
         _lib.tuning_set("gemm.sk", sk)
         _lib.check(L.nmi_linear_fp8_w8a16_grouped(xd.data_ptr(), K, M, K, arr, len(Ns), ws.data_ptr(), ws.numel(),
                                                   None), "grouped (column views)")
@@ -410,7 +423,7 @@ def test_grouped_prefill_is_one_launch_of_the_dma_kernel(M, Ns, K, _sk_reset):
         assert torch.all(ybig[:, total:] == 3.0)
         assert torch.count_nonzero(ws[:64 * 1024]) == 0, "flag region not re-armed"
         for i, ((_, w, s), yg, ys) in enumerate(zip(cases, outs, separate)):
-            if sk == 2:
+            if sk != 1:
                 assert np.array_equal(bits(yg), bits(ys)), f"group {i} sk={sk}"
             assert_parity(bits(yg), oracle_bits(x, w, s), f"grouped {i} sk={sk} N={Ns[i]}", per_row_scales=True)
 
@@ -421,10 +434,12 @@ def _late_flag_call(xd, wd, sd, y, ws):
     its bound and every kernel exits.  The call itself returns NMI_OK: the error is asynchronous."""
     _lib.tuning_set("gemm.sk_spin", 64)
     _lib.tuning_set("gemm.sk_lostflag", 1)
+    _lib.tuning_set("gemm.sk", 1)
     try:
         _gemm_call(xd, wd, sd, y, ws)
         torch.cuda.synchronize()
     finally:
+        _lib.tuning_set("gemm.sk", 0)
         _lib.tuning_set("gemm.sk_lostflag", 0)
         _lib.tuning_set("gemm.sk_spin", 0)
 

@@ -121,8 +121,8 @@ def test_mamba_forward_scan_output_matches_oracle():
 
 def test_mamba_forward_two_sequences_past_512_rows():
     """batch = 2 sequences of 300 tokens: 600 rows, so the projections run the M >= 512 GEMM (the
-    out_proj's 39 tiles on stream-K, its flags cleared by the block, the workspace sized for the
-    Mamba shapes) while each sequence alone (300 rows) would not.  Per sequence against the oracle
+    out_proj in 128 x 256 tiles, the workspace sized for the Mamba shapes) while each sequence
+    alone (300 rows) would not.  Per sequence against the oracle
     on the GPU's own in_proj output: conv state bit-exact, SSM state within the state bar, output
     end to end rel_l2 <= 4e-3."""
     announce("mamba_forward_two_sequences_600_rows")

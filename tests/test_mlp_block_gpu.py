@@ -75,9 +75,9 @@ def _dev(nw, upw, ups, dnw, dns):
 
 def _composed(x, nw, upw, ups, dnw, dns, ws=True):
     # The block hands its linears a workspace -- the short-prompt kernel's K split for
-    # 17 <= M < 512, stream-K for the few tiles of the down projection from M = 512 (the other
-    # kernels ignore it); the composition does the same, so that both run the same kernels in the
-    # same form (same float32 summation order).
+    # 17 <= M < 512, the stream-K form where it is forced (the other kernels ignore it); the
+    # composition does the same, so that both run the same kernels in the same form (same
+    # float32 summation order).
     h = ops.rmsnorm_bf16(x, nw, EPS)
     up = ops.linear_fp8_w8a16(h, upw, ups, use_workspace=ws)
     r = torch.relu(up)
@@ -179,6 +179,8 @@ def test_block_matches_oracle(M):
     ({"gemv.xg": 1}, [1]),                           # the fused form always stages x in LDS
     ({"gemm.tile": 20}, [600]),
     ({"gemm.tile": 21}, [600]),
+    ({"gemm.bm": 128}, [520]),                       # 128 x 256 tiles for both projections
+    ({"gemm.sk": 1}, [520]),                         # stream-K form of the 256 x 256 kernel
 ])
 def test_block_equals_composition_under_knobs(knobs, Ms):
     dev = _dev(*_weights(HIDDEN, INTER))
