@@ -143,6 +143,21 @@ def make_step(ops, xs, mats, ys, ws_use=True):
     return step
 
 
+def make_batch_step(ops, xs, mats, ys):
+    """The same step as one nmi_linear_fp8_w8a16_batch call: six jobs (q, k and v on the one
+    attention activation, o, up and down on their own), one launch of the skinny kernel."""
+    (wq, sq), (wk, sk), (wv, sv), (wo, so), (wu, su), (wd, sd) = mats
+    x_attn, x_o, x_up, x_down = xs
+    y_qkv, y_o, y_up, y_down = ys
+    jobs = [(x_attn, wq, sq), (x_attn, wk, sk), (x_attn, wv, sv), (x_o, wo, so), (x_up, wu, su), (x_down, wd, sd)]
+    outs = list(y_qkv) + [y_o, y_up, y_down]
+
+    def step():
+        ops.linear_fp8_w8a16_batch(jobs, outs=outs)
+
+    return step
+
+
 def step_buffers(dev, M, K_attn=3136):
     import torch
 
@@ -343,21 +358,27 @@ def bench_skinny(dev, reps=20):
     for M in synth.SKINNY_M:
         xs = tuple(synth.make_act(M, L[i].K, 2200 + M + i, dev, kind=L[i].act) for i in (0, 3, 4, 5))
         ys = step_buffers(dev, M)
-        steps = [make_step(ops, xs, copies[r], ys) for r in range(R)]
-        for s in steps:
-            s()
-        torch.cuda.synchronize()
-        g = T.capture(lambda: [s() for s in steps])
-        T.time_replays([g])
-        n = max(1, reps // R)
-        ms = T.time_replays([g] * n) / (n * R)
         b = sum(synth.linear_bytes(M, l.N, l.K) for l in L)
         f = sum(synth.linear_flops(M, l.N, l.K) for l in L)
-        res[f"M={M}"] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+        rec = {}
+        for form, make in (("four_launches", make_step), ("batch_one_launch", make_batch_step)):
+            steps = [make(ops, xs, copies[r], ys) for r in range(R)]
+            for s in steps:
+                s()
+            torch.cuda.synchronize()
+            g = T.capture(lambda: [s() for s in steps])
+            T.time_replays([g])
+            n = max(1, reps // R)
+            ms = T.time_replays([g] * n) / (n * R)
+            rec[form] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                          "TFLOP/s": round(f / (ms * 1e-3) / 1e12, 2)}
-        del g, steps
+            del g, steps
+        res[f"M={M}"] = dict(rec["four_launches"], batch_one_launch=rec["batch_one_launch"])
     del copies
-    return {"workload": "config2_skinny_decode_set", "launches_per_step": 4, "results": res}
+    return {"workload": "config2_skinny_decode_set", "launches_per_step": 4,
+            "note": "per-M figures: q|k|v grouped, o, up, down as four launches (the engine's form); "
+                    "batch_one_launch: the six linears as one nmi_linear_fp8_w8a16_batch launch",
+            "results": res}
 
 
 def bench_decode_stream(args, dev):

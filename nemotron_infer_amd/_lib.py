@@ -57,6 +57,7 @@ SIGNATURES = {
     "nmi_alloc_stats": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
     "nmi_sync": ([], _i),
     "nmi_async_status": ([], _i),
+    "nmi_linear_fp8_w8a16_batch": ([_vp, _i, _i, _vp], _i),
     "nmi_gemv_chain_create": ([_vp, _i, ctypes.POINTER(_vp)], _i),
     "nmi_gemv_chain_workspace_bytes": ([_i], _sz),
     "nmi_gemv_chain_launch": ([_vp, _vp, _sz, _vp], _i),
@@ -70,6 +71,14 @@ class LinearGroup(ctypes.Structure):
     """nmi_linear_group of include/nmi_fp8_linear.h."""
     _fields_ = [("w_e4m3", _vp), ("ldw", _i64), ("w_scale", _vp), ("y_bf16", _vp), ("ldy", _i64),
                 ("N", _i)]
+
+
+MAX_BATCH = 8
+
+
+class LinearJob(ctypes.Structure):
+    """nmi_linear_job of include/nmi_fp8_linear.h."""
+    _fields_ = [("x_bf16", _vp), ("ldx", _i64), ("K", _i), ("w", LinearGroup)]
 
 
 class GemvPhase(ctypes.Structure):

@@ -274,6 +274,41 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
                     static_cast<hipStream_t>(stream), fn);
 }
 
+int nmi_linear_fp8_w8a16_batch(const nmi_linear_job* jobs, int njobs, int M, void* stream) {
+    const char* fn = "nmi_linear_fp8_w8a16_batch";
+    static_assert(NMI_MAX_BATCH <= kS16MaxBatch, "batch size");
+    if (!jobs || njobs < 1 || njobs > NMI_MAX_BATCH)
+        return fail(NMI_ERR_INVALID_ARG, "%s: njobs=%d must be in [1, %d]", fn, njobs, NMI_MAX_BATCH);
+    if (take_async_error(fn)) return NMI_ERR_ASYNC;
+    GemvGroup g[NMI_MAX_BATCH];
+    const uint16_t* xs[NMI_MAX_BATCH];
+    int64_t ldxs[NMI_MAX_BATCH];
+    int Ks[NMI_MAX_BATCH];
+    int64_t rows = 0;
+    for (int i = 0; i < njobs; ++i) {
+        const nmi_linear_job& J = jobs[i];
+        const nmi_linear_group& G = J.w;
+        int rc = check_linear(J.x_bf16, J.ldx, G.w_e4m3, G.ldw, G.w_scale, G.y_bf16, G.ldy, M, G.N, J.K, fn);
+        if (rc) return rc;
+        rows += G.N;
+        g[i] = GemvGroup{static_cast<const uint8_t*>(G.w_e4m3), G.ldw, G.w_scale,
+                         static_cast<uint16_t*>(G.y_bf16), G.ldy, G.N, 0, 0, Epi{}};
+        xs[i] = static_cast<const uint16_t*>(J.x_bf16);
+        ldxs[i] = J.ldx;
+        Ks[i] = J.K;
+    }
+    if (rows > (int64_t)1 << 30) return fail(NMI_ERR_INVALID_ARG, "%s: too many rows in total", fn);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipSuccess;
+    if (M >= 2 && M <= 16 && launch_skinny16_batch(xs, ldxs, Ks, g, njobs, M, st, &e))
+        return hip_status(e, fn);
+    for (int i = 0; i < njobs; ++i) {
+        const int rc = dispatch(xs[i], ldxs[i], M, Ks[i], &g[i], 1, nullptr, 0, st, fn);
+        if (rc) return rc;
+    }
+    return NMI_OK;
+}
+
 // GEMV chain: the planned phase table and per-wave step counts live in device memory for the
 // handle's lifetime; one launch per segment (a run of phases up to the next one that waits).  A
 // segment of one phase (every phase of a fully dependent chain) is launched as the single GEMV

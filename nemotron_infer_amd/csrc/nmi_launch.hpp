@@ -114,6 +114,12 @@ hipError_t launch_skinny4_grouped(const uint16_t* x, int64_t ldx, int M, int K, 
 bool skinny16_wanted(int M, int K);
 bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
                              hipStream_t stream, hipError_t* err);
+// Independent linears in one launch of the same kernel: matrix i (groups[i]) times its own
+// activations xs[i] [M, Ks[i]] (row stride ldxs[i]); at most kS16MaxBatch of them.  Returns
+// false, launching nothing, where the kernel cannot take every one of them.
+constexpr int kS16MaxBatch = 8;
+bool launch_skinny16_batch(const uint16_t* const* xs, const int64_t* ldxs, const int* Ks, const GemvGroup* groups,
+                           int n, int M, hipStream_t stream, hipError_t* err);
 
 // The GEMV kernel for 1 <= M <= 4 activation rows (x row stride ldx elements).  With norm.w
 // set (only where gemv_norm_supported(M, K)), x is the raw input and every workgroup applies

@@ -43,7 +43,14 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// Matrices of one launch: up to kS16MaxGroups, each with its own activations (x, ldx, K): the
+// groups of a grouped call share them, a batch of independent linears does not.
+constexpr int kS16MaxGroups = 8;
+
 struct S16Group {
+    const uint16_t* x;
+    int64_t ldx;
+    int K;
     const uint8_t* W;
     int64_t ldw;
     const float* s;
@@ -58,11 +65,9 @@ struct S16Group {
 };
 
 struct S16Args {
-    const uint16_t* x;
-    int64_t ldx;
-    int M, K;
+    int M;
     int ngroups;
-    S16Group g[kMaxGroups];
+    S16Group g[kS16MaxGroups];
 };
 
 // Stores four outputs n0 .. n0 + 3 of activation row m (lane layout of the MFMA result).
@@ -105,7 +110,7 @@ skinny16_rows_kernel(const S16Args a) {
     const int tile = blockIdx.x;
     int gi = 0;
 #pragma unroll
-    for (int i = 1; i < kMaxGroups; ++i)
+    for (int i = 1; i < kS16MaxGroups; ++i)
         if (i < a.ngroups && tile >= a.g[i].tile_begin) gi = i;
     const S16Group& G = a.g[gi];
     const int row0 = (tile - G.tile_begin) * 16 * R;
@@ -116,21 +121,21 @@ skinny16_rows_kernel(const S16Args a) {
     const int r = lane & 15, p = lane >> 4;           // MFMA layout
     const int li = lane >> 4, lb = lane & 15;         // load layout: row 4 q + li, chunk lb
     const int M = a.M;
-    const int S = a.K >> 6;
+    const int S = G.K >> 6;
     const int G4 = (S + 3) >> 2;
     const int g_beg = wave * G4 / NW, g_end = (wave + 1) * G4 / NW;
     const int n = g_end - g_beg;
     const int nb = n;
-    const int C = a.K >> 4;                            // 16-byte chunks per row
+    const int C = G.K >> 4;                            // 16-byte chunks per row
 
     const uint8_t* wrow[R][4];
 #pragma unroll
     for (int j = 0; j < R; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) wrow[j][q] = G.W + (int64_t)min(row0 + 16 * j + 4 * q + li, G.N - 1) * G.ldw;
-    const uint16_t* xrow = a.x + (int64_t)min(r, M - 1) * a.ldx + 16 * p;
+    const uint16_t* xrow = G.x + (int64_t)min(r, M - 1) * G.ldx + 16 * p;
     const uint8_t* wdummy = G.W;
-    const uint16_t* xdummy = a.x;
+    const uint16_t* xdummy = G.x;
     uint8_t* st = stage[wave];
 
     struct Batch {
@@ -248,7 +253,7 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
     const int tile = blockIdx.x;
     int gi = 0;
 #pragma unroll
-    for (int i = 1; i < kMaxGroups; ++i)
+    for (int i = 1; i < kS16MaxGroups; ++i)
         if (i < a.ngroups && tile >= a.g[i].tile_begin) gi = i;
     const S16Group& G = a.g[gi];
     const int row0 = (tile - G.tile_begin) * 16 * R;
@@ -258,12 +263,12 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
     const int lane = tid & 63;
     const int r = lane & 15, p = lane >> 4;           // MFMA layout
     const int M = a.M;
-    const int S = a.K >> 6;
+    const int S = G.K >> 6;
     const int G4 = (S + 3) >> 2;
     const int g_beg = wave * G4 / NW, g_end = (wave + 1) * G4 / NW;
     const int n = g_end - g_beg;
-    const int CW = a.K >> 4;                           // 16-byte chunks per weight row
-    const int CX = a.K >> 3;                           // 16-byte chunks per activation row
+    const int CW = G.K >> 4;                           // 16-byte chunks per weight row
+    const int CX = G.K >> 3;                           // 16-byte chunks per activation row
 
     uint8_t* const slots = s16_lds + wave * D * kSlot;
     const uint32_t lds_slots = (uint32_t)(uintptr_t)(lds_void*)slots;
@@ -296,8 +301,8 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
 #pragma unroll
         for (int i = 0; i < XR / 2; ++i) {
             const int rho = 2 * i + xh;
-            const uint32_t xoff = (uint32_t)((int64_t)min(rho, M - 1) * a.ldx * 2);
-            dma16_lds(a.x, xoff + 16u * (uint32_t)min(g4 * 32 + (xl ^ rho), CX - 1), sw + (uint32_t)(kW + i * 1024));
+            const uint32_t xoff = (uint32_t)((int64_t)min(rho, M - 1) * G.ldx * 2);
+            dma16_lds(G.x, xoff + 16u * (uint32_t)min(g4 * 32 + (xl ^ rho), CX - 1), sw + (uint32_t)(kW + i * 1024));
         }
     };
 
@@ -382,9 +387,16 @@ __global__ __launch_bounds__(64 * NW) void skinny16_dma_kernel(const S16Args a) 
     }
 }
 
+// One matrix of a launch and its activations.
+struct S16Input {
+    const uint16_t* x;
+    int64_t ldx;
+    int K;
+};
+
 // Fills the launch's group table (the row tiles of each matrix in order); returns the tile count.
 template <int R>
-int s16_tables(S16Args& a, const GemvGroup* groups, int ng) {
+int s16_tables(S16Args& a, const GemvGroup* groups, const S16Input* in, int ng) {
     int tb = 0;
     for (int i = 0; i < ng; ++i) {
         const GemvGroup& G = groups[i];
@@ -393,28 +405,29 @@ int s16_tables(S16Args& a, const GemvGroup* groups, int ng) {
         const bool vec = (reinterpret_cast<uintptr_t>(G.s) & 15) == 0 && (reinterpret_cast<uintptr_t>(G.y) & 7) == 0 &&
                          (G.ldy & 3) == 0 &&
                          (!res || ((reinterpret_cast<uintptr_t>(e.res) & 7) == 0 && (e.ldres & 3) == 0));
-        a.g[i] = S16Group{G.W, G.ldw, G.s, G.y, G.ldy, res ? e.res : nullptr, e.ldres, G.N, tb, e.kind, vec ? 1 : 0};
+        a.g[i] = S16Group{in[i].x, in[i].ldx, in[i].K, G.W, G.ldw, G.s, G.y, G.ldy, res ? e.res : nullptr, e.ldres, G.N,
+                          tb, e.kind, vec ? 1 : 0};
         tb += (G.N + 16 * R - 1) / (16 * R);
     }
     return tb;
 }
 
 template <int R, int NW, int D, int XR>
-hipError_t s16_dma_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
+hipError_t s16_dma_launch(S16Args& a, const GemvGroup* groups, const S16Input* in, int ng, hipStream_t stream) {
     constexpr int lds = s16_dma_lds<R, NW, D, XR>();
     static_assert(lds <= 152 * 1024, "LDS");
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&skinny16_dma_kernel<R, NW, D, XR>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
-    const int tb = s16_tables<R>(a, groups, ng);
+    const int tb = s16_tables<R>(a, groups, in, ng);
     if (tb < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL((skinny16_dma_kernel<R, NW, D, XR>), dim3(tb), dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
 
 template <int R, int NW>
-hipError_t s16_rows_launch(S16Args& a, const GemvGroup* groups, int ng, hipStream_t stream) {
-    const int tb = s16_tables<R>(a, groups, ng);
+hipError_t s16_rows_launch(S16Args& a, const GemvGroup* groups, const S16Input* in, int ng, hipStream_t stream) {
+    const int tb = s16_tables<R>(a, groups, in, ng);
     if (tb < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL((skinny16_rows_kernel<R, NW, 2>), dim3(tb), dim3(64 * NW), 0, stream, a);
     return hipGetLastError();
@@ -433,20 +446,22 @@ bool skinny16_wanted(int M, int K) {
     return knob != 2 && M >= 2 && M <= 16;
 }
 
-bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
-                             hipStream_t stream, hipError_t* err) {
-    if (!skinny16_wanted(M, K) || ngroups < 1 || ngroups > kMaxGroups || K < 64 || K % 64 != 0) return false;
-    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (ldx & 7) != 0) return false;
+namespace {
+
+// The launch behind both entries below: matrices `groups` with their activations `in` (M rows
+// each), one row tile per workgroup.
+bool s16_launch(const GemvGroup* groups, const S16Input* in, int ngroups, int M, bool batch, hipStream_t stream,
+                hipError_t* err) {
+    if (ngroups < 1 || ngroups > kS16MaxGroups) return false;
     int64_t rows = 0;
     for (int i = 0; i < ngroups; ++i) {
+        if (!skinny16_wanted(M, in[i].K) || in[i].K < 64 || in[i].K % 64 != 0) return false;
+        if ((reinterpret_cast<uintptr_t>(in[i].x) & 15) != 0 || (in[i].ldx & 7) != 0) return false;
         if ((reinterpret_cast<uintptr_t>(groups[i].W) & 15) != 0 || (groups[i].ldw & 15) != 0) return false;
         rows += groups[i].N;
     }
     S16Args a{};
-    a.x = x;
-    a.ldx = ldx;
     a.M = M;
-    a.K = K;
     a.ngroups = ngroups;
     // Row tiles of 32 from 4096 rows (half the activation reads per weight byte), else 16 (more
     // workgroups); four waves per workgroup, two where the row tiles outnumber the CUs (more,
@@ -462,45 +477,68 @@ bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const
     // the noise.  Tuning knobs: s16.r (1, 2) forces the row tile, s16.w (2, 4) the waves, s16.t = 1
     // the row-run form.
     const Tuning& tn = tuning();
-    const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : (rows >= 4096 ? 2 : 1);
+    // A batch of independent linears (one launch over a whole decode set, thousands of row
+    // tiles) takes its own choices, measured on MI355X for config 2's six linears: row tiles of
+    // 16 at M <= 4 (M = 2 / 4: 27.2 / 28.0 against 29.8 / 31.4 us with 32), of 32 above; four
+    // waves above M = 8 (M = 16: 37.7 against 44.1 us with two), two at M <= 8.
+    const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : batch ? (M <= 4 ? 1 : 2) : (rows >= 4096 ? 2 : 1);
     int tiles = 0;
     for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
-    const bool four = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w == 4 : tiles <= device_info().num_cu;
-    bool dma_ok = (ldx * 2) * (int64_t)(M - 1) + 2 * (int64_t)K < ((int64_t)1 << 31);
+    const bool four = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w == 4 : batch ? M > 8 : tiles <= device_info().num_cu;
+    bool dma_ok = true;
     for (int i = 0; i < ngroups; ++i)
-        dma_ok = dma_ok && groups[i].ldw * (int64_t)(groups[i].N - 1) + K < ((int64_t)1 << 31);
+        dma_ok = dma_ok && (in[i].ldx * 2) * (int64_t)(M - 1) + 2 * (int64_t)in[i].K < ((int64_t)1 << 31) &&
+                 groups[i].ldw * (int64_t)(groups[i].N - 1) + in[i].K < ((int64_t)1 << 31);
     if (tn.s16_t != 1 && dma_ok) {
         if (M <= 4) {                                  // 4 staged activation rows
             const int f4 = (R == 2 ? 2 : 0) + (four ? 1 : 0);
             switch (f4) {
-                case 0: *err = s16_dma_launch<1, 2, 2, 4>(a, groups, ngroups, stream); break;
-                case 1: *err = s16_dma_launch<1, 4, 2, 4>(a, groups, ngroups, stream); break;
-                case 2: *err = s16_dma_launch<2, 2, 2, 4>(a, groups, ngroups, stream); break;
-                default: *err = s16_dma_launch<2, 4, 2, 4>(a, groups, ngroups, stream); break;
+                case 0: *err = s16_dma_launch<1, 2, 2, 4>(a, groups, in, ngroups, stream); break;
+                case 1: *err = s16_dma_launch<1, 4, 2, 4>(a, groups, in, ngroups, stream); break;
+                case 2: *err = s16_dma_launch<2, 2, 2, 4>(a, groups, in, ngroups, stream); break;
+                default: *err = s16_dma_launch<2, 4, 2, 4>(a, groups, in, ngroups, stream); break;
             }
             return true;
         }
         const int form = (M <= 8 ? 4 : 0) + (R == 2 ? 2 : 0) + (four ? 1 : 0);
         switch (form) {
-            case 0: *err = s16_dma_launch<1, 2, 2, 16>(a, groups, ngroups, stream); break;
-            case 1: *err = s16_dma_launch<1, 4, 2, 16>(a, groups, ngroups, stream); break;
-            case 2: *err = s16_dma_launch<2, 2, 2, 16>(a, groups, ngroups, stream); break;
-            case 3: *err = s16_dma_launch<2, 4, 2, 16>(a, groups, ngroups, stream); break;
-            case 4: *err = s16_dma_launch<1, 2, 2, 8>(a, groups, ngroups, stream); break;
-            case 5: *err = s16_dma_launch<1, 4, 2, 8>(a, groups, ngroups, stream); break;
-            case 6: *err = s16_dma_launch<2, 2, 2, 8>(a, groups, ngroups, stream); break;
-            default: *err = s16_dma_launch<2, 4, 2, 8>(a, groups, ngroups, stream); break;
+            case 0: *err = s16_dma_launch<1, 2, 2, 16>(a, groups, in, ngroups, stream); break;
+            case 1: *err = s16_dma_launch<1, 4, 2, 16>(a, groups, in, ngroups, stream); break;
+            case 2: *err = s16_dma_launch<2, 2, 2, 16>(a, groups, in, ngroups, stream); break;
+            case 3: *err = s16_dma_launch<2, 4, 2, 16>(a, groups, in, ngroups, stream); break;
+            case 4: *err = s16_dma_launch<1, 2, 2, 8>(a, groups, in, ngroups, stream); break;
+            case 5: *err = s16_dma_launch<1, 4, 2, 8>(a, groups, in, ngroups, stream); break;
+            case 6: *err = s16_dma_launch<2, 2, 2, 8>(a, groups, in, ngroups, stream); break;
+            default: *err = s16_dma_launch<2, 4, 2, 8>(a, groups, in, ngroups, stream); break;
         }
         return true;
     }
     const int form = (R == 2 ? 2 : 0) + (four ? 1 : 0);
     switch (form) {
-        case 0: *err = s16_rows_launch<1, 2>(a, groups, ngroups, stream); break;
-        case 1: *err = s16_rows_launch<1, 4>(a, groups, ngroups, stream); break;
-        case 2: *err = s16_rows_launch<2, 2>(a, groups, ngroups, stream); break;
-        default: *err = s16_rows_launch<2, 4>(a, groups, ngroups, stream); break;
+        case 0: *err = s16_rows_launch<1, 2>(a, groups, in, ngroups, stream); break;
+        case 1: *err = s16_rows_launch<1, 4>(a, groups, in, ngroups, stream); break;
+        case 2: *err = s16_rows_launch<2, 2>(a, groups, in, ngroups, stream); break;
+        default: *err = s16_rows_launch<2, 4>(a, groups, in, ngroups, stream); break;
     }
     return true;
+}
+
+}  // namespace
+
+bool launch_skinny16_grouped(const uint16_t* x, int64_t ldx, int M, int K, const GemvGroup* groups, int ngroups,
+                             hipStream_t stream, hipError_t* err) {
+    if (ngroups < 1 || ngroups > kMaxGroups) return false;
+    S16Input in[kMaxGroups];
+    for (int i = 0; i < ngroups; ++i) in[i] = S16Input{x, ldx, K};
+    return s16_launch(groups, in, ngroups, M, false, stream, err);
+}
+
+bool launch_skinny16_batch(const uint16_t* const* xs, const int64_t* ldxs, const int* Ks, const GemvGroup* groups,
+                           int n, int M, hipStream_t stream, hipError_t* err) {
+    if (n < 1 || n > kS16MaxGroups) return false;
+    S16Input in[kS16MaxGroups];
+    for (int i = 0; i < n; ++i) in[i] = S16Input{xs[i], ldxs[i], Ks[i]};
+    return s16_launch(groups, in, n, M, true, stream, err);
 }
 
 }  // namespace nmi

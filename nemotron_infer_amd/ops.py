@@ -144,6 +144,34 @@ def linear_fp8_w8a16_grouped(x: torch.Tensor, weights, outs=None, use_workspace:
     return outs
 
 
+def linear_fp8_w8a16_batch(jobs, outs=None):
+    """Independent linears (x_i, W_i, s_i) with the same M in one dispatch (one launch of the
+    skinny kernel for 2 <= M <= 16): returns [y_i] with y_i = bf16((x_i . e4m3(W_i)^T) * s_i)."""
+    n = len(jobs)
+    if not 1 <= n <= _lib.MAX_BATCH:
+        raise ValueError(f"1..{_lib.MAX_BATCH} jobs")
+    xs = [_as_2d(x) for x, _, _ in jobs]
+    M = xs[0].shape[0]
+    if any(x2.shape[0] != M for x2 in xs):
+        raise ValueError("every job's x must have the same number of rows M")
+    if outs is None:
+        outs = [torch.empty((M, w.shape[0]), dtype=torch.bfloat16, device=x.device) for x, w, _ in jobs]
+    if len(outs) != n:
+        raise ValueError(f"{n} jobs but {len(outs)} outputs")
+    arr = (_lib.LinearJob * n)()
+    for i, ((_, w, s), x2, y) in enumerate(zip(jobs, xs, outs)):
+        K = x2.shape[1]
+        w = _check_w(w, K)
+        _check_s(s, w.shape[0])
+        y2 = _check_out(y, M, w.shape[0], f"outs[{i}]")
+        _check_device(x2, w, s, y2)
+        arr[i] = _lib.LinearJob(x2.data_ptr(), x2.stride(0), K,
+                                _lib.LinearGroup(w.data_ptr(), w.stride(0), s.data_ptr(), y2.data_ptr(),
+                                                 y2.stride(0), w.shape[0]))
+    _lib.check(_lib.lib().nmi_linear_fp8_w8a16_batch(arr, n, M, _stream()), "nmi_linear_fp8_w8a16_batch")
+    return outs
+
+
 def gemv_fp8(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
              out: torch.Tensor | None = None) -> torch.Tensor:
     """M = 1 GEMV (ops/gemv.cuh:92-104 semantics): y[N] = bf16((W . x) * s).  x is a contiguous

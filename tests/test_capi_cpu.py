@@ -62,6 +62,27 @@ def test_linear_rejects_bad_arguments(args, code):
     assert rc == code
 
 
+@pytest.mark.parametrize("args,code", [
+    ((0, 64, FAKE, 64, FAKE, FAKE, 8, 1, 8, 64), _lib.NMI_ERR_INVALID_ARG),          # NULL x
+    ((FAKE, 64, FAKE, 64, FAKE, FAKE, 8, 2, 8, 72), _lib.NMI_ERR_INVALID_ARG),       # K % 16
+    ((FAKE, 64, FAKE + 8, 64, FAKE, FAKE, 8, 2, 8, 64), _lib.NMI_ERR_ALIGNMENT),     # W misaligned
+    ((FAKE, 64, FAKE, 64, FAKE, FAKE + 1, 8, 2, 8, 64), _lib.NMI_ERR_ALIGNMENT),     # y misaligned
+])
+def test_batch_rejects_bad_jobs(args, code):
+    """nmi_linear_fp8_w8a16_batch validates every job like nmi_linear_fp8_w8a16 (a bad second
+    job fails the call, which launches nothing), and the job count."""
+    x, ldx, w, ldw, s, y, ldy, M, N, K = args
+    good = _lib.LinearJob(FAKE, 64, 64, _lib.LinearGroup(FAKE, 64, FAKE, FAKE, 8, 8))
+    bad = _lib.LinearJob(x, ldx, K, _lib.LinearGroup(w, ldw, s, y, ldy, N))
+    L = _lib.lib()
+    arr = (_lib.LinearJob * 2)(good, bad)
+    assert L.nmi_linear_fp8_w8a16_batch(arr, 2, M, None) == code
+    assert L.nmi_last_error().decode().startswith("nmi_linear_fp8_w8a16_batch")
+    for n in (0, _lib.MAX_BATCH + 1):
+        assert L.nmi_linear_fp8_w8a16_batch(arr, n, 2, None) == _lib.NMI_ERR_INVALID_ARG
+    assert L.nmi_linear_fp8_w8a16_batch(None, 1, 2, None) == _lib.NMI_ERR_INVALID_ARG
+
+
 def test_gemv_and_decode_reject_bad_arguments():
     L = _lib.lib()
     assert L.nmi_gemv_fp8(FAKE, FAKE, FAKE, FAKE, 8, 3136 + 8, None) == _lib.NMI_ERR_INVALID_ARG
