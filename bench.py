@@ -625,7 +625,7 @@ def bench_attn_prefill(dev, reps=10):
     t = T.time_replays([gr]) / reps
     fl = sum(synth.linear_flops(S, w.shape[0], w.shape[1]) for w, _ in mats) + 2 * 2 * (S * (S + 1) // 2) * D * HQ
     res["attn_forward_block_S=2048"] = {"us": round(t * 1e3, 1), "TFLOP/s": round(fl / (t * 1e-3) / 1e12, 1),
-                                        "launches": 8}
+                                        "launches": 5}
     del gr
     return {"workload": "causal attention prefill (40 q heads, 8 KV heads, head 128) and attn_forward_fp8", **res}
 

@@ -84,12 +84,13 @@ int nmi_linear_fp8_w8a16(const void* x_bf16, int64_t ldx, const void* w_e4m3, in
                          void* stream);
 
 /*
- * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the 4x4x4 skinny
- * kernel (2 <= M <= 16, when the tuning knob s4.kg > 1 selects its K split) and the
- * short-prompt GEMM (17 <= M < 512) split K between workgroups, and the prefill GEMM (M >= 512)
- * split the k tiles of a few large tiles between all CUs (stream-K: fp32 partial tiles and
- * per-workgroup flags in the workspace; used when the 256 x 256 tiles cover at most half of
- * the CUs, e.g. N = 3136 at M = 2048).
+ * As nmi_linear_fp8_w8a16, with a caller-owned device workspace that lets the short-prompt
+ * GEMM (17 <= M < 512) split K between workgroups.  For M >= 512 the prefill GEMM needs none:
+ * where its 256 x 256 tiles would cover at most half of the CUs (e.g. N = 3136 at M = 2048) it
+ * takes 128 x 256 tiles instead.  Its stream-K form (the k tiles of a few large tiles split
+ * between all CUs: fp32 partial tiles and per-workgroup flags in the workspace) runs only under
+ * the tuning knob gemm.sk = 1 (or gemm.bm = 256), and nmi_linear_workspace_bytes sizes the
+ * workspace for it only then.
  * workspace: 256-byte aligned, at least nmi_linear_workspace_bytes(M, N, K) bytes, zero-filled
  * before its first use; every launch leaves it ready for the next one.  NULL / too small ->
  * the kernels run without the split (same results up to float32 summation order).  Two

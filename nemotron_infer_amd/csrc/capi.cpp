@@ -147,7 +147,7 @@ size_t linear_workspace_bytes(int M, int64_t total_n, int K) {
     return 0;                                         // the GEMV and skinny kernels use none
 }
 
-bool gemm_workspace_has_flags(int M) { return M >= 512 && choose_path(M) == Path::Gemm; }
+bool gemm_workspace_has_flags(int M) { return M >= 512 && choose_path(M) == Path::Gemm && gemm_workspace_bytes(M) > 0; }
 
 // M == 1 -> GEMV kernel, M == 2 -> GEMV kernel when it fuses the RMSNorm, else the 16x16x32
 // skinny kernel where it takes the shape (dispatch_linear), M <= 16 -> the skinny kernels

@@ -1229,8 +1229,12 @@ hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Only the stream-K form uses a workspace, and it runs only under gemm.sk = 1 (or with the
+// 128-row tiles forbidden, gemm.bm = 256): otherwise none, so that the blocks neither reserve
+// its 64 MiB nor clear its flags.
 size_t gemm_workspace_bytes(int M) {
-    if (M < 512 || tuning().gemm_sk == 2) return 0;
+    const Tuning& t = tuning();
+    if (M < 512 || t.gemm_sk == 2 || (t.gemm_sk != 1 && t.gemm_bm != 256)) return 0;
     return kSkFlagBytes + (size_t)device_info().num_cu * kDmaPartialBytes;
 }
 

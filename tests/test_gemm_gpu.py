@@ -409,6 +409,7 @@ def test_grouped_prefill_is_one_launch_of_the_dma_kernel(M, Ns, K, _sk_reset):
     offs = np.cumsum((0,) + Ns)
     ybig = torch.full((M, total + 8), 3.0, dtype=torch.bfloat16, device=DEV)
     outs = [ybig[:, offs[i]:offs[i + 1]] for i in range(len(Ns))]
+    _lib.tuning_set("gemm.sk", 1)                  # a workspace with room for the stream-K form
     ws = _gemm_ws(M, total, K)
     L = _lib.lib()
     arr = (_lib.LinearGroup * len(Ns))()
@@ -453,6 +454,7 @@ def test_stream_k_late_flag_is_reported_and_the_workspace_recovers(_sk_reset):
     announce("stream_k_late_flag", M, N, K)
     x, w, s = _case(M, N, K, 2718, outlier_frac=0.001)
     xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    _lib.tuning_set("gemm.sk", 1)                  # sized for the stream-K form
     ws = _gemm_ws(M, N, K)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
     err = _lib.NMI_WS_ERROR_OFFSET
@@ -485,6 +487,7 @@ def test_stream_k_late_flag_reaches_sync_ops_and_the_binding(_sk_reset):
     announce("stream_k_late_flag_front_ends", M, N, K)
     x, w, s = _case(M, N, K, 2719)
     xd, wd, sd = x_to_dev(x), w_to_dev(w), s_to_dev(s)
+    _lib.tuning_set("gemm.sk", 1)                  # sized for the stream-K form
     ws = _gemm_ws(M, N, K)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
     L = _lib.lib()
