@@ -27,7 +27,7 @@ namespace {
 constexpr int kN = kMambaDState;       // 128
 constexpr int kConvK = kMambaConvK;    // 4
 constexpr int kRowsPerWg = 8;          // SSM rows (p) per workgroup: 4 waves x 2 half-waves
-constexpr int kTC = 64;                // tokens per staged chunk
+constexpr int kTC = 32;                // tokens per staged chunk
 constexpr int kConvT = 64;             // tokens per conv thread
 
 __device__ __forceinline__ float silu(float v) { return v / (1.f + expf(-v)); }
@@ -66,9 +66,15 @@ __global__ __launch_bounds__(256) void mamba_conv_prefill_kernel(const MambaPref
     }
 }
 
-__global__ __launch_bounds__(256) void mamba_scan_kernel(const MambaPrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sB[kTC][kN];
-    __shared__ __attribute__((aligned(16))) uint16_t sC[kTC][kN];
+// Scan: one workgroup per (sequence, head, 8 rows of P), a 32-lane half-wave per row with the
+// row's N = 128 float32 states (4 per lane).  Tokens go in chunks of kTC = 32 staged in LDS: dt
+// (softplus) and the decay per token, then dt.B and C in float32 (each computed once per chunk
+// for all 8 rows, not per row and token), x per row; the next chunk's loads are in flight during
+// the scan.  Per token a lane updates its 4 states, s = fma(s, dA, (dt B) x), and forms its
+// 4-state part of y = S . C, summed over the half-wave (16-lane DPP sum, then lane 16 apart).
+__global__ __launch_bounds__(256, 4) void mamba_scan_kernel(const MambaPrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) float sdtB[kTC][kN];
+    __shared__ __attribute__((aligned(16))) float sC[kTC][kN];
     __shared__ __attribute__((aligned(16))) uint16_t sx[kTC][kRowsPerWg];
     __shared__ float sdt[kTC], sdA[kTC];
     __shared__ float sy[kTC][kRowsPerWg];
@@ -89,13 +95,13 @@ __global__ __launch_bounds__(256) void mamba_scan_kernel(const MambaPrefillArgs 
     const bool row_ok = p0 + r < a.P;
     const int nrows_wg = min(kRowsPerWg, a.P - p0);
 
-    // chunk staging: B and C rows (16 chunks of 16 B each per token: 1024 per chunk, 4 per
+    // chunk staging: B and C rows of kTC tokens (16 chunks of 16 B per token: 512 per chunk, 2 per
     // thread each), x (threads < kTC: 8 values, or fewer at the last split), dt (threads < kTC)
-    uint4 rb[4], rc[4], rx;
+    uint4 rb[2], rc[2], rx;
     uint16_t rdt;
     auto gload = [&](int t0) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 2; ++u) {
             const int i = tid + 256 * u;
             const int t = min(t0 + (i >> 4), S - 1), c = i & 15;
             const uint16_t* row = a.xc + (xrow0 + t) * a.xc_ld + a.inter;
@@ -117,42 +123,59 @@ __global__ __launch_bounds__(256) void mamba_scan_kernel(const MambaPrefillArgs 
             rdt = a.proj[(xrow0 + t) * a.proj_ld + a.inter + a.conv_dim + h];
         }
     };
-    auto sstore = [&]() {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = tid + 256 * u;
-            *reinterpret_cast<uint4*>(&sB[i >> 4][8 * (i & 15)]) = rb[u];
-            *reinterpret_cast<uint4*>(&sC[i >> 4][8 * (i & 15)]) = rc[u];
-        }
+    // Tokens past the end of the sequence get dt = 0, decay 1 and x = 0: their updates leave the
+    // states exactly as they are (fma(s, 1, 0) = s).
+    auto sstore = [&](int nt) {
         if (tid < kTC) {
-            *reinterpret_cast<uint4*>(&sx[tid][0]) = rx;
+            const bool live = tid < nt;
+            *reinterpret_cast<uint4*>(&sx[tid][0]) = live ? rx : uint4{0u, 0u, 0u, 0u};
             float dt = bf16_to_f32(rdt) + bias;
             dt = dt > 20.f ? dt : (dt < -20.f ? 0.f : logf(1.f + expf(dt)));
             dt = fminf(FLT_MAX, fmaxf(0.f, dt));
-            sdt[tid] = dt;
-            sdA[tid] = expf(nA * dt);
+            sdt[tid] = live ? dt : 0.f;
+            sdA[tid] = live ? expf(nA * dt) : 1.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + 256 * u;
+            const int t = i >> 4, c = i & 15;
+            const float dt = sdt[t];
+            const uint32_t bw[4] = {rb[u].x, rb[u].y, rb[u].z, rb[u].w};
+            const uint32_t cw[4] = {rc[u].x, rc[u].y, rc[u].z, rc[u].w};
+            float db[8], cf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                db[2 * e] = dt * bf16lo_to_f32(bw[e]);
+                db[2 * e + 1] = dt * bf16hi_to_f32(bw[e]);
+                cf[2 * e] = bf16lo_to_f32(cw[e]);
+                cf[2 * e + 1] = bf16hi_to_f32(cw[e]);
+            }
+            *reinterpret_cast<f32x4*>(&sdtB[t][8 * c]) = f32x4{db[0], db[1], db[2], db[3]};
+            *reinterpret_cast<f32x4*>(&sdtB[t][8 * c + 4]) = f32x4{db[4], db[5], db[6], db[7]};
+            *reinterpret_cast<f32x4*>(&sC[t][8 * c]) = f32x4{cf[0], cf[1], cf[2], cf[3]};
+            *reinterpret_cast<f32x4*>(&sC[t][8 * c + 4]) = f32x4{cf[4], cf[5], cf[6], cf[7]};
         }
     };
 
     float s[4] = {0.f, 0.f, 0.f, 0.f};
     gload(0);
     for (int t0 = 0; t0 < S; t0 += kTC) {
-        sstore();
+        const int nt = min(kTC, S - t0);
+        sstore(nt);
         __syncthreads();
         if (t0 + kTC < S) gload(t0 + kTC);                     // the next chunk, in flight during the scan
-        const int nt = min(kTC, S - t0);
-        for (int t = 0; t < nt; ++t) {
-            const uint2 bw = *reinterpret_cast<const uint2*>(&sB[t][4 * l]);
-            const uint2 cw = *reinterpret_cast<const uint2*>(&sC[t][4 * l]);
+#pragma unroll 4
+        for (int t = 0; t < kTC; ++t) {
+            const f32x4 db = *reinterpret_cast<const f32x4*>(&sdtB[t][4 * l]);
+            const f32x4 c = *reinterpret_cast<const f32x4*>(&sC[t][4 * l]);
             const float x = bf16_to_f32(sx[t][r]);
-            const float dt = sdt[t], dA = sdA[t];
-            const float B4[4] = {bf16lo_to_f32(bw.x), bf16hi_to_f32(bw.x), bf16lo_to_f32(bw.y), bf16hi_to_f32(bw.y)};
-            const float C4[4] = {bf16lo_to_f32(cw.x), bf16hi_to_f32(cw.x), bf16lo_to_f32(cw.y), bf16hi_to_f32(cw.y)};
+            const float dA = sdA[t];
             float y = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                s[i] = __builtin_fmaf(s[i], dA, (dt * B4[i]) * x);
-                y = __builtin_fmaf(s[i], C4[i], y);
+                s[i] = __builtin_fmaf(s[i], dA, db[i] * x);
+                y = __builtin_fmaf(s[i], c[i], y);
             }
             y = dpp_row_sum16(y);
             y += __shfl_xor(y, 16);
@@ -163,9 +186,9 @@ __global__ __launch_bounds__(256) void mamba_scan_kernel(const MambaPrefillArgs 
         if (tid < nt) {
             uint16_t* yr = a.y + (xrow0 + t0 + tid) * a.y_ld + h * a.P + p0;
             if (nrows_wg == kRowsPerWg && a.y_vec) {
-                const float* v = sy[tid];
-                *reinterpret_cast<uint4*>(yr) = uint4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]),
-                                                      pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
+                const float* vv = sy[tid];
+                *reinterpret_cast<uint4*>(yr) = uint4{pack_bf16(vv[0], vv[1]), pack_bf16(vv[2], vv[3]),
+                                                      pack_bf16(vv[4], vv[5]), pack_bf16(vv[6], vv[7])};
             } else {
                 for (int e = 0; e < nrows_wg; ++e) yr[e] = f32_to_bf16_rne(sy[tid][e]);
             }
