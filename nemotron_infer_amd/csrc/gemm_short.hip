@@ -253,7 +253,9 @@ __global__ __launch_bounds__(256, OCC) void gemm_short_kernel(const ShortArgs a)
 }
 
 // Sum of the splits' partials in split order, the scale, one rounding, the epilogue.  One
-// thread per 4 consecutive outputs of a row (16-byte partial loads when N % 4 == 0).
+// thread per 4 consecutive outputs of a row (16-byte partial loads when N % 4 == 0); the partials
+// of up to 8 splits are loaded before any is added (one memory round trip for them, not one per
+// split), the scales and residuals before the partials.
 __global__ __launch_bounds__(256) void gemm_short_reduce_kernel(const ShortArgs a) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int q_n = (a.N + 3) / 4;
@@ -262,21 +264,37 @@ __global__ __launch_bounds__(256) void gemm_short_reduce_kernel(const ShortArgs 
     const size_t stride = (size_t)a.M * a.N;
     const float* p = a.part + (size_t)m * a.N + n;
     const int cnt = min(4, a.N - n);
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    float sc[4], v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sc[e] = a.s[min(n + e, a.N - 1)];
+    uint16_t r[4] = {0, 0, 0, 0};
+    if (a.epi.kind == kEpiResidual)
+        for (int e = 0; e < cnt; ++e) r[e] = a.epi.res[(int64_t)m * a.epi.ldres + n + e];
     if (a.part_vec) {
-        for (int sp = 0; sp < a.splits; ++sp) {
-            const float4 f = *reinterpret_cast<const float4*>(p + sp * stride);
-            v[0] += f.x; v[1] += f.y; v[2] += f.z; v[3] += f.w;
+        for (int s0 = 0; s0 < a.splits; s0 += 8) {
+            float4 f[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (s0 + q < a.splits) f[q] = *reinterpret_cast<const float4*>(p + (size_t)(s0 + q) * stride);
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (s0 + q < a.splits) {
+                    v[0] += f[q].x; v[1] += f[q].y; v[2] += f[q].z; v[3] += f[q].w;
+                }
         }
     } else {
         for (int sp = 0; sp < a.splits; ++sp)
             for (int e = 0; e < cnt; ++e) v[e] += p[sp * stride + e];
     }
-    uint16_t r[4] = {0, 0, 0, 0};
-    if (a.epi.kind == kEpiResidual)
-        for (int e = 0; e < cnt; ++e) r[e] = a.epi.res[(int64_t)m * a.epi.ldres + n + e];
     uint16_t* yr = a.y + (int64_t)m * a.ldy + n;
-    for (int e = 0; e < cnt; ++e) yr[e] = epilogue(v[e], a.s[n + e], a.epi.kind, r[e]);
+    uint16_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = epilogue(v[e], sc[e], a.epi.kind, r[e]);
+    if (cnt == 4 && (reinterpret_cast<uintptr_t>(yr) & 7) == 0) {
+        *reinterpret_cast<uint2*>(yr) = uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    } else {
+        for (int e = 0; e < cnt; ++e) yr[e] = o[e];
+    }
 }
 
 template <int TN, int TM, int WN, int NS, int OCC>
@@ -308,33 +326,36 @@ namespace {
 // workgroups without splitting K (whose partials cost 8 M bytes per weight row and split).
 struct ShortCfg {
     int tn, tm, wn, ns, per_cu;
+    int round;           // workgroups per CU that one round of the K split aims at
     int bn() const { return 32 * tn * wn; }
     int bm() const { return 32 * tm * (kWaves / wn); }
 };
 constexpr ShortCfg kForms[] = {
-    {2, 1, 4, 7, 1},   // 0: 256 x 32
-    {1, 1, 4, 6, 2},   // 1: 128 x 32
-    {2, 2, 4, 6, 1},   // 2: 256 x 64
-    {1, 2, 4, 4, 2},   // 3: 128 x 64
-    {1, 1, 2, 6, 2},   // 4: 64 x 64
-    {2, 4, 4, 4, 1},   // 5: 256 x 128
-    {2, 2, 2, 4, 1},   // 6: 128 x 128
-    {1, 2, 2, 3, 2},   // 7: 64 x 128
+    {2, 1, 4, 7, 1, 1},   // 0: 256 x 32
+    {1, 1, 4, 6, 2, 2},   // 1: 128 x 32
+    {2, 2, 4, 6, 1, 1},   // 2: 256 x 64
+    {1, 2, 4, 4, 2, 1},   // 3: 128 x 64
+    {1, 1, 2, 6, 2, 2},   // 4: 64 x 64
+    {2, 4, 4, 4, 1, 1},   // 5: 256 x 128
+    {2, 2, 2, 4, 1, 1},   // 6: 128 x 128
+    {1, 2, 2, 3, 2, 2},   // 7: 64 x 128
 };
 constexpr int kNumForms = sizeof(kForms) / sizeof(kForms[0]);
 
-// The form for (M, N): among those whose x tile fits M best, the widest one whose tiles fill
-// three quarters of the workgroup slots without a K split; else the narrowest (then K is split).
-// Above M = 64 the 128 x 128 form with a 64 x 64 block per wave (fewest LDS reads per MFMA).
-// Measured on the config-3 shapes at M = 64 / 128 / 256: every form within ~15% of the others;
-// 128 x 128 ahead by 10% at M = 128 and 256.  Tuning knob gemm.short = f + 1 forces form f.
+// The form for (M, N).  M <= 32: the widest of 256 x 32 and 128 x 32 whose tiles fill three
+// quarters of the workgroup slots without a K split, else 128 x 32 (then K is split).  33 <= M
+// <= 64: 128 x 64 with K split to about one workgroup per CU -- the best of every form and split
+// count on each config-3 shape in a sweep (up / down / q|k|v at M = 64 19.7 / 17.7 / 14.2 us
+// against 23.4 / 20.6 / 15.6 for 64 x 64 tiles split to two per CU).  Above M = 64 the 128 x 128
+// form with a 64 x 64 block per wave (fewest LDS reads per MFMA; best or within 1% of the best at
+// M = 128 and 256).  Tuning knob gemm.short = f + 1 forces form f.
 int short_form(int M, int N) {
     const int forced = tuning().gemm_short;
     if (forced >= 1 && forced <= kNumForms) return forced - 1;
     int lo, hi;                                     // candidate forms, widest first
     if (M <= 32) { lo = 0; hi = 1; }
-    else if (M <= 64) { lo = 2; hi = 4; }
-    else { lo = 6; hi = 6; }                        // 128 x 128: measured ahead of 256 x 128 and 64 x 128
+    else if (M <= 64) return 3;
+    else { lo = 6; hi = 6; }
     const int cu = device_info().num_cu;
     for (int f = lo; f <= hi; ++f) {
         const ShortCfg& c = kForms[f];
@@ -352,9 +373,9 @@ int gemm_short_splits(int M, int N, int K) {
     const int tiles = ((N + bn - 1) / bn) * ((M + bm - 1) / bm);
     const int KT = K / kBK;
     if (tuning().gemm_splits > 0) return std::min(tuning().gemm_splits, KT);
-    // as many workgroups as run at once (one round), at least 4 k tiles each, and the partials
+    // one round of the form's target workgroups per CU, at least 4 k tiles each, and the partials
     // (4 M bytes per weight row and split, written and read back) at most the weight bytes
-    const int want = std::max(1, c.per_cu * device_info().num_cu / tiles);
+    const int want = std::max(1, c.round * device_info().num_cu / tiles);
     const int by_k = std::max(1, KT / 4);
     const int by_bytes = std::max(1, (int)((int64_t)K / (4 * (int64_t)M)));
     return std::max(1, std::min(want, std::min(by_k, by_bytes)));
