@@ -118,6 +118,12 @@ __global__ __launch_bounds__(256, 2) void sdpa_prefill_kernel(const PrefillArgs 
     float m = -INFINITY, l = 0.f;                               // raw score units
 
     gload(0);
+    // complete the query loads before the loop (with the first tile's, in flight together):
+    // otherwise the compiler's wait analysis, merging the loop paths with and without the next
+    // tile's prefetch, waits for that prefetch before the score MFMAs of every tile (loads retire
+    // in order), which puts a memory round trip on each tile's critical path
+#pragma unroll
+    for (int s = 0; s < 8; ++s) asm volatile("" ::"v"(qf[s]));
     sstore(0);
     __syncthreads();
     for (int t = 0; t < ntiles; ++t) {
