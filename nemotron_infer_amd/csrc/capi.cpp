@@ -497,6 +497,7 @@ int nmi_tuning_set(const char* knob, int value) {
     else if (!std::strcmp(knob, "s16.r")) t.s16_r = value;
     else if (!std::strcmp(knob, "s16.w")) t.s16_w = value;
     else if (!std::strcmp(knob, "s16.t")) t.s16_t = value;
+    else if (!std::strcmp(knob, "mamba.scan")) t.mamba_scan = value;
     else return fail(NMI_ERR_INVALID_ARG, "nmi_tuning_set: unknown knob '%s'", knob);
     return NMI_OK;
 }

@@ -200,6 +200,267 @@ __global__ __launch_bounds__(256, 4) void mamba_scan_kernel(const MambaPrefillAr
     }
 }
 
+// Chunked scan (the default): the same recurrence in the chunked matrix form of the reference's
+// ssd_scan_chunked.cuh, on bf16 MFMA.  One workgroup per (sequence, head, 16 rows of P), 64-token
+// chunks in order; with c_i = sum_{k <= i} dt_k A over the chunk (A = -exp(A_log); kept in log2
+// units), S0 the state entering it (rows p, columns n) and w_j = exp(c_63 - c_j) dt_j:
+//   y_i  = exp(c_i) (C_i . S0[p, :]) + sum_{j <= i} G_ij x_j + D x_i,
+//          G_ij = (C_i . B_j) exp(c_i - c_j) dt_j
+//   S    = exp(c_63) S0 + sum_j (w_j x_j) B_j^T.
+// C B^T is exact products of bf16 with float32 sums (v_mfma_f32_32x32x16_bf16); G, S0 and w x
+// enter their products in two bf16 parts (hi = bf16(v), lo = bf16(v - hi): about 16 significant
+// bits, finer than the reference's TF32 products) against exact bf16 x, C and B
+// (v_mfma_f32_16x16x32_bf16); the state accumulates in float32 MFMA registers across chunks.
+// Each SIMD issues a wave64 VALU instruction over 4 cycles, so the per-element work is kept on
+// MFMA: what remains on VALU per chunk is the decay weights, the G mask and the two-part splits.
+// Tokens past the end of the sequence get dt = 0 and x = 0: no weight, no decay.
+constexpr int kQ = 64;                 // tokens per chunk
+constexpr int kPW = 16;                // rows of P per workgroup
+
+// LDS (bytes): B and C chunks [64][128] bf16 (256-byte rows, 16-byte chunk c at c ^ (row & 15));
+// B^T [128][64] bf16 and X^T [16][64] bf16 (128-byte rows, chunk at c ^ ((row >> 1) & 7)); G hi /
+// lo [64][64] bf16 (the same); (w x)^T hi / lo [16][64] bf16 (the same); S0 hi / lo [16][128] bf16
+// (chunk at c ^ (p & 15)); per-token float32 arrays.
+constexpr int kOffB = 0, kOffC = 16384, kOffBT = 32768, kOffXT = 49152, kOffGh = 51200, kOffGl = 59392,
+              kOffWXh = 67584, kOffWXl = 69632, kOffS = 71680, kOffCum = 79872, kOffEcum = kOffCum + 256,
+              kOffW = kOffEcum + 256, kOffDt = kOffW + 256, kSsdLds = kOffDt + 256;
+
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ int bc_off(int row, int c) { return row * 256 + ((c ^ (row & 15)) << 4); }
+__device__ __forceinline__ int t_off(int row, int c) { return row * 128 + ((c ^ ((row >> 1) & 7)) << 4); }
+__device__ __forceinline__ int s_off(int p, int c) { return p * 256 + ((c ^ (p & 15)) << 4); }
+
+__global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int slices = (a.P + kPW - 1) / kPW;
+    const int h = blockIdx.x / slices, p0 = (blockIdx.x % slices) * kPW;
+    const int b = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, hh = lane >> 5;                  // 32x32x16 operand layout
+    const int l16 = lane & 15, g4 = lane >> 4;                  // 16x16x32 operand layout
+    const int grp = h / (a.H / a.G);
+    const int S = a.S;
+    const int pw = min(kPW, a.P - p0);
+    const size_t xrow0 = (size_t)b * S;
+    const float nA2 = -expf(a.A_log[h]) * 1.4426950408889634f;   // A in log2 units
+    const float bias = a.dt_bias[h];
+    const float Dh = a.D[h];
+    float* cum = reinterpret_cast<float*>(lds + kOffCum);        // c_j, log2 units
+    float* ecum = reinterpret_cast<float*>(lds + kOffEcum);      // exp(c_j)
+    float* wj = reinterpret_cast<float*>(lds + kOffW);           // exp(c_63 - c_j) dt_j
+    float* dts = reinterpret_cast<float*>(lds + kOffDt);
+
+    // chunk staging in registers (the next chunk's loads are in flight during this one): B and C
+    // rows (1024 chunks of 16 B each: 4 per thread), x (threads < 128: token tid / 2, P columns
+    // 8 (tid % 2) .. + 7 of the slice), dt (threads < 64)
+    uint4 rb[4], rc[4], rx = uint4{0u, 0u, 0u, 0u};
+    uint16_t rdt = 0;
+    auto gload = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = tid + 256 * u;
+            const int t = min(t0 + (q >> 4), S - 1), c = q & 15;
+            const uint16_t* row = a.xc + (xrow0 + t) * a.xc_ld + a.inter;
+            rb[u] = load16(row + grp * kN + 8 * c);
+            rc[u] = load16(row + a.G * kN + grp * kN + 8 * c);
+        }
+        if (tid < 2 * kQ) {
+            const int t = min(t0 + (tid >> 1), S - 1), pc = 8 * (tid & 1);
+            const uint16_t* xr = a.xc + (xrow0 + t) * a.xc_ld + h * a.P + p0 + pc;
+            if (a.x_vec && pc + 8 <= pw) {
+                rx = load16(xr);
+            } else {
+                uint16_t v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = pc + e < pw ? xr[e] : 0;
+                rx = uint4{v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16), v[4] | ((uint32_t)v[5] << 16),
+                           v[6] | ((uint32_t)v[7] << 16)};
+            }
+        }
+        if (tid < kQ) rdt = a.proj[(xrow0 + min(t0 + tid, S - 1)) * a.proj_ld + a.inter + a.conv_dim + h];
+    };
+
+    // the state, as two 16 x 16 MFMA accumulator blocks per wave: columns n = 16 (2 wave + nb) +
+    // l16, rows p = 4 g4 + r
+    f32x4 st[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) st[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // S0 hi / lo of the first chunk: zero (thread t clears 16 bytes of each)
+    *reinterpret_cast<uint4*>(lds + kOffS + 16 * tid) = uint4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<uint4*>(lds + kOffS + 4096 + 16 * tid) = uint4{0u, 0u, 0u, 0u};
+
+    gload(0);
+    for (int t0 = 0; t0 < S; t0 += kQ) {
+        const int nt = min(kQ, S - t0);
+        // (a) the staged chunk into LDS (every wave has finished the previous chunk: barrier at the
+        // end of the loop): B row-major and transposed, C, x^T; the decay weights (wave 0)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = tid + 256 * u;
+            const int j = q >> 4, cc = q & 15;
+            *reinterpret_cast<uint4*>(lds + kOffB + bc_off(j, cc)) = rb[u];
+            *reinterpret_cast<uint4*>(lds + kOffC + bc_off(j, cc)) = rc[u];
+            const uint32_t w[4] = {rb[u].x, rb[u].y, rb[u].z, rb[u].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int n = 8 * cc + e;
+                *reinterpret_cast<uint16_t*>(lds + kOffBT + t_off(n, j >> 3) + 2 * (j & 7)) =
+                    (uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+            }
+        }
+        if (tid < 2 * kQ) {
+            // x^T: token j = tid / 2 of P columns 8 (tid % 2) + e (zero past the sequence)
+            const int j = tid >> 1, pc = 8 * (tid & 1);
+            const uint4 v = j < nt ? rx : uint4{0u, 0u, 0u, 0u};
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                *reinterpret_cast<uint16_t*>(lds + kOffXT + t_off(pc + e, j >> 3) + 2 * (j & 7)) =
+                    (uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+        }
+        if (wave == 0) {
+            // softplus(dt + bias) (the reference's cut-offs), the chunk's inclusive cumulative
+            // log2-decay (finite even where dt saturates: a decay that small is a reset either way)
+            float dt = bf16_to_f32(rdt) + bias;
+            dt = dt > 20.f ? dt : (dt < -20.f ? 0.f : logf(1.f + expf(dt)));
+            dt = fminf(FLT_MAX, fmaxf(0.f, dt));
+            if (lane >= nt) dt = 0.f;
+            float v = fmaxf(nA2 * dt, -1e30f);
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const float u = __shfl_up(v, o);
+                if (lane >= o) v += u;
+            }
+            const float last = __shfl(v, 63);
+            cum[lane] = v;
+            ecum[lane] = fexp2(v);
+            wj[lane] = fexp2(last - v) * dt;
+            dts[lane] = dt;
+        }
+        if (t0 + kQ < S) gload(t0 + kQ);
+        __syncthreads();
+
+        // (b) C B^T, one 32 x 32 block per wave: rows i = 32 (wave / 2) + ..., columns j = 32 (wave
+        // % 2) + l32 (register r: row 8 (r / 4) + 4 hh + r % 4); G on and below the diagonal, in two
+        // bf16 parts; and (w x)^T in two bf16 parts (thread: row p = tid / 16, tokens 4 (tid % 16)
+        // .. + 3)
+        {
+            const int bi = wave >> 1, bj = wave & 1;
+            f32x16 cb;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) cb[r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const bf16x8 af = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(32 * bi + l32, 2 * s + hh));
+                const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + kOffB + bc_off(32 * bj + l32, 2 * s + hh));
+                cb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, cb, 0, 0, 0);
+            }
+            const int j = 32 * bj + l32;
+            const float cj = cum[j], dj = dts[j];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const float e = fexp2(fminf(cum[i] - cj, 0.f));
+                const float gv = j <= i ? cb[r] * e * dj : 0.f;
+                const uint32_t w = pack_bf16(gv, 0.f);
+                const uint32_t lo = pack_bf16(gv - __uint_as_float(w << 16), 0.f);
+                const int off = t_off(i, j >> 3) + 2 * (j & 7);
+                *reinterpret_cast<uint16_t*>(lds + kOffGh + off) = (uint16_t)w;
+                *reinterpret_cast<uint16_t*>(lds + kOffGl + off) = (uint16_t)lo;
+            }
+            const int p = tid >> 4, j4 = 4 * (tid & 15);
+            const uint2 xv = *reinterpret_cast<const uint2*>(lds + kOffXT + t_off(p, j4 >> 3) + 2 * (j4 & 7));
+            const f32x4 wv = *reinterpret_cast<const f32x4*>(wj + j4);
+            const float v0 = bf16lo_to_f32(xv.x) * wv[0], v1 = bf16hi_to_f32(xv.x) * wv[1];
+            const float v2 = bf16lo_to_f32(xv.y) * wv[2], v3 = bf16hi_to_f32(xv.y) * wv[3];
+            const uint32_t h01 = pack_bf16(v0, v1), h23 = pack_bf16(v2, v3);
+            const uint32_t l01 = pack_bf16(v0 - __uint_as_float(h01 << 16), v1 - __uint_as_float(h01 & 0xffff0000u));
+            const uint32_t l23 = pack_bf16(v2 - __uint_as_float(h23 << 16), v3 - __uint_as_float(h23 & 0xffff0000u));
+            *reinterpret_cast<uint2*>(lds + kOffWXh + t_off(p, j4 >> 3) + 2 * (j4 & 7)) = uint2{h01, h23};
+            *reinterpret_cast<uint2*>(lds + kOffWXl + t_off(p, j4 >> 3) + 2 * (j4 & 7)) = uint2{l01, l23};
+        }
+        __syncthreads();
+
+        // (c) y for rows i = 16 wave + ..., 16 columns p (lane (l16, g4) holds rows 4 g4 + r of
+        // column p = l16): exp(c_i) C_i . S0 + G x + D x; and the state's products
+        const float dec = ecum[kQ - 1];
+        {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8 af = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(16 * wave + l16, 4 * ks + g4));
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(lds + kOffS + s_off(l16, 4 * ks + g4));
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(lds + kOffS + 4096 + s_off(l16, 4 * ks + g4));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bh, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bl, acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] *= ecum[16 * wave + 4 * g4 + r];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(lds + kOffGh + t_off(16 * wave + l16, 4 * ks + g4));
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(lds + kOffGl + t_off(16 * wave + l16, 4 * ks + g4));
+                const bf16x8 bx = *reinterpret_cast<const bf16x8*>(lds + kOffXT + t_off(l16, 4 * ks + g4));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bx, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bx, acc, 0, 0, 0);
+            }
+            const int i0 = 16 * wave + 4 * g4;                      // 4 consecutive tokens of column p
+            const uint2 xv = *reinterpret_cast<const uint2*>(lds + kOffXT + t_off(l16, i0 >> 3) + 2 * (i0 & 7));
+            const float xf[4] = {bf16lo_to_f32(xv.x), bf16hi_to_f32(xv.x), bf16lo_to_f32(xv.y), bf16hi_to_f32(xv.y)};
+            if (l16 < pw) {
+                uint16_t* yp = a.y + (xrow0 + t0 + i0) * a.y_ld + h * a.P + p0 + l16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (i0 + r < nt) yp[(size_t)r * a.y_ld] = (uint16_t)pack_bf16(__builtin_fmaf(Dh, xf[r], acc[r]), 0.f);
+            }
+            // S = exp(c_63) S0 + (w x)^T B: rows p (A = (w x)^T, two parts), columns n (B = B^T rows)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) st[nb][r] *= dec;
+                const int n = 16 * (2 * wave + nb) + l16;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(lds + kOffWXh + t_off(l16, 4 * ks + g4));
+                    const bf16x8 al = *reinterpret_cast<const bf16x8*>(lds + kOffWXl + t_off(l16, 4 * ks + g4));
+                    const bf16x8 bb = *reinterpret_cast<const bf16x8*>(lds + kOffBT + t_off(n, 4 * ks + g4));
+                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bb, st[nb], 0, 0, 0);
+                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bb, st[nb], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+        // (d) the new state's two bf16 parts for the next chunk (S0 was read above: barrier)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int n = 16 * (2 * wave + nb) + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int pp = 4 * g4 + r;
+                const float v = st[nb][r];
+                const uint32_t w = pack_bf16(v, 0.f);
+                const uint32_t lo = pack_bf16(v - __uint_as_float(w << 16), 0.f);
+                const int off = s_off(pp, n >> 3) + 2 * (n & 7);
+                *reinterpret_cast<uint16_t*>(lds + kOffS + off) = (uint16_t)w;
+                *reinterpret_cast<uint16_t*>(lds + kOffS + 4096 + off) = (uint16_t)lo;
+            }
+        }
+        __syncthreads();
+    }
+    if (a.ssm_state) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int n = 16 * (2 * wave + nb) + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int pp = 4 * g4 + r;
+                if (pp < pw) a.ssm_state[(((size_t)b * a.H + h) * a.P + p0 + pp) * kN + n] = st[nb][r];
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_mamba_prefill_mixer(const MambaPrefillArgs& a, int batch, hipStream_t stream) {
@@ -207,8 +468,16 @@ hipError_t launch_mamba_prefill_mixer(const MambaPrefillArgs& a, int batch, hipS
                        dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int splits = (a.P + kRowsPerWg - 1) / kRowsPerWg;
-    hipLaunchKernelGGL(mamba_scan_kernel, dim3(a.H * splits, batch), dim3(256), 0, stream, a);
+    if (tuning().mamba_scan == 1) {
+        const int splits = (a.P + kRowsPerWg - 1) / kRowsPerWg;
+        hipLaunchKernelGGL(mamba_scan_kernel, dim3(a.H * splits, batch), dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&mamba_ssd_kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSsdLds);
+    if (attr != hipSuccess) return attr;
+    const int slices = (a.P + kPW - 1) / kPW;
+    hipLaunchKernelGGL(mamba_ssd_kernel, dim3(a.H * slices, batch), dim3(256), kSsdLds, stream, a);
     return hipGetLastError();
 }
 

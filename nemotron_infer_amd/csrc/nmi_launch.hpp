@@ -63,6 +63,7 @@ struct Tuning {
     int s16_r = 0;         // 16x16x32 skinny kernel: row tiles of 16 per workgroup (1, 2; 0: by rows)
     int s16_t = 0;         // 16x16x32 skinny kernel: 1 row runs (0: DMA where it fits)
     int s16_w = 0;         // 16x16x32 skinny kernel: waves per workgroup (2, 4; 0: by row tiles)
+    int mamba_scan = 0;    // Mamba-2 prefill scan: 0 chunked (MFMA), 1 the token recurrence
 };
 Tuning& tuning();
 
