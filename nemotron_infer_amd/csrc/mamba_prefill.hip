@@ -226,6 +226,25 @@ constexpr int kOffB = 0, kOffC = 16384, kOffBT = 32768, kOffXT = 49152, kOffGh =
               kOffW = kOffEcum + 256, kOffDt = kOffW + 256, kSsdLds = kOffDt + 256;
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// v shifted right by K lanes within each row of 16 (0 where the source lies before the row)
+template <int K>
+__device__ __forceinline__ float row_shr(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x110 + K, 0xf, 0xf, true));
+}
+// Inclusive prefix sum over the 64 lanes: a scan within each row of 16 by DPP row shifts, then
+// the totals of the rows before (read from lanes 15, 31, 47).
+__device__ __forceinline__ float wave_incl_sum(float v) {
+    v += row_shr<1>(v);
+    v += row_shr<2>(v);
+    v += row_shr<4>(v);
+    v += row_shr<8>(v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 15));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 47));
+    const int row = (threadIdx.x & 63) >> 4;
+    const float add = row == 0 ? 0.f : row == 1 ? r0 : row == 2 ? r0 + r1 : r0 + r1 + r2;
+    return v + add;
+}
 __device__ __forceinline__ int bc_off(int row, int c) { return row * 256 + ((c ^ (row & 15)) << 4); }
 __device__ __forceinline__ int t_off(int row, int c) { return row * 128 + ((c ^ ((row >> 1) & 7)) << 4); }
 __device__ __forceinline__ int s_off(int p, int c) { return p * 256 + ((c ^ (p & 15)) << 4); }
@@ -281,8 +300,8 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         if (tid < kQ) rdt = a.proj[(xrow0 + min(t0 + tid, S - 1)) * a.proj_ld + a.inter + a.conv_dim + h];
     };
 
-    // the state, as two 16 x 16 MFMA accumulator blocks per wave: columns n = 16 (2 wave + nb) +
-    // l16, rows p = 4 g4 + r
+    // the state, transposed, as two 16 x 16 MFMA accumulator blocks per wave: rows n = 16 (2 wave +
+    // nb) + 4 g4 + r, columns p = l16
     f32x4 st[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) st[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -294,20 +313,13 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     for (int t0 = 0; t0 < S; t0 += kQ) {
         const int nt = min(kQ, S - t0);
         // (a) the staged chunk into LDS (every wave has finished the previous chunk: barrier at the
-        // end of the loop): B row-major and transposed, C, x^T; the decay weights (wave 0)
+        // end of the loop): B and C row-major, x^T; the decay weights (wave 0)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int q = tid + 256 * u;
             const int j = q >> 4, cc = q & 15;
             *reinterpret_cast<uint4*>(lds + kOffB + bc_off(j, cc)) = rb[u];
             *reinterpret_cast<uint4*>(lds + kOffC + bc_off(j, cc)) = rc[u];
-            const uint32_t w[4] = {rb[u].x, rb[u].y, rb[u].z, rb[u].w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int n = 8 * cc + e;
-                *reinterpret_cast<uint16_t*>(lds + kOffBT + t_off(n, j >> 3) + 2 * (j & 7)) =
-                    (uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
-            }
         }
         if (tid < 2 * kQ) {
             // x^T: token j = tid / 2 of P columns 8 (tid % 2) + e (zero past the sequence)
@@ -326,13 +338,8 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             dt = dt > 20.f ? dt : (dt < -20.f ? 0.f : logf(1.f + expf(dt)));
             dt = fminf(FLT_MAX, fmaxf(0.f, dt));
             if (lane >= nt) dt = 0.f;
-            float v = fmaxf(nA2 * dt, -1e30f);
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const float u = __shfl_up(v, o);
-                if (lane >= o) v += u;
-            }
-            const float last = __shfl(v, 63);
+            const float v = wave_incl_sum(fmaxf(nA2 * dt, -1e30f));
+            const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
             cum[lane] = v;
             ecum[lane] = fexp2(v);
             wj[lane] = fexp2(last - v) * dt;
@@ -341,10 +348,11 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         if (t0 + kQ < S) gload(t0 + kQ);
         __syncthreads();
 
-        // (b) C B^T, one 32 x 32 block per wave: rows i = 32 (wave / 2) + ..., columns j = 32 (wave
-        // % 2) + l32 (register r: row 8 (r / 4) + 4 hh + r % 4); G on and below the diagonal, in two
-        // bf16 parts; and (w x)^T in two bf16 parts (thread: row p = tid / 16, tokens 4 (tid % 16)
-        // .. + 3)
+        // (b) B C^T, one 32 x 32 block per wave: columns i = 32 (wave / 2) + l32, rows j = 32 (wave
+        // % 2) + 8 (r / 4) + 4 hh + r % 4 (register r), so each group of four registers is four
+        // consecutive tokens j of one row i of G; G on and below the diagonal, in two bf16 parts
+        // (8-byte stores); B^T; and (w x)^T in two bf16 parts (thread: row p = tid / 16, tokens
+        // 4 (tid % 16) .. + 3)
         {
             const int bi = wave >> 1, bj = wave & 1;
             f32x16 cb;
@@ -352,22 +360,44 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             for (int r = 0; r < 16; ++r) cb[r] = 0.f;
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const bf16x8 af = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(32 * bi + l32, 2 * s + hh));
-                const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + kOffB + bc_off(32 * bj + l32, 2 * s + hh));
+                const bf16x8 af = *reinterpret_cast<const bf16x8*>(lds + kOffB + bc_off(32 * bj + l32, 2 * s + hh));
+                const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(32 * bi + l32, 2 * s + hh));
                 cb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, cb, 0, 0, 0);
             }
-            const int j = 32 * bj + l32;
-            const float cj = cum[j], dj = dts[j];
+            const int i = 32 * bi + l32;
+            const float ci = cum[i];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
-                const float e = fexp2(fminf(cum[i] - cj, 0.f));
-                const float gv = j <= i ? cb[r] * e * dj : 0.f;
-                const uint32_t w = pack_bf16(gv, 0.f);
-                const uint32_t lo = pack_bf16(gv - __uint_as_float(w << 16), 0.f);
-                const int off = t_off(i, j >> 3) + 2 * (j & 7);
-                *reinterpret_cast<uint16_t*>(lds + kOffGh + off) = (uint16_t)w;
-                *reinterpret_cast<uint16_t*>(lds + kOffGl + off) = (uint16_t)lo;
+            for (int k = 0; k < 4; ++k) {
+                const int j0 = 32 * bj + 8 * k + 4 * hh;
+                const f32x4 cj = *reinterpret_cast<const f32x4*>(cum + j0);
+                const f32x4 dj = *reinterpret_cast<const f32x4*>(dts + j0);
+                float gv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float d = fexp2(fminf(ci - cj[e], 0.f));
+                    gv[e] = j0 + e <= i ? cb[4 * k + e] * d * dj[e] : 0.f;
+                }
+                const uint32_t h01 = pack_bf16(gv[0], gv[1]), h23 = pack_bf16(gv[2], gv[3]);
+                const uint32_t l01 = pack_bf16(gv[0] - __uint_as_float(h01 << 16), gv[1] - __uint_as_float(h01 & 0xffff0000u));
+                const uint32_t l23 = pack_bf16(gv[2] - __uint_as_float(h23 << 16), gv[3] - __uint_as_float(h23 & 0xffff0000u));
+                const int off = t_off(i, j0 >> 3) + 2 * (j0 & 7);
+                *reinterpret_cast<uint2*>(lds + kOffGh + off) = uint2{h01, h23};
+                *reinterpret_cast<uint2*>(lds + kOffGl + off) = uint2{l01, l23};
+            }
+            // B^T rows from the row-major B: thread (n = tid % 128, token chunks 2 (tid / 128) + k,
+            // k = 0..3 of 8 tokens each) gathers 8 tokens of column n and stores 16 bytes
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int n = tid & 127, jc = 4 * (tid >> 7) + k;
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 8 * jc + 2 * e;
+                    const uint32_t lo = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j, n >> 3) + 2 * (n & 7));
+                    const uint32_t hi = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j + 1, n >> 3) + 2 * (n & 7));
+                    w[e] = lo | (hi << 16);
+                }
+                *reinterpret_cast<uint4*>(lds + kOffBT + t_off(n, jc)) = uint4{w[0], w[1], w[2], w[3]};
             }
             const int p = tid >> 4, j4 = 4 * (tid & 15);
             const uint2 xv = *reinterpret_cast<const uint2*>(lds + kOffXT + t_off(p, j4 >> 3) + 2 * (j4 & 7));
@@ -414,7 +444,8 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                 for (int r = 0; r < 4; ++r)
                     if (i0 + r < nt) yp[(size_t)r * a.y_ld] = (uint16_t)pack_bf16(__builtin_fmaf(Dh, xf[r], acc[r]), 0.f);
             }
-            // S = exp(c_63) S0 + (w x)^T B: rows p (A = (w x)^T, two parts), columns n (B = B^T rows)
+            // S^T = exp(c_63) S0^T + B^T (w x): rows n = 16 (2 wave + nb) + 4 g4 + r, columns p = l16
+            // (A = B^T rows, B = (w x)^T rows in two parts)
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
@@ -422,41 +453,36 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                 const int n = 16 * (2 * wave + nb) + l16;
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(lds + kOffWXh + t_off(l16, 4 * ks + g4));
-                    const bf16x8 al = *reinterpret_cast<const bf16x8*>(lds + kOffWXl + t_off(l16, 4 * ks + g4));
-                    const bf16x8 bb = *reinterpret_cast<const bf16x8*>(lds + kOffBT + t_off(n, 4 * ks + g4));
-                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bb, st[nb], 0, 0, 0);
-                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bb, st[nb], 0, 0, 0);
+                    const bf16x8 ab = *reinterpret_cast<const bf16x8*>(lds + kOffBT + t_off(n, 4 * ks + g4));
+                    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(lds + kOffWXh + t_off(l16, 4 * ks + g4));
+                    const bf16x8 bl = *reinterpret_cast<const bf16x8*>(lds + kOffWXl + t_off(l16, 4 * ks + g4));
+                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bh, st[nb], 0, 0, 0);
+                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bl, st[nb], 0, 0, 0);
                 }
             }
         }
         __syncthreads();
-        // (d) the new state's two bf16 parts for the next chunk (S0 was read above: barrier)
+        // (d) the new state's two bf16 parts for the next chunk (S0 was read above: barrier): four
+        // consecutive n of row p = l16 per block
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int n = 16 * (2 * wave + nb) + l16;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int pp = 4 * g4 + r;
-                const float v = st[nb][r];
-                const uint32_t w = pack_bf16(v, 0.f);
-                const uint32_t lo = pack_bf16(v - __uint_as_float(w << 16), 0.f);
-                const int off = s_off(pp, n >> 3) + 2 * (n & 7);
-                *reinterpret_cast<uint16_t*>(lds + kOffS + off) = (uint16_t)w;
-                *reinterpret_cast<uint16_t*>(lds + kOffS + 4096 + off) = (uint16_t)lo;
-            }
+            const int n0 = 16 * (2 * wave + nb) + 4 * g4;
+            const f32x4 v = st[nb];
+            const uint32_t h01 = pack_bf16(v[0], v[1]), h23 = pack_bf16(v[2], v[3]);
+            const uint32_t l01 = pack_bf16(v[0] - __uint_as_float(h01 << 16), v[1] - __uint_as_float(h01 & 0xffff0000u));
+            const uint32_t l23 = pack_bf16(v[2] - __uint_as_float(h23 << 16), v[3] - __uint_as_float(h23 & 0xffff0000u));
+            const int off = s_off(l16, n0 >> 3) + 2 * (n0 & 7);
+            *reinterpret_cast<uint2*>(lds + kOffS + off) = uint2{h01, h23};
+            *reinterpret_cast<uint2*>(lds + kOffS + 4096 + off) = uint2{l01, l23};
         }
         __syncthreads();
     }
-    if (a.ssm_state) {
+    if (a.ssm_state && l16 < pw) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int n = 16 * (2 * wave + nb) + l16;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int pp = 4 * g4 + r;
-                if (pp < pw) a.ssm_state[(((size_t)b * a.H + h) * a.P + p0 + pp) * kN + n] = st[nb][r];
-            }
+            const int n0 = 16 * (2 * wave + nb) + 4 * g4;
+            *reinterpret_cast<float4*>(a.ssm_state + (((size_t)b * a.H + h) * a.P + p0 + l16) * kN + n0) =
+                float4{st[nb][0], st[nb][1], st[nb][2], st[nb][3]};
         }
     }
 }
