@@ -10,11 +10,12 @@
 //          + dt_t B_t x_t (S_{-1} = 0), y_t = bf16(S_t . C_t + D x_t); final state S_{S-1}
 //          (ops/mamba2/ssd_scan_chunked.cuh:16-322: the same recurrence in chunked matrix form,
 //          its matrix products in TF32).
-// The scan here is the recurrence itself, in float32 throughout: one workgroup per (sequence,
-// head, 8 rows of P), a 32-lane half-wave per row holding the row's N = 128 states (4 per lane),
-// tokens in chunks of 64 staged in LDS (B and C of the head's group, x, dt and the decay), the
-// next chunk's loads issued before the current chunk is scanned.  Per token and row: 4 state
-// FMAs, 4 output FMAs and a 32-lane sum; parallel over B x H x P rows (7680 at the model's size).
+// The scan runs in that chunked form by default (mamba_ssd_kernel, on bf16 MFMA with two-part
+// operands; described at the kernel), or as the recurrence itself in float32 (mamba_scan_kernel,
+// tuning knob mamba.scan = 1): one workgroup per (sequence, head, 8 rows of P), a 32-lane
+// half-wave per row holding the row's N = 128 states (4 per lane), tokens in chunks staged in LDS
+// (B and C of the head's group, x, dt and the decay), the next chunk's loads issued before the
+// current chunk is scanned; per token and row 4 state FMAs, 4 output FMAs and a 32-lane sum.
 #include "nmi_device.hpp"
 #include "nmi_launch.hpp"
 

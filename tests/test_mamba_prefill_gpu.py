@@ -20,7 +20,7 @@ import numpy as np
 import pytest
 import torch
 
-from nemotron_infer_amd import ops, synth
+from nemotron_infer_amd import _lib, ops, synth
 from oracle import block, linear, mamba
 from tests.gpu_util import DEV, announce, bits, s_to_dev, w_to_dev, x_to_dev
 from tests.test_mamba_gpu import G, H, HIDDEN, INTER, N, P, PROJ, CONV_DIM, EPS, _bf16_np, _check_state, _params
@@ -201,3 +201,51 @@ def test_mamba_forward_batch_and_decode_continuation():
     torch.cuda.synchronize()
     r = linear.parity(bits(a1), bits(a2))
     assert r["nan_ok"] and r["rel_l2_all"] <= 4e-3, ("next decode step", r)
+
+
+@pytest.mark.parametrize("P_,S_", [(24, 130), (8, 64), (40, 1)])
+def test_mamba_forward_chunked_scan_partial_slices(P_, S_):
+    """The chunked scan (default) at head dims that leave a partial 16-row slice (24 = 16 + 8, 8,
+    40 = 16 + 16 + 8) and sequence lengths that end mid-chunk, two sequences per call: the final
+    SSM states within the state bar and the output end to end (rel_l2 <= 4e-3) against the
+    oracle per sequence, and the token recurrence (tuning knob mamba.scan = 1) on the same call
+    within the same bars of the chunked one."""
+    H_, G_, N_, HID = 8, 2, 128, 256
+    INTER_ = H_ * P_
+    CONV_ = INTER_ + 2 * G_ * N_
+    PROJ_ = INTER_ + CONV_ + H_
+    announce("mamba_forward_chunked", P_, S_)
+    iw, isc = synth.make_weight(PROJ_, HID, 9100 + P_, "cpu")
+    ow, osc = synth.make_weight(HID, INTER_, 9101 + P_, "cpu")
+    rng = np.random.default_rng(9102 + P_)
+    f = np.float32
+    prm = dict(conv_w=(rng.standard_normal((CONV_, 4)) * 0.3).astype(f), conv_b=(rng.standard_normal(CONV_) * 0.1).astype(f),
+               A_log=rng.uniform(-1.0, 1.5, H_).astype(f), D=rng.standard_normal(H_).astype(f),
+               dt_bias=(rng.standard_normal(H_) * 0.5).astype(f), gnorm_w=(1 + 0.1 * rng.standard_normal(INTER_)).astype(f))
+    norm = (1.0 + 0.1 * rng.standard_normal(HID)).astype(f)
+    dw = (torch.from_numpy(norm).to(DEV), w_to_dev(iw.numpy()), s_to_dev(isc.numpy()),
+          *[torch.from_numpy(prm[k]).to(DEV) for k in ("conv_w", "conv_b", "A_log", "D", "dt_bias", "gnorm_w")],
+          w_to_dev(ow.numpy()), s_to_dev(osc.numpy()))
+    x = _bf16_np((2 * S_, HID), 9103 + P_)
+    xd = x_to_dev(x)
+    res = {}
+    try:
+        for form in (0, 1):
+            _lib.tuning_set("mamba.scan", form)
+            ss = torch.zeros((2, H_, P_, N_), device=DEV)
+            out = ops.mamba_forward_fp8(xd, *dw, H_, P_, G_, batch=2, ssm_state_out=ss, eps=EPS)
+            torch.cuda.synchronize()
+            res[form] = (bits(out), ss.cpu().numpy())
+    finally:
+        _lib.tuning_set("mamba.scan", 0)
+    for b in range(2):
+        rows = slice(b * S_, (b + 1) * S_)
+        ref, _, ssr = mamba.mamba_forward_block_fp8(x[rows], norm, iw.numpy(), isc.numpy(), prm["conv_w"], prm["conv_b"],
+                                                    prm["A_log"], prm["D"], prm["dt_bias"], prm["gnorm_w"], ow.numpy(),
+                                                    osc.numpy(), H_, P_, G_, N_, EPS)
+        for form in (0, 1):
+            out, ss = res[form]
+            _check_state(ss[b:b + 1], ssr, f"ssm state P={P_} S={S_} seq {b} scan form {form}")
+            r = linear.parity(out[rows], ref)
+            assert r["nan_ok"] and r["rel_l2_all"] <= 4e-3, (f"P={P_} S={S_} seq {b} scan form {form}", r)
+    _check_state(res[0][1], res[1][1], f"chunked vs recurrence P={P_} S={S_}")
