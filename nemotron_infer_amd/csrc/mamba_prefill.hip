@@ -29,41 +29,50 @@ constexpr int kN = kMambaDState;       // 128
 constexpr int kConvK = kMambaConvK;    // 4
 constexpr int kRowsPerWg = 8;          // SSM rows (p) per workgroup: 4 waves x 2 half-waves
 constexpr int kTC = 32;                // tokens per staged chunk
-constexpr int kConvT = 64;             // tokens per conv thread
+constexpr int kConvT = 16;             // tokens per conv thread
 
 __device__ __forceinline__ float silu(float v) { return v / (1.f + expf(-v)); }
 
-// One thread per (channel, 64-token run): the conv with a 3-value window, SiLU, bf16.
+// One thread per (channel, 16-token run): the conv with a 3-value window, SiLU, bf16.  The run's
+// 19 inputs (3 before it) are all loaded before the first output is formed, so a thread waits for
+// one memory round trip rather than one per token.
 __global__ __launch_bounds__(256) void mamba_conv_prefill_kernel(const MambaPrefillArgs a) {
     const int c = blockIdx.x * 256 + threadIdx.x;
     const int t0 = blockIdx.y * kConvT;
     const int b = blockIdx.z;
     if (c >= a.conv_dim || t0 >= a.S) return;
-    const int t1 = min(t0 + kConvT, a.S);
+    const int n = min(kConvT, a.S - t0);
     const uint16_t* xin = a.proj + (size_t)b * a.S * a.proj_ld + a.inter + c;   // column c of xBC
     uint16_t* out = a.xc + (size_t)b * a.S * a.xc_ld + c;
     const float4 w = *reinterpret_cast<const float4*>(a.conv_w + (size_t)c * kConvK);
     const float bias = a.conv_b[c];
-    float s0 = t0 >= 3 ? bf16_to_f32(xin[(size_t)(t0 - 3) * a.proj_ld]) : 0.f;
-    float s1 = t0 >= 2 ? bf16_to_f32(xin[(size_t)(t0 - 2) * a.proj_ld]) : 0.f;
-    float s2 = t0 >= 1 ? bf16_to_f32(xin[(size_t)(t0 - 1) * a.proj_ld]) : 0.f;
-    for (int t = t0; t < t1; ++t) {
-        const float xt = bf16_to_f32(xin[(size_t)t * a.proj_ld]);
-        float acc = bias;
-        acc = __builtin_fmaf(w.x, s0, acc);
-        acc = __builtin_fmaf(w.y, s1, acc);
-        acc = __builtin_fmaf(w.z, s2, acc);
-        acc = __builtin_fmaf(w.w, xt, acc);
-        out[(size_t)t * a.xc_ld] = f32_to_bf16_rne(silu(acc));
-        s0 = s1;
-        s1 = s2;
-        s2 = xt;
+    float v[kConvT + 3];                                        // tokens t0 - 3 .. t0 + kConvT - 1
+#pragma unroll
+    for (int k = 0; k < kConvT + 3; ++k) {
+        const int t = t0 - 3 + k;
+        v[k] = (t >= 0 && k < n + 3) ? bf16_to_f32(xin[(size_t)t * a.proj_ld]) : 0.f;
     }
-    if (t1 == a.S && a.conv_state) {
+#pragma unroll
+    for (int k = 0; k < kConvT; ++k) {
+        if (k >= n) break;
+        float acc = bias;
+        acc = __builtin_fmaf(w.x, v[k], acc);
+        acc = __builtin_fmaf(w.y, v[k + 1], acc);
+        acc = __builtin_fmaf(w.z, v[k + 2], acc);
+        acc = __builtin_fmaf(w.w, v[k + 3], acc);
+        out[(size_t)(t0 + k) * a.xc_ld] = f32_to_bf16_rne(silu(acc));
+    }
+    if (t0 + n == a.S && a.conv_state) {
         float* st = a.conv_state + ((size_t)b * a.conv_dim + c) * (kConvK - 1);
-        st[0] = s0;
-        st[1] = s1;
-        st[2] = s2;
+        // the last three inputs: tokens S - 3 .. S - 1 (zero before the sequence)
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+            float val = 0.f;
+#pragma unroll
+            for (int k = 0; k < kConvT + 3; ++k)
+                if (k == n + e) val = v[k];
+            st[e] = val;
+        }
     }
 }
 
