@@ -293,7 +293,7 @@ def bench_prefill(dev, reps=20):
         del w, s, x, y, g
     tf = tot_f / (tot_ms * 1e-3) / 1e12
     return {"workload": "config3_prefill_m2048", "tflops": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_dma_kernel (4 waves, 256x256 tiles, DMA-fed LDS; stream-K when tiles < CUs / 2)",
+            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "kernel": "gemm_fp8_w8a16_dma_kernel (4 waves, 256x256 or 128x256 tiles by round count, DMA-fed LDS)",
             "shapes": out}
 
 

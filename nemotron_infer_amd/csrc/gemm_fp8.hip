@@ -1162,14 +1162,20 @@ hipError_t launch_dma_groups(const uint16_t* x, int64_t ldx, const GemvGroup* g,
     a.per_xcd = (T + 7) / 8;
     const int G = device_info().num_cu;             // one 144 KiB workgroup per CU
     const int gh_knob = tuning().gemm_gh;
-    // Where the 256 x 256 tiles cover at most half of the CUs, 128 x 256 tiles (at most twice as
-    // many, one round) give each workgroup a whole tile with the same MFMA work as half a tile
-    // of the stream-K form, without its partial-tile exchange (tuning knob gemm.bm: 128 forces
-    // them, 256 forbids them; gemm.sk = 1 keeps stream-K).  Measured on MI355X (same box):
-    // down_proj at M = 2048 (208 tiles of 128 x 256) 146.3 against 168.8 us in stream-K form;
-    // attention block at S = 2048 250 against 296 us; Mamba block at S = 512 336 against 376 us.
+    // 128 x 256 tiles where they finish sooner: with one workgroup per CU a grid of t tiles takes
+    // ceil(t / CUs) rounds, and a 128-row tile costs 0.525 of a 256-row one (its MFMA rate measured
+    // 4-5% lower: down_proj at M = 2048 1152 against 1208 TFLOP/s).  That takes them where the
+    // 256-row tiles cover at most half the CUs -- each workgroup then has a whole tile with the
+    // same MFMA work as half a tile of the stream-K form, without its partial-tile exchange:
+    // down_proj at M = 2048 (208 tiles) 146.3 against 168.8 us in stream-K form, attention block at
+    // S = 2048 250 against 296 us, Mamba block at S = 512 336 against 376 us -- and where the
+    // 256-row tiles leave a short last round: the Mamba in_proj at M = 2048 (552 tiles, 3 rounds,
+    // against 1104 in 5) took the block 531 -> 524 us.  Tuning knob gemm.bm: 128 forces them, 256
+    // forbids them; gemm.sk = 1 keeps stream-K.
     const int bm_knob = tuning().gemm_bm;
-    if (bm_knob != 256 && tuning().gemm_sk != 1 && (bm_knob == 128 || 2 * (int64_t)T <= G)) {
+    const int64_t T128 = (int64_t)((M + 127) / 128) * a.tiles_n;
+    const bool short_tiles = 21 * ((T128 + G - 1) / G) < 40 * (((int64_t)T + G - 1) / G);
+    if (bm_knob != 256 && tuning().gemm_sk != 1 && (bm_knob == 128 || short_tiles)) {
         const auto kernel128 =
             grouped ? &gemm_fp8_w8a16_dma_kernel<false, true, 128> : &gemm_fp8_w8a16_dma_kernel<false, false, 128>;
         a.tiles_m = (M + 127) / 128;
