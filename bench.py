@@ -511,8 +511,8 @@ def bench_mlp_block(dev, reps=5):
     return {"workload": "mlp_forward_fp8 block (hidden 3136, inter 12544)",
             "decode_m1": {"bytes": blk_bytes, "weight_copies_rotated": R, **res},
             "prefill_m2048": {"us": round(t * 1e3, 1), "TFLOP/s": round(fl / (t * 1e-3) / 1e12, 1),
-                              "launches": 4,
-                              "steps": "rmsnorm; stream-K flag clear; up GEMM + relu^2; down GEMM (stream-K) + residual"}}
+                              "launches": 3,
+                              "steps": "rmsnorm; up GEMM + relu^2; down GEMM (128 x 256 tiles) + residual"}}
 
 
 def bench_attn_decode(dev, reps=5):

@@ -76,8 +76,9 @@ struct FwdLayout {
     size_t gemm, normed, q, k, v, o, vt, total;
 };
 
-// The GEMMs' region (stream-K flags and partials from M = 512, the short-prompt kernel's K-split
-// partials below): the largest of the q, k, v (launched one by one on the GEMM path) and o needs.
+// The GEMMs' region (the short-prompt kernel's K-split partials below M = 512; from 512 the
+// stream-K flags and partials where that form is forced by tuning knob, else nothing):
+// the largest of the q, k, v (launched one by one on the GEMM path) and o needs.
 size_t gemm_region(int M, int hidden, int QD, int KD) {
     if (choose_path(M) != Path::Gemm) return 0;
     const size_t qkv = std::max(linear_workspace_bytes(M, (int64_t)QD + 2 * (int64_t)KD, hidden),

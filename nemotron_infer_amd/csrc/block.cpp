@@ -9,9 +9,10 @@
 // 16x16x32 skinny kernel does not take it) the RMSNorm is applied while that kernel stages its
 // activations -- two launches and one [M, inter] buffer.  Otherwise the RMSNorm is its own
 // launch (rmsnorm.hip) into a second buffer.  On the GEMM
-// path (M > 16) the workspace also holds the GEMMs' region: from M = 512 the stream-K flags and
-// partial tiles, whose flags one small kernel zeroes at the start of every call; below, the
-// short-prompt kernel's K-split partials (which need no initialisation).
+// path (M > 16) the workspace also holds the GEMMs' region: below M = 512 the short-prompt
+// kernel's K-split partials (which need no initialisation); from M = 512 nothing unless the
+// stream-K form is forced (tuning knob gemm.sk = 1 or gemm.bm = 256), whose flags and partial
+// tiles one small kernel zeroes at the start of every call.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>

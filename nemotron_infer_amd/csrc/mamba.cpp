@@ -70,8 +70,9 @@ struct FwdLayout {
     int64_t xc_ld;
 };
 
-// The GEMMs' region (stream-K flags and partials from M = 512, the short-prompt kernel's K-split
-// partials below): the larger of the in_proj and out_proj needs.
+// The GEMMs' region (the short-prompt kernel's K-split partials below M = 512; from 512 the
+// stream-K flags and partials where that form is forced by tuning knob, else nothing):
+// the larger of the in_proj and out_proj needs.
 size_t gemm_region(int M, int hidden, const MambaDims& d) {
     if (choose_path(M) != Path::Gemm) return 0;
     return round256(std::max(linear_workspace_bytes(M, d.proj, hidden), linear_workspace_bytes(M, hidden, d.inter)));
