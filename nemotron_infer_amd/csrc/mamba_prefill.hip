@@ -76,6 +76,73 @@ __global__ __launch_bounds__(256) void mamba_conv_prefill_kernel(const MambaPref
     }
 }
 
+// SiLU from the hardware exp2 and reciprocal (a few float32 ulp from v / (1 + exp(-v)); the
+// result is rounded to bf16): -inf and +inf limits hold (exp2 overflows to inf, its reciprocal to 0).
+__device__ __forceinline__ float silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * v));
+}
+
+// Vector form (row strides and the xBC column offset 16-byte aligned): one thread per (8
+// channels, 16-token run), 16-byte loads and stores of 8 channels; the run's 19 input rows are
+// all loaded before the first output is formed.
+__global__ __launch_bounds__(256) void mamba_conv_prefill_vec_kernel(const MambaPrefillArgs a) {
+    const int c0 = 8 * (int)(blockIdx.x * 256 + threadIdx.x);
+    const int t0 = blockIdx.y * kConvT;
+    const int b = blockIdx.z;
+    if (c0 >= a.conv_dim || t0 >= a.S) return;
+    const int n = min(kConvT, a.S - t0);
+    const uint16_t* xin = a.proj + (size_t)b * a.S * a.proj_ld + a.inter + c0;
+    uint16_t* out = a.xc + (size_t)b * a.S * a.xc_ld + c0;
+    uint4 v[kConvT + 3];                                        // tokens t0 - 3 .. t0 + kConvT - 1
+#pragma unroll
+    for (int k = 0; k < kConvT + 3; ++k) {
+        const int t = t0 - 3 + k;
+        v[k] = (t >= 0 && k < n + 3) ? load16(xin + (size_t)t * a.proj_ld) : uint4{0u, 0u, 0u, 0u};
+    }
+    float w[8][4], bias[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float4 wv = *reinterpret_cast<const float4*>(a.conv_w + (size_t)(c0 + e) * kConvK);
+        w[e][0] = wv.x; w[e][1] = wv.y; w[e][2] = wv.z; w[e][3] = wv.w;
+        bias[e] = a.conv_b[c0 + e];
+    }
+    auto ch = [](const uint4& q, int e) {                       // channel e of a row of 8
+        const uint32_t d = e < 2 ? q.x : e < 4 ? q.y : e < 6 ? q.z : q.w;
+        return e & 1 ? bf16hi_to_f32(d) : bf16lo_to_f32(d);
+    };
+#pragma unroll
+    for (int k = 0; k < kConvT; ++k) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float acc = bias[e];
+            acc = __builtin_fmaf(w[e][0], ch(v[k], e), acc);
+            acc = __builtin_fmaf(w[e][1], ch(v[k + 1], e), acc);
+            acc = __builtin_fmaf(w[e][2], ch(v[k + 2], e), acc);
+            acc = __builtin_fmaf(w[e][3], ch(v[k + 3], e), acc);
+            o[e] = silu_fast(acc);
+        }
+        if (k < n)
+            *reinterpret_cast<uint4*>(out + (size_t)(t0 + k) * a.xc_ld) =
+                uint4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])};
+    }
+    if (t0 + n == a.S && a.conv_state) {
+        // the last three inputs of each channel: tokens S - 3 .. S - 1 (zero before the sequence),
+        // read again (picking them from v by a run-time index would put v in scratch memory)
+        uint4 last[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int t = a.S - 3 + j;
+            last[j] = t >= 0 ? load16(xin + (size_t)t * a.proj_ld) : uint4{0u, 0u, 0u, 0u};
+        }
+        float* st = a.conv_state + ((size_t)b * a.conv_dim + c0) * (kConvK - 1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) st[3 * e + j] = ch(last[j], e);
+    }
+}
+
 // Scan: one workgroup per (sequence, head, 8 rows of P), a 32-lane half-wave per row with the
 // row's N = 128 float32 states (4 per lane).  Tokens go in chunks of kTC = 32 staged in LDS: dt
 // (softplus) and the decay per token, then dt.B and C in float32 (each computed once per chunk
@@ -500,8 +567,15 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
 }  // namespace
 
 hipError_t launch_mamba_prefill_mixer(const MambaPrefillArgs& a, int batch, hipStream_t stream) {
-    hipLaunchKernelGGL(mamba_conv_prefill_kernel, dim3((a.conv_dim + 255) / 256, (a.S + kConvT - 1) / kConvT, batch),
-                       dim3(256), 0, stream, a);
+    const bool vec = a.conv_dim % 8 == 0 && a.inter % 8 == 0 && a.proj_ld % 8 == 0 && a.xc_ld % 8 == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.proj) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.xc) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.conv_w) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL(mamba_conv_prefill_vec_kernel,
+                           dim3((a.conv_dim / 8 + 255) / 256, (a.S + kConvT - 1) / kConvT, batch), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(mamba_conv_prefill_kernel, dim3((a.conv_dim + 255) / 256, (a.S + kConvT - 1) / kConvT, batch),
+                           dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (tuning().mamba_scan == 1) {
