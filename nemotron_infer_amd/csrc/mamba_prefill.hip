@@ -300,7 +300,7 @@ constexpr int kPW = 16;                // rows of P per workgroup
 // (chunk at c ^ (p & 15)); per-token float32 arrays.
 constexpr int kOffB = 0, kOffC = 16384, kOffBT = 32768, kOffXT = 49152, kOffGh = 51200, kOffGl = 59392,
               kOffWXh = 67584, kOffWXl = 69632, kOffS = 71680, kOffCum = 79872, kOffEcum = kOffCum + 256,
-              kOffW = kOffEcum + 256, kOffDt = kOffW + 256, kSsdLds = kOffDt + 256;
+              kOffW = kOffEcum + 256, kOffDt = kOffW + 256, kOffFd = kOffDt + 256, kSsdLds = kOffFd + 256;
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // v shifted right by K lanes within each row of 16 (0 where the source lies before the row)
@@ -346,6 +346,7 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     float* ecum = reinterpret_cast<float*>(lds + kOffEcum);      // exp(c_j)
     float* wj = reinterpret_cast<float*>(lds + kOffW);           // exp(c_63 - c_j) dt_j
     float* dts = reinterpret_cast<float*>(lds + kOffDt);
+    float* fd = reinterpret_cast<float*>(lds + kOffFd);          // exp(-c_j) dt_j (where finite)
 
     // chunk staging in registers (the next chunk's loads are in flight during this one): B and C
     // rows (1024 chunks of 16 B each: 4 per thread), x (threads < 128: token tid / 2, P columns
@@ -421,16 +422,20 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             ecum[lane] = fexp2(v);
             wj[lane] = fexp2(last - v) * dt;
             dts[lane] = dt;
+            fd[lane] = fexp2(-v) * dt;
         }
         if (t0 + kQ < S) gload(t0 + kQ);
         __syncthreads();
 
-        // (b) B C^T, one 32 x 32 block per wave: columns i = 32 (wave / 2) + l32, rows j = 32 (wave
-        // % 2) + 8 (r / 4) + 4 hh + r % 4 (register r), so each group of four registers is four
-        // consecutive tokens j of one row i of G; G on and below the diagonal, in two bf16 parts
-        // (8-byte stores); B^T; and (w x)^T in two bf16 parts (thread: row p = tid / 16, tokens
-        // 4 (tid % 16) .. + 3)
-        {
+        // (b) B C^T in 32 x 32 blocks: wave 0 (i, j < 32), 2 (i >= 32 > j) and 3 (i, j >= 32) take
+        // one each -- columns i = 32 (wave / 2) + l32, rows j = 32 (wave % 2) + 8 (r / 4) + 4 hh +
+        // r % 4 (register r), so each group of four registers is four consecutive tokens j of one
+        // row i of G -- and form G on and below the diagonal in two bf16 parts (8-byte stores);
+        // the block above the diagonal is zero and never read.  Where the chunk's decay stays
+        // above 2^-100, exp(c_i - c_j) = exp(c_i) exp(-c_j) with both factors finite.  Every
+        // thread then moves 32 elements of B into B^T and forms 4 elements of (w x)^T in two bf16
+        // parts (row p = tid / 16, tokens 4 (tid % 16) .. + 3).
+        if (wave != 1) {
             const int bi = wave >> 1, bj = wave & 1;
             f32x16 cb;
 #pragma unroll
@@ -442,17 +447,24 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                 cb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, cb, 0, 0, 0);
             }
             const int i = 32 * bi + l32;
-            const float ci = cum[i];
+            const float ci = cum[i], ei = ecum[i];
+            const bool fact = cum[kQ - 1] > -100.f;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int j0 = 32 * bj + 8 * k + 4 * hh;
-                const f32x4 cj = *reinterpret_cast<const f32x4*>(cum + j0);
-                const f32x4 dj = *reinterpret_cast<const f32x4*>(dts + j0);
                 float gv[4];
+                if (fact) {
+                    const f32x4 fj = *reinterpret_cast<const f32x4*>(fd + j0);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float d = fexp2(fminf(ci - cj[e], 0.f));
-                    gv[e] = j0 + e <= i ? cb[4 * k + e] * d * dj[e] : 0.f;
+                    for (int e = 0; e < 4; ++e) gv[e] = j0 + e <= i ? cb[4 * k + e] * ei * fj[e] : 0.f;
+                } else {
+                    const f32x4 cj = *reinterpret_cast<const f32x4*>(cum + j0);
+                    const f32x4 dj = *reinterpret_cast<const f32x4*>(dts + j0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float d = fexp2(fminf(ci - cj[e], 0.f));
+                        gv[e] = j0 + e <= i ? cb[4 * k + e] * d * dj[e] : 0.f;
+                    }
                 }
                 const uint32_t h01 = pack_bf16(gv[0], gv[1]), h23 = pack_bf16(gv[2], gv[3]);
                 const uint32_t l01 = pack_bf16(gv[0] - __uint_as_float(h01 << 16), gv[1] - __uint_as_float(h01 & 0xffff0000u));
@@ -461,21 +473,23 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                 *reinterpret_cast<uint2*>(lds + kOffGh + off) = uint2{h01, h23};
                 *reinterpret_cast<uint2*>(lds + kOffGl + off) = uint2{l01, l23};
             }
-            // B^T rows from the row-major B: thread (n = tid % 128, token chunks 2 (tid / 128) + k,
-            // k = 0..3 of 8 tokens each) gathers 8 tokens of column n and stores 16 bytes
+        }
+        // B^T rows from the row-major B: thread (n = tid % 128, token chunks 4 (tid / 128) + k,
+        // k = 0..3 of 8 tokens each) gathers 8 tokens of column n and stores 16 bytes
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int n = tid & 127, jc = 4 * (tid >> 7) + k;
-                uint32_t w[4];
+        for (int k = 0; k < 4; ++k) {
+            const int n = tid & 127, jc = 4 * (tid >> 7) + k;
+            uint32_t w[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 8 * jc + 2 * e;
-                    const uint32_t lo = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j, n >> 3) + 2 * (n & 7));
-                    const uint32_t hi = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j + 1, n >> 3) + 2 * (n & 7));
-                    w[e] = lo | (hi << 16);
-                }
-                *reinterpret_cast<uint4*>(lds + kOffBT + t_off(n, jc)) = uint4{w[0], w[1], w[2], w[3]};
+            for (int e = 0; e < 4; ++e) {
+                const int j = 8 * jc + 2 * e;
+                const uint32_t lo = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j, n >> 3) + 2 * (n & 7));
+                const uint32_t hi = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j + 1, n >> 3) + 2 * (n & 7));
+                w[e] = lo | (hi << 16);
             }
+            *reinterpret_cast<uint4*>(lds + kOffBT + t_off(n, jc)) = uint4{w[0], w[1], w[2], w[3]};
+        }
+        {
             const int p = tid >> 4, j4 = 4 * (tid & 15);
             const uint2 xv = *reinterpret_cast<const uint2*>(lds + kOffXT + t_off(p, j4 >> 3) + 2 * (j4 & 7));
             const f32x4 wv = *reinterpret_cast<const f32x4*>(wj + j4);
@@ -506,6 +520,7 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             for (int r = 0; r < 4; ++r) acc[r] *= ecum[16 * wave + 4 * g4 + r];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
+                if (ks == 1 && wave < 2) break;                     // rows i < 32: G is zero at j >= 32
                 const bf16x8 ah = *reinterpret_cast<const bf16x8*>(lds + kOffGh + t_off(16 * wave + l16, 4 * ks + g4));
                 const bf16x8 al = *reinterpret_cast<const bf16x8*>(lds + kOffGl + t_off(16 * wave + l16, 4 * ks + g4));
                 const bf16x8 bx = *reinterpret_cast<const bf16x8*>(lds + kOffXT + t_off(l16, 4 * ks + g4));
