@@ -336,8 +336,8 @@ int nmi_attn_decode_fp8(const void* input_bf16, const float* norm_w, const void*
  * [H, S, 128] and its block transposes around it): q, o [S, >= n_heads*128] with head h at
  * column 128 h, k, v [S, >= n_kv_heads*128]; row strides ldq, ldk, ldv (multiples of 8) and ldo
  * (multiple of 4) in elements.  q, k, v 16-byte aligned, o 8-byte aligned.
- * workspace: nmi_sdpa_prefill_workspace_bytes(n_kv_heads, S) bytes (a transposed copy of v),
- * 16-byte aligned; NULL takes it from the bump allocator.  Two launches.
+ * No workspace: nmi_sdpa_prefill_workspace_bytes returns 0 and the workspace arguments are
+ * ignored (kept so that callers written against a sized workspace need no change).  One launch.
  */
 size_t nmi_sdpa_prefill_workspace_bytes(int n_kv_heads, int S);
 int nmi_sdpa_prefill_bf16(const void* q_bf16, int64_t ldq, const void* k_bf16, int64_t ldk, const void* v_bf16,

@@ -71,9 +71,9 @@ AttnLayout attn_layout(int hidden, int n_heads, int n_kv, int S_cache) {
 }
 
 // Prefill block workspace: the GEMMs' stream-K region (S >= 512), normed [S, hidden], q
-// [S, H*128], k and v [S, H_KV*128], o [S, H*128], V^T [H_KV, 128, ldvt].
+// [S, H*128], k and v [S, H_KV*128], o [S, H*128].
 struct FwdLayout {
-    size_t gemm, normed, q, k, v, o, vt, total;
+    size_t gemm, normed, q, k, v, o, total;
 };
 
 // The GEMMs' region (the short-prompt kernel's K-split partials below M = 512; from 512 the
@@ -95,8 +95,7 @@ FwdLayout fwd_layout(int S, int hidden, int n_heads, int n_kv) {
     L.k = L.q + round256((size_t)S * QD * 2);
     L.v = L.k + round256((size_t)S * KD * 2);
     L.o = L.v + round256((size_t)S * KD * 2);
-    L.vt = L.o + round256((size_t)S * QD * 2);
-    L.total = L.vt + round256((size_t)n_kv * kSdpaHead * sdpa_prefill_vt_ld(S) * 2);
+    L.total = L.o + round256((size_t)S * QD * 2);
     return L;
 }
 
@@ -107,8 +106,9 @@ bool heads_ok(int n_heads, int n_kv) { return n_kv >= 1 && n_heads >= n_kv && n_
 extern "C" {
 
 size_t nmi_sdpa_prefill_workspace_bytes(int n_kv_heads, int S) {
-    if (n_kv_heads < 1 || S < 1) return 0;
-    return (size_t)n_kv_heads * kSdpaHead * sdpa_prefill_vt_ld(S) * 2;
+    (void)n_kv_heads;
+    (void)S;
+    return 0;                                  // the kernel reads q, k and v as they are
 }
 
 int nmi_sdpa_prefill_bf16(const void* q_bf16, int64_t ldq, const void* k_bf16, int64_t ldk, const void* v_bf16,
@@ -130,25 +130,12 @@ int nmi_sdpa_prefill_bf16(const void* q_bf16, int64_t ldq, const void* k_bf16, i
         return fail(NMI_ERR_ALIGNMENT,
                     "nmi_sdpa_prefill_bf16: q, k, v must be 16-byte aligned with row strides multiple of 8 elements; "
                     "o 8-byte aligned with a row stride multiple of 4");
-    const size_t need = nmi_sdpa_prefill_workspace_bytes(n_kv_heads, S);
-    if (workspace) {
-        if (!aligned(workspace, 16))
-            return fail(NMI_ERR_ALIGNMENT, "nmi_sdpa_prefill_bf16: workspace must be 16-byte aligned");
-        if (workspace_bytes < need) {
-            set_last_error("%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
-            return NMI_ERR_WORKSPACE;
-        }
-    } else {
-        const int rc = nmi_alloc(need, &workspace);
-        if (rc != NMI_OK) return rc;
-    }
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    uint16_t* vt = static_cast<uint16_t*>(workspace);
-    hipError_t e = launch_kv_layout(static_cast<const uint16_t*>(k_bf16), ldk, static_cast<const uint16_t*>(v_bf16), ldv,
-                                    vt, S, n_kv_heads, nullptr, nullptr, 0, st);
-    if (e == hipSuccess)
-        e = launch_sdpa_prefill(static_cast<const uint16_t*>(q_bf16), ldq, static_cast<const uint16_t*>(k_bf16), ldk, vt,
-                                static_cast<uint16_t*>(o_bf16), ldo, S, n_heads, n_kv_heads, st);
+    (void)workspace;                           // no workspace: nmi_sdpa_prefill_workspace_bytes is 0
+    (void)workspace_bytes;
+    const hipError_t e = launch_sdpa_prefill(static_cast<const uint16_t*>(q_bf16), ldq,
+                                             static_cast<const uint16_t*>(k_bf16), ldk,
+                                             static_cast<const uint16_t*>(v_bf16), ldv, static_cast<uint16_t*>(o_bf16),
+                                             ldo, S, n_heads, n_kv_heads, static_cast<hipStream_t>(stream));
     return hip_status(e, fn);
 }
 
@@ -209,7 +196,6 @@ int nmi_attn_forward_fp8(const void* input_bf16, const float* norm_w, const void
     uint16_t* k = reinterpret_cast<uint16_t*>(base + lay.k);
     uint16_t* v = reinterpret_cast<uint16_t*>(base + lay.v);
     uint16_t* o = reinterpret_cast<uint16_t*>(base + lay.o);
-    uint16_t* vt = reinterpret_cast<uint16_t*>(base + lay.vt);
     hipError_t e = hipSuccess;
     if (gws && gemm_workspace_has_flags(S)) e = launch_sk_flags_clear(gemm_ws, st);   // the workspace may hold anything
     if (e != hipSuccess) return hip_status(e, fn);
@@ -228,10 +214,11 @@ int nmi_attn_forward_fp8(const void* input_bf16, const float* norm_w, const void
         if (e == hipSuccess) e = dispatch_linear(normed, hidden, S, hidden, qkv, 3, gemm_ws, gws, st);
     }
     if (e != hipSuccess) return hip_status(e, fn);
-    // V^T (and the caches), causal attention
-    e = launch_kv_layout(k, KD, v, KD, vt, S, n_kv_heads, caches ? static_cast<uint16_t*>(k_cache_bf16) : nullptr,
-                         caches ? static_cast<uint16_t*>(v_cache_bf16) : nullptr, cap, st);
-    if (e == hipSuccess) e = launch_sdpa_prefill(q, QD, k, KD, vt, o, QD, S, n_heads, n_kv_heads, st);
+    // the caches, causal attention
+    if (caches)
+        e = launch_kv_cache(k, KD, v, KD, S, n_kv_heads, static_cast<uint16_t*>(k_cache_bf16),
+                            static_cast<uint16_t*>(v_cache_bf16), cap, st);
+    if (e == hipSuccess) e = launch_sdpa_prefill(q, QD, k, KD, v, KD, o, QD, S, n_heads, n_kv_heads, st);
     if (e != hipSuccess) return hip_status(e, fn);
     // out = bf16(input + bf16(o_proj(o)))
     GemvGroup og{static_cast<const uint8_t*>(o_w_e4m3), QD, o_scale, static_cast<uint16_t*>(out_bf16), hidden, hidden,

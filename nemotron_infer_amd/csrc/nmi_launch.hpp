@@ -284,14 +284,13 @@ struct MambaPrefillArgs {
 };
 hipError_t launch_mamba_prefill_mixer(const MambaPrefillArgs& a, int batch, hipStream_t stream);
 
-// Causal attention over a prompt (sdpa_prefill.hip), token-major q [S, ldq], k [S, ldk], o
-// [S, ldo] (head h at column 128 h), V through V^T [H_KV, 128, sdpa_prefill_vt_ld(S)] written by
-// launch_kv_layout (which also fills the KV caches [H_KV, cap, 128] when given).
-int64_t sdpa_prefill_vt_ld(int S);
-hipError_t launch_kv_layout(const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, uint16_t* vt, int S,
-                            int H_KV, uint16_t* k_cache, uint16_t* v_cache, int cap, hipStream_t stream);
-hipError_t launch_sdpa_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k, int64_t ldk, const uint16_t* vt,
-                               uint16_t* o, int64_t ldo, int S, int H, int H_KV, hipStream_t stream);
+// Causal attention over a prompt (sdpa_prefill.hip), token-major q [S, ldq], k [S, ldk], v
+// [S, ldv], o [S, ldo] (head h at column 128 h); one launch, no workspace.  launch_kv_cache fills the
+// KV caches [H_KV, cap, 128] positions [0, S) from k and v.
+hipError_t launch_kv_cache(const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, int S, int H_KV,
+                           uint16_t* k_cache, uint16_t* v_cache, int cap, hipStream_t stream);
+hipError_t launch_sdpa_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k, int64_t ldk, const uint16_t* v,
+                               int64_t ldv, uint16_t* o, int64_t ldo, int S, int H, int H_KV, hipStream_t stream);
 
 hipError_t launch_sk_flags_clear(void* ws, hipStream_t stream);
 // Several matrices sharing x: one launch of the DMA-fed kernel where it takes them all (M >= 512),

@@ -392,10 +392,11 @@ def sdpa_prefill_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, n_heads
     _check_rows(out, S, n_heads * 128, "out")
     _check_device(q, k, v, out)
     L = _lib.lib()
-    need = L.nmi_sdpa_prefill_workspace_bytes(n_kv_heads, S)
-    ws = _block_ws(q.device, need)
+    need = L.nmi_sdpa_prefill_workspace_bytes(n_kv_heads, S)     # 0: the kernel reads q, k, v in place
+    ws = _block_ws(q.device, need) if need else None
     rc = L.nmi_sdpa_prefill_bf16(q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
-                                 out.data_ptr(), out.stride(0), S, n_heads, n_kv_heads, ws.data_ptr(), ws.numel(),
+                                 out.data_ptr(), out.stride(0), S, n_heads, n_kv_heads,
+                                 ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
                                  _stream())
     _lib.check(rc, "nmi_sdpa_prefill_bf16")
     return out
