@@ -295,12 +295,13 @@ constexpr int kQ = 64;                 // tokens per chunk
 constexpr int kPW = 16;                // rows of P per workgroup
 
 // LDS (bytes): B and C chunks [64][128] bf16 (256-byte rows, 16-byte chunk c at c ^ (row & 15));
-// B^T [128][64] bf16 and X^T [16][64] bf16 (128-byte rows, chunk at c ^ ((row >> 1) & 7)); G hi /
-// lo [64][64] bf16 (the same); (w x)^T hi / lo [16][64] bf16 (the same); S0 hi / lo [16][128] bf16
-// (chunk at c ^ (p & 15)); per-token float32 arrays.
-constexpr int kOffB = 0, kOffC = 16384, kOffBT = 32768, kOffXT = 49152, kOffGh = 51200, kOffGl = 59392,
-              kOffWXh = 67584, kOffWXl = 69632, kOffS = 71680, kOffCum = 79872, kOffEcum = kOffCum + 256,
-              kOffW = kOffEcum + 256, kOffDt = kOffW + 256, kOffFd = kOffDt + 256, kSsdLds = kOffFd + 256;
+// X^T [16][64] bf16 (128-byte rows, chunk at c ^ ((row >> 1) & 7)); G hi / lo [64][64] bf16 (the
+// same); (w x)^T hi / lo [16][64] bf16 (the same); S0 hi / lo [16][128] bf16 (chunk at c ^ (p &
+// 15)); two sets (chunk parity) of the per-token float32 arrays cum, ecum, w, dt, fd.
+constexpr int kOffB = 0, kOffC = 16384, kOffXT = 32768, kOffGh = 34816, kOffGl = 43008, kOffWXh = 51200,
+              kOffWXl = 53248, kOffS = 55296, kOffDec = 63488, kDecSet = 5 * 256, kSsdLds = kOffDec + 2 * kDecSet;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // v shifted right by K lanes within each row of 16 (0 where the source lies before the row)
@@ -342,17 +343,14 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     const float nA2 = -expf(a.A_log[h]) * 1.4426950408889634f;   // A in log2 units
     const float bias = a.dt_bias[h];
     const float Dh = a.D[h];
-    float* cum = reinterpret_cast<float*>(lds + kOffCum);        // c_j, log2 units
-    float* ecum = reinterpret_cast<float*>(lds + kOffEcum);      // exp(c_j)
-    float* wj = reinterpret_cast<float*>(lds + kOffW);           // exp(c_63 - c_j) dt_j
-    float* dts = reinterpret_cast<float*>(lds + kOffDt);
-    float* fd = reinterpret_cast<float*>(lds + kOffFd);          // exp(-c_j) dt_j (where finite)
+    // the decay arrays of set k (chunk parity): cum = c_j (log2 units), ecum = exp(c_j), wj =
+    // exp(c_63 - c_j) dt_j, dts = dt_j, fd = exp(-c_j) dt_j (where finite)
+    auto dec_arr = [&](int k, int i) { return reinterpret_cast<float*>(lds + kOffDec + k * kDecSet + i * 256); };
 
     // chunk staging in registers (the next chunk's loads are in flight during this one): B and C
     // rows (1024 chunks of 16 B each: 4 per thread), x (threads < 128: token tid / 2, P columns
-    // 8 (tid % 2) .. + 7 of the slice), dt (threads < 64)
+    // 8 (tid % 2) .. + 7 of the slice)
     uint4 rb[4], rc[4], rx = uint4{0u, 0u, 0u, 0u};
-    uint16_t rdt = 0;
     auto gload = [&](int t0) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -375,7 +373,40 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                            v[6] | ((uint32_t)v[7] << 16)};
             }
         }
-        if (tid < kQ) rdt = a.proj[(xrow0 + min(t0 + tid, S - 1)) * a.proj_ld + a.inter + a.conv_dim + h];
+    };
+    // dt of the chunk at t0 (wave 1 scans it one chunk ahead of its use)
+    auto load_dt = [&](int t0) {
+        return a.proj[(xrow0 + min(t0 + lane, S - 1)) * a.proj_ld + a.inter + a.conv_dim + h];
+    };
+    // Wave 1: softplus(dt + bias) (the reference's cut-offs) and the chunk's inclusive cumulative
+    // log2-decay (finite even where dt saturates: a decay that small is a reset either way), into
+    // decay set k; tokens at or past nt get dt = 0.
+    auto scan = [&](uint16_t dtb, int nt, int k) {
+        float dt = bf16_to_f32(dtb) + bias;
+        dt = dt > 20.f ? dt : (dt < -20.f ? 0.f : logf(1.f + expf(dt)));
+        dt = fminf(FLT_MAX, fmaxf(0.f, dt));
+        if (lane >= nt) dt = 0.f;
+        const float v = wave_incl_sum(fmaxf(nA2 * dt, -1e30f));
+        const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+        dec_arr(k, 0)[lane] = v;
+        dec_arr(k, 1)[lane] = fexp2(v);
+        dec_arr(k, 2)[lane] = fexp2(last - v) * dt;
+        dec_arr(k, 3)[lane] = dt;
+        dec_arr(k, 4)[lane] = fexp2(-v) * dt;
+    };
+    // B^T as the 16 x 16 x 32 A operand, straight from the row-major B chunk: rows n = n0 + l16,
+    // tokens 32 ks + 8 g4 + {0..7}, by two transposing reads (ds_read_b64_tr_b16: in each 16-lane
+    // group, output lane 4 a + b, element e is element b of source lane 4 e + a's 8 bytes; source
+    // lane s reads token row 32 ks + 8 g4 + 4 q + s / 4, columns n0 + 4 (s % 4) .. + 3)
+    auto bt_frag = [&](int n0, int ks) {
+        v4i16 v[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int j = 32 * ks + 8 * g4 + 4 * q + (l16 >> 2);
+            const int n = n0 + 4 * (l16 & 3);
+            v[q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds + kOffB + bc_off(j, n >> 3) + 2 * (n & 7)));
+        }
+        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
     };
 
     // the state, transposed, as two 16 x 16 MFMA accumulator blocks per wave: rows n = 16 (2 wave +
@@ -388,10 +419,25 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     *reinterpret_cast<uint4*>(lds + kOffS + 4096 + 16 * tid) = uint4{0u, 0u, 0u, 0u};
 
     gload(0);
-    for (int t0 = 0; t0 < S; t0 += kQ) {
+    // dt two chunks ahead (wave 1): chunk 0 scanned here, chunk c + 1 in chunk c's step (b)
+    uint16_t rdt1 = 0, rdt2 = 0;
+    if (wave == 1) {
+        const uint16_t rdt0 = load_dt(0);
+        rdt1 = load_dt(kQ);
+        scan(rdt0, min(kQ, S), 0);
+    }
+    // one chunk; rcur holds the next chunk's dt (wave 1), rnext receives the one after it (two
+    // register roles that alternate between calls, so no copy waits for a load in flight)
+    auto chunk = [&](int t0, uint16_t& rcur, uint16_t& rnext) {
+        const int par = (t0 / kQ) & 1;
+        const float* cum = dec_arr(par, 0);
+        const float* ecum = dec_arr(par, 1);
+        const float* wj = dec_arr(par, 2);
+        const float* dts = dec_arr(par, 3);
+        const float* fd = dec_arr(par, 4);
         const int nt = min(kQ, S - t0);
         // (a) the staged chunk into LDS (every wave has finished the previous chunk: barrier at the
-        // end of the loop): B and C row-major, x^T; the decay weights (wave 0)
+        // end of the loop): B and C row-major, x^T
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int q = tid + 256 * u;
@@ -409,22 +455,8 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                 *reinterpret_cast<uint16_t*>(lds + kOffXT + t_off(pc + e, j >> 3) + 2 * (j & 7)) =
                     (uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
         }
-        if (wave == 0) {
-            // softplus(dt + bias) (the reference's cut-offs), the chunk's inclusive cumulative
-            // log2-decay (finite even where dt saturates: a decay that small is a reset either way)
-            float dt = bf16_to_f32(rdt) + bias;
-            dt = dt > 20.f ? dt : (dt < -20.f ? 0.f : logf(1.f + expf(dt)));
-            dt = fminf(FLT_MAX, fmaxf(0.f, dt));
-            if (lane >= nt) dt = 0.f;
-            const float v = wave_incl_sum(fmaxf(nA2 * dt, -1e30f));
-            const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-            cum[lane] = v;
-            ecum[lane] = fexp2(v);
-            wj[lane] = fexp2(last - v) * dt;
-            dts[lane] = dt;
-            fd[lane] = fexp2(-v) * dt;
-        }
         if (t0 + kQ < S) gload(t0 + kQ);
+        if (wave == 1 && t0 + 2 * kQ < S) rnext = load_dt(t0 + 2 * kQ);
         __syncthreads();
 
         // (b) B C^T in 32 x 32 blocks: wave 0 (i, j < 32), 2 (i >= 32 > j) and 3 (i, j >= 32) take
@@ -432,10 +464,13 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         // r % 4 (register r), so each group of four registers is four consecutive tokens j of one
         // row i of G -- and form G on and below the diagonal in two bf16 parts (8-byte stores);
         // the block above the diagonal is zero and never read.  Where the chunk's decay stays
-        // above 2^-100, exp(c_i - c_j) = exp(c_i) exp(-c_j) with both factors finite.  Every
-        // thread then moves 32 elements of B into B^T and forms 4 elements of (w x)^T in two bf16
-        // parts (row p = tid / 16, tokens 4 (tid % 16) .. + 3).
-        if (wave != 1) {
+        // above 2^-100, exp(c_i - c_j) = exp(c_i) exp(-c_j) with both factors finite.  Wave 1
+        // meanwhile scans the next chunk's decay into the other set (its last readers finished
+        // before the previous chunk's closing barrier).  Every thread then forms 4 elements of
+        // (w x)^T in two bf16 parts (row p = tid / 16, tokens 4 (tid % 16) .. + 3).
+        if (wave == 1) {
+            if (t0 + kQ < S) scan(rcur, min(kQ, S - t0 - kQ), par ^ 1);
+        } else {
             const int bi = wave >> 1, bj = wave & 1;
             f32x16 cb;
 #pragma unroll
@@ -473,21 +508,6 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                 *reinterpret_cast<uint2*>(lds + kOffGh + off) = uint2{h01, h23};
                 *reinterpret_cast<uint2*>(lds + kOffGl + off) = uint2{l01, l23};
             }
-        }
-        // B^T rows from the row-major B: thread (n = tid % 128, token chunks 4 (tid / 128) + k,
-        // k = 0..3 of 8 tokens each) gathers 8 tokens of column n and stores 16 bytes
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int n = tid & 127, jc = 4 * (tid >> 7) + k;
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 8 * jc + 2 * e;
-                const uint32_t lo = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j, n >> 3) + 2 * (n & 7));
-                const uint32_t hi = *reinterpret_cast<const uint16_t*>(lds + kOffB + bc_off(j + 1, n >> 3) + 2 * (n & 7));
-                w[e] = lo | (hi << 16);
-            }
-            *reinterpret_cast<uint4*>(lds + kOffBT + t_off(n, jc)) = uint4{w[0], w[1], w[2], w[3]};
         }
         {
             const int p = tid >> 4, j4 = 4 * (tid & 15);
@@ -537,15 +557,14 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                     if (i0 + r < nt) yp[(size_t)r * a.y_ld] = (uint16_t)pack_bf16(__builtin_fmaf(Dh, xf[r], acc[r]), 0.f);
             }
             // S^T = exp(c_63) S0^T + B^T (w x): rows n = 16 (2 wave + nb) + 4 g4 + r, columns p = l16
-            // (A = B^T rows, B = (w x)^T rows in two parts)
+            // (A = B^T rows by transposing reads of B, B = (w x)^T rows in two parts)
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) st[nb][r] *= dec;
-                const int n = 16 * (2 * wave + nb) + l16;
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const bf16x8 ab = *reinterpret_cast<const bf16x8*>(lds + kOffBT + t_off(n, 4 * ks + g4));
+                    const bf16x8 ab = bt_frag(16 * (2 * wave + nb), ks);
                     const bf16x8 bh = *reinterpret_cast<const bf16x8*>(lds + kOffWXh + t_off(l16, 4 * ks + g4));
                     const bf16x8 bl = *reinterpret_cast<const bf16x8*>(lds + kOffWXl + t_off(l16, 4 * ks + g4));
                     st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bh, st[nb], 0, 0, 0);
@@ -568,6 +587,10 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             *reinterpret_cast<uint2*>(lds + kOffS + 4096 + off) = uint2{l01, l23};
         }
         __syncthreads();
+    };
+    for (int t0 = 0; t0 < S; t0 += 2 * kQ) {
+        chunk(t0, rdt1, rdt2);
+        if (t0 + kQ < S) chunk(t0 + kQ, rdt2, rdt1);
     }
     if (a.ssm_state && l16 < pw) {
 #pragma unroll
