@@ -284,10 +284,12 @@ __global__ __launch_bounds__(256, 4) void mamba_scan_kernel(const MambaPrefillAr
 //   y_i  = exp(c_i) (C_i . S0[p, :]) + sum_{j <= i} G_ij x_j + D x_i,
 //          G_ij = (C_i . B_j) exp(c_i - c_j) dt_j
 //   S    = exp(c_63) S0 + sum_j (w_j x_j) B_j^T.
-// C B^T is exact products of bf16 with float32 sums (v_mfma_f32_32x32x16_bf16); G, S0 and w x
-// enter their products in two bf16 parts (hi = bf16(v), lo = bf16(v - hi): about 16 significant
-// bits, finer than the reference's TF32 products) against exact bf16 x, C and B
-// (v_mfma_f32_16x16x32_bf16); the state accumulates in float32 MFMA registers across chunks.
+// All products on v_mfma_f32_16x16x32_bf16: C B^T exact bf16 products with float32 sums; G, S0
+// and w x enter their products in two bf16 parts (hi = bf16(v), lo = bf16(v - hi): about 16
+// significant bits, finer than the reference's TF32 products) against exact bf16 x, C and B; the
+// state accumulates in float32 MFMA registers across chunks.  Each wave forms the G rows of its
+// own 16 tokens and uses them straight from the MFMA output registers, so per chunk only the
+// staging of B, C and x and the state's two-part copy go through a barrier.
 // Each SIMD issues a wave64 VALU instruction over 4 cycles, so the per-element work is kept on
 // MFMA: what remains on VALU per chunk is the decay weights, the G mask and the two-part splits.
 // Tokens past the end of the sequence get dt = 0 and x = 0: no weight, no decay.
@@ -295,11 +297,11 @@ constexpr int kQ = 64;                 // tokens per chunk
 constexpr int kPW = 16;                // rows of P per workgroup
 
 // LDS (bytes): B and C chunks [64][128] bf16 (256-byte rows, 16-byte chunk c at c ^ (row & 15));
-// X^T [16][64] bf16 (128-byte rows, chunk at c ^ ((row >> 1) & 7)); G hi / lo [64][64] bf16 (the
-// same); (w x)^T hi / lo [16][64] bf16 (the same); S0 hi / lo [16][128] bf16 (chunk at c ^ (p &
-// 15)); two sets (chunk parity) of the per-token float32 arrays cum, ecum, w, dt, fd.
-constexpr int kOffB = 0, kOffC = 16384, kOffXT = 32768, kOffGh = 34816, kOffGl = 43008, kOffWXh = 51200,
-              kOffWXl = 53248, kOffS = 55296, kOffDec = 63488, kDecSet = 5 * 256, kSsdLds = kOffDec + 2 * kDecSet;
+// the x chunk [64][16] bf16 (32-byte rows); S0 hi / lo [16][128] bf16 (chunk at c ^ (p & 15)), two
+// buffers (chunk parity); two sets (chunk parity) of the per-token float32 arrays cum, ecum, w,
+// dt, fd.
+constexpr int kOffB = 0, kOffC = 16384, kOffX = 32768, kOffS = 34816, kSBuf = 8192, kOffDec = kOffS + 2 * kSBuf,
+              kDecSet = 5 * 256, kSsdLds = kOffDec + 2 * kDecSet;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
@@ -334,7 +336,6 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     const int b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l32 = lane & 31, hh = lane >> 5;                  // 32x32x16 operand layout
     const int l16 = lane & 15, g4 = lane >> 4;                  // 16x16x32 operand layout
     const int grp = h / (a.H / a.G);
     const int S = a.S;
@@ -394,10 +395,10 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         dec_arr(k, 3)[lane] = dt;
         dec_arr(k, 4)[lane] = fexp2(-v) * dt;
     };
-    // B^T as the 16 x 16 x 32 A operand, straight from the row-major B chunk: rows n = n0 + l16,
-    // tokens 32 ks + 8 g4 + {0..7}, by two transposing reads (ds_read_b64_tr_b16: in each 16-lane
-    // group, output lane 4 a + b, element e is element b of source lane 4 e + a's 8 bytes; source
-    // lane s reads token row 32 ks + 8 g4 + 4 q + s / 4, columns n0 + 4 (s % 4) .. + 3)
+    // Transposing LDS reads (ds_read_b64_tr_b16: in each 16-lane group, output lane 4 a + b, element
+    // e is element b of source lane 4 e + a's 8 bytes).  B^T as the A operand: rows n = n0 + l16,
+    // tokens 32 ks + 8 g4 + {0..7} (source lane s reads token row 32 ks + 8 g4 + 4 q + s / 4,
+    // columns n0 + 4 (s % 4) .. + 3).
     auto bt_frag = [&](int n0, int ks) {
         v4i16 v[2];
 #pragma unroll
@@ -408,26 +409,45 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         }
         return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
     };
+    // x^T: the four tokens j0 .. j0 + 3 of column p = l16 (j0 a multiple of 4) from the row-major
+    // x chunk (32-byte rows; source lane s reads row j0 + s / 4, columns 4 (s % 4) .. + 3)
+    auto xt4 = [&](int j0) {
+        return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds + kOffX + (j0 + (l16 >> 2)) * 32 + 8 * (l16 & 3)));
+    };
+    auto split = [&](const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const uint32_t w = pack_bf16(v[e], v[e + 1]);
+            hw[e >> 1] = w;
+            lw[e >> 1] = pack_bf16(v[e] - __uint_as_float(w << 16), v[e + 1] - __uint_as_float(w & 0xffff0000u));
+        }
+        hi = __builtin_bit_cast(bf16x8, uint4{hw[0], hw[1], hw[2], hw[3]});
+        lo = __builtin_bit_cast(bf16x8, uint4{lw[0], lw[1], lw[2], lw[3]});
+    };
 
     // the state, transposed, as two 16 x 16 MFMA accumulator blocks per wave: rows n = 16 (2 wave +
     // nb) + 4 g4 + r, columns p = l16
     f32x4 st[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) st[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // S0 hi / lo of the first chunk: zero (thread t clears 16 bytes of each)
+    // S0 hi / lo of the first chunk (buffer 0): zero (thread t clears 16 bytes of each)
     *reinterpret_cast<uint4*>(lds + kOffS + 16 * tid) = uint4{0u, 0u, 0u, 0u};
     *reinterpret_cast<uint4*>(lds + kOffS + 4096 + 16 * tid) = uint4{0u, 0u, 0u, 0u};
 
     gload(0);
-    // dt two chunks ahead (wave 1): chunk 0 scanned here, chunk c + 1 in chunk c's step (b)
+    // dt two chunks ahead (wave 1): chunk 0 scanned here, chunk c + 1 during chunk c
     uint16_t rdt1 = 0, rdt2 = 0;
     if (wave == 1) {
         const uint16_t rdt0 = load_dt(0);
         rdt1 = load_dt(kQ);
         scan(rdt0, min(kQ, S), 0);
     }
-    // one chunk; rcur holds the next chunk's dt (wave 1), rnext receives the one after it (two
-    // register roles that alternate between calls, so no copy waits for a load in flight)
+    // One chunk: (a) the staged chunk into LDS (B, C row-major; x row-major, zero past the
+    // sequence), the next chunk's loads, barrier; then each wave on its own (no barrier): rows
+    // i = 16 wave + l16 of G and y, rows n = 32 wave .. + 31 of the state; the new state's two-part
+    // copy into the other S0 buffer; barrier.  rcur holds the next chunk's dt (wave 1), rnext
+    // receives the one after it (register roles alternate between calls: no copy waits on a load).
     auto chunk = [&](int t0, uint16_t& rcur, uint16_t& rnext) {
         const int par = (t0 / kQ) & 1;
         const float* cum = dec_arr(par, 0);
@@ -436,8 +456,6 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         const float* dts = dec_arr(par, 3);
         const float* fd = dec_arr(par, 4);
         const int nt = min(kQ, S - t0);
-        // (a) the staged chunk into LDS (every wave has finished the previous chunk: barrier at the
-        // end of the loop): B and C row-major, x^T
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int q = tid + 256 * u;
@@ -446,145 +464,154 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             *reinterpret_cast<uint4*>(lds + kOffC + bc_off(j, cc)) = rc[u];
         }
         if (tid < 2 * kQ) {
-            // x^T: token j = tid / 2 of P columns 8 (tid % 2) + e (zero past the sequence)
             const int j = tid >> 1, pc = 8 * (tid & 1);
-            const uint4 v = j < nt ? rx : uint4{0u, 0u, 0u, 0u};
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                *reinterpret_cast<uint16_t*>(lds + kOffXT + t_off(pc + e, j >> 3) + 2 * (j & 7)) =
-                    (uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+            *reinterpret_cast<uint4*>(lds + kOffX + j * 32 + 2 * pc) = j < nt ? rx : uint4{0u, 0u, 0u, 0u};
         }
         if (t0 + kQ < S) gload(t0 + kQ);
         if (wave == 1 && t0 + 2 * kQ < S) rnext = load_dt(t0 + 2 * kQ);
         __syncthreads();
 
-        // (b) B C^T in 32 x 32 blocks: wave 0 (i, j < 32), 2 (i >= 32 > j) and 3 (i, j >= 32) take
-        // one each -- columns i = 32 (wave / 2) + l32, rows j = 32 (wave % 2) + 8 (r / 4) + 4 hh +
-        // r % 4 (register r), so each group of four registers is four consecutive tokens j of one
-        // row i of G -- and form G on and below the diagonal in two bf16 parts (8-byte stores);
-        // the block above the diagonal is zero and never read.  Where the chunk's decay stays
-        // above 2^-100, exp(c_i - c_j) = exp(c_i) exp(-c_j) with both factors finite.  Wave 1
-        // meanwhile scans the next chunk's decay into the other set (its last readers finished
-        // before the previous chunk's closing barrier).  Every thread then forms 4 elements of
-        // (w x)^T in two bf16 parts (row p = tid / 16, tokens 4 (tid % 16) .. + 3).
-        if (wave == 1) {
-            if (t0 + kQ < S) scan(rcur, min(kQ, S - t0 - kQ), par ^ 1);
-        } else {
-            const int bi = wave >> 1, bj = wave & 1;
-            f32x16 cb;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) cb[r] = 0.f;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const bf16x8 af = *reinterpret_cast<const bf16x8*>(lds + kOffB + bc_off(32 * bj + l32, 2 * s + hh));
-                const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(32 * bi + l32, 2 * s + hh));
-                cb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, cb, 0, 0, 0);
-            }
-            const int i = 32 * bi + l32;
-            const float ci = cum[i], ei = ecum[i];
-            const bool fact = cum[kQ - 1] > -100.f;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int j0 = 32 * bj + 8 * k + 4 * hh;
-                float gv[4];
-                if (fact) {
-                    const f32x4 fj = *reinterpret_cast<const f32x4*>(fd + j0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) gv[e] = j0 + e <= i ? cb[4 * k + e] * ei * fj[e] : 0.f;
-                } else {
-                    const f32x4 cj = *reinterpret_cast<const f32x4*>(cum + j0);
-                    const f32x4 dj = *reinterpret_cast<const f32x4*>(dts + j0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float d = fexp2(fminf(ci - cj[e], 0.f));
-                        gv[e] = j0 + e <= i ? cb[4 * k + e] * d * dj[e] : 0.f;
-                    }
-                }
-                const uint32_t h01 = pack_bf16(gv[0], gv[1]), h23 = pack_bf16(gv[2], gv[3]);
-                const uint32_t l01 = pack_bf16(gv[0] - __uint_as_float(h01 << 16), gv[1] - __uint_as_float(h01 & 0xffff0000u));
-                const uint32_t l23 = pack_bf16(gv[2] - __uint_as_float(h23 << 16), gv[3] - __uint_as_float(h23 & 0xffff0000u));
-                const int off = t_off(i, j0 >> 3) + 2 * (j0 & 7);
-                *reinterpret_cast<uint2*>(lds + kOffGh + off) = uint2{h01, h23};
-                *reinterpret_cast<uint2*>(lds + kOffGl + off) = uint2{l01, l23};
-            }
-        }
-        {
-            const int p = tid >> 4, j4 = 4 * (tid & 15);
-            const uint2 xv = *reinterpret_cast<const uint2*>(lds + kOffXT + t_off(p, j4 >> 3) + 2 * (j4 & 7));
-            const f32x4 wv = *reinterpret_cast<const f32x4*>(wj + j4);
-            const float v0 = bf16lo_to_f32(xv.x) * wv[0], v1 = bf16hi_to_f32(xv.x) * wv[1];
-            const float v2 = bf16lo_to_f32(xv.y) * wv[2], v3 = bf16hi_to_f32(xv.y) * wv[3];
-            const uint32_t h01 = pack_bf16(v0, v1), h23 = pack_bf16(v2, v3);
-            const uint32_t l01 = pack_bf16(v0 - __uint_as_float(h01 << 16), v1 - __uint_as_float(h01 & 0xffff0000u));
-            const uint32_t l23 = pack_bf16(v2 - __uint_as_float(h23 << 16), v3 - __uint_as_float(h23 & 0xffff0000u));
-            *reinterpret_cast<uint2*>(lds + kOffWXh + t_off(p, j4 >> 3) + 2 * (j4 & 7)) = uint2{h01, h23};
-            *reinterpret_cast<uint2*>(lds + kOffWXl + t_off(p, j4 >> 3) + 2 * (j4 & 7)) = uint2{l01, l23};
-        }
-        __syncthreads();
+        // wave 1: the next chunk's decay into the other set (its last readers finished before the
+        // previous chunk's closing barrier)
+        if (wave == 1 && t0 + kQ < S) scan(rcur, min(kQ, S - t0 - kQ), par ^ 1);
 
-        // (c) y for rows i = 16 wave + ..., 16 columns p (lane (l16, g4) holds rows 4 g4 + r of
-        // column p = l16): exp(c_i) C_i . S0 + G x + D x; and the state's products
-        const float dec = ecum[kQ - 1];
+        const int i = 16 * wave + l16;                           // this lane's token row of G and y
+        // C rows i as the B operand (k = n): used by C B^T and by S0 C^T
+        bf16x8 cf[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) cf[ks] = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(i, 4 * ks + g4));
+        // (C_i . B_j) for the token blocks jb <= wave: lane (column i, g4) holds j = 16 jb + 4 g4 + r
+        f32x4 cb[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            cb[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (jb <= wave) {
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + kOffB + bc_off(16 * jb + l16, 4 * ks + g4));
+                    cb[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, cf[ks], cb[jb], 0, 0, 0);
+                }
+            }
+        }
+        // y^T (rows p = 4 g4 + r, column i) = exp(c_i) (S0 C^T) + x^T G^T + D x
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const uint8_t* s0 = lds + kOffS + par * kSBuf;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8 af = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(16 * wave + l16, 4 * ks + g4));
-                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(lds + kOffS + s_off(l16, 4 * ks + g4));
-                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(lds + kOffS + 4096 + s_off(l16, 4 * ks + g4));
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bh, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bl, acc, 0, 0, 0);
+                const bf16x8 sh = *reinterpret_cast<const bf16x8*>(s0 + s_off(l16, 4 * ks + g4));
+                const bf16x8 sl = *reinterpret_cast<const bf16x8*>(s0 + 4096 + s_off(l16, 4 * ks + g4));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sh, cf[ks], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sl, cf[ks], acc, 0, 0, 0);
             }
+        }
+        const float ei = ecum[i];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] *= ecum[16 * wave + 4 * g4 + r];
+        for (int r = 0; r < 4; ++r) acc[r] *= ei;
+        // G_ij = (C_i . B_j) exp(c_i - c_j) dt_j on and below the diagonal, in two bf16 parts, as the
+        // B operand of pairs of token blocks (k = 8 g4 + 4 q + r <-> j = 16 (2 m + q) + 4 g4 + r), times
+        // the matching x^T (two transposing reads); where the chunk's decay stays above 2^-100,
+        // exp(c_i - c_j) = exp(c_i) exp(-c_j) with both factors finite
+        {
+            const float ci = cum[i];
+            const bool fact = cum[kQ - 1] > -100.f;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                if (ks == 1 && wave < 2) break;                     // rows i < 32: G is zero at j >= 32
-                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(lds + kOffGh + t_off(16 * wave + l16, 4 * ks + g4));
-                const bf16x8 al = *reinterpret_cast<const bf16x8*>(lds + kOffGl + t_off(16 * wave + l16, 4 * ks + g4));
-                const bf16x8 bx = *reinterpret_cast<const bf16x8*>(lds + kOffXT + t_off(l16, 4 * ks + g4));
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bx, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bx, acc, 0, 0, 0);
+            for (int m = 0; m < 2; ++m) {
+                if (2 * m <= wave) {
+                    float gv[8];
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const int jb = 2 * m + q;
+                        const int j0 = 16 * jb + 4 * g4;
+                        if (jb <= wave) {
+                            if (fact) {
+                                const f32x4 fj = *reinterpret_cast<const f32x4*>(fd + j0);
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) gv[4 * q + r] = j0 + r <= i ? cb[jb][r] * ei * fj[r] : 0.f;
+                            } else {
+                                const f32x4 cj = *reinterpret_cast<const f32x4*>(cum + j0);
+                                const f32x4 dj = *reinterpret_cast<const f32x4*>(dts + j0);
+#pragma unroll
+                                for (int r = 0; r < 4; ++r)
+                                    gv[4 * q + r] = j0 + r <= i ? cb[jb][r] * fexp2(fminf(ci - cj[r], 0.f)) * dj[r] : 0.f;
+                            }
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) gv[4 * q + r] = 0.f;
+                        }
+                    }
+                    bf16x8 gh, gl;
+                    split(gv, gh, gl);
+                    const v4i16 x0 = xt4(32 * m + 4 * g4), x1 = xt4(32 * m + 16 + 4 * g4);
+                    const bf16x8 xf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, gh, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, gl, acc, 0, 0, 0);
+                }
             }
-            const int i0 = 16 * wave + 4 * g4;                      // 4 consecutive tokens of column p
-            const uint2 xv = *reinterpret_cast<const uint2*>(lds + kOffXT + t_off(l16, i0 >> 3) + 2 * (i0 & 7));
+        }
+        {
+            // + D x: x[i][4 g4 .. + 3]; y[i][p0 + 4 g4 + r]
+            const uint2 xv = *reinterpret_cast<const uint2*>(lds + kOffX + i * 32 + 8 * g4);
             const float xf[4] = {bf16lo_to_f32(xv.x), bf16hi_to_f32(xv.x), bf16lo_to_f32(xv.y), bf16hi_to_f32(xv.y)};
-            if (l16 < pw) {
-                uint16_t* yp = a.y + (xrow0 + t0 + i0) * a.y_ld + h * a.P + p0 + l16;
+            float yv[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (i0 + r < nt) yp[(size_t)r * a.y_ld] = (uint16_t)pack_bf16(__builtin_fmaf(Dh, xf[r], acc[r]), 0.f);
+            for (int r = 0; r < 4; ++r) yv[r] = __builtin_fmaf(Dh, xf[r], acc[r]);
+            if (i < nt) {
+                uint16_t* yp = a.y + (xrow0 + t0 + i) * a.y_ld + h * a.P + p0 + 4 * g4;
+                if (a.y_vec && 4 * g4 + 4 <= pw) {
+                    *reinterpret_cast<uint2*>(yp) = uint2{pack_bf16(yv[0], yv[1]), pack_bf16(yv[2], yv[3])};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (4 * g4 + r < pw) yp[r] = (uint16_t)pack_bf16(yv[r], 0.f);
+                }
             }
-            // S^T = exp(c_63) S0^T + B^T (w x): rows n = 16 (2 wave + nb) + 4 g4 + r, columns p = l16
-            // (A = B^T rows by transposing reads of B, B = (w x)^T rows in two parts)
+        }
+        // S^T = exp(c_63) S0^T + B^T (w x): rows n = 16 (2 wave + nb) + 4 g4 + r, columns p = l16; A =
+        // B^T (transposing reads of B), B = (w x) in two parts (k = 8 g4 + 4 q + e <-> token
+        // 32 ks + 8 g4 + 4 q + e, x^T by transposing reads)
+        {
+            const float dec = ecum[kQ - 1];
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
+            for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) st[nb][r] *= dec;
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
+            for (int ks = 0; ks < 2; ++ks) {
+                float wv[8];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int j0 = 32 * ks + 8 * g4 + 4 * q;
+                    const v4i16 xq = xt4(j0);
+                    const f32x4 w4 = *reinterpret_cast<const f32x4*>(wj + j0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        wv[4 * q + e] = bf16_to_f32((uint16_t)xq[e]) * w4[e];
+                }
+                bf16x8 wh, wl;
+                split(wv, wh, wl);
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
                     const bf16x8 ab = bt_frag(16 * (2 * wave + nb), ks);
-                    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(lds + kOffWXh + t_off(l16, 4 * ks + g4));
-                    const bf16x8 bl = *reinterpret_cast<const bf16x8*>(lds + kOffWXl + t_off(l16, 4 * ks + g4));
-                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bh, st[nb], 0, 0, 0);
-                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bl, st[nb], 0, 0, 0);
+                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, wh, st[nb], 0, 0, 0);
+                    st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, wl, st[nb], 0, 0, 0);
                 }
             }
-        }
-        __syncthreads();
-        // (d) the new state's two bf16 parts for the next chunk (S0 was read above: barrier): four
-        // consecutive n of row p = l16 per block
+            // the new state's two bf16 parts into the other S0 buffer (its readers, the previous
+            // chunk, finished before that chunk's closing barrier): four consecutive n of row p =
+            // l16 per block
+            uint8_t* s1 = lds + kOffS + (par ^ 1) * kSBuf;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const int n0 = 16 * (2 * wave + nb) + 4 * g4;
-            const f32x4 v = st[nb];
-            const uint32_t h01 = pack_bf16(v[0], v[1]), h23 = pack_bf16(v[2], v[3]);
-            const uint32_t l01 = pack_bf16(v[0] - __uint_as_float(h01 << 16), v[1] - __uint_as_float(h01 & 0xffff0000u));
-            const uint32_t l23 = pack_bf16(v[2] - __uint_as_float(h23 << 16), v[3] - __uint_as_float(h23 & 0xffff0000u));
-            const int off = s_off(l16, n0 >> 3) + 2 * (n0 & 7);
-            *reinterpret_cast<uint2*>(lds + kOffS + off) = uint2{h01, h23};
-            *reinterpret_cast<uint2*>(lds + kOffS + 4096 + off) = uint2{l01, l23};
+            for (int nb = 0; nb < 2; ++nb) {
+                const int n0 = 16 * (2 * wave + nb) + 4 * g4;
+                const f32x4 v = st[nb];
+                const uint32_t h01 = pack_bf16(v[0], v[1]), h23 = pack_bf16(v[2], v[3]);
+                const uint32_t l01 = pack_bf16(v[0] - __uint_as_float(h01 << 16), v[1] - __uint_as_float(h01 & 0xffff0000u));
+                const uint32_t l23 = pack_bf16(v[2] - __uint_as_float(h23 << 16), v[3] - __uint_as_float(h23 & 0xffff0000u));
+                const int off = s_off(l16, n0 >> 3) + 2 * (n0 & 7);
+                *reinterpret_cast<uint2*>(s1 + off) = uint2{h01, h23};
+                *reinterpret_cast<uint2*>(s1 + 4096 + off) = uint2{l01, l23};
+            }
         }
         __syncthreads();
     };
