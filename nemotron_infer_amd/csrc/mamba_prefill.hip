@@ -20,6 +20,7 @@
 #include "nmi_launch.hpp"
 
 #include <cfloat>
+#include <type_traits>
 
 namespace nmi {
 
@@ -299,9 +300,9 @@ constexpr int kPW = 16;                // rows of P per workgroup
 // LDS (bytes): B and C chunks [64][128] bf16 (256-byte rows, 16-byte chunk c at c ^ (row & 15));
 // the x chunk [64][16] bf16 (32-byte rows); S0 hi / lo [16][128] bf16 (chunk at c ^ (p & 15)), two
 // buffers (chunk parity); two sets (chunk parity) of the per-token float32 arrays cum, ecum, w,
-// dt, fd.
+// dt.
 constexpr int kOffB = 0, kOffC = 16384, kOffX = 32768, kOffS = 34816, kSBuf = 8192, kOffDec = kOffS + 2 * kSBuf,
-              kDecSet = 5 * 256, kSsdLds = kOffDec + 2 * kDecSet;
+              kDecSet = 4 * 256, kSsdLds = kOffDec + 2 * kDecSet;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
@@ -345,14 +346,14 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     const float bias = a.dt_bias[h];
     const float Dh = a.D[h];
     // the decay arrays of set k (chunk parity): cum = c_j (log2 units), ecum = exp(c_j), wj =
-    // exp(c_63 - c_j) dt_j, dts = dt_j, fd = exp(-c_j) dt_j (where finite)
-    auto dec_arr = [&](int k, int i) { return reinterpret_cast<float*>(lds + kOffDec + k * kDecSet + i * 256); };
+    // exp(c_63 - c_j) dt_j, dts = dt_j
+    auto dec_arr = [&](int k, int i) __attribute__((always_inline)) { return reinterpret_cast<float*>(lds + kOffDec + k * kDecSet + i * 256); };
 
     // chunk staging in registers (the next chunk's loads are in flight during this one): B and C
     // rows (1024 chunks of 16 B each: 4 per thread), x (threads < 128: token tid / 2, P columns
     // 8 (tid % 2) .. + 7 of the slice)
     uint4 rb[4], rc[4], rx = uint4{0u, 0u, 0u, 0u};
-    auto gload = [&](int t0) {
+    auto gload = [&](int t0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int q = tid + 256 * u;
@@ -376,13 +377,13 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         }
     };
     // dt of the chunk at t0 (wave 1 scans it one chunk ahead of its use)
-    auto load_dt = [&](int t0) {
+    auto load_dt = [&](int t0) __attribute__((always_inline)) {
         return a.proj[(xrow0 + min(t0 + lane, S - 1)) * a.proj_ld + a.inter + a.conv_dim + h];
     };
     // Wave 1: softplus(dt + bias) (the reference's cut-offs) and the chunk's inclusive cumulative
     // log2-decay (finite even where dt saturates: a decay that small is a reset either way), into
     // decay set k; tokens at or past nt get dt = 0.
-    auto scan = [&](uint16_t dtb, int nt, int k) {
+    auto scan = [&](uint16_t dtb, int nt, int k) __attribute__((always_inline)) {
         float dt = bf16_to_f32(dtb) + bias;
         dt = dt > 20.f ? dt : (dt < -20.f ? 0.f : logf(1.f + expf(dt)));
         dt = fminf(FLT_MAX, fmaxf(0.f, dt));
@@ -393,13 +394,12 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         dec_arr(k, 1)[lane] = fexp2(v);
         dec_arr(k, 2)[lane] = fexp2(last - v) * dt;
         dec_arr(k, 3)[lane] = dt;
-        dec_arr(k, 4)[lane] = fexp2(-v) * dt;
     };
     // Transposing LDS reads (ds_read_b64_tr_b16: in each 16-lane group, output lane 4 a + b, element
     // e is element b of source lane 4 e + a's 8 bytes).  B^T as the A operand: rows n = n0 + l16,
     // tokens 32 ks + 8 g4 + {0..7} (source lane s reads token row 32 ks + 8 g4 + 4 q + s / 4,
     // columns n0 + 4 (s % 4) .. + 3).
-    auto bt_frag = [&](int n0, int ks) {
+    auto bt_frag = [&](int n0, int ks) __attribute__((always_inline)) {
         v4i16 v[2];
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     };
     // x^T: the four tokens j0 .. j0 + 3 of column p = l16 (j0 a multiple of 4) from the row-major
     // x chunk (32-byte rows; source lane s reads row j0 + s / 4, columns 4 (s % 4) .. + 3)
-    auto xt4 = [&](int j0) {
+    auto xt4 = [&](int j0) __attribute__((always_inline)) {
         return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds + kOffX + (j0 + (l16 >> 2)) * 32 + 8 * (l16 & 3)));
     };
     auto split = [&](const float (&v)[8], bf16x8& hi, bf16x8& lo) {
@@ -448,13 +448,13 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
     // i = 16 wave + l16 of G and y, rows n = 32 wave .. + 31 of the state; the new state's two-part
     // copy into the other S0 buffer; barrier.  rcur holds the next chunk's dt (wave 1), rnext
     // receives the one after it (register roles alternate between calls: no copy waits on a load).
-    auto chunk = [&](int t0, uint16_t& rcur, uint16_t& rnext) {
+    auto chunk = [&](auto W, int t0, uint16_t& rcur, uint16_t& rnext) __attribute__((always_inline)) {
+        constexpr int w = decltype(W)::value;                    // this wave (a constant per instantiation)
         const int par = (t0 / kQ) & 1;
         const float* cum = dec_arr(par, 0);
         const float* ecum = dec_arr(par, 1);
         const float* wj = dec_arr(par, 2);
         const float* dts = dec_arr(par, 3);
-        const float* fd = dec_arr(par, 4);
         const int nt = min(kQ, S - t0);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -468,29 +468,27 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             *reinterpret_cast<uint4*>(lds + kOffX + j * 32 + 2 * pc) = j < nt ? rx : uint4{0u, 0u, 0u, 0u};
         }
         if (t0 + kQ < S) gload(t0 + kQ);
-        if (wave == 1 && t0 + 2 * kQ < S) rnext = load_dt(t0 + 2 * kQ);
+        if (w == 1 && t0 + 2 * kQ < S) rnext = load_dt(t0 + 2 * kQ);
         __syncthreads();
 
         // wave 1: the next chunk's decay into the other set (its last readers finished before the
         // previous chunk's closing barrier)
-        if (wave == 1 && t0 + kQ < S) scan(rcur, min(kQ, S - t0 - kQ), par ^ 1);
+        if (w == 1 && t0 + kQ < S) scan(rcur, min(kQ, S - t0 - kQ), par ^ 1);
 
-        const int i = 16 * wave + l16;                           // this lane's token row of G and y
+        const int i = 16 * w + l16;                              // this lane's token row of G and y
         // C rows i as the B operand (k = n): used by C B^T and by S0 C^T
         bf16x8 cf[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) cf[ks] = *reinterpret_cast<const bf16x8*>(lds + kOffC + bc_off(i, 4 * ks + g4));
-        // (C_i . B_j) for the token blocks jb <= wave: lane (column i, g4) holds j = 16 jb + 4 g4 + r
-        f32x4 cb[4];
+        // (C_i . B_j) for the token blocks jb <= w: lane (column i, g4) holds j = 16 jb + 4 g4 + r
+        f32x4 cb[w + 1];
 #pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
+        for (int jb = 0; jb <= w; ++jb) {
             cb[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (jb <= wave) {
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + kOffB + bc_off(16 * jb + l16, 4 * ks + g4));
-                    cb[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, cf[ks], cb[jb], 0, 0, 0);
-                }
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + kOffB + bc_off(16 * jb + l16, 4 * ks + g4));
+                cb[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, cf[ks], cb[jb], 0, 0, 0);
             }
         }
         // y^T (rows p = 4 g4 + r, column i) = exp(c_i) (S0 C^T) + x^T G^T + D x
@@ -508,33 +506,26 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         const float ei = ecum[i];
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] *= ei;
-        // G_ij = (C_i . B_j) exp(c_i - c_j) dt_j on and below the diagonal, in two bf16 parts, as the
+        // G_ij = (C_i . B_j) exp2(min(c_i - c_j, 0)) dt_j on and below the diagonal (one exp2 per
+        // element: no factorisation, so no range test and no branch), in two bf16 parts, as the
         // B operand of pairs of token blocks (k = 8 g4 + 4 q + r <-> j = 16 (2 m + q) + 4 g4 + r), times
-        // the matching x^T (two transposing reads); where the chunk's decay stays above 2^-100,
-        // exp(c_i - c_j) = exp(c_i) exp(-c_j) with both factors finite
+        // the matching x^T (two transposing reads)
         {
             const float ci = cum[i];
-            const bool fact = cum[kQ - 1] > -100.f;
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                if (2 * m <= wave) {
+            for (int m = 0; 2 * m <= w; ++m) {
+                {
                     float gv[8];
 #pragma unroll
                     for (int q = 0; q < 2; ++q) {
                         const int jb = 2 * m + q;
                         const int j0 = 16 * jb + 4 * g4;
-                        if (jb <= wave) {
-                            if (fact) {
-                                const f32x4 fj = *reinterpret_cast<const f32x4*>(fd + j0);
+                        if (jb <= w) {
+                            const f32x4 cj = *reinterpret_cast<const f32x4*>(cum + j0);
+                            const f32x4 dj = *reinterpret_cast<const f32x4*>(dts + j0);
 #pragma unroll
-                                for (int r = 0; r < 4; ++r) gv[4 * q + r] = j0 + r <= i ? cb[jb][r] * ei * fj[r] : 0.f;
-                            } else {
-                                const f32x4 cj = *reinterpret_cast<const f32x4*>(cum + j0);
-                                const f32x4 dj = *reinterpret_cast<const f32x4*>(dts + j0);
-#pragma unroll
-                                for (int r = 0; r < 4; ++r)
-                                    gv[4 * q + r] = j0 + r <= i ? cb[jb][r] * fexp2(fminf(ci - cj[r], 0.f)) * dj[r] : 0.f;
-                            }
+                            for (int r = 0; r < 4; ++r)
+                                gv[4 * q + r] = j0 + r <= i ? cb[jb][r] * fexp2(fminf(ci - cj[r], 0.f)) * dj[r] : 0.f;
                         } else {
 #pragma unroll
                             for (int r = 0; r < 4; ++r) gv[4 * q + r] = 0.f;
@@ -592,7 +583,7 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
                 split(wv, wh, wl);
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
-                    const bf16x8 ab = bt_frag(16 * (2 * wave + nb), ks);
+                    const bf16x8 ab = bt_frag(16 * (2 * w + nb), ks);
                     st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, wh, st[nb], 0, 0, 0);
                     st[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, wl, st[nb], 0, 0, 0);
                 }
@@ -603,7 +594,7 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
             uint8_t* s1 = lds + kOffS + (par ^ 1) * kSBuf;
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
-                const int n0 = 16 * (2 * wave + nb) + 4 * g4;
+                const int n0 = 16 * (2 * w + nb) + 4 * g4;
                 const f32x4 v = st[nb];
                 const uint32_t h01 = pack_bf16(v[0], v[1]), h23 = pack_bf16(v[2], v[3]);
                 const uint32_t l01 = pack_bf16(v[0] - __uint_as_float(h01 << 16), v[1] - __uint_as_float(h01 & 0xffff0000u));
@@ -615,9 +606,18 @@ __global__ __launch_bounds__(256, 2) void mamba_ssd_kernel(const MambaPrefillArg
         }
         __syncthreads();
     };
-    for (int t0 = 0; t0 < S; t0 += 2 * kQ) {
-        chunk(t0, rdt1, rdt2);
-        if (t0 + kQ < S) chunk(t0 + kQ, rdt2, rdt1);
+    // each wave runs a loop specialised to its index (the same barriers in every instantiation)
+    auto run = [&](auto W) __attribute__((always_inline)) {
+        for (int t0 = 0; t0 < S; t0 += 2 * kQ) {
+            chunk(W, t0, rdt1, rdt2);
+            if (t0 + kQ < S) chunk(W, t0 + kQ, rdt2, rdt1);
+        }
+    };
+    switch (wave) {
+        case 0: run(std::integral_constant<int, 0>{}); break;
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        default: run(std::integral_constant<int, 3>{}); break;
     }
     if (a.ssm_state && l16 < pw) {
 #pragma unroll
