@@ -53,6 +53,7 @@ struct PrefillArgs {
     uint16_t* o;            // [S, ldo], head h at column 128 h
     int64_t ldq, ldk, ldv, ldo;
     int S, H, H_KV, qtiles;
+    int nslot;              // workgroups per pass of the dispatcher (one per CU)
     float scale2;           // log2(e) / sqrt(128)
 };
 
@@ -70,9 +71,15 @@ __global__ __launch_bounds__(256, 2) void sdpa_prefill_kernel(const PrefillArgs 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, l32 = lane & 31;
-    // longest tiles first over all heads: workgroup g takes query tile qtiles - 1 - g / H of head g % H
-    const int qt = a.qtiles - 1 - (int)blockIdx.x / a.H;
-    const int head = (int)blockIdx.x - (int)blockIdx.x / a.H * a.H;
+    // Tiles by rank, longest first over all heads: rank r is query tile qtiles - 1 - r / H of head
+    // r % H.  The dispatcher gives each CU one workgroup per pass (workgroups g and g + nslot
+    // share a CU), so the second pass takes its ranks in reverse: a CU then holds a long and a
+    // short tile of about the same sum; the rest follow longest first.
+    const int total = a.qtiles * a.H, g = (int)blockIdx.x;
+    const int n2 = min(2 * a.nslot, total);
+    const int rank = (g >= a.nslot && g < n2) ? a.nslot + (n2 - 1 - g) : g;
+    const int qt = a.qtiles - 1 - rank / a.H;
+    const int head = rank - rank / a.H * a.H;
     const int kvh = head / (a.H / a.H_KV);
     const int q0 = qt * kBQ;
     const int qw = q0 + 32 * wave;                              // the wave's first query row
@@ -374,6 +381,7 @@ hipError_t launch_sdpa_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k
     a.H = H;
     a.H_KV = H_KV;
     a.qtiles = (S + kBQ - 1) / kBQ;
+    a.nslot = device_info().num_cu;
     a.scale2 = 1.4426950408889634f / sqrtf((float)kD);
     hipLaunchKernelGGL(sdpa_prefill_kernel, dim3(a.qtiles * H), dim3(256), kLds, stream, a);
     return hipGetLastError();
