@@ -44,6 +44,21 @@ def test_sdpa_prefill_matches_oracle(S):
     assert_parity(bits(o), attention.sdpa_prefill(q, k, v, H_KV), f"S={S}")
 
 
+@pytest.mark.parametrize("S", [1537, 2048])
+def test_sdpa_prefill_long_prompts(S):
+    """Prompts of 1537 and 2048 tokens (8 query heads, 2 KV heads): query tiles up to 32 key tiles
+    long, so every stage refill, the partial last key tile and the tile-rank order of the launch
+    are exercised at the bench's length."""
+    H, n_kv = 8, 2
+    announce("sdpa_prefill_long", S)
+    q = _bf16_np((S, H * D), 700 + S)
+    k = _bf16_np((S, n_kv * D), 800 + S)
+    v = _bf16_np((S, n_kv * D), 900 + S)
+    o = ops.sdpa_prefill_bf16(x_to_dev(q), x_to_dev(k), x_to_dev(v), H, n_kv)
+    torch.cuda.synchronize()
+    assert_parity(bits(o), attention.sdpa_prefill(q, k, v, n_kv), f"S={S}")
+
+
 @pytest.mark.parametrize("H,n_kv", [(8, 8), (12, 4), (6, 1), (16, 2)])
 def test_sdpa_prefill_gqa_and_packed_rows(H, n_kv):
     """q, k and v as column slices of one packed [S, (H + 2 n_kv) * 128] buffer (the layout of a
