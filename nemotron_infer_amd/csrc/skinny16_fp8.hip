@@ -394,18 +394,30 @@ struct S16Input {
     int K;
 };
 
-// Fills the launch's group table (the row tiles of each matrix in order); returns the tile count.
+// Fills the launch's group table (the row tiles of each matrix in turn); returns the tile count.
+// The matrices go in order of decreasing K (a stable order): a tile's time grows with K, and the
+// dispatcher hands out workgroups in tile order, so the longest tiles start in the first round
+// and the short ones fill the gaps behind them instead of forming the launch's tail (config 2's
+// batch: down_proj's K = 12544 tiles, four times an up_proj tile, were dispatched last).  Which
+// workgroup computes a tile does not change its result.
 template <int R>
 int s16_tables(S16Args& a, const GemvGroup* groups, const S16Input* in, int ng) {
-    int tb = 0;
+    int order[kS16MaxGroups];
     for (int i = 0; i < ng; ++i) {
+        int j = i;
+        for (; j > 0 && in[order[j - 1]].K < in[i].K; --j) order[j] = order[j - 1];
+        order[j] = i;
+    }
+    int tb = 0;
+    for (int t = 0; t < ng; ++t) {
+        const int i = order[t];
         const GemvGroup& G = groups[i];
         const Epi& e = G.epi;
         const bool res = e.kind == kEpiResidual;
         const bool vec = (reinterpret_cast<uintptr_t>(G.s) & 15) == 0 && (reinterpret_cast<uintptr_t>(G.y) & 7) == 0 &&
                          (G.ldy & 3) == 0 &&
                          (!res || ((reinterpret_cast<uintptr_t>(e.res) & 7) == 0 && (e.ldres & 3) == 0));
-        a.g[i] = S16Group{in[i].x, in[i].ldx, in[i].K, G.W, G.ldw, G.s, G.y, G.ldy, res ? e.res : nullptr, e.ldres, G.N,
+        a.g[t] = S16Group{in[i].x, in[i].ldx, in[i].K, G.W, G.ldw, G.s, G.y, G.ldy, res ? e.res : nullptr, e.ldres, G.N,
                           tb, e.kind, vec ? 1 : 0};
         tb += (G.N + 16 * R - 1) / (16 * R);
     }
