@@ -490,13 +490,14 @@ bool s16_launch(const GemvGroup* groups, const S16Input* in, int ngroups, int M,
     // the row-run form.
     const Tuning& tn = tuning();
     // A batch of independent linears (one launch over a whole decode set, thousands of row
-    // tiles) takes its own choices, measured on MI355X for config 2's six linears: row tiles of
-    // 16 at M <= 4 (M = 2 / 4: 27.2 / 28.0 against 29.8 / 31.4 us with 32), of 32 above; four
-    // waves above M = 8 (M = 16: 37.7 against 44.1 us with two), two at M <= 8.
-    const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : batch ? (M <= 4 ? 1 : 2) : (rows >= 4096 ? 2 : 1);
+    // tiles, the longest-K matrices first) takes its own choices, measured on MI355X for config
+    // 2's six linears (one box, the other forms in brackets): row tiles of 16 up to M = 8 (M = 8
+    // 26.8 us [28.3 with 32]), of 32 above (M = 16 29.5 [41.4 with 16]); two waves per workgroup
+    // above M = 4 (M = 16 29.5 [32.1 with four]), four at M <= 4 (M = 2 22.9 [23.3 with two]).
+    const int R = tn.s16_r == 1 || tn.s16_r == 2 ? tn.s16_r : batch ? (M <= 8 ? 1 : 2) : (rows >= 4096 ? 2 : 1);
     int tiles = 0;
     for (int i = 0; i < ngroups; ++i) tiles += (groups[i].N + 16 * R - 1) / (16 * R);
-    const bool four = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w == 4 : batch ? M > 8 : tiles <= device_info().num_cu;
+    const bool four = tn.s16_w == 2 || tn.s16_w == 4 ? tn.s16_w == 4 : batch ? M <= 4 : tiles <= device_info().num_cu;
     bool dma_ok = true;
     for (int i = 0; i < ngroups; ++i)
         dma_ok = dma_ok && (in[i].ldx * 2) * (int64_t)(M - 1) + 2 * (int64_t)in[i].K < ((int64_t)1 << 31) &&
