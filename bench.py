@@ -4,7 +4,7 @@
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--no-extras]
                     [--only stream|decode|prefill|prefill_small|block|skinny|attn|mamba|engine|prefill_attn|prefill_mamba]
 
-Headline (``value``): BASELINE config 4, the full decode-step weight stream at M = 1 -- 4
+Headline (``value``): config 4 of the reference's benchmark, the full decode-step weight stream at M = 1 -- 4
 attention layers (q|k|v grouped: they share one normed input, model/attention_block.cuh:400-402;
 then o), 17 MLP layers (up, down) and 21 Mamba layers (in_proj with ragged N = 14690, out_proj
 with K = 6272): 92 GEMVs over 2.87 GB of e4m3 weights, each GEMV on its own seeded activation.
@@ -885,7 +885,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the fp8 linear "
-              f"path is single-GPU, and how it would shard is a design note (DESIGN.md)", file=sys.stderr)
+              f"path is single-GPU here; how it would shard is a design note, not code", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -134,12 +134,13 @@ int nmi_linear_fp8_w8a16_grouped(const void* x_bf16, int64_t ldx, int M, int K,
 
 /*
  * Independent linears in one dispatch: job i computes y_i[M, N_i] = bf16((x_i . e4m3(W_i)^T) * s_i)
- * with its own activations x_i [M, K_i] -- a set of projections whose inputs are all ready, as
- * BASELINE config 2 runs the decode shapes.  No counterpart in the reference, which launches one
+ * with its own activations x_i [M, K_i] -- a set of projections whose inputs are all ready (the
+ * decode shapes with an independent activation row per sequence).  No counterpart in the reference, which launches one
  * GEMV or GEMM per projection (ops/gemv.cuh:92-104, ops/gemm.cuh:325-337); it is the skinny-M
  * sibling of the GEMV chain below.  For 2 <= M <= 16, when the 16x16x32 skinny kernel takes
  * every job (K_i % 64 == 0, 16-byte aligned x_i rows and W_i rows), the jobs run as one kernel
- * launch (one row tile per workgroup over all of the jobs' rows); otherwise each job runs as
+ * launch (one row tile per workgroup over all of the jobs' rows, the jobs of largest K_i first:
+ * their tiles take longest, so they start in the first round); otherwise each job runs as
  * nmi_linear_fp8_w8a16 (no workspace) would run it, one after another.  Every output is the one
  * a separate call with the same kernel schedule gives.  Each job is validated like
  * nmi_linear_fp8_w8a16; 1 <= njobs <= NMI_MAX_BATCH.

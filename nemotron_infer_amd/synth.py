@@ -1,4 +1,4 @@
-"""Seeded synthetic workloads of the benchmark configurations.
+"""Seeded synthetic workloads of the benchmark configurations (the reference benchmark's configs 0-4).
 
 Weights: float32 N(0, 0.02) from a seeded generator, per-tensor scale s = amax / 448,
 codes = RNE(clamp(W / s, +-448)) as float8_e4m3fn, the scale broadcast to a per-row vector

@@ -28,5 +28,5 @@ Pinning (what checks each function against something other than itself)
 No function of this oracle is "parity unpinned".
 
 The reference itself cannot be compiled here (CUDA/nvcc/cuBLASLt only), so there is no
-``oracle/_ref`` build; see DESIGN.md.
+``oracle/_ref`` build.
 """
