@@ -51,7 +51,7 @@ ROTATION_BYTES = 1 << 30
 # FETCH_SIZE / WRITE_SIZE runs of `bench.py --only stream` scaled by a 256 MiB copy
 # (profiles/gemv_chain_config4_decode_stream.md).  Re-measured when the GEMV kernels change;
 # reported as roofline.traffic next to the algorithmic bytes.  None until measured.
-MEASURED_TRAFFIC = {"chain_config4": 2904229512}
+MEASURED_TRAFFIC = {"chain_config4": 2902926840}
 
 
 def log(*a):
